@@ -1,0 +1,120 @@
+/*
+ * rocm_qlora_amd -- C ABI of the MI355X (gfx950) quantized-linear library.
+ *
+ * Every entry point takes plain device pointers, 64-bit sizes and dtype codes,
+ * launches asynchronously on the given HIP stream, never allocates device
+ * memory, never synchronises the host, and returns an rq status code
+ * (RQ_OK == 0).  Argument validation happens before any launch, so a non-zero
+ * status means nothing was enqueued (except RQ_ERR_HIP, reported from
+ * hipGetLastError after a launch).
+ *
+ * Buffer layouts are the ones rocm_qlora's QuantLinear keeps in its
+ * state_dict (quantization/quant_linear.py:38-53, double_quant.py:185-196):
+ * flat row-major [N, K] weights, NF4 packed two codes per byte with the even
+ * element in the low nibble (quant_ops.py:119-124), one absmax per block of
+ * `block_size` consecutive flat elements.
+ */
+#ifndef ROCM_QLORA_AMD_H
+#define ROCM_QLORA_AMD_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes for float tensors */
+#define RQ_DTYPE_F32  0
+#define RQ_DTYPE_BF16 1
+#define RQ_DTYPE_F16  2
+
+/* second-level (double-quant) code formats, double_quant.py:72-87 */
+#define RQ_C2_FP8_E4M3FNUZ 0   /* torch.float8_e4m3fnuz codes */
+#define RQ_C2_INT8         1   /* round(c1 / c2s * 127) int8 fallback */
+
+/* status codes */
+#define RQ_OK                 0
+#define RQ_ERR_NULL_POINTER   1
+#define RQ_ERR_BAD_DTYPE      2
+#define RQ_ERR_BAD_SHAPE      3
+#define RQ_ERR_BAD_ALIGNMENT  4
+#define RQ_ERR_UNSUPPORTED    5
+#define RQ_ERR_WORKSPACE      6
+#define RQ_ERR_HIP            7
+
+/* Human-readable text for a status code (static storage). */
+const char* rq_status_string(int status);
+
+/* Library ABI version (major * 10000 + minor * 100 + patch). */
+int rq_version(void);
+
+/* Target architecture the code objects were built for ("gfx950"). */
+const char* rq_build_arch(void);
+
+/* ------------------------------------------------------------------------
+ * NF4 codec
+ * ------------------------------------------------------------------------ */
+
+/* Replaces quantize_int4(tensor, block_size) -- quant_ops.py:80-126.
+ * w: `numel` elements of w_dtype.  The flat tensor is zero-padded to a
+ * multiple of block_size (then to even), numel_padded = result.
+ * packed: numel_padded / 2 bytes.  absmax: numel_padded / block_size values
+ * of w_dtype (clamped at 1e-12 in that dtype, as torch.clamp does).
+ * block_size must be even and >= 2. */
+int rq_nf4_quantize(const void* w, int w_dtype, int64_t numel, int64_t block_size,
+                    uint8_t* packed, void* absmax, hipStream_t stream);
+
+/* Replaces dequantize_int4(packed, scales, block_size) -- quant_ops.py:128-150
+ * followed by the caller's `[:n_out].to(out_dtype)` (quant_linear.py:191-193).
+ * out[i] = dtype(T[code_i] * float(absmax[i / block_size])) for i < n_out,
+ * n_out <= 2 * n_packed, (2 * n_packed) % block_size == 0. */
+int rq_nf4_dequantize(const uint8_t* packed, const void* absmax, int absmax_dtype,
+                      int64_t n_packed, int64_t block_size,
+                      void* out, int out_dtype, int64_t n_out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Double quantization of the NF4 absmax
+ * ------------------------------------------------------------------------ */
+
+/* Second stage of double_quantize -- double_quant.py:58-87.
+ * c1: n_c1 absmax values of c1_dtype.  Zero-padded to a multiple of block2.
+ * c2: ceil(n_c1 / block2) * block2 codes (c2_format); c2_scales:
+ * ceil(n_c1 / block2) values of c1_dtype. */
+int rq_dq_quantize(const void* c1, int c1_dtype, int64_t n_c1, int64_t block2,
+                   int c2_format, uint8_t* c2, void* c2_scales, hipStream_t stream);
+
+/* Replaces double_dequantize(state) -- double_quant.py:99-122:
+ * c1'[b] = float(c2[b]) * float(c2_scales[b / block2])   (fnuz), or
+ *        = (float(c2[b]) / 127) * float(c2_scales[...])  (int8);
+ * out[i] = dtype(T[code_i] * c1'[i / block1]) for i < n_out. */
+int rq_dq_dequantize(const uint8_t* packed, const uint8_t* c2, int c2_format,
+                     const void* c2_scales, int c2s_dtype,
+                     int64_t n_packed, int64_t block1, int64_t block2,
+                     void* out, int out_dtype, int64_t n_out, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * INT8 codec
+ * ------------------------------------------------------------------------ */
+
+/* Replaces quantize_int8(tensor, block_size, per_channel) -- quant_ops.py:17-53.
+ * block_size > 0: blockwise over the flat rows*cols elements (zero-padded to a
+ *   multiple of block_size); q has numel_padded entries, scales numel_padded /
+ *   block_size values of w_dtype.
+ * block_size == 0: per output row; q is [rows, cols], scales [rows].
+ * scale = clamp(absmax / 127, 1e-12) in w_dtype; q = int8(round_half_even(w / scale)). */
+int rq_int8_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols,
+                     int64_t block_size, int8_t* q, void* scales, hipStream_t stream);
+
+/* Replaces dequantize_int8 -- quant_ops.py:55-78 (+ caller's cast):
+ * out[i] = dtype(float(q[i]) * float(scale)), scale per block (block_size > 0)
+ * or per row of `cols` elements (block_size == 0). */
+int rq_int8_dequantize(const int8_t* q, const void* scales, int scales_dtype,
+                       int64_t rows, int64_t cols, int64_t block_size,
+                       void* out, int out_dtype, int64_t n_out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ROCM_QLORA_AMD_H */

@@ -1,0 +1,202 @@
+// Shared device/host helpers for the rocm-qlora MI355X (gfx950) kernels.
+//
+// Numeric conventions follow the PyTorch CPU semantics that rocm_qlora's
+// quantized-linear path is written in (quantization/quant_ops.py,
+// quantization/double_quant.py): reduced-precision arithmetic is done in fp32
+// and rounded to the storage type with round-to-nearest-even; divisions are
+// IEEE correctly rounded (hipcc's default for fp32 '/').
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rocm_qlora_amd.h"
+
+namespace rq {
+
+// ---------------------------------------------------------------------------
+// NF4 code book.  quant_ops.py:10-15 lists 16 Python doubles; torch rounds
+// them to fp32 (quant_ops.py:87, :134).  The fp32 bit patterns are written out
+// so no decimal-literal double rounding can creep in.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kNF4Bits[16] = {
+    0xBF800000u, 0xBF3239B1u, 0xBF066B30u, 0xBECA32A0u,
+    0xBE91A24Du, 0xBE3D353Fu, 0xBDBA7871u, 0x00000000u,
+    0x3DA2FAFFu, 0x3E24CAE3u, 0x3E7C04DDu, 0x3EAD033Au,
+    0x3EE1A4B8u, 0x3F1007ABu, 0x3F3913B3u, 0x3F800000u};
+
+// fp32 value of the clamp floor `1e-12` once cast to each storage dtype
+// (torch.clamp(min=1e-12) casts the bound to the tensor dtype; fp16 underflows
+// to zero).
+constexpr uint32_t kClampF32 = 0x2B8CBCCCu;  // fp32(1e-12)
+constexpr uint32_t kClampBF16 = 0x2B8D0000u; // bf16(1e-12)
+
+// Native clang vector types (required by the nontemporal load/store builtins
+// and by the MFMA builtins).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float u2f(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t f2u(float f) { return __float_as_uint(f); }
+
+// bf16 <-> fp32 -------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) { return u2f(uint32_t(b) << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 bits.  NaN stays NaN (quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return uint16_t((u >> 16) | 0x0040u);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+// fp16 <-> fp32 (hardware conversions are IEEE RNE) -------------------------
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return float(__builtin_bit_cast(_Float16, h));
+}
+__device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+// Load/store one element of a runtime-selected float dtype ------------------
+__device__ __forceinline__ float load_as_f32(const void* p, int64_t i, int dt) {
+  if (dt == RQ_DTYPE_F32) return static_cast<const float*>(p)[i];
+  if (dt == RQ_DTYPE_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// Round an fp32 value to the storage dtype and back (the value torch would
+// hold after an op whose result dtype is `dt`).
+__device__ __forceinline__ float round_to(float v, int dt) {
+  if (dt == RQ_DTYPE_BF16) return bf16_to_f32(f32_to_bf16_rne(v));
+  if (dt == RQ_DTYPE_F16) return f16_to_f32(f32_to_f16_rne(v));
+  return v;
+}
+
+__device__ __forceinline__ void store_from_f32(void* p, int64_t i, int dt, float v) {
+  if (dt == RQ_DTYPE_F32) static_cast<float*>(p)[i] = v;
+  else if (dt == RQ_DTYPE_BF16) static_cast<uint16_t*>(p)[i] = f32_to_bf16_rne(v);
+  else static_cast<uint16_t*>(p)[i] = f32_to_f16_rne(v);
+}
+
+// NaN-propagating max of |v| (torch's max reduction returns NaN if any input
+// is NaN; fmaxf would drop it).
+__device__ __forceinline__ float absmax_nan(float m, float v) {
+  float a = fabsf(v);
+  return (a > m || a != a) ? a : m;
+}
+__device__ __forceinline__ float max_nan(float m, float a) {
+  return (a > m || a != a || m != m) ? ((m != m) ? m : a) : m;
+}
+
+// torch.clamp(s, min=1e-12) in storage dtype `dt` (NaN propagates).
+__device__ __forceinline__ float clamp_floor(float s, int dt) {
+  float lo = (dt == RQ_DTYPE_F32) ? u2f(kClampF32) : (dt == RQ_DTYPE_BF16 ? u2f(kClampBF16) : 0.0f);
+  return (s != s) ? s : fmaxf(s, lo);
+}
+
+// ---------------------------------------------------------------------------
+// float8_e4m3fnuz: sign bit 7, 4 exponent bits (bias 8), 3 mantissa bits; no
+// infinities, no negative zero, 0x80 is the only NaN; max finite 240.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline float fnuz_to_f32(uint8_t c) {
+  if (c == 0x80) return __builtin_nanf("");
+  uint32_t e = (c >> 3) & 0xF, m = c & 0x7;
+  float mag;
+  if (e == 0) {
+    mag = float(m) * (1.0f / 1024.0f);              // m * 2^-10
+  } else {
+    // (8 + m) * 2^(e - 11), built exactly from exponent bits
+    uint32_t bits = ((e - 8 + 127) << 23) | (m << 20);
+    mag = __builtin_bit_cast(float, bits);
+  }
+  return (c & 0x80) ? -mag : mag;
+}
+
+// fp32 -> e4m3fnuz with round-to-nearest-even.  |v| that rounds to >= 256, and
+// NaN, give 0x80 (the format's NaN), as torch's cast does; values that round to
+// zero give +0 (the format has no -0).
+__host__ __device__ inline uint8_t f32_to_fnuz_rne(float v) {
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return 0x80;             // NaN
+  if (a >= 0x43800000u) return 0x80;            // >= 256 (incl. inf)
+  uint32_t code;
+  if (a < 0x3C000000u) {                        // below 2^-7: subnormal range
+    // quantum 2^-10: q = round_even(|v| * 2^10), exact scaling by 2^10
+    float s = __builtin_bit_cast(float, a) * 1024.0f;
+    uint32_t sb = __builtin_bit_cast(uint32_t, s);
+    // round_even of s in [0, 8): manual RNE on the fp32 encoding
+    int32_t ex = int32_t((sb >> 23) & 0xFF) - 127;
+    uint32_t q;
+    if (sb == 0) {
+      q = 0;
+    } else if (ex < -1) {
+      q = 0;                                    // s < 0.5
+    } else {
+      uint32_t mant = (sb & 0x7FFFFFu) | 0x800000u;
+      int32_t sh = 23 - ex;                     // bits below the integer point
+      uint32_t ip = mant >> sh;
+      uint32_t rem = mant & ((1u << sh) - 1u);
+      uint32_t half = 1u << (sh - 1);
+      if (rem > half || (rem == half && (ip & 1u))) ip += 1;
+      q = ip;
+    }
+    code = q;                                   // q == 8 lands on 2^-7 (e=1,m=0)
+  } else {
+    uint32_t e = ((a >> 23) & 0xFF) - 127 + 8;  // 1..15
+    uint32_t mant = a & 0x7FFFFFu;
+    uint32_t keep = mant >> 20;                 // top 3 bits
+    uint32_t rem = mant & 0xFFFFFu;
+    code = (e << 3) | keep;
+    if (rem > 0x80000u || (rem == 0x80000u && (keep & 1u))) code += 1;
+    if (code >= 0x80) return 0x80;              // rounded past 240 -> NaN
+  }
+  if (code == 0) return 0;
+  return uint8_t(code | sign);
+}
+
+// float8_e4m3fn (OCP, the gfx950 MFMA format): bias 7, max 448, 0x7F/0xFF NaN.
+// fnuz value v has the same bit pattern as fn value 2v; the value-preserving
+// re-encoding used for the MFMA operands is f32_to_fn_rne(fnuz_to_f32(c)).
+__host__ __device__ inline uint8_t f32_to_fn_rne(float v) {
+  uint32_t u = __builtin_bit_cast(uint32_t, v);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return 0x7F;
+  if (a >= 0x43E80000u) return uint8_t(0x7E | sign);   // >= 464: saturate (not hit)
+  uint32_t code;
+  if (a < 0x3C800000u) {                               // below 2^-6: subnormal
+    float s = __builtin_bit_cast(float, a) * 512.0f;   // quantum 2^-9
+    uint32_t sb = __builtin_bit_cast(uint32_t, s);
+    int32_t ex = int32_t((sb >> 23) & 0xFF) - 127;
+    uint32_t q;
+    if (sb == 0 || ex < -1) {
+      q = 0;
+    } else {
+      uint32_t mant = (sb & 0x7FFFFFu) | 0x800000u;
+      int32_t sh = 23 - ex;
+      uint32_t ip = mant >> sh;
+      uint32_t rem = mant & ((1u << sh) - 1u);
+      uint32_t half = 1u << (sh - 1);
+      if (rem > half || (rem == half && (ip & 1u))) ip += 1;
+      q = ip;
+    }
+    code = q;
+  } else {
+    uint32_t e = ((a >> 23) & 0xFF) - 127 + 7;
+    uint32_t mant = a & 0x7FFFFFu;
+    uint32_t keep = mant >> 20;
+    uint32_t rem = mant & 0xFFFFFu;
+    code = (e << 3) | keep;
+    if (rem > 0x80000u || (rem == 0x80000u && (keep & 1u))) code += 1;
+    if (code >= 0x7F) code = 0x7E;                      // saturate at 448
+  }
+  return uint8_t(code | sign);
+}
+
+__host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace rq
