@@ -113,6 +113,39 @@ int rq_int8_dequantize(const int8_t* q, const void* scales, int scales_dtype,
                        int64_t rows, int64_t cols, int64_t block_size,
                        void* out, int out_dtype, int64_t n_out, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * NF4 quantized linear with bias and LoRA
+ * ------------------------------------------------------------------------ */
+
+/* Bytes of device workspace rq_nf4_linear needs for these sizes (0 when
+ * none).  The caller allocates it (256-byte aligned) and passes it in. */
+int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, int64_t N, int64_t rank,
+                                 int64_t* bytes);
+
+/* Replaces QuantLinear.forward for bits=4 (quant_linear.py:121-197, single
+ * and double quant branches) fused with LoRALinear.forward
+ * (lora_layer.py:51-70), and the reference's native entry point
+ * launch_int4_dequant_matmul (hip_kernels/int4_matmul.hip:413-437):
+ *   y[M, N] = RND(RND(x W^T + RND(bias)) + RND(RND(RND(xl A^T) RND(B)^T) * scaling))
+ * with RND the rounding to x_dtype (bf16 or fp16) and W = T[code] * scale.
+ *   x: [M, K] rows of stride ldx; w_packed: flat N*K/2 bytes; block_size a
+ *   power of two >= 64 dividing K; absmax: N*K/block_size scales of
+ *   absmax_dtype, or -- when c2 != NULL -- the c2_scales of the double
+ *   quantization (one per block2 codes in c2, format c2_format).
+ *   bias: [N] or NULL.  LoRA (rank > 0, lora_a and lora_b non-NULL): xl
+ *   (lora_x, or x when NULL) [M, K] stride ld_lora_x, A [rank, K], B [N, rank]
+ *   stride ld_lora_b, both of lora_dtype.  y: [M, N] stride ldy, x_dtype.
+ * M <= 16 runs the decode GEMV; larger M the MFMA GEMM. */
+int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                  const uint8_t* w_packed, int64_t N, int64_t block_size,
+                  const void* absmax, int absmax_dtype,
+                  const uint8_t* c2, int c2_format, int64_t block2,
+                  const void* bias, int bias_dtype,
+                  const void* lora_x, int64_t ld_lora_x, const void* lora_a, const void* lora_b,
+                  int64_t ld_lora_b, int lora_dtype, int64_t rank, float scaling,
+                  void* y, int64_t ldy, void* workspace, int64_t workspace_bytes,
+                  hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

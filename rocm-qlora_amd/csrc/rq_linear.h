@@ -1,0 +1,70 @@
+// Host/device interfaces shared by the NF4 linear kernels (GEMV, GEMM, dX).
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "rq_common.h"
+
+namespace rq {
+
+// Largest activation row count served by the decode GEMV; larger M goes to
+// the MFMA GEMM.
+constexpr int64_t kGemvMaxM = 16;
+
+// Unpacked arguments of rq_nf4_linear (see include/rocm_qlora_amd.h).
+struct LinearArgs {
+  const void* x;
+  int x_dtype;
+  int64_t M, K, ldx;
+  const uint8_t* w_packed;
+  int64_t N, block_size;
+  const void* absmax;  // absmax, or c2_scales when c2 != nullptr
+  int absmax_dtype;
+  const uint8_t* c2;
+  int c2_format;
+  int64_t block2;
+  const void* bias;
+  int bias_dtype;
+  const void* lora_x;
+  int64_t ld_lora_x;
+  const void* lora_a;
+  const void* lora_b;
+  int64_t ld_lora_b;
+  int lora_dtype;
+  int64_t rank;
+  float scaling;
+  void* y;
+  int64_t ldy;
+};
+
+// Epilogue inputs as the kernels see them.
+struct LinearEpi {
+  const void* bias;
+  int bias_dt;
+  int rank;
+  const float* u;  // [u_splits, M, rank] fp32 partials of x . A^T
+  int u_splits;
+  const void* lora_b;
+  int64_t ld_lora_b;
+  int lora_dt;
+  float scaling;
+  void* y;
+  int64_t ldy;
+};
+
+struct GemvPlan {
+  int R, nw, S, grid, u_splits;
+  size_t lds_bytes, ws_bytes, u_offset;
+};
+
+GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus);
+int validate_linear(const LinearArgs& L);
+LinearEpi make_epi(const LinearArgs& L, float* u_parts, int u_splits);
+int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream);
+int gemv_workspace(const LinearArgs& L, size_t* bytes);
+int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream);
+int gemm_workspace(const LinearArgs& L, size_t* bytes);
+int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream);
+
+}  // namespace rq

@@ -1,0 +1,157 @@
+// gfx950 matrix-core helpers shared by the NF4 linear kernels.
+//
+// Lane layouts (checked on the hardware for v_mfma_f32_16x16x32_{bf16,f16}):
+//   A[16 x 32]: lane l holds A[l % 16][8 * (l / 16) + e], e = 0..7
+//   B[32 x 16]: lane l holds B[8 * (l / 16) + e][l % 16]
+//   D[16 x 16]: lane l, register r holds D[4 * (l / 16) + r][l % 16]
+// and for v_mfma_f32_32x32x16_{bf16,f16}:
+//   A[32 x 16]: lane l holds A[l % 32][8 * (l / 32) + e]
+//   B[16 x 32]: lane l holds B[8 * (l / 32) + e][l % 32]
+//   D[32 x 32]: lane l, register r holds D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32]
+#pragma once
+
+#include "rq_common.h"
+
+namespace rq {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// Eight 16-bit operand elements carried as four dwords.
+struct Op8 {
+  u32x4 v;
+};
+
+template <int XT>
+__device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
+  if constexpr (XT == RQ_DTYPE_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+template <int XT>
+__device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
+  if constexpr (XT == RQ_DTYPE_BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// Round-to-nearest-even of an fp32 value to the 16-bit operand type, as bits.
+template <int XT>
+__device__ __forceinline__ uint32_t to_x16(float v) {
+  if constexpr (XT == RQ_DTYPE_BF16) return f32_to_bf16_rne(v);
+  else return f32_to_f16_rne(v);
+}
+
+template <int XT>
+__device__ __forceinline__ float from_x16(uint32_t b) {
+  if constexpr (XT == RQ_DTYPE_BF16) return bf16_to_f32(uint16_t(b));
+  else return f16_to_f32(uint16_t(b));
+}
+
+template <int XT>
+__device__ __forceinline__ float round_x(float v) {
+  return from_x16<XT>(to_x16<XT>(v));
+}
+
+// Two fp32 values rounded (RNE, v_cvt_pk_*_f32) into one dword of 16-bit
+// operand elements, `lo` in the low half.
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+template <int XT>
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  if constexpr (XT == RQ_DTYPE_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// ---------------------------------------------------------------------------
+// Byte -> fp32 codebook pair table for exact dequantization.  Entry e (a
+// packed NF4 byte) holds fp32 T[e & 15] (the even element) and T[e >> 4].
+// Each lane multiplies by its block scale and rounds once, which reproduces
+// the reference's RND(T[code] * scale) bit for bit.  The table is replicated
+// 32 times (entry e, copy c at qword e * 32 + c, lane l uses copy l % 32):
+// a ds_read_b64 serves 16 lanes per cycle, and those 16 lanes read 16
+// distinct copies covering all 32 banks, so lookups never conflict.
+// ---------------------------------------------------------------------------
+constexpr int kF32PairLutQwords = 256 * 32;  // 64 KiB
+
+__device__ __forceinline__ void fill_f32pair_lut(u32x2* lut, int tid, int nthreads) {
+  for (int i = tid; i < kF32PairLutQwords; i += nthreads) {
+    const int e = i >> 5;
+    lut[i] = u32x2{kNF4Bits[e & 15], kNF4Bits[e >> 4]};
+  }
+}
+
+// RND(T * s) for the 8 codes of one packed dword (k ascending), as an MFMA
+// operand.  lane_off = (lane % 32) * 8 sits in byte 0; v_perm_b32 builds the
+// byte address (code byte << 8) | lane_off.
+template <int XT>
+__device__ __forceinline__ u32x4 expand8_scaled(const u32x2* lut, uint32_t word, uint32_t lane_off, float s) {
+  uint32_t r[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t addr = __builtin_amdgcn_perm(word, lane_off, 0x0C0C0000u | (uint32_t(4 + j) << 8));
+    const u32x2 p = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(lut) + addr);
+    r[j] = cvt_pk<XT>(__fmul_rn(u2f(p.x), s), __fmul_rn(u2f(p.y), s));
+  }
+  return u32x4{r[0], r[1], r[2], r[3]};
+}
+
+// ---------------------------------------------------------------------------
+// Byte -> operand-pair table.  Entry e (a packed NF4 byte) holds the two
+// codebook values T[e & 15] (low half, the even element) and T[e >> 4] (high
+// half) rounded to the operand type: exactly the dword the MFMA B operand
+// wants for two consecutive k.  It is replicated once per lane of a wave
+// (entry e, copy c at dword e * 64 + c) so that every lane reads its own bank
+// and a lookup never conflicts, whatever bytes the 64 lanes hold.
+// ---------------------------------------------------------------------------
+constexpr int kPairLutDwords = 256 * 64;
+
+template <int XT>
+__device__ __forceinline__ void fill_pair_lut(uint32_t* lut, int tid, int nthreads) {
+  for (int i = tid; i < kPairLutDwords; i += nthreads) {
+    const int e = i >> 6;
+    const uint32_t lo = to_x16<XT>(u2f(kNF4Bits[e & 15]));
+    const uint32_t hi = to_x16<XT>(u2f(kNF4Bits[e >> 4]));
+    lut[i] = lo | (hi << 16);
+  }
+}
+
+// Byte address of the table entry for byte j of `word`, for the lane whose
+// copy offset (lane * 4, < 256) sits in byte 0 of `lane_off`: one v_perm_b32
+// builds (byte << 8) | lane_off.
+__device__ __forceinline__ uint32_t pair_lut_addr(uint32_t word, uint32_t lane_off, int j) {
+  const uint32_t sel = 0x0C0C0000u | (uint32_t(4 + j) << 8);
+  return __builtin_amdgcn_perm(word, lane_off, sel);
+}
+
+__device__ __forceinline__ uint32_t pair_lut_get(const uint32_t* lut, uint32_t word, uint32_t lane_off,
+                                                 int j) {
+  return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut) +
+                                            pair_lut_addr(word, lane_off, j));
+}
+
+// Expand one dword of packed NF4 (8 codes, k ascending) into an 8-element
+// operand.
+__device__ __forceinline__ u32x4 expand8(const uint32_t* lut, uint32_t word, uint32_t lane_off) {
+  u32x4 r;
+  r.x = pair_lut_get(lut, word, lane_off, 0);
+  r.y = pair_lut_get(lut, word, lane_off, 1);
+  r.z = pair_lut_get(lut, word, lane_off, 2);
+  r.w = pair_lut_get(lut, word, lane_off, 3);
+  return r;
+}
+
+}  // namespace rq

@@ -33,6 +33,13 @@ SIGNATURES = {
     "rq_dq_dequantize": [_P, _P, _I32, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P],
     "rq_int8_quantize": [_P, _I32, _I64, _I64, _I64, _P, _P, _P],
     "rq_int8_dequantize": [_P, _P, _I32, _I64, _I64, _I64, _P, _I32, _I64, _P],
+    "rq_nf4_linear_workspace_size": [_I32, _I64, _I64, _I64, _I64, _P],
+    "rq_nf4_linear": [_P, _I32, _I64, _I64, _I64,            # x, dtype, M, K, ldx
+                      _P, _I64, _I64, _P, _I32,              # packed, N, block, absmax, dtype
+                      _P, _I32, _I64,                        # c2, c2 format, block2
+                      _P, _I32,                              # bias, dtype
+                      _P, _I64, _P, _P, _I64, _I32, _I64, _F32,  # lora x, ld, A, B, ldB, dtype, rank, scaling
+                      _P, _I64, _P, _I64, _P],               # y, ldy, workspace, bytes, stream
 }
 _RESTYPE = {"rq_status_string": ctypes.c_char_p, "rq_build_arch": ctypes.c_char_p}
 

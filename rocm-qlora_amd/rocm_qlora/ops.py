@@ -1,0 +1,126 @@
+"""Functional entry points of the MI355X quantized-linear path.
+
+Each function validates and lays out torch tensors, then calls one C-ABI
+entry point of librocm_qlora_amd.so on the current HIP stream.  There is no
+CPU or library fallback for bf16/fp16 activations: a tensor off the GPU, or a
+missing library, raises.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from rocm_qlora import _native as nat
+from rocm_qlora._device import on
+
+
+def _rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
+    """[..., K] -> 2-D [rows, K] view with unit inner stride, and its row stride."""
+    t2 = t.reshape(-1, K)
+    if t2.stride(-1) != 1 or (t2.shape[0] > 1 and t2.stride(0) < K):
+        t2 = t2.contiguous()
+    return t2, (t2.stride(0) if t2.shape[0] > 1 else K)
+
+
+def _workspace(x_dtype: torch.dtype, M: int, K: int, N: int, rank: int, dev) -> Optional[torch.Tensor]:
+    import ctypes
+    nbytes = ctypes.c_int64(0)
+    nat.call("rq_nf4_linear_workspace_size", nat.dtype_code(x_dtype), M, K, N, rank, ctypes.byref(nbytes))
+    if nbytes.value == 0:
+        return None
+    return torch.empty(nbytes.value, dtype=torch.uint8, device=dev)
+
+
+def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optional[torch.Tensor],
+               out_features: int, block_size: int = 64, bias: Optional[torch.Tensor] = None, *,
+               c2: Optional[torch.Tensor] = None, c2_scales: Optional[torch.Tensor] = None,
+               blocksize_2: int = 256, use_fp8_c2: bool = True,
+               lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
+               scaling: float = 0.0, lora_x: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x . dequant(W)^T + bias (+ LoRA) for an NF4 weight stored flat
+    (quant_linear.py:182-197 and lora_layer.py:60-70 in one kernel launch
+    sequence).  x: [..., K] bf16/fp16 on the GPU; output has x's dtype."""
+    K = x.shape[-1]
+    N = int(out_features)
+    if x.dtype == torch.float32:
+        return _nf4_linear_fp32(x, weight_quant, weight_scales, N, block_size, bias, c2, c2_scales,
+                                blocksize_2, use_fp8_c2, lora_a, lora_b, scaling, lora_x)
+    xcode = nat.dtype_code(x.dtype)
+    dq = c2 is not None
+    scales = c2_scales if dq else weight_scales
+    dev = nat.require_gpu(x, weight_quant, scales, bias, lora_a, lora_b, c2)
+    packed = weight_quant.reshape(-1)
+    if packed.dtype != torch.uint8:
+        raise TypeError(f"NF4 weight_quant must be uint8, got {packed.dtype}")
+    if packed.numel() * 2 < N * K:
+        raise RuntimeError(f"weight_quant holds {packed.numel() * 2} codes, need {N}x{K}")
+    packed = packed.contiguous()
+    scales = scales.reshape(-1).contiguous()
+    if K % 64 or block_size % 64 or K % block_size or block_size & (block_size - 1):
+        raise RuntimeError(f"NF4 linear needs K % 64 == 0 and a power-of-two block_size >= 64 "
+                           f"dividing K (K={K}, block_size={block_size})")
+    n_blocks = N * K // block_size
+    if dq:
+        if c2.numel() < n_blocks or scales.numel() * blocksize_2 < n_blocks:
+            raise RuntimeError("c2 / c2_scales too short for the weight")
+    elif scales.numel() < n_blocks:
+        raise RuntimeError(f"weight_scales holds {scales.numel()} values, need {n_blocks}")
+    lead = x.shape[:-1]
+    with on(dev):
+        x2, ldx = _rows(x, K)
+        M = x2.shape[0]
+        y = torch.empty((M, N), dtype=x.dtype, device=dev)
+        if M == 0:
+            return y.reshape(*lead, N)
+        rank = 0
+        la = lb = xl = None
+        ldxl = ldb = 0
+        lcode = 0
+        if lora_a is not None and lora_b is not None and lora_a.shape[0] > 0:
+            rank = lora_a.shape[0]
+            if lora_a.shape[1] != K or lora_b.shape != (N, rank):
+                raise RuntimeError(f"LoRA shapes {tuple(lora_a.shape)} / {tuple(lora_b.shape)} do not fit "
+                                   f"{N}x{K}")
+            if lora_b.dtype != lora_a.dtype:
+                lora_b = lora_b.to(lora_a.dtype)
+            la = lora_a.contiguous()
+            lb = lora_b.contiguous()
+            ldb = rank
+            lcode = nat.dtype_code(la.dtype)
+            if lora_x is not None:
+                xl, ldxl = _rows(lora_x.to(x.dtype), K)
+        b = bias.contiguous() if bias is not None else None
+        ws = _workspace(x.dtype, M, K, N, rank, dev)
+        codes = c2.reshape(-1).view(torch.uint8).contiguous() if dq else None
+        nat.call("rq_nf4_linear",
+                 x2.data_ptr(), xcode, M, K, ldx,
+                 packed.data_ptr(), N, block_size, scales.data_ptr(), nat.dtype_code(scales.dtype),
+                 nat.ptr(codes), nat.C2_FP8_E4M3FNUZ if use_fp8_c2 else nat.C2_INT8, blocksize_2,
+                 nat.ptr(b), nat.dtype_code(b.dtype) if b is not None else 0,
+                 nat.ptr(xl), ldxl, nat.ptr(la), nat.ptr(lb), ldb, lcode, rank, float(scaling),
+                 y.data_ptr(), N, nat.ptr(ws), ws.numel() if ws is not None else 0,
+                 nat.stream_handle(dev))
+    return y.reshape(*lead, N)
+
+
+def _nf4_linear_fp32(x, weight_quant, weight_scales, N, block_size, bias, c2, c2_scales, blocksize_2,
+                     use_fp8_c2, lora_a, lora_b, scaling, lora_x):
+    """fp32 activations: the weight is dequantized to fp32 by the HIP codec
+    kernel and multiplied by the library fp32 GEMM (quant_linear.py:189-197
+    computes in fp32 for fp32 inputs; the MFMA kernels take bf16/fp16)."""
+    from rocm_qlora.quantization.quant_ops import nf4_dequantize_to
+    from rocm_qlora.quantization.double_quant import dq_dequantize_to
+    K = x.shape[-1]
+    nat.require_gpu(x, weight_quant)
+    if c2 is not None:
+        w = dq_dequantize_to(weight_quant, c2, c2_scales, block_size, blocksize_2, use_fp8_c2,
+                             torch.float32, N * K)
+    else:
+        w = nf4_dequantize_to(weight_quant, weight_scales, block_size, torch.float32, N * K)
+    y = F.linear(x, w.view(N, K), bias.to(x.dtype) if bias is not None else None)
+    if lora_a is not None and lora_b is not None and lora_a.shape[0] > 0:
+        xl = x if lora_x is None else lora_x
+        y = y + (xl @ lora_a.to(x.dtype).T @ lora_b.to(x.dtype).T * scaling)
+    return y
