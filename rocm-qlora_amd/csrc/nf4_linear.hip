@@ -20,66 +20,94 @@
 namespace rq {
 
 // ---------------------------------------------------------------------------
-// Scale providers: fp32 scale of flat 64-aligned block b.
+// Element loads with the dtype fixed at compile time (no branches in the
+// kernels' load sequences).
 // ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ float ld_f32(const void* __restrict__ p, int64_t i) {
+  if constexpr (DT == RQ_DTYPE_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == RQ_DTYPE_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  else return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+// Scale providers: the fp32 scale of flat block b in two steps -- load()
+// issues the loads and returns raw bits, value() converts them where the
+// scale is used (single quantization: absmax of dtype SDT; double
+// quantization: c2 code times its c2_scales entry).
+template <int SDT>
 struct ScaleAbsmax {
   const void* p;
-  int dt;
-  __device__ __forceinline__ float operator()(int64_t b) const { return load_as_f32(p, b, dt); }
+  typedef uint32_t Raw;
+  __device__ __forceinline__ Raw load(int64_t b) const {
+    if constexpr (SDT == RQ_DTYPE_F32) return static_cast<const uint32_t*>(p)[b];
+    else return static_cast<const uint16_t*>(p)[b];
+  }
+  __device__ __forceinline__ float value(Raw r) const {
+    if constexpr (SDT == RQ_DTYPE_F32) return u2f(r);
+    else if constexpr (SDT == RQ_DTYPE_BF16) return bf16_to_f32(uint16_t(r));
+    else return f16_to_f32(uint16_t(r));
+  }
+  __device__ __forceinline__ float operator()(int64_t b) const { return value(load(b)); }
 };
 
+template <int SDT>
 struct ScaleDQ {
   const uint8_t* c2;
   const void* c2s;
-  int c2s_dt;
   int fmt;
+  int bs2_shift;  // log2(block2), or -1 when block2 is not a power of two
   int64_t bs2;
-  __device__ __forceinline__ float operator()(int64_t b) const {
-    const float hi = load_as_f32(c2s, b / bs2, c2s_dt);
-    const float lo = fmt == RQ_C2_FP8_E4M3FNUZ ? fnuz_to_f32(c2[b])
-                                               : __fdiv_rn(float(int8_t(c2[b])), 127.0f);
+  struct Raw {
+    uint32_t code, hi;
+  };
+  __device__ __forceinline__ Raw load(int64_t b) const {
+    const int64_t g = bs2_shift >= 0 ? (b >> bs2_shift) : b / bs2;
+    Raw r;
+    r.code = c2[b];
+    if constexpr (SDT == RQ_DTYPE_F32) r.hi = static_cast<const uint32_t*>(c2s)[g];
+    else r.hi = static_cast<const uint16_t*>(c2s)[g];
+    return r;
+  }
+  __device__ __forceinline__ float value(Raw r) const {
+    float hi;
+    if constexpr (SDT == RQ_DTYPE_F32) hi = u2f(r.hi);
+    else if constexpr (SDT == RQ_DTYPE_BF16) hi = bf16_to_f32(uint16_t(r.hi));
+    else hi = f16_to_f32(uint16_t(r.hi));
+    const uint8_t c = uint8_t(r.code);
+    const float lo = fmt == RQ_C2_FP8_E4M3FNUZ ? fnuz_to_f32(c) : __fdiv_rn(float(int8_t(c)), 127.0f);
     return __fmul_rn(lo, hi);
   }
+  __device__ __forceinline__ float operator()(int64_t b) const { return value(load(b)); }
 };
 
-// 16 consecutive activations of one row as two 8-element operands.
-template <int XT>
-__device__ __forceinline__ void load_x16(const uint16_t* __restrict__ p, bool vec, u32x4& a0, u32x4& a1) {
-  if (vec) {
-    a0 = *reinterpret_cast<const u32x4*>(p);
-    a1 = *reinterpret_cast<const u32x4*>(p + 8);
-  } else {
-    uint32_t w[8];
+// 8 consecutive activations of one row as an MFMA operand.
+__device__ __forceinline__ u32x4 load_x8(const uint16_t* __restrict__ p, bool vec) {
+  if (vec) return *reinterpret_cast<const u32x4*>(p);
+  uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) w[j] = uint32_t(p[2 * j]) | (uint32_t(p[2 * j + 1]) << 16);
-    a0 = u32x4{w[0], w[1], w[2], w[3]};
-    a1 = u32x4{w[4], w[5], w[6], w[7]};
-  }
+  for (int j = 0; j < 4; ++j) w[j] = uint32_t(p[2 * j]) | (uint32_t(p[2 * j + 1]) << 16);
+  return u32x4{w[0], w[1], w[2], w[3]};
 }
 
 // ---------------------------------------------------------------------------
-// Epilogue shared by the GEMV, the split-K finisher and the GEMM.
+// Epilogue shared by the GEMV, the split-K finisher and the GEMM.  Every
+// global load of a finishing step is issued before its first use, so a tile
+// pays one memory round trip, not one per LoRA rank.
 // ---------------------------------------------------------------------------
 template <int XT>
-__device__ __forceinline__ float lora_term(const LinearEpi& e, const float* __restrict__ u_row, int64_t n) {
-  float l = 0.0f;
-  for (int j = 0; j < e.rank; ++j)
-    l = __fmaf_rn(u_row[j], round_x<XT>(load_as_f32(e.lora_b, n * e.ld_lora_b + j, e.lora_dt)), l);
-  return round_x<XT>(__fmul_rn(round_x<XT>(l), e.scaling));
-}
-
-template <int XT>
-__device__ __forceinline__ float epilogue_value(const LinearEpi& e, const float* __restrict__ u_row,
-                                                int64_t n, float acc) {
+__device__ __forceinline__ float finish_value(const LinearEpi& e, int64_t n, float acc, float lora_sum) {
   float v = acc;
   if (e.bias) v = __fadd_rn(v, round_x<XT>(load_as_f32(e.bias, n, e.bias_dt)));
   v = round_x<XT>(v);
-  if (e.rank > 0) v = round_x<XT>(__fadd_rn(v, lora_term<XT>(e, u_row, n)));
+  if (e.rank > 0) {
+    const float l = round_x<XT>(__fmul_rn(round_x<XT>(lora_sum), e.scaling));
+    v = round_x<XT>(__fadd_rn(v, l));
+  }
   return v;
 }
 
-// Stage RND(u[m, :]) for rows [m0, m0 + rows) into LDS (sums the u_splits
-// partial products written by lora_u_kernel).
+// Stage RND(u[m, :]) for rows [m0, m0 + rows) into LDS: the sum of the
+// u_splits partial products lora_u_kernel wrote (8 loads in flight).
 template <int XT>
 __device__ __forceinline__ void stage_u(const LinearEpi& e, int64_t M, int64_t m0, int rows, float* us,
                                         int tid, int nthreads) {
@@ -89,147 +117,357 @@ __device__ __forceinline__ void stage_u(const LinearEpi& e, int64_t M, int64_t m
     const int64_t m = m0 + i / e.rank;
     const int j = i % e.rank;
     float s = 0.0f;
-    if (m < M)
-      for (int k = 0; k < e.u_splits; ++k) s = __fadd_rn(s, e.u[(int64_t(k) * M + m) * e.rank + j]);
+    if (m < M) {
+      for (int k0 = 0; k0 < e.u_splits; k0 += 8) {
+        float p[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          p[k] = (k0 + k < e.u_splits) ? e.u[(int64_t(k0 + k) * M + m) * e.rank + j] : 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (k0 + k < e.u_splits) s = __fadd_rn(s, p[k]);
+      }
+    }
     us[i] = round_x<XT>(s);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Decode GEMV: y[M <= 16, N] = x[M, K] . W^T, W NF4 (block size multiple of
-// 64, K % 64 == 0).
+// Decode GEMV: y[M <= 16, N] = x[M, K] . W^T, W NF4 (block size a power of
+// two >= 64 dividing K, K % 64 == 0).
 //
-// One 16x16x32 MFMA step: A = 16 activation rows (rows >= M are zero), B =
-// 16 weight rows x 32 k.  Lane (i = l % 16, q = l / 16) feeds row i of both
-// operands with k = 64 kb + 16 q + 8 s + (0..7), s = 0, 1: each lane loads 8
-// packed bytes of its weight row per 64-block (a whole wave load covers 16
-// rows x 32 contiguous bytes) and one scale.  D row m = 4 (l / 16) + r,
-// column = weight row l % 16.
+// HBM access: a "segment" is 256 k of a 16-row tile, 128 contiguous bytes per
+// row.  A wave reads it with two 1 KiB loads, 8 lanes x 16 B per row (full
+// 128-byte lines; narrower per-row pieces cost HBM efficiency):
+//   load A: lane (n = l % 16, q = l / 16) reads row n % 8,     chunk q + 4 [n >= 8]
+//   load B: lane (n, q)                   reads row 8 + n % 8, chunk q + 4 [n < 8]
+// (chunk = 16 B = 32 k).  Then X1 = n < 8 ? A : B holds row n, chunk q in
+// every lane, and X2 = row_ror8(n >= 8 ? A : B) (a DPP rotate by 8 within
+// each 16-lane row) holds row n, chunk q + 4: the 16x16x32 MFMA B-operand
+// layout (lane l = row l % 16, k group l / 16) with no LDS round trip.
+// Steps 0-3 take X1's dwords, steps 4-7 X2's; the activation operand (A,
+// rows = tokens, zero past M) uses the same k order.  Each dword of codes
+// becomes RND(T[code] * scale) through the LDS pair table.
 //
-// Work item = (group of R 16-row tiles, K split s).  The waves of a
-// workgroup split the item's blocks; their fp32 partials are summed in a
-// fixed order through LDS, so results are deterministic.
+// Grid (G, S), 1024 threads: workgroup (g, s) owns K split s (at most 16
+// segments) and visits 16-row tiles g, g + G, ...  Wave w always covers
+// segment w of the split, so its activation operands stay in registers.
+// Every load goes out as raw bits and is converted only where it is used,
+// and every prefetch is unconditional (past the end it re-reads the last
+// tile), so the in-order load counter lets the math of tile j run while the
+// loads of tiles j + 1 and j + 2 are in flight: about 96 KiB per CU, near
+// what HBM's ~3 us loaded latency needs at full bandwidth.  Each tile ends with one
+// barrier: the 16 partial tiles are summed in a fixed order through LDS (so
+// results are deterministic) and finished from LDS -- the tile's LoRA B rows
+// and bias were fetched with its weights, one value per thread.
 // ---------------------------------------------------------------------------
+constexpr int kGemvThreads = 1024;
+constexpr int kGemvWaves = kGemvThreads / 64;
+constexpr int kSegK = 256;
+constexpr int kGemvMaxFusedRank = kGemvThreads / 16;  // B values of a tile, one per thread
+constexpr int kGemvMaxUSplits = 16;
+constexpr int kGemvDepth = 2;  // tiles whose loads are in flight per wave
+
 struct GemvArgs {
   const uint16_t* x;
   int64_t ldx;
   const uint8_t* packed;
   int64_t M, N, K;
   int64_t blocks_per_row;  // K / block_size
-  int64_t bs_shift;        // log2(block_size / 64)
-  int S;                   // K splits
-  int R;                   // row tiles per item (runtime copy of the template value)
+  int bs_log2;             // log2(block_size)
+  int S;                   // K splits (gridDim.y)
+  bool direct;             // epilogue in this kernel (else fp32 partials to ws)
   bool xvec;
-  float* ws;               // [S, M, N] partials when S > 1
+  float* ws;               // [S, M, N] partials when !direct
 };
 
-template <int XT, int R, class Scale>
-__global__ __launch_bounds__(1024) void nf4_gemv_kernel(GemvArgs a, Scale scale, LinearEpi e) {
-  extern __shared__ uint32_t smem[];
-  const int tid = threadIdx.x, nthreads = blockDim.x;
-  const int nw = nthreads >> 6, wave = tid >> 6, lane = tid & 63;
-  u32x2* lut = reinterpret_cast<u32x2*>(smem);
-  float* red = reinterpret_cast<float*>(lut + kF32PairLutQwords);  // [nw][R][16][16]
-  float* us = red + nw * R * 256;                                   // [16][rank]
-  fill_f32pair_lut(lut, tid, nthreads);
-  if (a.S == 1) stage_u<XT>(e, a.M, 0, 16, us, tid, nthreads);
-  __syncthreads();
+// One element of a runtime float dtype as two raw 16-bit loads, the same
+// whatever the dtype (fp32: both halves; 16-bit: the element twice), so that
+// no load depends on a branch.  The halves stay apart until raw_to_f32, at
+// the point of use, so carrying them never forces a wait on the load.
+struct Raw16x2 {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ Raw16x2 load_raw(const void* p, int64_t i, int dt) {
+  const uint16_t* h = static_cast<const uint16_t*>(p);
+  const int64_t lo = dt == RQ_DTYPE_F32 ? 2 * i : i;
+  const int64_t hi = dt == RQ_DTYPE_F32 ? 2 * i + 1 : i;
+  return Raw16x2{h[lo], h[hi]};
+}
+__device__ __forceinline__ float raw_to_f32(const Raw16x2& r, int dt) {
+  return dt == RQ_DTYPE_F32 ? u2f(r.lo | (r.hi << 16))
+                            : (dt == RQ_DTYPE_BF16 ? bf16_to_f32(uint16_t(r.lo)) : f16_to_f32(uint16_t(r.lo)));
+}
 
-  const int i16 = lane & 15, q = lane >> 4;
-  const uint32_t lane_off = uint32_t(lane & 31) * 8u;
-  const int64_t KB = a.K >> 6;
+template <class Scale>
+struct GemvTileLoads {
+  u32x4 a, b;
+  typename Scale::Raw s1, s2;
+};
+
+struct GemvLane {
+  int n16, q;
+  int64_t seg;  // this wave's segment
+  bool live;    // the wave has a segment of this split
+};
+
+// tile < 0 marks a prefetch past the workgroup's last tile: every lane then
+// reads one shared 16-byte address (and scale 0), which keeps the number of
+// loads static -- so the in-order load counter stays exact across the loop --
+// at the cost of a single cache line.
+template <class Scale>
+__device__ __forceinline__ void gemv_issue_tile(GemvTileLoads<Scale>& L, const GemvArgs& a, const Scale& scale,
+                                                int64_t tile, const GemvLane& w) {
+  if (tile < 0) {
+    L.a = *reinterpret_cast<const u32x4*>(a.packed);
+    L.b = L.a;
+    L.s1 = scale.load(0);
+    L.s2 = L.s1;
+    return;
+  }
   const int64_t half_k = a.K >> 1;
-  const bool xlive = i16 < a.M;
-  const uint16_t* xrow = a.x + (xlive ? i16 : 0) * a.ldx + 16 * q;
-  const int64_t rows_per_item = 16 * R;
-  const int64_t n_groups = (a.N + rows_per_item - 1) / rows_per_item;
-  const int64_t n_items = n_groups * a.S;
+  const int64_t r0 = tile * 16;
+  int64_t rowA = r0 + (w.n16 & 7), rowB = r0 + 8 + (w.n16 & 7), rowS = r0 + w.n16;
+  rowA = rowA < a.N ? rowA : a.N - 1;  // dead rows re-read a live row; never stored
+  rowB = rowB < a.N ? rowB : a.N - 1;
+  rowS = rowS < a.N ? rowS : a.N - 1;
+  const int cA = w.q + (w.n16 >= 8 ? 4 : 0), cB = w.q + (w.n16 < 8 ? 4 : 0);
+  const int64_t sk = w.seg * kSegK;
+  // chunks past K (a last, partial segment) re-read the row's last chunk
+  int64_t kA = sk + 32 * cA, kB = sk + 32 * cB;
+  kA = kA < a.K ? kA : a.K - 32;
+  kB = kB < a.K ? kB : a.K - 32;
+  L.a = *reinterpret_cast<const u32x4*>(a.packed + rowA * half_k + (kA >> 1));
+  L.b = *reinterpret_cast<const u32x4*>(a.packed + rowB * half_k + (kB >> 1));
+  int64_t k1 = sk + 32 * w.q, k2 = k1 + 128;
+  k1 = k1 < a.K ? k1 : a.K - 1;
+  k2 = k2 < a.K ? k2 : a.K - 1;
+  L.s1 = scale.load(rowS * a.blocks_per_row + (k1 >> a.bs_log2));
+  L.s2 = scale.load(rowS * a.blocks_per_row + (k2 >> a.bs_log2));
+}
 
-  for (int64_t item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int64_t g = item / a.S;
-    const int s = int(item % a.S);
-    const int64_t kb0 = (KB * s) / a.S, kb1 = (KB * (s + 1)) / a.S;
-    const int64_t wb0 = kb0 + ((kb1 - kb0) * wave) / nw;
-    const int64_t wb1 = kb0 + ((kb1 - kb0) * (wave + 1)) / nw;
-    const int64_t nbase = g * rows_per_item;
+// LoRA B and bias of one tile as raw bits: thread t holds B[tile row t / 64,
+// t % 64] (rank <= 64) and, for t < 16, bias[tile row t].
+struct GemvEpiLoads {
+  Raw16x2 lb, bias;
+};
 
-    const uint8_t* wrow[R];
-    int64_t srow[R];
-#pragma unroll
-    for (int t = 0; t < R; ++t) {
-      int64_t n = nbase + 16 * t + i16;
-      n = n < a.N ? n : a.N - 1;  // dead rows re-read a live row; never stored
-      wrow[t] = a.packed + n * half_k + 8 * q;
-      srow[t] = n * a.blocks_per_row;
-    }
-    f32x4 acc[R];
-#pragma unroll
-    for (int t = 0; t < R; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+__device__ __forceinline__ void gemv_issue_epi(GemvEpiLoads& E, const GemvArgs& a, const LinearEpi& e,
+                                               int64_t tile, int tid) {
+  // always the same loads: without LoRA or bias, or past the last tile, they
+  // read x[0] instead
+  const bool past = tile < 0;
+  tile = past ? 0 : tile;
+  int64_t bn = tile * 16 + (tid >> 6);
+  bn = bn < a.N ? bn : a.N - 1;
+  const int j = tid & 63;
+  const bool has_b = e.rank > 0 && !past;
+  E.lb = load_raw(has_b ? e.lora_b : static_cast<const void*>(a.x),
+                  has_b ? bn * e.ld_lora_b + (j < e.rank ? j : 0) : 0, has_b ? e.lora_dt : RQ_DTYPE_BF16);
+  int64_t cn = tile * 16 + (tid & 15);
+  cn = cn < a.N ? cn : a.N - 1;
+  const bool has_bias = e.bias != nullptr && !past;
+  E.bias = load_raw(has_bias ? e.bias : static_cast<const void*>(a.x), has_bias ? cn : 0,
+                    has_bias ? e.bias_dt : RQ_DTYPE_BF16);
+}
 
-    int64_t kb = wb0;
-    // two blocks per iteration: all loads first, then the math
-    for (; kb + 2 <= wb1; kb += 2) {
-      u32x4 xa[2][2];
-      u32x2 wv[2][R];
-      float sc[2][R];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        if (xlive) load_x16<XT>(xrow + 64 * (kb + u), a.xvec, xa[u][0], xa[u][1]);
-        else xa[u][0] = xa[u][1] = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-        for (int t = 0; t < R; ++t) {
-          wv[u][t] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(wrow[t] + 32 * (kb + u)));
-          sc[u][t] = scale(srow[t] + ((kb + u) >> a.bs_shift));
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-#pragma unroll
-        for (int t = 0; t < R; ++t) {
-          acc[t] = mfma16x16x32<XT>(xa[u][0], expand8_scaled<XT>(lut, wv[u][t].x, lane_off, sc[u][t]), acc[t]);
-          acc[t] = mfma16x16x32<XT>(xa[u][1], expand8_scaled<XT>(lut, wv[u][t].y, lane_off, sc[u][t]), acc[t]);
-        }
-      }
-    }
-    for (; kb < wb1; ++kb) {
-      u32x4 xa0, xa1;
-      if (xlive) load_x16<XT>(xrow + 64 * kb, a.xvec, xa0, xa1);
-      else xa0 = xa1 = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int t = 0; t < R; ++t) {
-        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(wrow[t] + 32 * kb));
-        const float sc = scale(srow[t] + (kb >> a.bs_shift));
-        acc[t] = mfma16x16x32<XT>(xa0, expand8_scaled<XT>(lut, w.x, lane_off, sc), acc[t]);
-        acc[t] = mfma16x16x32<XT>(xa1, expand8_scaled<XT>(lut, w.y, lane_off, sc), acc[t]);
-      }
-    }
+__device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x128, 0xF, 0xF, false));
+}
 
-    // ordered cross-wave reduction and epilogue
+template <int XT, class Scale>
+__device__ __forceinline__ f32x4 gemv_tile(const GemvTileLoads<Scale>& L, const Scale& scale, const u32x4 (&xa)[8],
+                                           const u32x2* lut, uint32_t lane_off, int n16) {
+  const bool lo = n16 < 8;
+  const u32x4 X1 = lo ? L.a : L.b;
+  const u32x4 Y = lo ? L.b : L.a;
+  const u32x4 X2 = u32x4{row_ror8(Y.x), row_ror8(Y.y), row_ror8(Y.z), row_ror8(Y.w)};
+  const float s1 = scale.value(L.s1), s2 = scale.value(L.s2);
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  acc = mfma16x16x32<XT>(xa[0], expand8_scaled<XT>(lut, X1.x, lane_off, s1), acc);
+  acc = mfma16x16x32<XT>(xa[1], expand8_scaled<XT>(lut, X1.y, lane_off, s1), acc);
+  acc = mfma16x16x32<XT>(xa[2], expand8_scaled<XT>(lut, X1.z, lane_off, s1), acc);
+  acc = mfma16x16x32<XT>(xa[3], expand8_scaled<XT>(lut, X1.w, lane_off, s1), acc);
+  acc = mfma16x16x32<XT>(xa[4], expand8_scaled<XT>(lut, X2.x, lane_off, s2), acc);
+  acc = mfma16x16x32<XT>(xa[5], expand8_scaled<XT>(lut, X2.y, lane_off, s2), acc);
+  acc = mfma16x16x32<XT>(xa[6], expand8_scaled<XT>(lut, X2.z, lane_off, s2), acc);
+  acc = mfma16x16x32<XT>(xa[7], expand8_scaled<XT>(lut, X2.w, lane_off, s2), acc);
+  return acc;
+}
+
+// LDS staging of one tile: 16 wave partials [16][16 m][16 n], RND(B)
+// [16][rank], RND(bias) [16].
+struct GemvStage {
+  float* part;
+  float* lb;
+  float* bias;
+};
+
+template <int XT>
+__device__ __forceinline__ void gemv_publish(const f32x4& acc, const GemvEpiLoads& E, const GemvStage& st,
+                                             const GemvArgs& a, const LinearEpi& e, int wave, int q, int n16,
+                                             int tid) {
 #pragma unroll
-    for (int t = 0; t < R; ++t)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) red[((wave * R + t) * 16 + 4 * q + r) * 16 + i16] = acc[t][r];
-    __syncthreads();
-    for (int idx = tid; idx < R * 256; idx += nthreads) {
-      const int t = idx >> 8, m = (idx >> 4) & 15, nn = idx & 15;
-      const int64_t n = nbase + 16 * t + nn;
-      if (m < a.M && n < a.N) {
-        float v = 0.0f;
-        for (int w = 0; w < nw; ++w) v = __fadd_rn(v, red[((w * R + t) * 16 + m) * 16 + nn]);
-        if (a.S == 1) {
-          v = epilogue_value<XT>(e, us + m * e.rank, n, v);
-          static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
-        } else {
-          a.ws[(int64_t(s) * a.M + m) * a.N + n] = v;
-        }
-      }
-    }
-    __syncthreads();
+  for (int r = 0; r < 4; ++r) st.part[(wave * 16 + 4 * q + r) * 16 + n16] = acc[r];
+  if (a.direct) {
+    const int j = tid & 63;
+    if (j < e.rank) st.lb[(tid >> 6) * e.rank + j] = round_x<XT>(raw_to_f32(E.lb, e.lora_dt));
+    if (tid < 16) st.bias[tid] = e.bias ? round_x<XT>(raw_to_f32(E.bias, e.bias_dt)) : 0.0f;
   }
 }
 
-// Split-K finisher: y = epilogue(sum_s ws[s]).  One workgroup per 16 rows of
-// activations x 256 columns.
+template <int XT>
+__device__ __forceinline__ void gemv_finish(const GemvArgs& a, const LinearEpi& e, const GemvStage& st,
+                                            const float* us, int64_t tile, int s, int tid) {
+  if (tid >= 256) return;
+  const int m = tid >> 4, nn = tid & 15;
+  const int64_t n = tile * 16 + nn;
+  if (m >= a.M || n >= a.N) return;
+  float p[kGemvWaves];
+#pragma unroll
+  for (int w = 0; w < kGemvWaves; ++w) p[w] = st.part[(w * 16 + m) * 16 + nn];
+  float v = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kGemvWaves; ++w) v = __fadd_rn(v, p[w]);
+  if (!a.direct) {
+    a.ws[(int64_t(s) * a.M + m) * a.N + n] = v;
+    return;
+  }
+  if (e.bias) v = __fadd_rn(v, st.bias[nn]);
+  v = round_x<XT>(v);
+  if (e.rank > 0) {
+    float l = 0.0f;
+    for (int j0 = 0; j0 < e.rank; j0 += 8) {
+      float uu[8], bb[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        const bool ok = j0 + jj < e.rank;
+        uu[jj] = ok ? us[m * e.rank + j0 + jj] : 0.0f;
+        bb[jj] = ok ? st.lb[nn * e.rank + j0 + jj] : 0.0f;
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) l = __fmaf_rn(uu[jj], bb[jj], l);
+    }
+    l = round_x<XT>(__fmul_rn(round_x<XT>(l), e.scaling));
+    v = round_x<XT>(__fadd_rn(v, l));
+  }
+  static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
+}
+
+template <int XT, class Scale>
+__global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(GemvArgs a, Scale scale, LinearEpi e) {
+  // The table is the kernel's only static LDS array, so it sits at address
+  // 0 and every lookup's base folds into the instruction's offset field.
+  __shared__ u32x2 lut[kF32PairLutQwords];
+  extern __shared__ uint32_t smem[];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int rank = (a.direct && e.rank > 0) ? e.rank : 0;  // LoRA staging only when fused here
+  // dynamic LDS: 2 tile stages, then RND(u)
+  const int stage_floats = kGemvWaves * 256 + 16 * rank + 16;
+  GemvStage st[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    float* base = reinterpret_cast<float*>(smem) + i * stage_floats;
+    st[i] = GemvStage{base, base + kGemvWaves * 256, base + kGemvWaves * 256 + 16 * rank};
+  }
+  float* us = reinterpret_cast<float*>(smem) + 2 * stage_floats;  // [16][rank]
+
+  GemvLane w;
+  w.n16 = lane & 15;
+  w.q = lane >> 4;
+  const int s = blockIdx.y;
+  const int64_t nsegs = (a.K + kSegK - 1) / kSegK;
+  const int64_t sg0 = (nsegs * s) / a.S, sg1 = (nsegs * (s + 1)) / a.S;
+  w.live = sg0 + wave < sg1;
+  w.seg = w.live ? sg0 + wave : sg0;  // a wave without a segment re-reads one; its activations are zero
+  const int64_t n_tiles = (a.N + 15) / 16;
+  const int64_t step = gridDim.x;
+  const int64_t first = blockIdx.x;
+  const int64_t n_mine = first < n_tiles ? (n_tiles - 1 - first) / step + 1 : 0;
+  auto tile_at = [&](int64_t j) -> int64_t { return j < n_mine ? first + j * step : -1; };
+  if (n_mine == 0) return;
+
+  // 1. activation operands (stationary): step st -> k = seg * 256 + 128
+  //    (st / 4) + 32 q + 8 (st % 4); zero past M, past K and for a wave
+  //    without a segment.  2. the RND(u) partials.  3. the first two tiles.
+  u32x4 xraw[8];
+  const bool mlive = w.n16 < a.M && w.live;
+  {
+    const uint16_t* xrow = a.x + (w.n16 < a.M ? w.n16 : 0) * a.ldx;
+#pragma unroll
+    for (int stp = 0; stp < 8; ++stp) {
+      int64_t k = w.seg * kSegK + 128 * (stp >> 2) + 32 * w.q + 8 * (stp & 3);
+      k = k < a.K ? k : 0;
+      xraw[stp] = load_x8(xrow + k, a.xvec);
+    }
+  }
+  // RND(u) partials: thread t < 16 rank sums u[split][t / rank][t % rank]
+  // (every address clamped into the buffer, so the loads are unconditional)
+  float up[kGemvMaxUSplits];
+  const bool has_u = a.direct && rank > 0;
+  {
+    const int u_idx = (has_u && tid < 16 * rank) ? tid : 0;
+    const int64_t u_m0 = has_u ? u_idx / rank : 0;
+    const int64_t u_m = u_m0 < a.M ? u_m0 : a.M - 1;
+    const int u_j = has_u ? u_idx % rank : 0;
+#pragma unroll
+    for (int k = 0; k < kGemvMaxUSplits; ++k) up[k] = 0.0f;
+    if (has_u) {
+#pragma unroll
+      for (int k = 0; k < kGemvMaxUSplits; ++k) {
+        const int kk = k < e.u_splits ? k : 0;
+        up[k] = e.u[(int64_t(kk) * a.M + u_m) * rank + u_j];
+      }
+    }
+  }
+  constexpr int D = kGemvDepth;
+  GemvTileLoads<Scale> buf[D];
+  GemvEpiLoads ebuf[2];  // the epilogue values run two tiles ahead
+#pragma unroll
+  for (int i = 0; i < D; ++i) gemv_issue_tile(buf[i], a, scale, tile_at(i), w);
+  gemv_issue_epi(ebuf[0], a, e, tile_at(0), tid);
+  gemv_issue_epi(ebuf[1], a, e, tile_at(1), tid);
+
+  u32x4 xa[8];
+#pragma unroll
+  for (int stp = 0; stp < 8; ++stp) {
+    const int64_t k = w.seg * kSegK + 128 * (stp >> 2) + 32 * w.q + 8 * (stp & 3);
+    xa[stp] = (mlive && k < a.K) ? xraw[stp] : u32x4{0u, 0u, 0u, 0u};
+  }
+  fill_f32pair_lut<kGemvThreads>(lut, tid);
+  if (has_u && tid < 16 * rank) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kGemvMaxUSplits; ++k)
+      if (k < e.u_splits) sum = __fadd_rn(sum, up[k]);
+    us[tid] = (tid / rank) < a.M ? round_x<XT>(sum) : 0.0f;
+  }
+  __syncthreads();
+
+  const uint32_t lane_off = uint32_t(lane & 31) * 8u;
+  // D tiles per iteration so the ring index is static; the refill D tiles
+  // ahead is unconditional
+  for (int64_t j = 0; j < n_mine; j += D) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      if (j + i >= n_mine) break;
+      const f32x4 acc = gemv_tile<XT>(buf[i], scale, xa, lut, lane_off, w.n16);
+      gemv_issue_tile(buf[i], a, scale, tile_at(j + i + D), w);
+      // consecutive tiles alternate LDS stages and epilogue buffers
+      const GemvStage& sg = ((j + i) & 1) ? st[1] : st[0];
+      GemvEpiLoads& eb = ((j + i) & 1) ? ebuf[1] : ebuf[0];
+      gemv_publish<XT>(acc, eb, sg, a, e, wave, w.q, w.n16, tid);
+      gemv_issue_epi(eb, a, e, tile_at(j + i + 2), tid);
+      __syncthreads();
+      gemv_finish<XT>(a, e, sg, us, tile_at(j + i), s, tid);
+    }
+  }
+}
+
+// Split-K finisher (and the LoRA epilogue for any M): y = finish(sum_s
+// ws[s]).  Workgroup = 256 columns x 16 activation rows; B values are read 8
+// at a time, all in flight together, and reused for the 16 rows.
 template <int XT>
 __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* __restrict__ ws, int S, int64_t M,
                                                               int64_t N, LinearEpi e) {
@@ -239,11 +477,36 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* __res
   __syncthreads();
   const int64_t n = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (n >= N) return;
-  for (int mm = 0; mm < 16 && m0 + mm < M; ++mm) {
+  const int rows = int(M - m0 < 16 ? M - m0 : 16);
+  float lsum[16];
+#pragma unroll
+  for (int mm = 0; mm < 16; ++mm) lsum[mm] = 0.0f;
+  for (int j0 = 0; j0 < e.rank; j0 += 8) {
+    float b[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; ++jj)
+      b[jj] = (j0 + jj < e.rank) ? round_x<XT>(load_as_f32(e.lora_b, n * e.ld_lora_b + j0 + jj, e.lora_dt)) : 0.0f;
+#pragma unroll
+    for (int mm = 0; mm < 16; ++mm)
+      if (mm < rows)
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          if (j0 + jj < e.rank) lsum[mm] = __fmaf_rn(us[mm * e.rank + j0 + jj], b[jj], lsum[mm]);
+  }
+#pragma unroll
+  for (int mm = 0; mm < 16; ++mm) {
+    if (mm >= rows) break;
     const int64_t m = m0 + mm;
+    float p[8];
     float v = 0.0f;
-    for (int s = 0; s < S; ++s) v = __fadd_rn(v, ws[(int64_t(s) * M + m) * N + n]);
-    v = epilogue_value<XT>(e, us + mm * e.rank, n, v);
+    for (int s0 = 0; s0 < S; s0 += 8) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) p[k] = (s0 + k < S) ? ws[(int64_t(s0 + k) * M + m) * N + n] : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        if (s0 + k < S) v = __fadd_rn(v, p[k]);
+    }
+    v = finish_value<XT>(e, n, v, lsum[mm]);
     static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
   }
 }
@@ -252,26 +515,31 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* __res
 // LoRA down-projection partials: up[ks, m, j] = sum_{k in split ks}
 // xl[m, k] * RND(A[j, k]).  A (rank x K) is the trainable fp32 (or
 // activation-dtype) parameter; it is rounded to the activation dtype on load,
-// as lora_layer.py:67's `self.lora_A.to(x.dtype)` does.  One workgroup per
-// (16 rows of xl, 16 rows of A, K split); its 4 waves split the K range and
-// reduce through LDS.
+// as lora_layer.py:67's `self.lora_A.to(x.dtype)` does.  Workgroup = (16 rows
+// of xl, 16 rows of A, K split of at most 16 steps of 32 k); each of its 4
+// waves loads its (at most 4) steps' operands at once, then runs the MFMAs,
+// and the waves reduce through LDS.
 // ---------------------------------------------------------------------------
+constexpr int kLoraUStepsPerWave = 4;
+
 template <int XT>
-__device__ __forceinline__ u32x4 load_a8(const void* p, int dt, int64_t off, int64_t k, int64_t K, bool live) {
+__device__ __forceinline__ u32x4 load_a8(const void* p, int dt, int64_t off, bool live, bool vec32) {
+  if (!live) return u32x4{0u, 0u, 0u, 0u};
+  if (dt == RQ_DTYPE_F32 && vec32) {
+    const f32x4* v = reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + off);
+    const f32x4 a = v[0], b = v[1];
+    return u32x4{cvt_pk<XT>(a.x, a.y), cvt_pk<XT>(a.z, a.w), cvt_pk<XT>(b.x, b.y), cvt_pk<XT>(b.z, b.w)};
+  }
   uint32_t w[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t k0 = k + 2 * j, k1 = k + 2 * j + 1;
-    const float v0 = (live && k0 < K) ? load_as_f32(p, off + k0, dt) : 0.0f;
-    const float v1 = (live && k1 < K) ? load_as_f32(p, off + k1, dt) : 0.0f;
-    w[j] = to_x16<XT>(v0) | (to_x16<XT>(v1) << 16);
-  }
+  for (int j = 0; j < 4; ++j)
+    w[j] = cvt_pk<XT>(load_as_f32(p, off + 2 * j, dt), load_as_f32(p, off + 2 * j + 1, dt));
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
 template <int XT>
-__global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict__ xl, int64_t ldxl,
-                                                     const void* __restrict__ A, int a_dt, int64_t M,
+__global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict__ xl, int64_t ldxl, bool xvec,
+                                                     const void* __restrict__ A, int a_dt, bool avec, int64_t M,
                                                      int64_t K, int rank, int KS, float* __restrict__ up) {
   __shared__ float red[4][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -279,28 +547,33 @@ __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict_
   const int64_t m = int64_t(blockIdx.x) * 16 + i16;
   const int64_t j = int64_t(blockIdx.y) * 16 + i16;
   const int ks = blockIdx.z;
-  const int64_t nsteps = (K + 31) / 32;
+  const int64_t nsteps = K / 32;
   const int64_t s0 = (nsteps * ks) / KS, s1 = (nsteps * (ks + 1)) / KS;
   const int64_t w0 = s0 + ((s1 - s0) * wave) / 4, w1 = s0 + ((s1 - s0) * (wave + 1)) / 4;
   const bool mlive = m < M, jlive = j < rank;
-  f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int64_t st = w0; st < w1; ++st) {
-    const int64_t k = 32 * st + 8 * q;
-    u32x4 av, bv;
-    {
-      uint32_t w[4];
+  u32x4 av[kLoraUStepsPerWave], bv[kLoraUStepsPerWave];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int64_t k0 = k + 2 * t, k1 = k0 + 1;
-        const uint32_t lo = (mlive && k0 < K) ? xl[m * ldxl + k0] : 0u;
-        const uint32_t hi = (mlive && k1 < K) ? xl[m * ldxl + k1] : 0u;
-        w[t] = lo | (hi << 16);
+  for (int t = 0; t < kLoraUStepsPerWave; ++t) {
+    const int64_t k = 32 * (w0 + t) + 8 * q;
+    const bool live = w0 + t < w1;
+    if (live && mlive) {
+      const uint16_t* p = xl + m * ldxl + k;
+      if (xvec) {
+        av[t] = *reinterpret_cast<const u32x4*>(p);
+      } else {
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) w[h] = uint32_t(p[2 * h]) | (uint32_t(p[2 * h + 1]) << 16);
+        av[t] = u32x4{w[0], w[1], w[2], w[3]};
       }
-      av = u32x4{w[0], w[1], w[2], w[3]};
+    } else {
+      av[t] = u32x4{0u, 0u, 0u, 0u};
     }
-    bv = load_a8<XT>(A, a_dt, j * K, k, K, jlive);
-    d = mfma16x16x32<XT>(av, bv, d);
+    bv[t] = load_a8<XT>(A, a_dt, j * K + k, live && jlive, avec);
   }
+  f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int t = 0; t < kLoraUStepsPerWave; ++t) d = mfma16x16x32<XT>(av[t], bv[t], d);
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[wave][(4 * q + r) * 16 + i16] = d[r];
   __syncthreads();
@@ -309,6 +582,7 @@ __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict_
   const int64_t om = int64_t(blockIdx.x) * 16 + mm, oj = int64_t(blockIdx.y) * 16 + jj;
   if (om < M && oj < rank) {
     float v = 0.0f;
+#pragma unroll
     for (int w = 0; w < 4; ++w) v = __fadd_rn(v, red[w][idx]);
     up[(int64_t(ks) * M + om) * rank + oj] = v;
   }
@@ -327,42 +601,51 @@ static int device_cus() {
 
 GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus) {
   GemvPlan p{};
-  const int64_t KB = K / 64;
+  const int64_t nsegs = (K + kSegK - 1) / kSegK;
   const int64_t tiles = (N + 15) / 16;
-  p.R = 1;
-  int S = 1;
-  while (S < 8 && tiles * S < cus && KB / (S * 2) >= 4) S *= 2;
+  p.nw = kGemvWaves;
+  p.RT = 1;
+  int S = int((nsegs + kGemvWaves - 1) / kGemvWaves);
+  while (S < 8 && tiles * S < cus && nsegs >= 2 * S * (kGemvWaves / 2)) S *= 2;
   p.S = S;
-  const int64_t blocks_per_item = KB / S;
-  int64_t nw = blocks_per_item / 4;
-  p.nw = int(nw < 1 ? 1 : (nw > 16 ? 16 : nw));
-  p.lds_bytes = size_t(kF32PairLutQwords) * 8 + size_t(p.nw) * p.R * 256 * 4 + size_t(16) * (rank > 0 ? rank : 0) * 4;
-  const int per_cu = int(160 * 1024 / p.lds_bytes) > 0 ? int(160 * 1024 / p.lds_bytes) : 1;
-  const int64_t items = ((N + 16 * p.R - 1) / (16 * p.R)) * S;
-  p.grid = int(items < int64_t(cus) * per_cu ? items : int64_t(cus) * per_cu);
   p.u_splits = 0;
   if (rank > 0) {
-    const int64_t mt = (M + 15) / 16, jt = (rank + 15) / 16;
-    int ks = 1;
-    while (ks < 16 && mt * jt * ks < cus && (K / 32) / (ks * 2) >= 16) ks *= 2;
-    p.u_splits = ks;
+    const int64_t steps_per_wg = 4 * kLoraUStepsPerWave;
+    p.u_splits = int((K / 32 + steps_per_wg - 1) / steps_per_wg);
   }
-  p.ws_bytes = 0;
-  if (S > 1) p.ws_bytes += size_t(S) * M * N * 4;
+  // the fused epilogue stages one B value per thread and sums <= 16 u splits
+  p.direct = S == 1 && rank <= kGemvMaxFusedRank && p.u_splits <= kGemvMaxUSplits;
+  const int64_t r = p.direct && rank > 0 ? rank : 0;
+  // dynamic part only (the 64 KiB table is static): 2 tile stages + RND(u)
+  p.lds_bytes = (size_t(2) * (kGemvWaves * 256 + 16 * r + 16) + 16 * r) * 4;
+  int per_cu = int((160 * 1024) / (p.lds_bytes + size_t(kF32PairLutQwords) * 8));
+  per_cu = per_cu < 1 ? 1 : per_cu;
+  const int64_t slots = int64_t(cus) * per_cu / S;
+  p.grid = int(tiles < slots ? tiles : (slots > 0 ? slots : 1));
+  p.ws_bytes = p.direct ? 0 : size_t(S) * M * N * 4;
   p.u_offset = (p.ws_bytes + 255) & ~size_t(255);
   if (rank > 0) p.ws_bytes = p.u_offset + size_t(p.u_splits) * M * rank * 4;
   return p;
 }
 
+static int pow2_shift(int64_t v) {
+  if (v <= 0 || (v & (v - 1))) return -1;
+  int s = 0;
+  while ((int64_t(1) << s) < v) ++s;
+  return s;
+}
+
 template <int XT>
 static int launch_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream) {
   dim3 grid(unsigned((L.M + 15) / 16), unsigned((L.rank + 15) / 16), unsigned(ks));
-  lora_u_kernel<XT><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(L.lora_x), L.ld_lora_x,
-                                              L.lora_a, L.lora_dtype, L.M, L.K, int(L.rank), ks, up);
+  const bool xvec = aligned(L.lora_x, 16) && L.ld_lora_x % 8 == 0;
+  const bool avec = aligned(L.lora_a, 16);
+  lora_u_kernel<XT><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(L.lora_x), L.ld_lora_x, xvec,
+                                              L.lora_a, L.lora_dtype, avec, L.M, L.K, int(L.rank), ks, up);
   return rq_check_launch();
 }
 
-template <int XT, int R, class Scale>
+template <int XT, class Scale>
 static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, const LinearEpi& e,
                          float* ws, hipStream_t stream) {
   GemvArgs a;
@@ -373,33 +656,42 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.N = L.N;
   a.K = L.K;
   a.blocks_per_row = L.K / L.block_size;
-  int sh = 0;
-  while ((int64_t(64) << sh) < L.block_size) ++sh;
-  a.bs_shift = sh;
+  a.bs_log2 = pow2_shift(L.block_size);
   a.S = p.S;
-  a.R = R;
+  a.direct = p.direct;
   a.xvec = aligned(L.x, 16) && (L.ldx % 8 == 0);
   a.ws = ws;
-  auto kern = nf4_gemv_kernel<XT, R, Scale>;
-  static bool attr_set = false;  // one instantiation per (XT, R, Scale)
+  auto kern = nf4_gemv_kernel<XT, Scale>;
+  static bool attr_set = false;  // one flag per instantiation
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024) != hipSuccess)
+                            160 * 1024 - kF32PairLutQwords * 8) != hipSuccess)
       return RQ_ERR_HIP;
     attr_set = true;
   }
-  kern<<<p.grid, p.nw * 64, p.lds_bytes, stream>>>(a, scale, e);
+  dim3 grid(unsigned(p.grid), unsigned(p.S));
+  kern<<<grid, kGemvThreads, p.lds_bytes, stream>>>(a, scale, e);
   return rq_check_launch();
 }
 
 template <int XT>
 static int run_gemv(const LinearArgs& L, const GemvPlan& p, const LinearEpi& e, float* ws, hipStream_t stream) {
   if (L.c2) {
-    ScaleDQ sc{L.c2, L.absmax, L.absmax_dtype, L.c2_format, L.block2};
-    return launch_gemv_t<XT, 1>(L, p, sc, e, ws, stream);
+    const int sh = pow2_shift(L.block2);
+    switch (L.absmax_dtype) {
+      case RQ_DTYPE_F32:
+        return launch_gemv_t<XT>(L, p, ScaleDQ<RQ_DTYPE_F32>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, ws, stream);
+      case RQ_DTYPE_BF16:
+        return launch_gemv_t<XT>(L, p, ScaleDQ<RQ_DTYPE_BF16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, ws, stream);
+      default:
+        return launch_gemv_t<XT>(L, p, ScaleDQ<RQ_DTYPE_F16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, ws, stream);
+    }
   }
-  ScaleAbsmax sc{L.absmax, L.absmax_dtype};
-  return launch_gemv_t<XT, 1>(L, p, sc, e, ws, stream);
+  switch (L.absmax_dtype) {
+    case RQ_DTYPE_F32: return launch_gemv_t<XT>(L, p, ScaleAbsmax<RQ_DTYPE_F32>{L.absmax}, e, ws, stream);
+    case RQ_DTYPE_BF16: return launch_gemv_t<XT>(L, p, ScaleAbsmax<RQ_DTYPE_BF16>{L.absmax}, e, ws, stream);
+    default: return launch_gemv_t<XT>(L, p, ScaleAbsmax<RQ_DTYPE_F16>{L.absmax}, e, ws, stream);
+  }
 }
 
 template <int XT>
@@ -415,7 +707,8 @@ int validate_linear(const LinearArgs& L) {
   if (L.x_dtype != RQ_DTYPE_BF16 && L.x_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
   if (!valid_float_dtype(L.absmax_dtype)) return RQ_ERR_BAD_DTYPE;
   if (L.bias && !valid_float_dtype(L.bias_dtype)) return RQ_ERR_BAD_DTYPE;
-  if (L.rank > 0 && !valid_float_dtype(L.lora_dtype)) return RQ_ERR_BAD_DTYPE;
+  // LoRA A/B: fp32 (the trainable parameters) or the activation dtype
+  if (L.rank > 0 && L.lora_dtype != RQ_DTYPE_F32 && L.lora_dtype != L.x_dtype) return RQ_ERR_BAD_DTYPE;
   if (L.c2 && L.c2_format != RQ_C2_FP8_E4M3FNUZ && L.c2_format != RQ_C2_INT8) return RQ_ERR_BAD_DTYPE;
   if (L.M < 0 || L.N < 1 || L.K < 64 || L.K % 64 != 0) return RQ_ERR_BAD_SHAPE;
   if (L.block_size < 64 || L.block_size % 64 != 0 || L.K % L.block_size != 0) return RQ_ERR_BAD_SHAPE;
@@ -470,7 +763,7 @@ int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   const LinearEpi e = make_epi(L, up, p.u_splits);
   if (L.x_dtype == RQ_DTYPE_BF16) st = run_gemv<RQ_DTYPE_BF16>(L, p, e, ws, stream);
   else st = run_gemv<RQ_DTYPE_F16>(L, p, e, ws, stream);
-  if (st != RQ_OK || p.S == 1) return st;
+  if (st != RQ_OK || p.direct) return st;
   if (L.x_dtype == RQ_DTYPE_BF16) return launch_splitk_epilogue<RQ_DTYPE_BF16>(L, p, e, ws, stream);
   return launch_splitk_epilogue<RQ_DTYPE_F16>(L, p, e, ws, stream);
 }

@@ -18,11 +18,6 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// Eight 16-bit operand elements carried as four dwords.
-struct Op8 {
-  u32x4 v;
-};
-
 template <int XT>
 __device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
   if constexpr (XT == RQ_DTYPE_BF16) {
@@ -87,11 +82,25 @@ __device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
 // ---------------------------------------------------------------------------
 constexpr int kF32PairLutQwords = 256 * 32;  // 64 KiB
 
-__device__ __forceinline__ void fill_f32pair_lut(u32x2* lut, int tid, int nthreads) {
-  for (int i = tid; i < kF32PairLutQwords; i += nthreads) {
-    const int e = i >> 5;
-    lut[i] = u32x2{kNF4Bits[e & 15], kNF4Bits[e >> 4]};
-  }
+// Fill by NT (512 or 1024) threads.  Thread t writes copy t % 32 of the
+// entries whose low nibble is (t / 32) % 16 and whose high nibble is in its
+// share of 0..15; each unrolled store's high-nibble value is an immediate, so
+// the fill issues no loads at all.
+__device__ __forceinline__ uint32_t nf4_bits(int i) {
+  uint32_t v = kNF4Bits[0];
+#pragma unroll
+  for (int j = 1; j < 16; ++j) v = (i == j) ? kNF4Bits[j] : v;
+  return v;
+}
+
+template <int NT>
+__device__ __forceinline__ void fill_f32pair_lut(u32x2* lut, int tid) {
+  static_assert(NT == 512 || NT == 1024, "table fill expects 512 or 1024 threads");
+  constexpr int kPer = 16 / (NT / 512);
+  const int c = tid & 31, lo = (tid >> 5) & 15, j0 = (tid >> 9) * kPer;
+  const uint32_t lo_bits = nf4_bits(lo);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) lut[(lo + 16 * (j0 + j)) * 32 + c] = u32x2{lo_bits, nf4_bits(j0 + j)};
 }
 
 // RND(T * s) for the 8 codes of one packed dword (k ascending), as an MFMA
@@ -107,51 +116,6 @@ __device__ __forceinline__ u32x4 expand8_scaled(const u32x2* lut, uint32_t word,
     r[j] = cvt_pk<XT>(__fmul_rn(u2f(p.x), s), __fmul_rn(u2f(p.y), s));
   }
   return u32x4{r[0], r[1], r[2], r[3]};
-}
-
-// ---------------------------------------------------------------------------
-// Byte -> operand-pair table.  Entry e (a packed NF4 byte) holds the two
-// codebook values T[e & 15] (low half, the even element) and T[e >> 4] (high
-// half) rounded to the operand type: exactly the dword the MFMA B operand
-// wants for two consecutive k.  It is replicated once per lane of a wave
-// (entry e, copy c at dword e * 64 + c) so that every lane reads its own bank
-// and a lookup never conflicts, whatever bytes the 64 lanes hold.
-// ---------------------------------------------------------------------------
-constexpr int kPairLutDwords = 256 * 64;
-
-template <int XT>
-__device__ __forceinline__ void fill_pair_lut(uint32_t* lut, int tid, int nthreads) {
-  for (int i = tid; i < kPairLutDwords; i += nthreads) {
-    const int e = i >> 6;
-    const uint32_t lo = to_x16<XT>(u2f(kNF4Bits[e & 15]));
-    const uint32_t hi = to_x16<XT>(u2f(kNF4Bits[e >> 4]));
-    lut[i] = lo | (hi << 16);
-  }
-}
-
-// Byte address of the table entry for byte j of `word`, for the lane whose
-// copy offset (lane * 4, < 256) sits in byte 0 of `lane_off`: one v_perm_b32
-// builds (byte << 8) | lane_off.
-__device__ __forceinline__ uint32_t pair_lut_addr(uint32_t word, uint32_t lane_off, int j) {
-  const uint32_t sel = 0x0C0C0000u | (uint32_t(4 + j) << 8);
-  return __builtin_amdgcn_perm(word, lane_off, sel);
-}
-
-__device__ __forceinline__ uint32_t pair_lut_get(const uint32_t* lut, uint32_t word, uint32_t lane_off,
-                                                 int j) {
-  return *reinterpret_cast<const uint32_t*>(reinterpret_cast<const char*>(lut) +
-                                            pair_lut_addr(word, lane_off, j));
-}
-
-// Expand one dword of packed NF4 (8 codes, k ascending) into an 8-element
-// operand.
-__device__ __forceinline__ u32x4 expand8(const uint32_t* lut, uint32_t word, uint32_t lane_off) {
-  u32x4 r;
-  r.x = pair_lut_get(lut, word, lane_off, 0);
-  r.y = pair_lut_get(lut, word, lane_off, 1);
-  r.z = pair_lut_get(lut, word, lane_off, 2);
-  r.w = pair_lut_get(lut, word, lane_off, 3);
-  return r;
 }
 
 }  // namespace rq

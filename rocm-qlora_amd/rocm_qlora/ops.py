@@ -83,6 +83,8 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
             if lora_a.shape[1] != K or lora_b.shape != (N, rank):
                 raise RuntimeError(f"LoRA shapes {tuple(lora_a.shape)} / {tuple(lora_b.shape)} do not fit "
                                    f"{N}x{K}")
+            if lora_a.dtype not in (torch.float32, x.dtype):
+                lora_a = lora_a.float()
             if lora_b.dtype != lora_a.dtype:
                 lora_b = lora_b.to(lora_a.dtype)
             la = lora_a.contiguous()

@@ -53,12 +53,17 @@ def test_gemv_llama3_shapes_bf16(dev, M, K, N):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("case", ["plain", "bias", "odd_n", "block128", "strided_x", "dropout_x", "no_lora"])
+@pytest.mark.parametrize("case", ["plain", "bias", "odd_n", "block128", "strided_x", "dropout_x", "no_lora",
+                                  "k320", "k64", "rank96", "rank256", "bf16_lora"])
 def test_gemv_variants(dev, dtype, case):
     N, K, M = (1000 if case == "odd_n" else 768), 512, 5
+    K = {"k320": 320, "k64": 64}.get(case, K)
+    rank = {"rank96": 96, "rank256": 256}.get(case, 16)
     bs = 128 if case == "block128" else 64
     print(f"gemv variant {case} {dtype}", flush=True)
-    w, x, a, b, bvec = _inputs(N, K, M, dtype, seed=7, bias=(case == "bias"))
+    w, x, a, b, bvec = _inputs(N, K, M, dtype, seed=7, rank=rank, bias=(case == "bias"))
+    if case == "bf16_lora":
+        a, b = a.to(dtype), b.to(dtype)
     packed, absmax = quantize_int4(w.to(dev), bs)
     xd = x.to(dev)
     xl = None
