@@ -16,121 +16,9 @@
 #include "rq_mfma.h"
 #include "rq_launch.h"
 #include "rq_linear.h"
+#include "rq_linear_dev.h"
 
 namespace rq {
-
-// ---------------------------------------------------------------------------
-// Element loads with the dtype fixed at compile time (no branches in the
-// kernels' load sequences).
-// ---------------------------------------------------------------------------
-template <int DT>
-__device__ __forceinline__ float ld_f32(const void* __restrict__ p, int64_t i) {
-  if constexpr (DT == RQ_DTYPE_F32) return static_cast<const float*>(p)[i];
-  else if constexpr (DT == RQ_DTYPE_BF16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
-  else return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
-}
-
-// Scale providers: the fp32 scale of flat block b in two steps -- load()
-// issues the loads and returns raw bits, value() converts them where the
-// scale is used (single quantization: absmax of dtype SDT; double
-// quantization: c2 code times its c2_scales entry).
-template <int SDT>
-struct ScaleAbsmax {
-  const void* p;
-  typedef uint32_t Raw;
-  __device__ __forceinline__ Raw load(int64_t b) const {
-    if constexpr (SDT == RQ_DTYPE_F32) return static_cast<const uint32_t*>(p)[b];
-    else return static_cast<const uint16_t*>(p)[b];
-  }
-  __device__ __forceinline__ float value(Raw r) const {
-    if constexpr (SDT == RQ_DTYPE_F32) return u2f(r);
-    else if constexpr (SDT == RQ_DTYPE_BF16) return bf16_to_f32(uint16_t(r));
-    else return f16_to_f32(uint16_t(r));
-  }
-  __device__ __forceinline__ float operator()(int64_t b) const { return value(load(b)); }
-};
-
-template <int SDT>
-struct ScaleDQ {
-  const uint8_t* c2;
-  const void* c2s;
-  int fmt;
-  int bs2_shift;  // log2(block2), or -1 when block2 is not a power of two
-  int64_t bs2;
-  struct Raw {
-    uint32_t code, hi;
-  };
-  __device__ __forceinline__ Raw load(int64_t b) const {
-    const int64_t g = bs2_shift >= 0 ? (b >> bs2_shift) : b / bs2;
-    Raw r;
-    r.code = c2[b];
-    if constexpr (SDT == RQ_DTYPE_F32) r.hi = static_cast<const uint32_t*>(c2s)[g];
-    else r.hi = static_cast<const uint16_t*>(c2s)[g];
-    return r;
-  }
-  __device__ __forceinline__ float value(Raw r) const {
-    float hi;
-    if constexpr (SDT == RQ_DTYPE_F32) hi = u2f(r.hi);
-    else if constexpr (SDT == RQ_DTYPE_BF16) hi = bf16_to_f32(uint16_t(r.hi));
-    else hi = f16_to_f32(uint16_t(r.hi));
-    const uint8_t c = uint8_t(r.code);
-    const float lo = fmt == RQ_C2_FP8_E4M3FNUZ ? fnuz_to_f32(c) : __fdiv_rn(float(int8_t(c)), 127.0f);
-    return __fmul_rn(lo, hi);
-  }
-  __device__ __forceinline__ float operator()(int64_t b) const { return value(load(b)); }
-};
-
-// 8 consecutive activations of one row as an MFMA operand.
-__device__ __forceinline__ u32x4 load_x8(const uint16_t* __restrict__ p, bool vec) {
-  if (vec) return *reinterpret_cast<const u32x4*>(p);
-  uint32_t w[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) w[j] = uint32_t(p[2 * j]) | (uint32_t(p[2 * j + 1]) << 16);
-  return u32x4{w[0], w[1], w[2], w[3]};
-}
-
-// ---------------------------------------------------------------------------
-// Epilogue shared by the GEMV, the split-K finisher and the GEMM.  Every
-// global load of a finishing step is issued before its first use, so a tile
-// pays one memory round trip, not one per LoRA rank.
-// ---------------------------------------------------------------------------
-template <int XT>
-__device__ __forceinline__ float finish_value(const LinearEpi& e, int64_t n, float acc, float lora_sum) {
-  float v = acc;
-  if (e.bias) v = __fadd_rn(v, round_x<XT>(load_as_f32(e.bias, n, e.bias_dt)));
-  v = round_x<XT>(v);
-  if (e.rank > 0) {
-    const float l = round_x<XT>(__fmul_rn(round_x<XT>(lora_sum), e.scaling));
-    v = round_x<XT>(__fadd_rn(v, l));
-  }
-  return v;
-}
-
-// Stage RND(u[m, :]) for rows [m0, m0 + rows) into LDS: the sum of the
-// u_splits partial products lora_u_kernel wrote (8 loads in flight).
-template <int XT>
-__device__ __forceinline__ void stage_u(const LinearEpi& e, int64_t M, int64_t m0, int rows, float* us,
-                                        int tid, int nthreads) {
-  if (e.rank <= 0) return;
-  const int total = rows * e.rank;
-  for (int i = tid; i < total; i += nthreads) {
-    const int64_t m = m0 + i / e.rank;
-    const int j = i % e.rank;
-    float s = 0.0f;
-    if (m < M) {
-      for (int k0 = 0; k0 < e.u_splits; k0 += 8) {
-        float p[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          p[k] = (k0 + k < e.u_splits) ? e.u[(int64_t(k0 + k) * M + m) * e.rank + j] : 0.0f;
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (k0 + k < e.u_splits) s = __fadd_rn(s, p[k]);
-      }
-    }
-    us[i] = round_x<XT>(s);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Decode GEMV: y[M <= 16, N] = x[M, K] . W^T, W NF4 (block size a power of
@@ -153,13 +41,13 @@ __device__ __forceinline__ void stage_u(const LinearEpi& e, int64_t M, int64_t m
 // segments) and visits 16-row tiles g, g + G, ...  Wave w always covers
 // segment w of the split, so its activation operands stay in registers.
 // Every load goes out as raw bits and is converted only where it is used,
-// and every prefetch is unconditional (past the end it re-reads the last
-// tile), so the in-order load counter lets the math of tile j run while the
-// loads of tiles j + 1 and j + 2 are in flight: about 96 KiB per CU, near
-// what HBM's ~3 us loaded latency needs at full bandwidth.  Each tile ends with one
-// barrier: the 16 partial tiles are summed in a fixed order through LDS (so
-// results are deterministic) and finished from LDS -- the tile's LoRA B rows
-// and bias were fetched with its weights, one value per thread.
+// and every prefetch is unconditional (past the workgroup's last tile it
+// reads one shared address), so the in-order load counter stays exact and
+// the math of tile j runs while the next tile's loads are in flight.  Each
+// tile ends with one barrier: the 16 partial tiles are summed in a fixed
+// order through LDS (so results are deterministic) and finished from LDS --
+// the tile's LoRA B rows and bias were fetched with its weights, one value
+// per thread.
 // ---------------------------------------------------------------------------
 constexpr int kGemvThreads = 1024;
 constexpr int kGemvWaves = kGemvThreads / 64;
@@ -180,24 +68,6 @@ struct GemvArgs {
   bool xvec;
   float* ws;               // [S, M, N] partials when !direct
 };
-
-// One element of a runtime float dtype as two raw 16-bit loads, the same
-// whatever the dtype (fp32: both halves; 16-bit: the element twice), so that
-// no load depends on a branch.  The halves stay apart until raw_to_f32, at
-// the point of use, so carrying them never forces a wait on the load.
-struct Raw16x2 {
-  uint32_t lo, hi;
-};
-__device__ __forceinline__ Raw16x2 load_raw(const void* p, int64_t i, int dt) {
-  const uint16_t* h = static_cast<const uint16_t*>(p);
-  const int64_t lo = dt == RQ_DTYPE_F32 ? 2 * i : i;
-  const int64_t hi = dt == RQ_DTYPE_F32 ? 2 * i + 1 : i;
-  return Raw16x2{h[lo], h[hi]};
-}
-__device__ __forceinline__ float raw_to_f32(const Raw16x2& r, int dt) {
-  return dt == RQ_DTYPE_F32 ? u2f(r.lo | (r.hi << 16))
-                            : (dt == RQ_DTYPE_BF16 ? bf16_to_f32(uint16_t(r.lo)) : f16_to_f32(uint16_t(r.lo)));
-}
 
 template <class Scale>
 struct GemvTileLoads {
@@ -523,21 +393,6 @@ __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* __res
 constexpr int kLoraUStepsPerWave = 4;
 
 template <int XT>
-__device__ __forceinline__ u32x4 load_a8(const void* p, int dt, int64_t off, bool live, bool vec32) {
-  if (!live) return u32x4{0u, 0u, 0u, 0u};
-  if (dt == RQ_DTYPE_F32 && vec32) {
-    const f32x4* v = reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + off);
-    const f32x4 a = v[0], b = v[1];
-    return u32x4{cvt_pk<XT>(a.x, a.y), cvt_pk<XT>(a.z, a.w), cvt_pk<XT>(b.x, b.y), cvt_pk<XT>(b.z, b.w)};
-  }
-  uint32_t w[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    w[j] = cvt_pk<XT>(load_as_f32(p, off + 2 * j, dt), load_as_f32(p, off + 2 * j + 1, dt));
-  return u32x4{w[0], w[1], w[2], w[3]};
-}
-
-template <int XT>
 __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict__ xl, int64_t ldxl, bool xvec,
                                                      const void* __restrict__ A, int a_dt, bool avec, int64_t M,
                                                      int64_t K, int rank, int KS, float* __restrict__ up) {
@@ -551,29 +406,31 @@ __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict_
   const int64_t s0 = (nsteps * ks) / KS, s1 = (nsteps * (ks + 1)) / KS;
   const int64_t w0 = s0 + ((s1 - s0) * wave) / 4, w1 = s0 + ((s1 - s0) * (wave + 1)) / 4;
   const bool mlive = m < M, jlive = j < rank;
-  u32x4 av[kLoraUStepsPerWave], bv[kLoraUStepsPerWave];
-#pragma unroll
-  for (int t = 0; t < kLoraUStepsPerWave; ++t) {
-    const int64_t k = 32 * (w0 + t) + 8 * q;
-    const bool live = w0 + t < w1;
-    if (live && mlive) {
-      const uint16_t* p = xl + m * ldxl + k;
-      if (xvec) {
-        av[t] = *reinterpret_cast<const u32x4*>(p);
-      } else {
-        uint32_t w[4];
-#pragma unroll
-        for (int h = 0; h < 4; ++h) w[h] = uint32_t(p[2 * h]) | (uint32_t(p[2 * h + 1]) << 16);
-        av[t] = u32x4{w[0], w[1], w[2], w[3]};
-      }
-    } else {
-      av[t] = u32x4{0u, 0u, 0u, 0u};
-    }
-    bv[t] = load_a8<XT>(A, a_dt, j * K + k, live && jlive, avec);
-  }
   f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t b0 = w0; b0 < w1; b0 += kLoraUStepsPerWave) {
+    u32x4 av[kLoraUStepsPerWave], bv[kLoraUStepsPerWave];
 #pragma unroll
-  for (int t = 0; t < kLoraUStepsPerWave; ++t) d = mfma16x16x32<XT>(av[t], bv[t], d);
+    for (int t = 0; t < kLoraUStepsPerWave; ++t) {
+      const int64_t k = 32 * (b0 + t) + 8 * q;
+      const bool live = b0 + t < w1;
+      if (live && mlive) {
+        const uint16_t* p = xl + m * ldxl + k;
+        if (xvec) {
+          av[t] = *reinterpret_cast<const u32x4*>(p);
+        } else {
+          uint32_t w[4];
+#pragma unroll
+          for (int h = 0; h < 4; ++h) w[h] = uint32_t(p[2 * h]) | (uint32_t(p[2 * h + 1]) << 16);
+          av[t] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+      } else {
+        av[t] = u32x4{0u, 0u, 0u, 0u};
+      }
+      bv[t] = load_a8<XT>(A, a_dt, j * K + k, live && jlive, avec);
+    }
+#pragma unroll
+    for (int t = 0; t < kLoraUStepsPerWave; ++t) d = mfma16x16x32<XT>(av[t], bv[t], d);
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[wave][(4 * q + r) * 16 + i16] = d[r];
   __syncthreads();
@@ -591,14 +448,6 @@ __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-static int device_cus() {
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 256;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-    return 256;
-  return cus;
-}
-
 GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus) {
   GemvPlan p{};
   const int64_t nsegs = (K + kSegK - 1) / kSegK;
@@ -626,13 +475,6 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus) {
   p.u_offset = (p.ws_bytes + 255) & ~size_t(255);
   if (rank > 0) p.ws_bytes = p.u_offset + size_t(p.u_splits) * M * rank * 4;
   return p;
-}
-
-static int pow2_shift(int64_t v) {
-  if (v <= 0 || (v & (v - 1))) return -1;
-  int s = 0;
-  while ((int64_t(1) << s) < v) ++s;
-  return s;
 }
 
 template <int XT>

@@ -1,0 +1,147 @@
+"""GPU parity of the NF4 prefill/training GEMM (M > 16 activation rows): HIP
+MFMA kernel through the C ABI vs the oracle's restatement of
+QuantLinear.forward + LoRALinear.forward (quant_linear.py:182-197,
+lora_layer.py:60-70) on the same seeded inputs.  Tolerance rtol = atol = 1e-2
+in the activation dtype.  Output rows are independent, so the full-size
+Llama-3-8B cases run the whole GEMM on the GPU and check a seeded sample of
+rows (always including the first and last tile rows) against the oracle."""
+import math
+
+import pytest
+import torch
+
+from oracle import qlora_ref as R
+from rocm_qlora import ops
+from rocm_qlora.quantization import quantize_int4, double_quantize
+
+pytestmark = pytest.mark.gpu
+
+RTOL = ATOL = 1e-2
+
+
+def _inputs(N, K, M, dtype, seed, rank=64, bias=False):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * 0.02
+    x = torch.randn(M, K, generator=g).to(dtype)
+    a = torch.empty(rank, K)
+    torch.nn.init.kaiming_uniform_(a, a=math.sqrt(5), generator=g)
+    b = torch.randn(N, rank, generator=g) * 0.01
+    bvec = (torch.randn(N, generator=g) * 0.1) if bias else None
+    return w, x, a, b, bvec
+
+
+def _check(got, ref):
+    got = got.cpu().float()
+    ref = ref.float()
+    assert got.shape == ref.shape
+    err = (got - ref).abs()
+    bad = err > ATOL + RTOL * ref.abs()
+    assert not bad.any(), f"{int(bad.sum())} of {bad.numel()} outside tol; max err {float(err.max()):.4g}"
+
+
+def _sample_rows(M, n, seed):
+    g = torch.Generator().manual_seed(seed)
+    rows = torch.randperm(M, generator=g)[:n]
+    edge = torch.tensor([0, 255, 256, M - 1])
+    return torch.unique(torch.cat([rows, edge[edge < M]]))
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)])
+def test_gemm_llama3_shapes_bf16(dev, K, N):
+    """Config: prefill dequant-GEMM, M=2048 bf16 tokens, LoRA r=64 alpha=16 fused."""
+    M, rank = 2048, 64
+    print(f"gemm bf16 K={K} N={N} M={M}", flush=True)
+    w, x, a, b, _ = _inputs(N, K, M, torch.bfloat16, seed=K + N)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=a.to(dev), lora_b=b.to(dev),
+                       scaling=16.0 / rank)
+    rows = _sample_rows(M, 60, K * N)
+    ref = R.nf4_lora_linear(x[rows], packed.cpu(), absmax.cpu(), None, a, b, 16.0 / rank, N, 64)
+    _check(y.cpu()[rows], ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", ["plain", "bias", "odd_n", "odd_m", "m17", "block128", "strided_x",
+                                  "dropout_x", "no_lora", "k64", "k320", "rank16", "rank96", "rank256",
+                                  "bf16_lora", "tiles8"])
+def test_gemm_variants(dev, dtype, case):
+    N, K, M = 640, 512, 300
+    N = {"odd_n": 1000, "tiles8": 512}.get(case, N)
+    M = {"odd_m": 777, "m17": 17, "tiles8": 512}.get(case, M)
+    K = {"k64": 64, "k320": 320}.get(case, K)
+    rank = {"rank16": 16, "rank96": 96, "rank256": 256}.get(case, 64)
+    bs = 128 if case == "block128" else 64
+    print(f"gemm variant {case} {dtype}", flush=True)
+    w, x, a, b, bvec = _inputs(N, K, M, dtype, seed=11, rank=rank, bias=(case == "bias"))
+    if case == "bf16_lora":
+        a, b = a.to(dtype), b.to(dtype)
+    packed, absmax = quantize_int4(w.to(dev), bs)
+    xd = x.to(dev)
+    xl = None
+    if case == "strided_x":
+        big = torch.zeros(M, K + 72, dtype=dtype, device=dev)
+        big[:, 40:40 + K] = xd
+        xd = big[:, 40:40 + K]
+    if case == "dropout_x":
+        xl = (x * (torch.rand(x.shape, generator=torch.Generator().manual_seed(3)) > 0.3)).to(dtype)
+    la, lb = (None, None) if case == "no_lora" else (a.to(dev), b.to(dev))
+    y = ops.nf4_linear(xd, packed, absmax, N, bs, bias=None if bvec is None else bvec.to(dev),
+                       lora_a=la, lora_b=lb, scaling=0.5, lora_x=None if xl is None else xl.to(dev))
+    wf = R.dequantize_int4(packed.cpu(), absmax.cpu(), bs)
+    base = R.quant_linear_forward(x, wf, bvec, N, K)
+    if la is None:
+        ref = base
+    else:
+        lx = x if xl is None else xl
+        lora = lx @ a.to(dtype).T @ b.to(dtype).T * 0.5
+        ref = base + lora.to(base.dtype)
+    _check(y, ref)
+
+
+def test_gemm_double_quant(dev):
+    N, K, M = 1024, 2048, 512
+    w, x, a, b, _ = _inputs(N, K, M, torch.bfloat16, seed=23)
+    st = double_quantize(w.to(dev), 64, 256)
+    y = ops.nf4_linear(x.to(dev), st.W_quant, None, N, 64, c2=st.c2, c2_scales=st.c2_scales,
+                       blocksize_2=256, use_fp8_c2=True, lora_a=a.to(dev), lora_b=b.to(dev), scaling=0.25)
+    wf = R.double_dequantize(st.W_quant.cpu(), st.c2.cpu(), st.c2_scales.cpu(), (N, K), 64, 256, True)
+    base = R.quant_linear_forward(x, wf.reshape(-1), None, N, K)
+    ref = R.lora_forward(x, base, a, b, 0.25)
+    _check(y, ref)
+
+
+def test_gemm_deterministic(dev):
+    N, K, M = 2048, 2048, 1024
+    w, x, a, b, _ = _inputs(N, K, M, torch.bfloat16, seed=9)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    args = (x.to(dev), packed, absmax, N, 64)
+    kw = dict(lora_a=a.to(dev), lora_b=b.to(dev), scaling=0.25)
+    y1 = ops.nf4_linear(*args, **kw)
+    y2 = ops.nf4_linear(*args, **kw)
+    assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dq", [False, True])
+def test_gemm_weight_operand_bit_exact(dev, dtype, dq):
+    """One-hot activation rows pick single weights: y[m, n] = RND(W[n, k_m])
+    must equal the reference's dequantized weight cast to x's dtype bit for
+    bit (quant_ops.py:144-148, quant_linear.py:191-193; double_quant.py:108-118).
+    300 rows cover two 256-row tiles and every k position mod 64."""
+    N, K, M = 384, 1024, 300
+    g = torch.Generator().manual_seed(19)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    ks = torch.randint(0, K, (M,), generator=g)
+    ks[:64] = torch.arange(64) + 128
+    x = torch.zeros(M, K, dtype=dtype)
+    x[torch.arange(M), ks] = 1.0
+    if dq:
+        st = double_quantize(w.to(dev), 64, 256)
+        y = ops.nf4_linear(x.to(dev), st.W_quant, None, N, 64, c2=st.c2, c2_scales=st.c2_scales)
+        wf = R.double_dequantize(st.W_quant.cpu(), st.c2.cpu(), st.c2_scales.cpu(), (N, K), 64, 256, True)
+    else:
+        packed, absmax = quantize_int4(w.to(dev), 64)
+        y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64)
+        wf = R.dequantize_int4(packed.cpu(), absmax.cpu(), 64)[:N * K].reshape(N, K)
+    ref = wf.to(dtype)[:, ks].T
+    assert torch.equal(y.cpu().view(torch.int16), ref.contiguous().view(torch.int16))
