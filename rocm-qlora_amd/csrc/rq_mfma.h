@@ -40,24 +40,6 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
   }
 }
 
-// Round-to-nearest-even of an fp32 value to the 16-bit operand type, as bits.
-template <int XT>
-__device__ __forceinline__ uint32_t to_x16(float v) {
-  if constexpr (XT == RQ_DTYPE_BF16) return f32_to_bf16_rne(v);
-  else return f32_to_f16_rne(v);
-}
-
-template <int XT>
-__device__ __forceinline__ float from_x16(uint32_t b) {
-  if constexpr (XT == RQ_DTYPE_BF16) return bf16_to_f32(uint16_t(b));
-  else return f16_to_f32(uint16_t(b));
-}
-
-template <int XT>
-__device__ __forceinline__ float round_x(float v) {
-  return from_x16<XT>(to_x16<XT>(v));
-}
-
 // Two fp32 values rounded (RNE, v_cvt_pk_*_f32) into one dword of 16-bit
 // operand elements, `lo` in the low half.
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -69,6 +51,28 @@ __device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
   const f32x2 v = {lo, hi};
   if constexpr (XT == RQ_DTYPE_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
   else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
+// Round-to-nearest-even of an fp32 value to the 16-bit operand type, as bits
+// (the hardware conversions: v_cvt_pk_bf16_f32 / v_cvt_f16_f32, which round
+// finite values exactly as torch's casts do; a NaN stays a quiet NaN).
+template <int XT>
+__device__ __forceinline__ uint32_t to_x16(float v) {
+  if constexpr (XT == RQ_DTYPE_BF16) return cvt_pk<XT>(v, 0.0f) & 0xFFFFu;
+  else return f32_to_f16_rne(v);
+}
+
+template <int XT>
+__device__ __forceinline__ float from_x16(uint32_t b) {
+  if constexpr (XT == RQ_DTYPE_BF16) return bf16_to_f32(uint16_t(b));
+  else return f16_to_f32(uint16_t(b));
+}
+
+// RND: the fp32 value an fp32 -> operand-dtype -> fp32 round trip yields.
+template <int XT>
+__device__ __forceinline__ float round_x(float v) {
+  if constexpr (XT == RQ_DTYPE_BF16) return u2f(cvt_pk<XT>(v, 0.0f) << 16);
+  else return float(static_cast<_Float16>(v));
 }
 
 // ---------------------------------------------------------------------------
