@@ -2,40 +2,56 @@
 //   y[M, N] = RND(RND(x W^T + RND(bias)) + RND(RND(RND(u) RND(B)^T) * scaling))
 // with W = RND(T[code] * scale) dequantized exactly as the reference does
 // (quant_ops.py:144-148 then .to(x.dtype), quant_linear.py:191-193) and the
-// LoRA term of lora_layer.py:67-70 fused into the epilogue (u = xl A^T comes
-// from lora_u_kernel, summed and rounded by lora_u_round_kernel).
+// LoRA term of lora_layer.py:67-70 fused into the epilogue (RND(u) and RND(B)
+// come from the LoRA operand kernels of rq_lora.hip).
 //
-// Workgroup tile BM x BN, BM = 4 waves x 32 MB rows.  Each wave owns 32 MB
-// token rows and all BN feature columns as 32x32 blocks of
-// v_mfma_f32_32x32x16_{bf16,f16}.  K advances 64 at a time -- one NF4 block
-// per weight row, so one scale per row per step:
-//   * activations stream from global memory (L2) straight into registers in
-//     the MFMA operand layout; every activation row is loaded by exactly one
-//     wave, so there is no redundant activation traffic and none of it passes
-//     through LDS;
-//   * the BN x 64 weight slice is loaded packed (two steps ahead),
-//     dequantized once per workgroup through the LDS pair table, rounded to
-//     the activation dtype and written to a padded LDS tile (double
-//     buffered), from which every wave reads its weight operands.
+// Workgroup tile 256 tokens x 128 features, 4 waves; wave w owns rows
+// 64 w .. 64 w + 63 and all 128 columns as 2 x 4 blocks of
+// v_mfma_f32_32x32x16_{bf16,f16}.  K advances 64 per step -- one NF4 block
+// per weight row, one scale per row per step.  LDS (160 KiB, all of it):
+//   [0, 64K)     the fp32 pair table for exact dequantization (address 0,
+//                so lookups fold their base into the instruction offset);
+//   [64K, 128K)  activation ring: 2 steps x 4 waves x 64 rows x 128 bytes;
+//   [128K, 160K) weight tiles: 2 steps x 128 rows x 128 bytes.
+// Both LDS layouts store 16-byte chunk c of row r at slot c ^ ((r / 2) & 7)
+// of the row: the LDS serves 16 lanes x 16 bytes (its 64 banks) per cycle,
+// and 16 consecutive rows then cover 16 distinct 16-byte bank groups (row
+// parity picks the 128-byte half), so the MFMA operand reads and the
+// dequantizer's row-segment stores are conflict-free.
+//   * Activations go from global memory straight into the ring with
+//     global_load_lds_dwordx4: each instruction moves 8 whole 128-byte rows
+//     (8 cache lines; loads that spread 32 rows over one instruction cost the
+//     vector L1 32 line lookups and stall the MFMA stream).  Each wave loads
+//     and reads only its own rows, so the ring needs no workgroup barrier.
+//   * Packed weights (16 bytes per thread per step) and their scales sit in
+//     registers four steps ahead; each step dequantizes the next step's tile
+//     through the pair table into the other weight tile.
 // Tiles are numbered so that the workgroups of one XCD (workgroup id mod 8)
-// share activation row slices, which then stay in that XCD's L2.
+// share activation row slices, which then stay in that XCD's L2, and their
+// k loops start staggered so that only one of them misses on each slice.
 #include "rq_mfma.h"
 #include "rq_launch.h"
 #include "rq_linear.h"
 #include "rq_linear_dev.h"
+#include "rq_lora.h"
 
 namespace rq {
 
 constexpr int kGemmThreads = 256;
+constexpr int kGemmBM = 256;
+constexpr int kGemmBN = 128;
 constexpr int kGemmBK = 64;
-constexpr int kWPitch = kGemmBK + 8;  // operand elements per LDS weight row: the pad spreads rows over banks
-constexpr int kLutBytes = kF32PairLutQwords * 8;
-constexpr int kWDepth = 4;  // packed-weight prefetch distance in k-steps
-
-template <int BN>
-constexpr int gemm_lds_bytes() {
-  return kLutBytes + 2 * BN * kWPitch * 2;
-}
+constexpr int kGemmMB = 2;  // 32-row blocks per wave
+constexpr int kGemmNB = 4;  // 32-column blocks per wave
+constexpr int kLutBytes = kF32PairLutQwords * 8;     // 64 KiB
+constexpr int kXWaveBytes = 64 * 128;                // one wave's rows of one step
+constexpr int kXStepBytes = 4 * kXWaveBytes;         // 32 KiB
+constexpr int kWTileBytes = kGemmBN * 128;           // 16 KiB
+constexpr int kXRingOff = kLutBytes;
+constexpr int kWTileOff = kXRingOff + 2 * kXStepBytes;
+constexpr int kGemmLds = kWTileOff + 2 * kWTileBytes;  // 160 KiB
+constexpr int kWDepth = 4;                           // packed-weight prefetch distance in steps
+static_assert(kGemmLds == 160 * 1024, "LDS plan");
 
 struct GemmArgs {
   const uint16_t* x;
@@ -53,138 +69,144 @@ struct GemmEpi {
   int bias_dt;
   int rank, rank16;      // LoRA rank and rank rounded up to 16
   const uint16_t* u;     // RND(u) [M][rank16], zero padded
-  const void* lora_b;
-  int64_t ld_lora_b;
-  int lora_dt;
+  const uint16_t* bl;    // RND(B) [N][rank16], zero padded
   float scaling;
   uint16_t* y;
   int64_t ldy;
 };
 
-// 16 bytes at element offset `off` of a 16-bit array (unsigned 32-bit offset
-// from a wave-uniform base: the SGPR-base + VGPR-offset load form).
-__device__ __forceinline__ u32x4 ld16(const uint16_t* base, uint32_t off) {
-  const uint32_t byte_off = off * 2u;
-  return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + byte_off);
-}
+// Byte offset of 16-byte chunk c of row r in a swizzled 128-byte-row tile.
+__device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) { return r * 128u + ((c ^ ((r >> 1) & 7u)) << 4); }
 
-// One k-step's packed weights for this thread: BN rows x 32 bytes over 256
-// threads -- 16 bytes of one row (BN = 128) or a whole 32-byte row (BN = 256).
-template <int BN, class Scale>
+// One k-step's packed weights for this thread: 16 bytes (32 codes) of row
+// tid / 2, half tid % 2 of the step, and the row's scale.
+template <class Scale>
 struct GemmWLoads {
-  static constexpr int kChunks = BN / 128;  // 16-byte chunks per thread
-  u32x4 w[kChunks];
+  u32x4 w;
   typename Scale::Raw s;
 };
 
-template <int BN>
-__device__ __forceinline__ int w_row(int tid) { return BN == 128 ? (tid >> 1) : tid; }
-template <int BN>
-__device__ __forceinline__ int w_chunk(int tid) { return BN == 128 ? (tid & 1) : 0; }
-
-template <int BN, class Scale>
-__device__ __forceinline__ void gemm_issue_w(GemmWLoads<BN, Scale>& L, const GemmArgs& a, const Scale& scale,
+template <class Scale>
+__device__ __forceinline__ void gemm_issue_w(GemmWLoads<Scale>& L, const GemmArgs& a, const Scale& scale,
                                              uint32_t wrow, int64_t n, int64_t kt) {
-  constexpr int C = GemmWLoads<BN, Scale>::kChunks;
   const uint32_t off = wrow + uint32_t(kt) * 32u;  // byte offset; the host keeps the weights under 4 GiB
-#pragma unroll
-  for (int c = 0; c < C; ++c) L.w[c] = *reinterpret_cast<const u32x4*>(a.packed + (off + 16u * c));
+  L.w = *reinterpret_cast<const u32x4*>(a.packed + off);
   L.s = scale.load(n * a.blocks_per_row + ((kt * kGemmBK) >> a.bs_log2));
 }
 
-// Dequantize one k-step into an LDS weight tile (row-major, kWPitch).
-template <int XT, int BN, class Scale>
-__device__ __forceinline__ void gemm_dequant_w(const GemmWLoads<BN, Scale>& L, const Scale& scale, uint16_t* wt,
-                                               const u32x2* lut, uint32_t lane_off, int tid) {
-  constexpr int C = GemmWLoads<BN, Scale>::kChunks;
-  const float s = scale.value(L.s);
-  uint16_t* dst = wt + w_row<BN>(tid) * kWPitch + 32 * w_chunk<BN>(tid);
-#pragma unroll
-  for (int c = 0; c < C; ++c) {
-    const u32x4 v = L.w[c];
-    *reinterpret_cast<u32x4*>(dst + 32 * c) = expand8_scaled<XT>(lut, v.x, lane_off, s);
-    *reinterpret_cast<u32x4*>(dst + 32 * c + 8) = expand8_scaled<XT>(lut, v.y, lane_off, s);
-    *reinterpret_cast<u32x4*>(dst + 32 * c + 16) = expand8_scaled<XT>(lut, v.z, lane_off, s);
-    *reinterpret_cast<u32x4*>(dst + 32 * c + 24) = expand8_scaled<XT>(lut, v.w, lane_off, s);
-  }
+// Waits until at most N vector-memory loads of this wave are outstanding.
+// The activation ring is read through LDS, which the compiler's own wait
+// insertion does not track, so the kernel places these waits itself.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Activation operands: lane (i, q) of a wave feeds row i of each 32-row
-// block; within a 64-k step, sub-step s of the MFMA chain takes k = 16 s +
-// 8 q + e (e = 0..7), so the two lanes of a row load 32 contiguous bytes per
-// instruction (one half of a 64-byte sector, not two quarters of two), and
-// the four sub-steps cover the row's 128 bytes.  The weight operands read
-// from LDS use the same k order (any consistent permutation of k leaves the
-// dot product unchanged).
-//
-// One 64-k step for a wave's (32 MB) x BN tile, software-pipelined by hand
-// so that the matrix cores never wait on the other work of the wave: an
-// MFMA occupies the core for 32 cycles, in which the wave can issue a few
-// VALU, LDS and vector-memory instructions, so that work is spread between
-// the MFMAs rather than batched after them (in-order issue would otherwise
-// leave the core idle while the batch drains).  Sub-step s (k = 16 s + 8 q +
-// e, eight MFMAs in four pairs):
-//   head:   the weight-operand reads of sub-step s + 1;
-//   pair 0: one activation load (step j + 3, into xf, the register set step
-//           j - 1 used; element offset knext), or the packed weights of step
-//           j + 4 into wl_fill once the activations are all issued;
-//   pair 1: table addresses and lookups for dword s + 1 of this thread's
-//           packed weights of the next tile;
-//   pair 2, 3: scale-multiply and round dword s's lookups (issued a
-//           sub-step earlier), then store the 8 dequantized weights to LDS.
-// Scheduling fences pin each group, so every wait on the memory counter
-// covers only loads issued at least a step earlier and every wait on the
-// LDS counter covers reads issued a pair group or more earlier.
-template <int XT, int MB, int NB, int BN, bool DEQ, class Scale>
-__device__ __forceinline__ void gemm_step(f32x16 (&acc)[MB][NB], const u32x4 (&xa)[MB][4], u32x4 (&xf)[MB][4],
-                                          const uint16_t* wt, int i32, int q, const uint32_t (&xo)[MB],
-                                          int64_t knext, const GemmWLoads<BN, Scale>& wq, GemmWLoads<BN, Scale>& wl_fill,
-                                          const GemmArgs& a, const Scale& scale, uint32_t wrow, int64_t wn,
-                                          int64_t kfill, uint16_t* wdst, const u32x2* lut, uint32_t lane_off) {
-  constexpr int C = GemmWLoads<BN, Scale>::kChunks;
-  static_assert(NB == 4, "four MFMA pairs per sub-step");
-  static_assert(MB * 4 < 16, "activation loads fit in the pair-0 slots");
+// Workgroup barrier for the k loop: this wave's LDS stores are complete and
+// at most N of its vector-memory loads are still outstanding, then s_barrier.
+// (__syncthreads() would also drain every global load -- including the
+// packed-weight prefetch issued just before -- and expose a full memory
+// latency on every step.)
+template <int N>
+__device__ __forceinline__ void step_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// One direct-to-LDS load: 16 bytes per lane from global memory (wave-uniform
+// base + 32-bit byte offset) to LDS address lds_addr + 16 * lane.  Written
+// as inline assembly so that the compiler's wait insertion does not treat it
+// as an outstanding LDS access (it would otherwise drain every LDS read with
+// lgkmcnt(0) after each such load); the kernel waits for these loads itself
+// (wait_vmcnt / step_barrier).  The static LDS block starts at address 0, so
+// LDS addresses are byte offsets into it.
+__device__ __forceinline__ void dma16(const void* base, uint32_t byte_off, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(byte_off), "s"(base), "s"(lds_addr)
+               : "memory", "m0");
+}
+
+// Issue this wave's 8 direct-to-LDS loads of one step's activations
+// (instruction t: rows 8t .. 8t + 7 of the wave, lane l -> row r = 8t + l / 8,
+// slot l % 8, which holds chunk (l % 8) ^ ((r / 2) & 7)).  xo[t] is the
+// lane's element offset at k-step 0.
+__device__ __forceinline__ void x_dma(const GemmArgs& a, const uint32_t (&xo)[8], int64_t kstep, uint32_t dst) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t) dma16(a.x, (xo[t] + uint32_t(kstep) * kGemmBK) * 2u, dst + t * 1024);
+}
+
+// One 64-k step for a wave's 64 x 128 tile, software-pipelined by hand so
+// that the matrix cores never wait on the rest of the wave's work: an MFMA
+// keeps the core busy for 32 cycles, in which the wave can issue a few VALU,
+// LDS and vector-memory instructions, so that work is spread between the
+// MFMAs (in-order issue would otherwise leave the core idle while a batch of
+// it drains).  Sub-step s (k = 16 s + 8 q + e, eight MFMAs in four pairs):
+//   head:   activation and weight operand reads of sub-step s + 1;
+//   pair 0: (s < 2) four of the eight direct-to-LDS loads of step j + 1;
+//   pair 1: table lookups for dword s + 1 of this thread's packed weights
+//           of step j + 1;
+//   pair 2, 3: scale-multiply and round dword s's lookups, store the eight
+//           dequantized weights to the other weight tile; after the last
+//           pair, the packed weights of step j + 4 (the last loads of the
+//           step, so the next step's activation wait leaves them in flight).
+// Scheduling fences pin each group.
+template <int XT, bool DEQ, class Scale>
+__device__ __forceinline__ void gemm_step(f32x16 (&acc)[kGemmMB][kGemmNB], const uint8_t* xr, const uint8_t* wt,
+                                          int i32, int q, const GemmArgs& a, const uint32_t (&xo)[8],
+                                          int64_t kx, uint32_t xdst, const GemmWLoads<Scale>& wq,
+                                          GemmWLoads<Scale>& wl_fill, const Scale& scale, uint32_t wrow, int64_t wn,
+                                          int64_t kfill, uint8_t* wdst, uint32_t wrow_tile, uint32_t whalf,
+                                          const u32x2* lut, uint32_t lane_off) {
+  // Everything derived from the packed weights (scale, the 16 table
+  // addresses) is computed here, before this step's direct-to-LDS loads:
+  // those loads are invisible to the compiler's wait counting, so a later
+  // use of a loaded register would make it wait on them too.
   float sc = 0.0f;
-  if constexpr (DEQ) sc = scale.value(wq.s);
-  auto word_of = [&](int c, int s) -> uint32_t {
-    return s == 0 ? wq.w[c].x : s == 1 ? wq.w[c].y : s == 2 ? wq.w[c].z : wq.w[c].w;
+  uint32_t taddr[4][4];
+  if constexpr (DEQ) {
+    sc = scale.value(wq.s);
+    const uint32_t words[4] = {wq.w.x, wq.w.y, wq.w.z, wq.w.w};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int h = 0; h < 4; ++h)
+        taddr[s][h] = __builtin_amdgcn_perm(words[s], lane_off, 0x0C0C0000u | (uint32_t(4 + h) << 8));
+  }
+  auto lookup = [&](u32x2 (&lk)[4], int s) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+      lk[h] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(lut) + taddr[s][h]);
   };
-  auto lookup = [&](u32x2 (&lk)[C][4], int s) {
+  auto read_ops = [&](u32x4 (&xa)[kGemmMB], u32x4 (&b)[kGemmNB], int s) {
+    const uint32_t c = uint32_t(2 * s + q);
 #pragma unroll
-    for (int c = 0; c < C; ++c)
+    for (int mb = 0; mb < kGemmMB; ++mb)
+      xa[mb] = *reinterpret_cast<const u32x4*>(xr + swz(uint32_t(32 * mb + i32), c));
 #pragma unroll
-      for (int h = 0; h < 4; ++h) {
-        const uint32_t addr = __builtin_amdgcn_perm(word_of(c, s), lane_off, 0x0C0C0000u | (uint32_t(4 + h) << 8));
-        lk[c][h] = *reinterpret_cast<const u32x2*>(reinterpret_cast<const char*>(lut) + addr);
-      }
+    for (int nb = 0; nb < kGemmNB; ++nb)
+      b[nb] = *reinterpret_cast<const u32x4*>(wt + swz(uint32_t(32 * nb + i32), c));
   };
-  u32x4 b[NB], bn[NB];
-  u32x2 lk[C][4], lkn[C][4];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-    b[nb] = *reinterpret_cast<const u32x4*>(wt + (32 * nb + i32) * kWPitch + 8 * q);
+  u32x4 xa[kGemmMB], b[kGemmNB], xan[kGemmMB], bn[kGemmNB];
+  u32x2 lk[4], lkn[4];
+  read_ops(xa, b, 0);
   if constexpr (DEQ) lookup(lk, 0);
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    if (s < 3) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        bn[nb] = *reinterpret_cast<const u32x4*>(wt + (32 * nb + i32) * kWPitch + 8 * q + 16 * (s + 1));
-    }
+    if (s < 3) read_ops(xan, bn, s + 1);
     __builtin_amdgcn_sched_barrier(0);
-    uint32_t r[C][4];
+    uint32_t r[4];
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
+    for (int nb = 0; nb < kGemmNB; ++nb) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma32x32x16<XT>(xa[mb][s], b[nb], acc[mb][nb]);
+      for (int mb = 0; mb < kGemmMB; ++mb) acc[mb][nb] = mfma32x32x16<XT>(xa[mb], b[nb], acc[mb][nb]);
       if (nb == 0) {
-        // activation loads: 4 MB pieces over the 4 sub-steps' pair-0 slots,
-        // MB per slot, a row block's pieces in line order
+        if (s < 2) {
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          xf[mb][s] = ld16(a.x, xo[mb] + uint32_t(knext) + 16u * s);
-        if (s == 3) gemm_issue_w<BN>(wl_fill, a, scale, wrow, wn, kfill);
+          for (int t = 4 * s; t < 4 * s + 4; ++t) {
+            dma16(a.x, (xo[t] + uint32_t(kx) * kGemmBK) * 2u, xdst + t * 1024);
+          }
+        }
       } else if (nb == 1) {
         if constexpr (DEQ) {
           if (s < 3) lookup(lkn, s + 1);
@@ -192,40 +214,29 @@ __device__ __forceinline__ void gemm_step(f32x16 (&acc)[MB][NB], const u32x4 (&x
       } else if constexpr (DEQ) {
         const int h0 = nb == 2 ? 0 : 2;
 #pragma unroll
-        for (int c = 0; c < C; ++c)
-#pragma unroll
-          for (int h = h0; h < h0 + 2; ++h)
-            r[c][h] = cvt_pk<XT>(__fmul_rn(u2f(lk[c][h].x), sc), __fmul_rn(u2f(lk[c][h].y), sc));
-        if (nb == 3) {
-#pragma unroll
-          for (int c = 0; c < C; ++c)
-            *reinterpret_cast<u32x4*>(wdst + 32 * c + 8 * s) = u32x4{r[c][0], r[c][1], r[c][2], r[c][3]};
-        }
+        for (int h = h0; h < h0 + 2; ++h) r[h] = cvt_pk<XT>(__fmul_rn(u2f(lk[h].x), sc), __fmul_rn(u2f(lk[h].y), sc));
+        if (nb == 3)
+          *reinterpret_cast<u32x4*>(wdst + swz(wrow_tile, 4u * whalf + uint32_t(s))) = u32x4{r[0], r[1], r[2], r[3]};
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     if (s < 3) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) b[nb] = bn[nb];
+      for (int mb = 0; mb < kGemmMB; ++mb) xa[mb] = xan[mb];
 #pragma unroll
-      for (int c = 0; c < C; ++c)
+      for (int nb = 0; nb < kGemmNB; ++nb) b[nb] = bn[nb];
 #pragma unroll
-        for (int h = 0; h < 4; ++h) lk[c][h] = lkn[c][h];
+      for (int h = 0; h < 4; ++h) lk[h] = lkn[h];
     }
   }
+  gemm_issue_w(wl_fill, a, scale, wrow, wn, kfill);
+  __builtin_amdgcn_sched_barrier(0);
 }
 
-template <int XT, int BN, int MB, class Scale>
+template <int XT, class Scale>
 __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a, Scale scale, GemmEpi e) {
-  constexpr int NB = BN / 32;  // 32-wide column blocks per wave
-  constexpr int BM = 4 * 32 * MB;
-  // One static LDS block: the pair table at address 0 (lookups fold their
-  // base into the instruction offset), then two weight tiles.  The epilogue
-  // reuses all of it for RND(lora_B) rows.
-  __shared__ __attribute__((aligned(16))) uint8_t lds[gemm_lds_bytes<BN>()];
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
   u32x2* lut = reinterpret_cast<u32x2*>(lds);
-  uint16_t* wt0 = reinterpret_cast<uint16_t*>(lds + kLutBytes);
-  uint16_t* wt1 = wt0 + BN * kWPitch;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int i32 = lane & 31, q = lane >> 5;
@@ -235,30 +246,34 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a, Scal
   const int64_t g = blockIdx.x;
   const int64_t t = a.xcd_map ? (g % 8) * (T / 8) + g / 8 : g;
   const int64_t mt = t / a.tiles_n, nt = t % a.tiles_n;
-  const int64_t m0 = mt * BM, n0 = nt * BN;
-  const int64_t m0w = m0 + 32 * MB * wave;
+  const int64_t m0 = mt * kGemmBM, n0 = nt * kGemmBN;
+  const int64_t m0w = m0 + 64 * wave;
   const int64_t nk = a.K / kGemmBK;
 
-  // Per-lane element offsets from the activation base (32-bit: the host
-  // keeps the activations under 4 GiB), so the loads use the SGPR-base form.
-  uint32_t xo[MB];
+  // Activation DMA lanes: per instruction t, row r = 8t + lane / 8 of the
+  // wave, chunk (lane % 8) ^ ((r / 2) & 7); element offsets are 32-bit (the
+  // host keeps the activations under 4 GiB).
+  uint32_t xo[8];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    int64_t m = m0w + 32 * mb + i32;
+  for (int tt = 0; tt < 8; ++tt) {
+    const int r = 8 * tt + (lane >> 3);
+    int64_t m = m0w + r;
     m = m < a.M ? m : a.M - 1;  // rows past M re-read a live row; never stored
-    xo[mb] = uint32_t(m * a.ldx + 8 * q);
+    xo[tt] = uint32_t(m * a.ldx + 8 * ((lane & 7) ^ ((r >> 1) & 7)));
   }
-  int64_t wn = n0 + w_row<BN>(tid);
+  uint8_t* xring = lds + kXRingOff + wave * kXWaveBytes;  // + (step & 1) * kXStepBytes
+  const uint32_t xring_addr = __builtin_amdgcn_readfirstlane(uint32_t(kXRingOff + wave * kXWaveBytes));
+  uint8_t* wtile = lds + kWTileOff;                       // + (step & 1) * kWTileBytes
+  const uint32_t wrow_tile = uint32_t(tid >> 1), whalf = uint32_t(tid & 1);
+  int64_t wn = n0 + wrow_tile;
   wn = wn < a.N ? wn : a.N - 1;  // rows past N re-read a live row; never stored
-  const uint32_t wrow = uint32_t(wn * (a.K >> 1) + 16 * w_chunk<BN>(tid));  // byte offset of this thread's row segment
+  const uint32_t wrow = uint32_t(wn * (a.K >> 1) + 16 * whalf);  // byte offset of this thread's row segment
 
-  // Staggered start: workgroups that share an activation row slice begin
-  // their k loop at different steps (wrapping around K), so all but the
-  // first to reach a step find its activations already in L2 instead of
-  // all of them waiting on the same HBM fetch.  Step j covers k-step
-  // ks(j) = (j + k_off) mod nk; the fp32 sum order changes, nothing else.
+  // Staggered start: step j covers k-step ks(j) = (j + k_off) mod nk.
   const int nk32 = __builtin_amdgcn_readfirstlane(int(nk));
-  const int k_off = __builtin_amdgcn_readfirstlane(int(((nt & 31) * nk) >> 5));
+  // (workgroups sharing a weight tile, one per XCD, are staggered too, so
+  // that one of them misses on each weight line and the rest hit the MALL)
+  const int k_off = __builtin_amdgcn_readfirstlane(int((((nt + 4 * mt) & 31) * nk) >> 5));
   auto ks = [&](int64_t j) -> int64_t {
     int v = int(j) + k_off;
     v = v >= nk32 ? v - nk32 : v;
@@ -266,51 +281,51 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a, Scal
     return v;
   };
 
-  // Register pipelines: packed weights kWDepth steps ahead (wl[j % 4] holds
-  // step j + 4 once step j has issued it), activations three steps ahead
-  // (xa[j % 4] holds step j; step j fills xa[(j + 3) % 4]).
-  GemmWLoads<BN, Scale> wl[kWDepth];
+  // prologue: activations of step 0, packed weights of steps 0..3, the
+  // table, and step 0's weight tile
+  x_dma(a, xo, ks(0), xring_addr);
+  GemmWLoads<Scale> wl[kWDepth];
 #pragma unroll
-  for (int d = 0; d < kWDepth; ++d) gemm_issue_w<BN>(wl[d], a, scale, wrow, wn, ks(d));
-  u32x4 xa[4][MB][4];
-#pragma unroll
-  for (int h = 0; h < 3; ++h)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) xa[h][mb][s] = ld16(a.x, xo[mb] + uint32_t(ks(h) * kGemmBK) + 16u * s);
-
+  for (int d = 0; d < kWDepth; ++d) gemm_issue_w(wl[d], a, scale, wrow, wn, ks(d));
   fill_f32pair_lut<kGemmThreads * 2>(lut, tid);  // the 512-thread fill pattern, in two halves
   fill_f32pair_lut<kGemmThreads * 2>(lut, tid + kGemmThreads);
   __syncthreads();
   const uint32_t lane_off = uint32_t(lane & 31) * 8u;
-  gemm_dequant_w<XT, BN>(wl[0], scale, wt0, lut, lane_off, tid);
+  {
+    const float sc = scale.value(wl[0].s);
+    const uint32_t words[4] = {wl[0].w.x, wl[0].w.y, wl[0].w.z, wl[0].w.w};
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      *reinterpret_cast<u32x4*>(wtile + swz(wrow_tile, 4u * whalf + uint32_t(s))) =
+          expand8_scaled<XT>(lut, words[s], lane_off, sc);
+  }
+  wait_vmcnt<0>();
   __syncthreads();
 
-  f32x16 acc[MB][NB];
+  f32x16 acc[kGemmMB][kGemmNB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int mb = 0; mb < kGemmMB; ++mb)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int nb = 0; nb < kGemmNB; ++nb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
 
-  // Step j: MFMAs on tile j % 2 and xa[j % 4]; loads of activations j + 3
-  // into xa[(j + 3) % 4] and packed weights j + 4 into wl[j % 4]; dequantize
-  // step j + 1 from wl[(j + 1) % 4] into tile (j + 1) % 2; barrier.  Four
-  // steps per iteration index every register set and tile statically; the
-  // loop has a single exit, so the accumulators stay in place.  Steps past
-  // the end wrap around K (in bounds; their results are never used).
-  uint16_t* wd[2];
-  wd[0] = wt0 + w_row<BN>(tid) * kWPitch + 32 * w_chunk<BN>(tid);  // this thread's row segment
-  wd[1] = wd[0] + BN * kWPitch;
-  const uint16_t* wts[2] = {wt0, wt1};
-#define RQ_GEMM_STEP(J, P)                                                                                \
-  do {                                                                                                    \
-    gemm_step<XT, MB, NB, BN, true>(acc, xa[P], xa[((P) + 3) & 3], wts[(P) & 1], i32, q, xo,               \
-                                    ks((J) + 3) * kGemmBK, wl[((P) + 1) & 3], wl[P], a, scale, wrow, wn,   \
-                                    ks((J) + kWDepth), wd[((P) + 1) & 1], lut, lane_off);                  \
-    __syncthreads();                                                                                      \
+  // Step j: MFMAs on weight tile j % 2 and activation ring slot j % 2;
+  // direct-to-LDS loads of activations j + 1 into slot (j + 1) % 2;
+  // dequantize step j + 1 from wl[(j + 1) % 4] into tile (j + 1) % 2;
+  // packed weights j + 4 into wl[j % 4]; then wait for this wave's
+  // activation loads (all but the step's kW trailing weight loads) and
+  // barrier.  Four steps per iteration index every register set statically;
+  // the loop has a single exit, so the accumulators stay in place.  Steps
+  // past the end wrap around K (in bounds; their results are never used).
+  constexpr int kW = 1 + Scale::kLoads;  // vector-memory loads of one gemm_issue_w
+#define RQ_GEMM_STEP(J, P)                                                                                  \
+  do {                                                                                                      \
+    gemm_step<XT, true>(acc, xring + ((P) & 1) * kXStepBytes, wtile + ((P) & 1) * kWTileBytes, i32, q, a, xo, \
+                        ks((J) + 1), xring_addr + (((P) + 1) & 1) * kXStepBytes, wl[((P) + 1) & 3], wl[P], scale, \
+                        wrow, wn, ks((J) + kWDepth), wtile + (((P) + 1) & 1) * kWTileBytes, wrow_tile, whalf,  \
+                        lut, lane_off);                                                                     \
+    step_barrier<kW>();                                                                                     \
   } while (0)
   int64_t j = 0;
   for (; j + 4 <= nk; j += 4) {
@@ -324,47 +339,63 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a, Scal
   if (rem > 1) RQ_GEMM_STEP(j + 1, 1);
   if (rem > 2) RQ_GEMM_STEP(j + 2, 2);
 #undef RQ_GEMM_STEP
+  wait_vmcnt<0>();  // nothing may still be landing in LDS when the epilogue reuses it
 
-  // ---- epilogue.  base = RND(acc + RND(bias)); the LoRA product
-  // RND(u) RND(B)^T accumulates per 32-column block by MFMA (u operands from
-  // the rounded u rows in global memory, RND(B) rows staged in LDS); then
-  // y = RND(base + RND(RND(lora) * scaling)).
+  // ---- epilogue.  y = RND(RND(acc + RND(bias)) + RND(RND(lora) * scaling))
+  // with lora = RND(u) RND(B)^T accumulated by MFMA in chunks of 64 ranks,
+  // both operands staged from their pre-rounded 16-bit copies into LDS
+  // (u rows of the tile, B rows of the tile, 144-byte pitch).
   const int rank = e.rank;
-  const int r16 = e.rank16;
-  const int bpitch = r16 + 8;
-  uint16_t* bs = reinterpret_cast<uint16_t*>(lds);  // [BN][bpitch]
+  f32x16 lo[kGemmMB][kGemmNB];
+#pragma unroll
+  for (int mb = 0; mb < kGemmMB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < kGemmNB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) lo[mb][nb][r] = 0.0f;
   if (rank > 0) {
-    __syncthreads();  // every wave is done with the weight tiles and the table
-    for (int idx = tid; idx < BN * r16; idx += kGemmThreads) {
-      const int r = idx / r16, j = idx - r * r16;
-      const int64_t n = n0 + r;
-      const float v = (j < rank && n < a.N) ? load_as_f32(e.lora_b, n * e.ld_lora_b + j, e.lora_dt) : 0.0f;
-      bs[r * bpitch + j] = uint16_t(to_x16<XT>(v));
-    }
-    __syncthreads();
-  }
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int64_t n = n0 + 32 * nb + i32;
-    const float bias = (e.bias && n < a.N) ? round_x<XT>(load_as_f32(e.bias, n, e.bias_dt)) : 0.0f;
-    f32x16 lo[MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) lo[mb][r] = 0.0f;
-    for (int s = 0; s < r16 / 16; ++s) {
-      const u32x4 ub = *reinterpret_cast<const u32x4*>(bs + (32 * nb + i32) * bpitch + 16 * s + 8 * q);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        int64_t m = m0w + 32 * mb + i32;
+    constexpr int kP = 72;  // staging pitch in elements
+    uint16_t* us = reinterpret_cast<uint16_t*>(lds);   // [256][kP]
+    uint16_t* bs = us + kGemmBM * kP;                  // [128][kP]
+    for (int j0 = 0; j0 < e.rank16; j0 += 64) {
+      const int w8 = (e.rank16 - j0 < 64 ? e.rank16 - j0 : 64) / 8;  // 16-byte chunks per row
+      __syncthreads();  // the tiles, ring and table (first chunk) or the last chunk's operands are free
+      for (int idx = tid; idx < kGemmBM * w8; idx += kGemmThreads) {
+        const int r = idx / w8, c = idx - r * w8;
+        int64_t m = m0 + r;
         m = m < a.M ? m : a.M - 1;
-        const u32x4 ua = *reinterpret_cast<const u32x4*>(e.u + m * r16 + 16 * s + 8 * q);
-        lo[mb] = mfma32x32x16<XT>(ua, ub, lo[mb]);
+        *reinterpret_cast<u32x4*>(us + r * kP + 8 * c) =
+            *reinterpret_cast<const u32x4*>(e.u + m * e.rank16 + j0 + 8 * c);
+      }
+      for (int idx = tid; idx < kGemmBN * w8; idx += kGemmThreads) {
+        const int r = idx / w8, c = idx - r * w8;
+        int64_t n = n0 + r;
+        n = n < a.N ? n : a.N - 1;
+        *reinterpret_cast<u32x4*>(bs + r * kP + 8 * c) =
+            *reinterpret_cast<const u32x4*>(e.bl + n * e.rank16 + j0 + 8 * c);
+      }
+      __syncthreads();
+      for (int s = 0; s < w8 / 2; ++s) {
+        u32x4 ua[kGemmMB];
+#pragma unroll
+        for (int mb = 0; mb < kGemmMB; ++mb)
+          ua[mb] = *reinterpret_cast<const u32x4*>(us + (64 * wave + 32 * mb + i32) * kP + 16 * s + 8 * q);
+#pragma unroll
+        for (int nb = 0; nb < kGemmNB; ++nb) {
+          const u32x4 ub = *reinterpret_cast<const u32x4*>(bs + (32 * nb + i32) * kP + 16 * s + 8 * q);
+#pragma unroll
+          for (int mb = 0; mb < kGemmMB; ++mb) lo[mb][nb] = mfma32x32x16<XT>(ua[mb], ub, lo[mb][nb]);
+        }
       }
     }
-    if (n >= a.N) continue;
+  }
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+  for (int nb = 0; nb < kGemmNB; ++nb) {
+    const int64_t n = n0 + 32 * nb + i32;
+    if (n >= a.N) continue;
+    const float bias = e.bias ? round_x<XT>(load_as_f32(e.bias, n, e.bias_dt)) : 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < kGemmMB; ++mb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t m = m0w + 32 * mb + 8 * (r >> 2) + 4 * q + (r & 3);
@@ -372,66 +403,49 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a, Scal
         float v = acc[mb][nb][r];
         if (e.bias) v = __fadd_rn(v, bias);
         v = round_x<XT>(v);
-        if (rank > 0) v = round_x<XT>(__fadd_rn(v, round_x<XT>(__fmul_rn(round_x<XT>(lo[mb][r]), e.scaling))));
+        if (rank > 0)
+          v = round_x<XT>(__fadd_rn(v, round_x<XT>(__fmul_rn(round_x<XT>(lo[mb][nb][r]), e.scaling))));
         e.y[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
       }
     }
   }
 }
 
-// RND(u) for the epilogue: the sum of the KS fp32 partial products that
-// lora_u_kernel wrote ([KS][M][rank]), rounded to the activation dtype, as
-// [M][rank16] with zero padding.
-template <int XT>
-__global__ __launch_bounds__(256) void lora_u_round_kernel(const float* __restrict__ up, int KS, int64_t M,
-                                                           int rank, int rank16, uint16_t* __restrict__ u16) {
-  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= M * rank16) return;
-  const int64_t m = i / rank16;
-  const int j = int(i - m * rank16);
-  float v = 0.0f;
-  if (j < rank)
-    for (int k = 0; k < KS; ++k) v = __fadd_rn(v, up[(int64_t(k) * M + m) * rank + j]);
-  u16[i] = uint16_t(to_x16<XT>(v));
-}
-
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 struct GemmPlan {
-  int BN, MB;
   int tiles_m, tiles_n;
   bool xcd_map;
-  int u_splits, rank16;
-  size_t ws_bytes, u16_offset;
+  int rank16;
+  LoraRowsPlan lr;
+  size_t u16_offset, bl16_offset, ws_bytes;
 };
 
-static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank) {
+static GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus) {
   GemmPlan p{};
-  p.MB = 2;
-  p.BN = 128;
-  p.tiles_m = int((M + 4 * 32 * p.MB - 1) / (4 * 32 * p.MB));
-  p.tiles_n = int((N + p.BN - 1) / p.BN);
+  p.tiles_m = int((M + kGemmBM - 1) / kGemmBM);
+  p.tiles_n = int((N + kGemmBN - 1) / kGemmBN);
   const int64_t T = int64_t(p.tiles_m) * p.tiles_n;
   p.xcd_map = T % 8 == 0;
   p.rank16 = int((rank + 15) & ~int64_t(15));
-  p.u_splits = 0;
   p.ws_bytes = 0;
   if (rank > 0) {
-    const int64_t steps_per_wg = 16;  // 32-k steps per lora_u workgroup
-    p.u_splits = int((K / 32 + steps_per_wg - 1) / steps_per_wg);
-    p.u16_offset = (size_t(p.u_splits) * M * rank * 4 + 255) & ~size_t(255);
-    p.ws_bytes = p.u16_offset + size_t(M) * p.rank16 * 2;
+    // [lora_rows partials][RND(A) r x K][RND(u) M x r16][RND(B) N x r16]
+    p.lr = plan_lora_rows(M, K, rank, cus);
+    p.u16_offset = p.lr.part_bytes + p.lr.s16_bytes;
+    p.bl16_offset = p.u16_offset + ((size_t(M) * p.rank16 * 2 + 255) & ~size_t(255));
+    p.ws_bytes = p.bl16_offset + size_t(N) * p.rank16 * 2;
   }
   return p;
 }
 
 int gemm_workspace(const LinearArgs& L, size_t* bytes) {
-  *bytes = plan_gemm(L.M, L.N, L.K, L.rank).ws_bytes;
+  *bytes = plan_gemm(L.M, L.N, L.K, L.rank, device_cus()).ws_bytes;
   return RQ_OK;
 }
 
-template <int XT, int BN, int MB, class Scale>
+template <int XT, class Scale>
 static int launch_gemm_t(const LinearArgs& L, const GemmPlan& p, Scale scale, const GemmEpi& e,
                          hipStream_t stream) {
   GemmArgs a;
@@ -447,14 +461,14 @@ static int launch_gemm_t(const LinearArgs& L, const GemmPlan& p, Scale scale, co
   a.tiles_n = p.tiles_n;
   a.xcd_map = p.xcd_map;
   const unsigned grid = unsigned(int64_t(p.tiles_m) * p.tiles_n);
-  nf4_gemm_kernel<XT, BN, MB, Scale><<<grid, kGemmThreads, 0, stream>>>(a, scale, e);
+  nf4_gemm_kernel<XT, Scale><<<grid, kGemmThreads, 0, stream>>>(a, scale, e);
   return rq_check_launch();
 }
 
 template <int XT, class Scale>
 static int launch_gemm_cfg(const LinearArgs& L, const GemmPlan& p, Scale scale, const GemmEpi& e,
                            hipStream_t stream) {
-  return launch_gemm_t<XT, 128, 2>(L, p, scale, e, stream);
+  return launch_gemm_t<XT>(L, p, scale, e, stream);
 }
 
 template <int XT>
@@ -477,21 +491,13 @@ static int run_gemm(const LinearArgs& L, const GemmPlan& p, const GemmEpi& e, hi
   }
 }
 
-template <int XT>
-static int launch_u_round(const float* up, int ks, int64_t M, int rank, int rank16, uint16_t* u16,
-                          hipStream_t stream) {
-  const int64_t total = M * rank16;
-  lora_u_round_kernel<XT><<<unsigned((total + 255) / 256), 256, 0, stream>>>(up, ks, M, rank, rank16, u16);
-  return rq_check_launch();
-}
-
 int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream) {
   // the activation operands are loaded 16 bytes at a time
   if (!aligned(L.x, 16) || L.ldx % 8 != 0) return RQ_ERR_BAD_ALIGNMENT;
   // activation and packed-weight loads use 32-bit byte offsets
   if (double(L.M) * double(L.ldx) * 2.0 >= 4294967296.0 || double(L.N) * double(L.K) * 0.5 >= 4294967296.0)
     return RQ_ERR_UNSUPPORTED;
-  const GemmPlan p = plan_gemm(L.M, L.N, L.K, L.rank);
+  const GemmPlan p = plan_gemm(L.M, L.N, L.K, L.rank, device_cus());
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
   if (workspace && !aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;
   GemmEpi e{};
@@ -499,21 +505,23 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   e.bias_dt = L.bias_dtype;
   e.rank = int(L.rank > 0 ? L.rank : 0);
   e.rank16 = p.rank16;
-  e.lora_b = L.lora_b;
-  e.ld_lora_b = L.ld_lora_b;
-  e.lora_dt = L.lora_dtype;
   e.scaling = L.scaling;
   e.y = static_cast<uint16_t*>(L.y);
   e.ldy = L.ldy;
-  int st;
   if (e.rank > 0) {
-    float* up = static_cast<float*>(workspace);
-    uint16_t* u16 = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + p.u16_offset);
-    if ((st = run_lora_u(L, p.u_splits, up, stream)) != RQ_OK) return st;
-    st = L.x_dtype == RQ_DTYPE_BF16 ? launch_u_round<RQ_DTYPE_BF16>(up, p.u_splits, L.M, e.rank, p.rank16, u16, stream)
-                                    : launch_u_round<RQ_DTYPE_F16>(up, p.u_splits, L.M, e.rank, p.rank16, u16, stream);
+    char* ws = static_cast<char*>(workspace);
+    uint16_t* u16 = reinterpret_cast<uint16_t*>(ws + p.u16_offset);
+    uint16_t* bl16 = reinterpret_cast<uint16_t*>(ws + p.bl16_offset);
+    // u = RND(xl . RND(A)^T), A [r][K] row-major (lora_layer.py:67)
+    int st = run_lora_rows(L.x_dtype, static_cast<const uint16_t*>(L.lora_x), L.ld_lora_x, L.M, L.K, L.lora_a,
+                           L.lora_dtype, L.K, 1, e.rank, false, 1.0f, p.lr, reinterpret_cast<float*>(ws),
+                           reinterpret_cast<uint16_t*>(ws + p.lr.part_bytes), u16, p.rank16, stream);
+    if (st != RQ_OK) return st;
+    // RND(B), B [N][r] with row stride ld_lora_b
+    st = run_lora_round(L.x_dtype, L.lora_b, L.lora_dtype, L.ld_lora_b, 1, L.N, e.rank, p.rank16, bl16, stream);
     if (st != RQ_OK) return st;
     e.u = u16;
+    e.bl = bl16;
   }
   if (L.x_dtype == RQ_DTYPE_BF16) return run_gemm<RQ_DTYPE_BF16>(L, p, e, stream);
   return run_gemm<RQ_DTYPE_F16>(L, p, e, stream);

@@ -23,6 +23,7 @@ __device__ __forceinline__ float ld_f32(const void* __restrict__ p, int64_t i) {
 // quantization: c2 code times its c2_scales entry).
 template <int SDT>
 struct ScaleAbsmax {
+  static constexpr int kLoads = 1;  // vector-memory loads per scale
   const void* p;
   typedef uint32_t Raw;
   __device__ __forceinline__ Raw load(int64_t b) const {
@@ -39,6 +40,7 @@ struct ScaleAbsmax {
 
 template <int SDT>
 struct ScaleDQ {
+  static constexpr int kLoads = 2;  // vector-memory loads per scale
   const uint8_t* c2;
   const void* c2s;
   int fmt;
