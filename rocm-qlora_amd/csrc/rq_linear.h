@@ -68,4 +68,30 @@ int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
 int gemm_workspace(const LinearArgs& L, size_t* bytes);
 int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream);
 
+// Unpacked arguments of rq_nf4_linear_dx (see include/rocm_qlora_amd.h).
+struct DxArgs {
+  const void* dy;
+  int dy_dtype;
+  int64_t M, N, lddy;
+  const uint8_t* w_packed;
+  int64_t K, block_size;
+  const void* absmax;  // absmax, or c2_scales when c2 != nullptr
+  int absmax_dtype;
+  const uint8_t* c2;
+  int c2_format;
+  int64_t block2;
+  const void* lora_a;
+  const void* lora_b;
+  int64_t ld_lora_b;
+  int lora_dtype;
+  int64_t rank;
+  float scaling;
+  void* dx;
+  int64_t lddx;
+};
+
+int validate_dx(const DxArgs& D);
+int dx_workspace(const DxArgs& D, size_t* bytes);
+int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t stream);
+
 }  // namespace rq

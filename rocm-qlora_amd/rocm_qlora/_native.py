@@ -40,6 +40,12 @@ SIGNATURES = {
                       _P, _I32,                              # bias, dtype
                       _P, _I64, _P, _P, _I64, _I32, _I64, _F32,  # lora x, ld, A, B, ldB, dtype, rank, scaling
                       _P, _I64, _P, _I64, _P],               # y, ldy, workspace, bytes, stream
+    "rq_nf4_linear_dx_workspace_size": [_I32, _I64, _I64, _I64, _I64, _P],
+    "rq_nf4_linear_dx": [_P, _I32, _I64, _I64, _I64,         # dy, dtype, M, N, lddy
+                         _P, _I64, _I64, _P, _I32,           # packed, K, block, absmax, dtype
+                         _P, _I32, _I64,                     # c2, c2 format, block2
+                         _P, _P, _I64, _I32, _I64, _F32,     # A, B, ldB, dtype, rank, scaling
+                         _P, _I64, _P, _I64, _P],            # dx, lddx, workspace, bytes, stream
 }
 _RESTYPE = {"rq_status_string": ctypes.c_char_p, "rq_build_arch": ctypes.c_char_p}
 

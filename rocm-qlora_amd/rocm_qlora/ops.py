@@ -126,3 +126,66 @@ def _nf4_linear_fp32(x, weight_quant, weight_scales, N, block_size, bias, c2, c2
         xl = x if lora_x is None else lora_x
         y = y + (xl @ lora_a.to(x.dtype).T @ lora_b.to(x.dtype).T * scaling)
     return y
+
+
+def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optional[torch.Tensor],
+                  in_features: int, block_size: int = 64, *,
+                  c2: Optional[torch.Tensor] = None, c2_scales: Optional[torch.Tensor] = None,
+                  blocksize_2: int = 256, use_fp8_c2: bool = True,
+                  lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
+                  scaling: float = 0.0) -> torch.Tensor:
+    """dX = dY . dequant(W) (+ the LoRA term ((dY * s) . B) . A) for an NF4
+    weight stored flat (dequant_matmul.py:338-351, lora_layer.py:67
+    differentiated).  dy: [..., N] bf16/fp16 on the GPU, N % 64 == 0;
+    output [..., K] in dy's dtype."""
+    N = dy.shape[-1]
+    K = int(in_features)
+    dq = c2 is not None
+    scales = c2_scales if dq else weight_scales
+    dev = nat.require_gpu(dy, weight_quant, scales, lora_a, lora_b, c2)
+    packed = weight_quant.reshape(-1)
+    if packed.dtype != torch.uint8:
+        raise TypeError(f"NF4 weight_quant must be uint8, got {packed.dtype}")
+    if packed.numel() * 2 < N * K:
+        raise RuntimeError(f"weight_quant holds {packed.numel() * 2} codes, need {N}x{K}")
+    packed = packed.contiguous()
+    scales = scales.reshape(-1).contiguous()
+    lead = dy.shape[:-1]
+    with on(dev):
+        dy2, lddy = _rows(dy, N)
+        M = dy2.shape[0]
+        if dy2.data_ptr() % 16:
+            dy2, lddy = dy2.contiguous().clone(), N
+        dx = torch.empty((M, K), dtype=dy.dtype, device=dev)
+        if M == 0:
+            return dx.reshape(*lead, K)
+        rank = 0
+        la = lb = None
+        ldb = 0
+        lcode = 0
+        if lora_a is not None and lora_b is not None and lora_a.shape[0] > 0:
+            rank = lora_a.shape[0]
+            if lora_a.shape[1] != K or lora_b.shape != (N, rank):
+                raise RuntimeError(f"LoRA shapes {tuple(lora_a.shape)} / {tuple(lora_b.shape)} do not fit "
+                                   f"{N}x{K}")
+            if lora_a.dtype not in (torch.float32, dy.dtype):
+                lora_a = lora_a.float()
+            if lora_b.dtype != lora_a.dtype:
+                lora_b = lora_b.to(lora_a.dtype)
+            la = lora_a.contiguous()
+            lb = lora_b.contiguous()
+            ldb = rank
+            lcode = nat.dtype_code(la.dtype)
+        import ctypes
+        nbytes = ctypes.c_int64(0)
+        nat.call("rq_nf4_linear_dx_workspace_size", nat.dtype_code(dy.dtype), M, N, K, rank, ctypes.byref(nbytes))
+        ws = torch.empty(nbytes.value, dtype=torch.uint8, device=dev) if nbytes.value else None
+        codes = c2.reshape(-1).view(torch.uint8).contiguous() if dq else None
+        nat.call("rq_nf4_linear_dx",
+                 dy2.data_ptr(), nat.dtype_code(dy.dtype), M, N, lddy,
+                 packed.data_ptr(), K, block_size, scales.data_ptr(), nat.dtype_code(scales.dtype),
+                 nat.ptr(codes), nat.C2_FP8_E4M3FNUZ if use_fp8_c2 else nat.C2_INT8, blocksize_2,
+                 nat.ptr(la), nat.ptr(lb), ldb, lcode, rank, float(scaling),
+                 dx.data_ptr(), K, nat.ptr(ws), ws.numel() if ws is not None else 0,
+                 nat.stream_handle(dev))
+    return dx.reshape(*lead, K)

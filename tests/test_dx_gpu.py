@@ -1,0 +1,133 @@
+"""GPU parity of the NF4 dX backward (dX = dY . W_deq + ((dY * s) . B) . A):
+HIP MFMA kernel through the C ABI vs the oracle's restatement of
+_FusedNF4MatmulFunc.backward (dequant_matmul.py:338-351) plus the adapter's
+input gradient (lora_layer.py:67 differentiated), on the same seeded inputs.
+Tolerance rtol = atol = 1e-2 in dY's dtype.  Output rows are independent, so
+the full-size Llama-3-8B cases check a seeded sample of rows."""
+import math
+
+import pytest
+import torch
+
+from oracle import qlora_ref as R
+from rocm_qlora import ops
+from rocm_qlora.quantization import quantize_int4, double_quantize
+
+pytestmark = pytest.mark.gpu
+
+RTOL = ATOL = 1e-2
+
+
+def _inputs(N, K, M, dtype, seed, rank=64):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * 0.02
+    dy = (torch.randn(M, N, generator=g) * 1e-2).to(dtype)
+    a = torch.empty(rank, K)
+    torch.nn.init.kaiming_uniform_(a, a=math.sqrt(5), generator=g)
+    b = torch.randn(N, rank, generator=g) * 0.01
+    return w, dy, a, b
+
+
+def _check(got, ref):
+    got = got.cpu().float()
+    ref = ref.float()
+    assert got.shape == ref.shape
+    err = (got - ref).abs()
+    bad = err > ATOL + RTOL * ref.abs()
+    assert not bad.any(), f"{int(bad.sum())} of {bad.numel()} outside tol; max err {float(err.max()):.4g}"
+
+
+def _sample_rows(M, n, seed):
+    g = torch.Generator().manual_seed(seed)
+    rows = torch.randperm(M, generator=g)[:n]
+    edge = torch.tensor([0, 255, 256, M - 1])
+    return torch.unique(torch.cat([rows, edge[edge < M]]))
+
+
+@pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)])
+def test_dx_llama3_shapes_bf16(dev, K, N):
+    """Config: training backward dX, M=2048 bf16, dY ~ N(0, 1e-2), LoRA r=64 alpha=16."""
+    M, rank = 2048, 64
+    print(f"dx bf16 K={K} N={N} M={M}", flush=True)
+    w, dy, a, b = _inputs(N, K, M, torch.bfloat16, seed=K + 3 * N)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    dx = ops.nf4_linear_dx(dy.to(dev), packed, absmax, K, 64, lora_a=a.to(dev), lora_b=b.to(dev),
+                           scaling=16.0 / rank)
+    rows = _sample_rows(M, 48, K * N + 1)
+    ref = R.nf4_dx(dy[rows], packed.cpu(), absmax.cpu(), N, K, a, b, 16.0 / rank, 64)
+    _check(dx.cpu()[rows], ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", ["plain", "no_lora", "m1", "m5", "m17", "odd_m", "k_tail", "block128",
+                                  "rank16", "rank96", "rank256", "bf16_lora", "strided_dy", "n64"])
+def test_dx_variants(dev, dtype, case):
+    N, K, M = 512, 640, 300
+    M = {"m1": 1, "m5": 5, "m17": 17, "odd_m": 777}.get(case, M)
+    K = {"k_tail": 320}.get(case, K)
+    N = {"n64": 64}.get(case, N)
+    rank = {"rank16": 16, "rank96": 96, "rank256": 256}.get(case, 64)
+    bs = 128 if case == "block128" else 64
+    print(f"dx variant {case} {dtype}", flush=True)
+    w, dy, a, b = _inputs(N, K, M, dtype, seed=13, rank=rank)
+    if case == "bf16_lora":
+        a, b = a.to(dtype), b.to(dtype)
+    packed, absmax = quantize_int4(w.to(dev), bs)
+    dyd = dy.to(dev)
+    if case == "strided_dy":
+        big = torch.zeros(M, N + 64, dtype=dtype, device=dev)
+        big[:, 32:32 + N] = dyd
+        dyd = big[:, 32:32 + N]
+    la, lb = (None, None) if case == "no_lora" else (a.to(dev), b.to(dev))
+    dx = ops.nf4_linear_dx(dyd, packed, absmax, K, bs, lora_a=la, lora_b=lb, scaling=0.5)
+    ref = R.nf4_dx(dy, packed.cpu(), absmax.cpu(), N, K,
+                   None if la is None else a, None if lb is None else b, 0.5, bs)
+    _check(dx, ref)
+
+
+def test_dx_double_quant(dev):
+    N, K, M = 1024, 2048, 512
+    w, dy, a, b = _inputs(N, K, M, torch.bfloat16, seed=29)
+    st = double_quantize(w.to(dev), 64, 256)
+    dx = ops.nf4_linear_dx(dy.to(dev), st.W_quant, None, K, 64, c2=st.c2, c2_scales=st.c2_scales,
+                           lora_a=a.to(dev), lora_b=b.to(dev), scaling=0.25)
+    wf = R.double_dequantize(st.W_quant.cpu(), st.c2.cpu(), st.c2_scales.cpu(), (N, K), 64, 256, True)
+    base = torch.mm(dy, wf.reshape(N, K).to(dy.dtype))
+    g = (dy * 0.25) @ b.to(dy.dtype)
+    ref = base + (g @ a.to(dy.dtype)).to(base.dtype)
+    _check(dx, ref)
+
+
+def test_dx_deterministic(dev):
+    N, K, M = 2048, 2048, 1024
+    w, dy, a, b = _inputs(N, K, M, torch.bfloat16, seed=31)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    args = (dy.to(dev), packed, absmax, K, 64)
+    kw = dict(lora_a=a.to(dev), lora_b=b.to(dev), scaling=0.25)
+    assert torch.equal(ops.nf4_linear_dx(*args, **kw), ops.nf4_linear_dx(*args, **kw))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dq", [False, True])
+def test_dx_weight_operand_bit_exact(dev, dtype, dq):
+    """One-hot dY rows pick single weight rows: dX[m, :] = RND(W[n_m, :]) must
+    equal the reference's dequantized weight cast to dY's dtype bit for bit
+    (quant_ops.py:144-148, double_quant.py:108-118): pins the transposing
+    dequantizer's index mapping."""
+    N, K, M = 256, 640, 300
+    g = torch.Generator().manual_seed(37)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    ns = torch.randint(0, N, (M,), generator=g)
+    ns[:64] = torch.arange(64) + 64
+    dy = torch.zeros(M, N, dtype=dtype)
+    dy[torch.arange(M), ns] = 1.0
+    if dq:
+        st = double_quantize(w.to(dev), 64, 256)
+        dx = ops.nf4_linear_dx(dy.to(dev), st.W_quant, None, K, 64, c2=st.c2, c2_scales=st.c2_scales)
+        wf = R.double_dequantize(st.W_quant.cpu(), st.c2.cpu(), st.c2_scales.cpu(), (N, K), 64, 256, True)
+    else:
+        packed, absmax = quantize_int4(w.to(dev), 64)
+        dx = ops.nf4_linear_dx(dy.to(dev), packed, absmax, K, 64)
+        wf = R.dequantize_int4(packed.cpu(), absmax.cpu(), 64)[:N * K]
+    ref = wf.reshape(N, K).to(dtype)[ns]
+    assert torch.equal(dx.cpu().view(torch.int16), ref.contiguous().view(torch.int16))
