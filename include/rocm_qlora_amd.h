@@ -167,6 +167,49 @@ int rq_nf4_linear_dx(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t
                      int64_t rank, float scaling, void* dx, int64_t lddx,
                      void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * INT8 and FP8 linears
+ * ------------------------------------------------------------------------ */
+
+/* Replaces QuantLinear.forward for bits=8 (quant_linear.py:189-197 with
+ * dequantize_int8, quant_ops.py:55-78) and the reference's native entry point
+ * launch_int8_dequant_matmul (hip_kernels/int4_matmul.hip:440-458):
+ *   y[M, N] = RND(x W^T + RND(bias)),  W = RND(float(q) * scale)
+ *   x: [M, K] bf16/fp16 rows of stride ldx (K % 64 == 0); q: [N, K] int8;
+ *   block_size 0: one scale per output row (scales [N]); otherwise blockwise
+ *   over the flat weight (power of two >= 64 dividing K; scales [N*K/block]);
+ *   scales of scales_dtype; bias [N] or NULL; y: [M, N] stride ldy.
+ * M <= 16 runs a weight-streaming GEMV, larger M the MFMA GEMM. */
+int rq_int8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                   const int8_t* q, int64_t N, int64_t block_size,
+                   const void* scales, int scales_dtype, const void* bias, int bias_dtype,
+                   void* y, int64_t ldy, hipStream_t stream);
+
+/* Bytes of workspace rq_fp8_quantize needs. */
+int rq_fp8_quantize_workspace_size(int64_t* bytes);
+
+/* Replaces the per-tensor FP8 quantization of _FP8LinearFunc.forward
+ * (fp8/fp8_linear.py:33-42): *scale = fp32(double(max|t|) / 240) (device
+ * fp32), codes[r, c] = e4m3fnuz(RND_dtype(float(t[r, c]) / *scale)).
+ * t: [rows, cols] of t_dtype (fp32/bf16/fp16), row stride ld; codes dense. */
+int rq_fp8_quantize(const void* t, int t_dtype, int64_t rows, int64_t cols, int64_t ld,
+                    uint8_t* codes, float* scale, void* workspace, int64_t workspace_bytes,
+                    hipStream_t stream);
+
+/* Bytes of workspace rq_fp8_linear needs for M rows of K activations. */
+int rq_fp8_linear_workspace_size(int64_t M, int64_t K, int64_t* bytes);
+
+/* Replaces _FP8LinearFunc.forward (fp8/fp8_linear.py:27-60) for a weight
+ * already quantized by rq_fp8_quantize: x is quantized per tensor the same
+ * way, then y = RND(RND(sum_k x8 w8 * x_scale * w_scale) + bias) with the
+ * e4m3fnuz products summed exactly in fp32.
+ *   x: [M, K] bf16/fp16 stride ldx (K % 64 == 0); w_codes: [N, K] e4m3fnuz;
+ *   w_scale: device fp32; bias [N] or NULL; y: [M, N] stride ldy. */
+int rq_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                  const uint8_t* w_codes, int64_t N, const float* w_scale,
+                  const void* bias, int bias_dtype, void* y, int64_t ldy,
+                  void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

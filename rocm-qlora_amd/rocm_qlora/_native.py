@@ -46,6 +46,15 @@ SIGNATURES = {
                          _P, _I32, _I64,                     # c2, c2 format, block2
                          _P, _P, _I64, _I32, _I64, _F32,     # A, B, ldB, dtype, rank, scaling
                          _P, _I64, _P, _I64, _P],            # dx, lddx, workspace, bytes, stream
+    "rq_int8_linear": [_P, _I32, _I64, _I64, _I64,           # x, dtype, M, K, ldx
+                       _P, _I64, _I64, _P, _I32,             # q, N, block, scales, dtype
+                       _P, _I32, _P, _I64, _P],              # bias, dtype, y, ldy, stream
+    "rq_fp8_quantize_workspace_size": [_P],
+    "rq_fp8_quantize": [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _I64, _P],
+    "rq_fp8_linear_workspace_size": [_I64, _I64, _P],
+    "rq_fp8_linear": [_P, _I32, _I64, _I64, _I64,            # x, dtype, M, K, ldx
+                      _P, _I64, _P, _P, _I32,                # codes, N, w scale, bias, dtype
+                      _P, _I64, _P, _I64, _P],               # y, ldy, workspace, bytes, stream
 }
 _RESTYPE = {"rq_status_string": ctypes.c_char_p, "rq_build_arch": ctypes.c_char_p}
 

@@ -189,3 +189,103 @@ def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: O
                  dx.data_ptr(), K, nat.ptr(ws), ws.numel() if ws is not None else 0,
                  nat.stream_handle(dev))
     return dx.reshape(*lead, K)
+
+
+def _aligned_rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
+    """2-D [rows, K] view with a 16-byte aligned base and a row stride that
+    keeps every row 16-byte aligned (the MFMA kernels load 16 bytes at a time)."""
+    t2, ld = _rows(t, K)
+    if t2.data_ptr() % 16 or ld % 8:
+        t2 = t2.contiguous().clone()
+        ld = K
+    return t2, ld
+
+
+def int8_linear(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, out_features: int,
+                block_size: int = 0, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y = x . (q * scale)^T + bias for int8 weights (quant_ops.py:55-78 then
+    quant_linear.py:193-197).  q: [N, K] (or flat N*K) int8; block_size 0 ->
+    one scale per output row ([N] scales, the row-absmax recipe), otherwise
+    blockwise over the flat weight (QuantLinear bits=8 uses 64).
+    x: [..., K] bf16/fp16 on the GPU; output has x's dtype."""
+    K = x.shape[-1]
+    N = int(out_features)
+    if x.dtype == torch.float32:
+        from rocm_qlora.quantization.quant_ops import dequantize_int8
+        w = dequantize_int8(q.reshape(N, K) if block_size == 0 else q.reshape(-1), scales,
+                            block_size if block_size else 64)
+        return F.linear(x, w.reshape(-1)[:N * K].reshape(N, K), bias)
+    dev = nat.require_gpu(x, q, scales, bias)
+    if q.dtype != torch.int8:
+        raise TypeError(f"int8 weights expected, got {q.dtype}")
+    qf = q.reshape(-1).contiguous()
+    if qf.numel() < N * K:
+        raise RuntimeError(f"q holds {qf.numel()} values, need {N}x{K}")
+    sc = scales.reshape(-1).contiguous()
+    need = N if block_size == 0 else N * K // block_size
+    if sc.numel() < need:
+        raise RuntimeError(f"scales hold {sc.numel()} values, need {need}")
+    lead = x.shape[:-1]
+    with on(dev):
+        x2, ldx = _aligned_rows(x, K)
+        M = x2.shape[0]
+        y = torch.empty((M, N), dtype=x.dtype, device=dev)
+        if M == 0:
+            return y.reshape(*lead, N)
+        b = bias.contiguous() if bias is not None else None
+        nat.call("rq_int8_linear", x2.data_ptr(), nat.dtype_code(x.dtype), M, K, ldx,
+                 qf.data_ptr(), N, block_size, sc.data_ptr(), nat.dtype_code(sc.dtype),
+                 nat.ptr(b), nat.dtype_code(b.dtype) if b is not None else 0,
+                 y.data_ptr(), N, nat.stream_handle(dev))
+    return y.reshape(*lead, N)
+
+
+def fp8_quantize(t: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-tensor e4m3fnuz quantization of fp8_linear.py:33-42 on the GPU:
+    returns (codes as torch.float8_e4m3fnuz [rows, cols], fp32 0-dim scale),
+    scale = fp32(double(max|t|) / 240), codes = fnuz(RND(t / scale))."""
+    dev = nat.require_gpu(t)
+    t2 = t.reshape(-1, t.shape[-1]) if t.dim() != 2 else t
+    rows, cols = t2.shape
+    with on(dev):
+        src, ld = _rows(t2, cols)
+        codes = torch.empty((rows, cols), dtype=torch.uint8, device=dev)
+        scale = torch.empty((), dtype=torch.float32, device=dev)
+        import ctypes
+        nb = ctypes.c_int64(0)
+        nat.call("rq_fp8_quantize_workspace_size", ctypes.byref(nb))
+        ws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
+        nat.call("rq_fp8_quantize", src.data_ptr(), nat.dtype_code(t.dtype), rows, cols, ld,
+                 codes.data_ptr(), scale.data_ptr(), ws.data_ptr(), ws.numel(), nat.stream_handle(dev))
+    return codes.view(torch.float8_e4m3fnuz), scale
+
+
+def fp8_linear(x: torch.Tensor, w_codes: torch.Tensor, w_scale: torch.Tensor,
+               bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """_FP8LinearFunc.forward (fp8_linear.py:27-60) for a weight quantized by
+    fp8_quantize: x is quantized per tensor, the e4m3fnuz products are summed
+    exactly in fp32, scaled by x_scale * w_scale, rounded to x's dtype, and
+    the bias is added.  x: [..., K] bf16/fp16 on the GPU."""
+    K = x.shape[-1]
+    wc = w_codes.reshape(-1, K)
+    N = wc.shape[0]
+    dev = nat.require_gpu(x, w_codes, w_scale, bias)
+    wc = wc.view(torch.uint8).contiguous()
+    ws_scale = w_scale.reshape(()).to(torch.float32).contiguous()
+    lead = x.shape[:-1]
+    with on(dev):
+        x2, ldx = _aligned_rows(x, K)
+        M = x2.shape[0]
+        y = torch.empty((M, N), dtype=x.dtype, device=dev)
+        if M == 0:
+            return y.reshape(*lead, N)
+        import ctypes
+        nb = ctypes.c_int64(0)
+        nat.call("rq_fp8_linear_workspace_size", M, K, ctypes.byref(nb))
+        ws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
+        b = bias.to(x.dtype).contiguous() if bias is not None else None
+        nat.call("rq_fp8_linear", x2.data_ptr(), nat.dtype_code(x.dtype), M, K, ldx,
+                 wc.data_ptr(), N, ws_scale.data_ptr(), nat.ptr(b),
+                 nat.dtype_code(b.dtype) if b is not None else 0,
+                 y.data_ptr(), N, ws.data_ptr(), ws.numel(), nat.stream_handle(dev))
+    return y.reshape(*lead, N)

@@ -1,0 +1,151 @@
+"""GPU parity of the INT8 and FP8 linears (HIP kernels through the C ABI) vs
+the oracle's restatements: row-absmax / blockwise INT8 dequantize-then-
+F.linear (quant_ops.py:17-78, quant_linear.py:193-197) and the FP8
+_FP8LinearFunc recipe (fp8_linear.py:27-60).  Tolerance rtol = atol = 1e-2
+in the activation dtype for outputs; the FP8 quantization (codes and scale)
+and the INT8 weight operand are bit-exact.  Full Llama-3-70B MLP shapes
+(K=8192, N=28672) are checked on a seeded sample of output rows and
+columns, which the oracle computes from the selected weight rows only."""
+import pytest
+import torch
+
+from oracle import qlora_ref as R
+from rocm_qlora import ops
+from rocm_qlora.quantization import quantize_int8
+
+pytestmark = pytest.mark.gpu
+
+RTOL = ATOL = 1e-2
+
+
+def _check(got, ref):
+    got = got.cpu().float()
+    ref = ref.float()
+    assert got.shape == ref.shape
+    err = (got - ref).abs()
+    bad = err > ATOL + RTOL * ref.abs()
+    assert not bad.any(), f"{int(bad.sum())} of {bad.numel()} outside tol; max err {float(err.max()):.4g}"
+
+
+def _weights(N, K, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(N, K, generator=g) * 0.02).to(dtype)
+
+
+def _x(M, K, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(M, K, generator=g).to(dtype)
+
+
+@pytest.mark.parametrize("M", [1, 512, 4096])
+def test_int8_row_absmax_llama70b_mlp(dev, M):
+    """Config: INT8 per-output-row absmax weights (N(0,0.02)), bf16 x, K=8192, N=28672."""
+    K, N = 8192, 28672
+    print(f"int8 row-absmax M={M}", flush=True)
+    w = _weights(N, K, seed=5).to(dev)
+    q, s = quantize_int8(w, per_channel=True)
+    x = _x(M, K, torch.bfloat16, seed=M)
+    y = ops.int8_linear(x.to(dev), q, s, N, block_size=0)
+    g = torch.Generator().manual_seed(M + 1)
+    rows = torch.randperm(M, generator=g)[:16]
+    cols = torch.cat([torch.randperm(N, generator=g)[:256], torch.tensor([0, N - 1])])
+    ref = R.int8_linear(x[rows], q[cols].cpu(), s[cols].cpu())
+    _check(y.cpu()[rows][:, cols], ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", ["m1", "m5", "m16", "m17", "m300", "blockwise", "bias", "odd_n", "k64",
+                                  "bf16_scales"])
+def test_int8_variants(dev, dtype, case):
+    N, K = 704, 512
+    M = {"m1": 1, "m5": 5, "m16": 16, "m17": 17}.get(case, 300)
+    N = 1000 if case == "odd_n" else N
+    K = 64 if case == "k64" else K
+    print(f"int8 variant {case} {dtype}", flush=True)
+    w = _weights(N, K, seed=7).to(dev)
+    if case == "bf16_scales":
+        w = w.to(torch.bfloat16)
+    block = 64 if case == "blockwise" else 0
+    if block:
+        q, s = quantize_int8(w, block_size=64)
+    else:
+        q, s = quantize_int8(w, per_channel=True)
+    g = torch.Generator().manual_seed(3)
+    bias = (torch.randn(N, generator=g) * 0.1) if case == "bias" else None
+    x = _x(M, K, dtype, seed=11)
+    y = ops.int8_linear(x.to(dev), q, s, N, block_size=block, bias=None if bias is None else bias.to(dev))
+    if block:
+        wf = R.dequantize_int8(q.cpu(), s.cpu(), 64)[:N * K].reshape(N, K)
+    else:
+        wf = R.dequantize_int8(q.cpu().reshape(N, K), s.cpu())
+    ref = torch.nn.functional.linear(x, wf.to(dtype), None if bias is None else bias.to(dtype))
+    _check(y, ref)
+
+
+@pytest.mark.parametrize("M", [7, 300])
+@pytest.mark.parametrize("block", [0, 64])
+def test_int8_weight_operand_bit_exact(dev, M, block):
+    """One-hot activation rows pick single weights: y[m, n] = RND(q * s) bit
+    for bit (GEMV path for M <= 16, MFMA GEMM otherwise)."""
+    N, K = 384, 1024
+    w = _weights(N, K, seed=17).to(dev)
+    q, s = quantize_int8(w, block_size=64) if block else quantize_int8(w, per_channel=True)
+    g = torch.Generator().manual_seed(19)
+    ks = torch.randint(0, K, (M,), generator=g)
+    x = torch.zeros(M, K, dtype=torch.bfloat16)
+    x[torch.arange(M), ks] = 1.0
+    y = ops.int8_linear(x.to(dev), q, s, N, block_size=block)
+    if block:
+        wf = R.dequantize_int8(q.cpu(), s.cpu(), 64)[:N * K].reshape(N, K)
+    else:
+        wf = R.dequantize_int8(q.cpu().reshape(N, K), s.cpu())
+    ref = wf.to(torch.bfloat16)[:, ks].T
+    assert torch.equal(y.cpu().view(torch.int16), ref.contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_fp8_quantize_bit_exact(dev, dtype):
+    """Codes and scale of the per-tensor e4m3fnuz recipe (fp8_linear.py:33-42)
+    equal the oracle's bit for bit; the absmax element encodes to 0x7F."""
+    t = (torch.randn(257, 1000, generator=torch.Generator().manual_seed(23)) * 0.05).to(dtype)
+    t[3, 7] = 0.9
+    codes, scale = ops.fp8_quantize(t.to(dev))
+    rc, rs = R.fp8_quantize_tensor(t)
+    assert float(scale) == float(rs)
+    assert torch.equal(codes.view(torch.uint8).cpu(), rc.view(torch.uint8))
+    assert int(codes.view(torch.uint8)[3, 7]) == 0x7F
+
+
+@pytest.mark.parametrize("M", [1, 512, 4096])
+def test_fp8_llama70b_mlp(dev, M):
+    """Config: FP8 e4m3 weights and activations with per-tensor fp32 scales,
+    K=8192, N=28672, bf16 output vs dequantize-then-matmul."""
+    K, N = 8192, 28672
+    print(f"fp8 M={M}", flush=True)
+    w = _weights(N, K, seed=29, dtype=torch.bfloat16)
+    wc, ws = ops.fp8_quantize(w.to(dev))
+    x = _x(M, K, torch.bfloat16, seed=31 + M)
+    y = ops.fp8_linear(x.to(dev), wc, ws)
+    # the oracle's recipe on the sampled output block
+    x8, xs = R.fp8_quantize_tensor(x)
+    w8, wsr = R.fp8_quantize_tensor(w)
+    assert float(ws) == float(wsr)
+    g = torch.Generator().manual_seed(M + 2)
+    rows = torch.randperm(M, generator=g)[:16]
+    cols = torch.cat([torch.randperm(N, generator=g)[:256], torch.tensor([0, N - 1])])
+    ref = ((x8[rows].to(torch.float32) * xs) @ (w8[cols].to(torch.float32) * wsr).T).to(torch.bfloat16)
+    _check(y.cpu()[rows][:, cols], ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [1, 16, 17, 333])
+def test_fp8_variants(dev, dtype, M):
+    N, K = 640, 768
+    w = _weights(N, K, seed=37, dtype=dtype)
+    x = _x(M, K, dtype, seed=41)
+    g = torch.Generator().manual_seed(43)
+    bias = (torch.randn(N, generator=g) * 0.1).to(dtype)
+    wc, ws = ops.fp8_quantize(w.to(dev))
+    y = ops.fp8_linear(x.to(dev), wc, ws, bias.to(dev))
+    ref = R.fp8_linear(x, w, bias)
+    _check(y, ref)
