@@ -210,3 +210,19 @@ def fp8_linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = 
     if bias is not None:
         y = y + bias
     return y
+
+
+def lora_linear_grads(x: torch.Tensor, weight_fp: torch.Tensor, bias: Optional[torch.Tensor],
+                      lora_a: torch.Tensor, lora_b: torch.Tensor, scaling: float, dy: torch.Tensor):
+    """Gradients of LoRALinear(QuantLinear).forward on the CPU path
+    (quant_linear.py:189-197 then lora_layer.py:67-70), by torch autograd on
+    the same expression: returns (y, dX, dA, dB) with dA / dB in the
+    parameters' dtype."""
+    N, K = lora_b.shape[0], x.shape[-1]
+    x = x.detach().clone().requires_grad_(True)
+    a = lora_a.detach().clone().requires_grad_(True)
+    b = lora_b.detach().clone().requires_grad_(True)
+    base = quant_linear_forward(x, weight_fp, bias, N, K)
+    y = lora_forward(x, base, a, b, scaling)
+    y.backward(dy)
+    return y.detach(), x.grad, a.grad, b.grad

@@ -1,6 +1,7 @@
 """rocm_qlora (MI355X build): the quantized-linear path of rocm-qlora --
 NF4 / double-quant / INT8 / FP8 codecs and linears, with the LoRA term fused
--- as hand-written HIP kernels for gfx950 behind the reference's Python API.
+-- as hand-written HIP kernels for gfx950 behind the reference's Python API
+(rocm_qlora/__init__.py:16-104 of the reference, the quantized-linear names).
 
 Importing this package has no side effects: the kernels are compiled ahead of
 time (rocm-qlora_amd/build.py) and loaded on first use.
@@ -12,3 +13,29 @@ from rocm_qlora.quantization import (  # noqa: E402
     double_quantize, double_dequantize, DoubleQuantState,
     estimate_double_quant_savings, patch_quant_linear_for_double_quant,
 )
+from rocm_qlora.quantization.quant_linear import QuantLinear  # noqa: E402
+from rocm_qlora.lora.lora_layer import LoRALinear  # noqa: E402
+from rocm_qlora.model.quantize_model import quantize_model, enable_all_kernels  # noqa: E402
+from rocm_qlora.kernels import (  # noqa: E402
+    fused_dequant_int8_matmul, fused_dequant_nf4_matmul, get_device_info, is_triton_available,
+)
+from rocm_qlora.hip_kernels import (  # noqa: E402
+    is_hip_kernel_available, enable_hip_kernels, hip_dequant_int4_matmul, hip_dequant_int8_matmul,
+    benchmark_hip_vs_triton,
+)
+from rocm_qlora.hip_kernels.build_utils import (  # noqa: E402
+    find_hipcc, is_hipcc_available, compile_hip_kernel, get_or_compile_int4_kernel,
+)
+
+__all__ = [
+    "quantize_model", "QuantLinear", "LoRALinear",
+    "fused_dequant_int8_matmul", "fused_dequant_nf4_matmul",
+    "get_device_info", "is_triton_available", "enable_all_kernels",
+    "is_hip_kernel_available", "enable_hip_kernels", "hip_dequant_int4_matmul", "hip_dequant_int8_matmul",
+    "benchmark_hip_vs_triton", "find_hipcc", "is_hipcc_available", "compile_hip_kernel",
+    "get_or_compile_int4_kernel",
+    "quantize_int8", "dequantize_int8", "quantize_int4", "dequantize_int4",
+    "double_quantize", "double_dequantize", "DoubleQuantState",
+    "estimate_double_quant_savings", "patch_quant_linear_for_double_quant",
+    "__version__",
+]

@@ -1,0 +1,141 @@
+"""FP8 compute for LoRA layers (fp8/fp8_linear.py of the reference).
+
+Storage stays QuantLinear (NF4 / INT8); the base matmul runs in e4m3fnuz
+with per-tensor scales on the gfx950 FP8 kernels: x and W are quantized
+with scale = fp32(max|t| / 240) and codes = fnuz(RND(t / scale)), their
+products are summed in fp32, scaled by x_scale * w_scale and rounded to x's
+dtype, then the bias is added (fp8_linear.py:27-60).  Backward gives dX =
+dY . W (the base weight is frozen).  The LoRA term stays in x's dtype.
+"""
+from __future__ import annotations
+
+import contextlib
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from rocm_qlora import ops
+from rocm_qlora.fp8.fp8_config import detect_fp8_support, FP8Config, get_fp8_recipe
+from rocm_qlora.lora.lora_layer import LoRALinear
+
+_FNUZ_MAX = 240.0
+
+
+def _fp8_forward(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor],
+                 w_q: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
+    if x.dtype in (torch.bfloat16, torch.float16):
+        wc, ws = w_q if w_q is not None else ops.fp8_quantize(w)
+        return ops.fp8_linear(x, wc, ws, bias)
+    # fp32 activations: the same codes and scales from the HIP quantizer,
+    # decoded and multiplied by the library GEMM in fp32
+    x2 = x.reshape(-1, x.shape[-1])
+    xc, xs = ops.fp8_quantize(x2)
+    wc, ws = w_q if w_q is not None else ops.fp8_quantize(w)
+    out = (xc.to(torch.float32) * xs) @ (wc.to(torch.float32) * ws).T
+    out = out.to(x.dtype).reshape(*x.shape[:-1], -1)
+    return out + bias if bias is not None else out
+
+
+class _FP8LinearFunc(torch.autograd.Function):
+    """FP8 forward, dX = dY . W backward (fp8_linear.py:19-67)."""
+
+    @staticmethod
+    def forward(ctx, x, w_fp16, bias, w_q=None):
+        ctx.save_for_backward(w_fp16)
+        ctx.has_bias = bias is not None
+        ctx.fp8_used = True
+        return _fp8_forward(x, w_fp16, bias, w_q)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (w,) = ctx.saved_tensors
+        return grad_output @ w.to(grad_output.dtype), None, None, None
+
+
+class FP8LinearWrapper(nn.Module):
+    """Runs a LoRALinear's base matmul in FP8 (fp8_linear.py:69-118).  Backend
+    'native' (this package's FP8 kernels) when FP8 is supported and enabled,
+    'transformer_engine' when TE is importable and preferred, else 'bf16'
+    (the wrapped layer unchanged).  The FP8 weight codes are cached until the
+    stored weight changes."""
+
+    def __init__(self, base_lora_linear: nn.Module, config: Optional[FP8Config] = None):
+        super().__init__()
+        self.config = config if config is not None else FP8Config()
+        self.base = base_lora_linear
+        self.fp8_info = detect_fp8_support()
+        if not self.config.enabled or not self.fp8_info["fp8_supported"]:
+            self.backend = "bf16"
+        elif self.fp8_info["transformer_engine_available"] and self.config.use_transformer_engine:
+            self.backend = "transformer_engine"
+            self.te_recipe = get_fp8_recipe(self.config)
+        elif self.fp8_info["fp8_dtypes_available"]:
+            self.backend = "native"
+        else:
+            self.backend = "bf16"
+        self._cache_key = None
+        self._cache = None
+
+    def _weight(self, dtype: torch.dtype):
+        ql = self.base.base_layer
+        key = (ql.weight_quant.data_ptr(), ql.weight_quant._version, dtype,
+               getattr(ql, "c2", ql.weight_scales).data_ptr())
+        if self._cache_key != key:
+            w = ql.dequantized_weight(dtype)
+            self._cache = (w, ops.fp8_quantize(w) if dtype != torch.float32 else None)
+            self._cache_key = key
+        return self._cache
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.backend == "transformer_engine":
+            import transformer_engine.pytorch as te
+            with te.fp8_autocast(enabled=True, fp8_recipe=self.te_recipe):
+                return self.base(x)
+        if self.backend == "native":
+            ql = self.base.base_layer
+            w, w_q = self._weight(x.dtype)
+            bias = ql.bias.to(x.dtype) if ql.bias is not None else None
+            base_out = _FP8LinearFunc.apply(x, w, bias, w_q)
+            lora_out = (self.base.lora_dropout(x) @ self.base.lora_A.t().to(x.dtype)
+                        @ self.base.lora_B.t().to(x.dtype) * self.base.scaling)
+            return base_out + lora_out.to(base_out.dtype)
+        return self.base(x)
+
+    def extra_repr(self) -> str:
+        return f"backend={self.backend}, fp8_supported={self.fp8_info['fp8_supported']}"
+
+
+def wrap_model_for_fp8(model: nn.Module, config: Optional[FP8Config] = None) -> Tuple[nn.Module, Dict[str, Any]]:
+    """Wrap every LoRALinear in an FP8LinearWrapper (fp8_linear.py:120-160).
+    Unlike the reference, no environment variables are set: the FP8 kernels
+    need no NCCL stream priority or hardware-queue settings."""
+    config = config if config is not None else FP8Config()
+    info = detect_fp8_support()
+    status = {"enabled": False, "backend": "bf16", "layers_wrapped": 0, "reason": info["reason"]}
+    if not info["fp8_supported"] and config.enabled:
+        return model, status
+    targets = [(n, m) for n, m in model.named_modules() if isinstance(m, LoRALinear)]
+    for name, module in targets:
+        parent_name, _, child = name.rpartition(".")
+        parent = model.get_submodule(parent_name) if parent_name else model
+        wrapped = FP8LinearWrapper(module, config)
+        setattr(parent, child, wrapped)
+        status["layers_wrapped"] += 1
+        status["backend"] = wrapped.backend
+        status["enabled"] = wrapped.backend != "bf16"
+    return model, status
+
+
+def enable_fp8_autocast(model: nn.Module, config: Optional[FP8Config] = None):
+    """TransformerEngine fp8_autocast when TE is importable and preferred,
+    else a null context (fp8_linear.py:162-174)."""
+    config = config if config is not None else FP8Config()
+    try:
+        import transformer_engine.pytorch as te
+        if config.use_transformer_engine:
+            return te.fp8_autocast(enabled=True, fp8_recipe=get_fp8_recipe(config))
+    except ImportError:
+        pass
+    return contextlib.nullcontext()

@@ -15,6 +15,10 @@ import torch.nn.functional as F
 from rocm_qlora import _native as nat
 from rocm_qlora._device import on
 
+# activation rows up to which the NF4 linear runs as a weight-streaming GEMV
+# (kGemvMaxM in csrc/rq_linear.h); above it, the MFMA GEMM
+GEMV_MAX_M = 16
+
 
 def _rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
     """[..., K] -> 2-D [rows, K] view with unit inner stride, and its row stride."""
@@ -71,6 +75,8 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
     with on(dev):
         x2, ldx = _rows(x, K)
         M = x2.shape[0]
+        if M > GEMV_MAX_M:  # the MFMA GEMM streams x in 16-byte pieces
+            x2, ldx = _aligned_rows(x2, K)
         y = torch.empty((M, N), dtype=x.dtype, device=dev)
         if M == 0:
             return y.reshape(*lead, N)

@@ -9,16 +9,11 @@ from rocm_qlora.quantization.double_quant import (
 
 __all__ = [
     "quantize_int8", "dequantize_int8",
-    "quantize_int4", "dequantize_int4",
+    "NF4_VALUES", "quantize_int4", "dequantize_int4",
     "QuantLinear",
     "double_quantize", "double_dequantize",
     "DoubleQuantState", "estimate_double_quant_savings",
     "patch_quant_linear_for_double_quant",
 ]
 
-
-def __getattr__(name):
-    if name == "QuantLinear":
-        from rocm_qlora.quantization.quant_linear import QuantLinear
-        return QuantLinear
-    raise AttributeError(name)
+from rocm_qlora.quantization.quant_linear import QuantLinear  # noqa: E402
