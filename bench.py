@@ -1,24 +1,33 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X NF4 quantized-linear path at Llama-3-8B projection shapes.
 
-One step is one Llama-3-8B decoder layer's seven NF4 projections (q, k, v,
-o, gate, up, down; in x out = 4096x4096, 4096x1024 twice, 4096x4096,
-4096x14336 twice, 14336x4096) run as decode dequant-GEMVs with the LoRA term
-fused (M = 1 token, bf16 activations, NF4 block 64 with fp32 absmax, LoRA
-r = 16, alpha = 32).  `value` is the whole step's algorithmic HBM bytes
-divided by its time, with every input resident in HBM.  Weights rotate over
-enough layer copies (> 512 MB) that the 256 MB MALL cannot serve them.  The
-step is captured once per layer copy as a HIP graph and replayed.
+Headline (`value`, GB/s): one step is one Llama-3-8B decoder layer's seven
+NF4 projections (q, k, v, o, gate, up, down; in x out = 4096x4096,
+4096x1024 twice, 4096x4096, 4096x14336 twice, 14336x4096) run as decode
+dequant-GEMVs with the LoRA term fused (M = 1 token by default, bf16
+activations N(0,1), weights N(0,0.02) quantized to NF4 block 64 with fp32
+absmax, LoRA r = 16, alpha = 32).  `value` is the step's algorithmic HBM
+bytes divided by its time, with every input resident in HBM.  Weights rotate
+over enough layer copies (> 512 MB) that the 256 MB MALL cannot serve them.
+The step is captured once per layer copy as a HIP graph and replayed.
 
-Alongside: the roofline of the dominant kernel (the GEMV at the gate/up
-shape, timed with HIP events over back-to-back launches on the stream it
-runs on), and the CPU baseline: the oracle's restatement of the reference's
-CPU path (dequantize_int4 -> .to(bf16) -> F.linear + LoRA) over a bounded
-sample of the same step on the host cores.
+Also reported:
+  roofline      the dominant kernel (the GEMV at the gate/up shape, no LoRA),
+                timed with HIP events over back-to-back launches on the stream
+                they run on; algorithmic bytes / average launch time vs 8 TB/s.
+  gemm          the prefill/training shapes: the same seven projections at
+                M = 2048 tokens with LoRA r = 64, alpha = 16, forward and dX
+                backward, TFLOP/s and fraction of the 2.5 PFLOP/s bf16 MFMA peak.
+  cpu_baseline  the oracle's restatement of the reference's CPU path
+                (dequantize_int4 -> .to(bf16) -> F.linear + LoRA) over a bounded
+                sample of the same decode step on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m M] [--no-gemm] [--no-cpu]
+    python bench.py --summarize-profile DIR   # per-kernel, per-grid rocprofv3 kernel-trace table
 """
 import argparse
+import csv
+import glob
 import json
 import math
 import os
@@ -30,6 +39,7 @@ for _p in (ROOT, os.path.join(ROOT, "rocm-qlora_amd")):
     if _p not in sys.path:
         sys.path.insert(0, _p)
 
+METRIC = "NF4 dequant-GEMV GB/s + GEMM TFLOP/s (% roofline), Llama-3-8B proj shapes"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 
@@ -38,11 +48,17 @@ LLAMA3_8B_PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o",
                   ("gate", 4096, 14336), ("up", 4096, 14336), ("down", 14336, 4096)]
 RANK, ALPHA, BLOCK = 16, 32, 64
 SCALING = ALPHA / RANK
+GEMM_M, GEMM_RANK, GEMM_ALPHA = 2048, 64, 16
+
+# HBM traffic of the roofline kernel per launch, measured with rocprofv3 --pmc
+# FETCH_SIZE / WRITE_SIZE and scaled by the same counters' reading for a copy
+# kernel of known size; keyed by (kernel, M, K, N).  None where not measured.
+MEASURED_TRAFFIC = {}
 
 
 def gemv_bytes(M, N, K, rank=RANK, scale_bytes=4):
-    """Algorithmic HBM bytes of one fused NF4 LoRA linear: packed codes, absmax,
-    activations in and out, LoRA A and B (bf16 accounting)."""
+    """Algorithmic HBM bytes of one fused NF4 LoRA linear: packed codes,
+    absmax, activations in and out, LoRA A and B (bf16 accounting)."""
     return N * K // 2 + (N * K // BLOCK) * scale_bytes + M * K * 2 + M * N * 2 + (rank * K + N * rank) * 2
 
 
@@ -51,7 +67,12 @@ def kernel_bytes(M, N, K, scale_bytes=4):
     return N * K // 2 + (N * K // BLOCK) * scale_bytes + M * K * 2 + M * N * 2
 
 
-def make_layer(dev, seed):
+def gemm_flops(M, N, K, rank):
+    """2MNK + 2Mr(K + N): base product plus the two LoRA products."""
+    return 2 * M * N * K + 2 * M * rank * (K + N)
+
+
+def make_layer(dev, seed, rank=RANK):
     import torch
     from rocm_qlora.quantization import quantize_int4
     g = torch.Generator(device=dev).manual_seed(seed)
@@ -60,18 +81,68 @@ def make_layer(dev, seed):
         w = torch.randn(N, K, generator=g, device=dev) * 0.02
         packed, absmax = quantize_int4(w, BLOCK)
         del w
-        a = (torch.rand(RANK, K, generator=g, device=dev) * 2 - 1) / math.sqrt(K)  # kaiming_uniform(a=sqrt 5)
-        b = torch.randn(N, RANK, generator=g, device=dev) * 0.01
+        a = (torch.rand(rank, K, generator=g, device=dev) * 2 - 1) / math.sqrt(K)  # kaiming_uniform(a=sqrt 5)
+        b = torch.randn(N, rank, generator=g, device=dev) * 0.01
         layer[name] = (packed, absmax, a, b, N, K)
     return layer
 
 
+class _Range:
+    """A roctx range (rocprofv3 --marker-trace) naming a timed region, so a
+    profile can attribute kernel launches to it; a no-op where torch has no
+    range support."""
+
+    def __init__(self, name):
+        self.name = name
+
+    def __enter__(self):
+        import torch
+        try:
+            torch.cuda.nvtx.range_push(self.name)
+            self.ok = True
+        except Exception:
+            self.ok = False
+        return self
+
+    def __exit__(self, *exc):
+        import torch
+        if self.ok:
+            torch.cuda.nvtx.range_pop()
+
+
+def _time_graph(graph, reps):
+    """ms per replay, HIP events on the stream the replays run on."""
+    import torch
+    cur = torch.cuda.current_stream()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    graph.replay()
+    torch.cuda.synchronize()
+    t0.record(cur)
+    for _ in range(reps):
+        graph.replay()
+    t1.record(cur)
+    torch.cuda.synchronize()
+    return t0.elapsed_time(t1) / reps
+
+
+def _capture(fn, stream):
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(g, stream=stream):
+            fn()
+    torch.cuda.synchronize()
+    return g
+
+
 def cpu_baseline(layer_cpu, xs_cpu, budget_s=20.0):
     """The oracle's CPU restatement of the reference path over whole decode
-    steps, as many as fit in about budget_s (at least one)."""
-    import torch
+    steps, as many as fit in about budget_s (at least one), on torch's
+    default intra-op thread count."""
     from oracle import qlora_ref as R
-    torch.set_num_threads(os.cpu_count() or 1)
 
     def step():
         for name, K, N in LLAMA3_8B_PROJ:
@@ -85,8 +156,94 @@ def cpu_baseline(layer_cpu, xs_cpu, budget_s=20.0):
     t0 = time.perf_counter()
     for _ in range(n):
         step()
-    dt = (time.perf_counter() - t0) / n
-    return dt, n
+    return (time.perf_counter() - t0) / n, n
+
+
+def bench_gemm(dev, stream):
+    """Config: M = 2048 bf16 tokens N(0,1), LoRA r = 64, alpha = 16, dY
+    N(0,1e-2); per-shape forward and dX graphs, 20 replays each."""
+    import torch
+    from rocm_qlora import ops
+    layer = make_layer(dev, 4242, rank=GEMM_RANK)
+    s = GEMM_ALPHA / GEMM_RANK
+    g = torch.Generator(device=dev).manual_seed(11)
+    xs = {K: torch.randn(GEMM_M, K, generator=g, device=dev).to(torch.bfloat16) for K in (4096, 14336)}
+    per = {}
+    tot = {"fwd": [0.0, 0.0], "dx": [0.0, 0.0]}
+    for name, K, N in LLAMA3_8B_PROJ:
+        packed, absmax, a, b, _, _ = layer[name]
+        dy = (torch.randn(GEMM_M, N, generator=g, device=dev) * 1e-2).to(torch.bfloat16)
+        x = xs[K]
+        gf = _capture(lambda: ops.nf4_linear(x, packed, absmax, N, BLOCK, lora_a=a, lora_b=b, scaling=s),
+                      stream)
+        gd = _capture(lambda: ops.nf4_linear_dx(dy, packed, absmax, K, BLOCK, lora_a=a, lora_b=b, scaling=s),
+                      stream)
+        fl = gemm_flops(GEMM_M, N, K, GEMM_RANK)
+        with _Range(f"rq-gemm-fwd {name} M={GEMM_M} K={K} N={N}"):
+            ms_f = _time_graph(gf, 20)
+        with _Range(f"rq-gemm-dx {name} M={GEMM_M} K={K} N={N}"):
+            ms_d = _time_graph(gd, 20)
+        per[name] = {"fwd_us": round(ms_f * 1e3, 2), "fwd_tflops": round(fl / ms_f / 1e9, 1),
+                     "dx_us": round(ms_d * 1e3, 2), "dx_tflops": round(fl / ms_d / 1e9, 1)}
+        tot["fwd"][0] += fl
+        tot["fwd"][1] += ms_f
+        tot["dx"][0] += fl
+        tot["dx"][1] += ms_d
+        del gf, gd, dy
+    fwd = tot["fwd"][0] / tot["fwd"][1] / 1e9
+    dx = tot["dx"][0] / tot["dx"][1] / 1e9
+    return {"workload": f"Llama-3-8B 7 NF4 projections, M={GEMM_M} bf16, LoRA r={GEMM_RANK} alpha={GEMM_ALPHA} "
+                        f"fused, forward Y and backward dX",
+            "fwd_tflops": round(fwd, 1), "fwd_frac": round(fwd / BF16_PEAK_TFLOPS, 4),
+            "dx_tflops": round(dx, 1), "dx_frac": round(dx / BF16_PEAK_TFLOPS, 4),
+            "peak_tflops": BF16_PEAK_TFLOPS, "per_shape": per}
+
+
+def _short(name, n=70):
+    return name if len(name) <= n else name[:n - 3] + "..."
+
+
+def summarize_profile(path):
+    """From a rocprofv3 CSV trace (`-f csv`): count / average / min kernel
+    duration per (kernel, grid), and, when a marker trace is present, per
+    kernel inside each of bench.py's named ranges (rq-...), which is how the
+    roofline launches are told apart from the other launches of the same
+    kernel."""
+    files = glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        sys.exit(f"no *kernel_trace.csv under {path}")
+    launches = []
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                launches.append((row["Kernel_Name"], int(row.get("Grid_Size_X", row.get("Grid_Size", 0)) or 0),
+                                 int(row.get("Workgroup_Size_X", row.get("Workgroup_Size", 0)) or 0),
+                                 int(row["Start_Timestamp"]), int(row["End_Timestamp"])))
+    groups = {}
+    for name, gx, wx, t0, t1 in launches:
+        groups.setdefault((name, gx, wx), []).append((t1 - t0) / 1e3)
+    print(f"{'kernel':<70} {'grid_x':>9} {'wg_x':>5} {'n':>6} {'avg_us':>10} {'min_us':>10}")
+    for (name, gx, wx), ds in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        print(f"{_short(name):<70} {gx:>9} {wx:>5} {len(ds):>6} {sum(ds) / len(ds):>10.2f} {min(ds):>10.2f}")
+    ranges = []
+    for f in glob.glob(os.path.join(path, "**", "*marker_api_trace.csv"), recursive=True):
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                msg = row.get("Function", "") or row.get("Message", "")
+                if msg.startswith("rq-"):
+                    ranges.append((msg, int(row["Start_Timestamp"]), int(row["End_Timestamp"])))
+    if ranges:
+        print()
+        print(f"{'range / kernel':<70} {'n':>6} {'avg_us':>10} {'min_us':>10} {'sum_us':>10}")
+        for msg, r0, r1 in sorted(ranges, key=lambda r: r[1]):
+            print(msg)
+            per = {}
+            for name, gx, wx, t0, t1 in launches:
+                if r0 <= t0 <= r1:
+                    per.setdefault(name, []).append((t1 - t0) / 1e3)
+            for name, ds in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+                print(f"  {_short(name, 68):<68} {len(ds):>6} {sum(ds) / len(ds):>10.2f} {min(ds):>10.2f} "
+                      f"{sum(ds):>10.1f}")
 
 
 def main():
@@ -95,8 +252,13 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--m", type=int, default=1, help="decode tokens per step (activation rows)")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the M=2048 GEMM section")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--summarize-profile", metavar="DIR", help="summarize a rocprofv3 CSV kernel trace and exit")
     args = ap.parse_args()
+    if args.summarize_profile:
+        summarize_profile(args.summarize_profile)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path is built and measured on a single MI355X; "
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
@@ -107,48 +269,37 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     M = args.m
+    print(f"bench: decode GEMV M={M}", file=sys.stderr, flush=True)
 
     layer_bytes = sum(N * K // 2 + (N * K // BLOCK) * 4 for _, K, N in LLAMA3_8B_PROJ)
-    n_copies = max(2, math.ceil(520e6 / layer_bytes / 2) * 2)  # gate+up alone exceed 512 MB
+    n_copies = max(2, math.ceil(520e6 / layer_bytes / 2) * 2)
     layers = [make_layer(dev, 1000 + c) for c in range(n_copies)]
     gx = torch.Generator(device=dev).manual_seed(7)
     xs = {K: torch.randn(M, K, generator=gx, device=dev).to(torch.bfloat16) for K in (4096, 14336)}
+    stream = torch.cuda.Stream()
 
     def step(layer):
-        out = []
         for name, K, N in LLAMA3_8B_PROJ:
             packed, absmax, a, b, _, _ = layer[name]
-            out.append(ops.nf4_linear(xs[K], packed, absmax, N, BLOCK, lora_a=a, lora_b=b, scaling=SCALING))
-        return out
+            ops.nf4_linear(xs[K], packed, absmax, N, BLOCK, lora_a=a, lora_b=b, scaling=SCALING)
 
-    # warm every path (first launches set kernel attributes), then capture
-    for layer in layers:
-        step(layer)
-    torch.cuda.synchronize()
-    graphs = []
-    stream = torch.cuda.Stream()
-    with torch.cuda.stream(stream):
-        for layer in layers:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=stream):
-                step(layer)
-            graphs.append(g)
-    torch.cuda.synchronize()
-
+    graphs = [_capture(lambda L=layer: step(L), stream) for layer in layers]
     for i in range(args.warmup):
         graphs[i % n_copies].replay()
     torch.cuda.synchronize()
+    cur = torch.cuda.current_stream()
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    cur = torch.cuda.current_stream()
-    t0.record(cur)
-    for i in range(args.steps):
-        graphs[i % n_copies].replay()
-    t1.record(cur)
-    torch.cuda.synchronize()
+    with _Range("rq-decode-step"):
+        t0.record(cur)
+        for i in range(args.steps):
+            graphs[i % n_copies].replay()
+        t1.record(cur)
+        torch.cuda.synchronize()
     ms_step = t0.elapsed_time(t1) / args.steps
     step_bytes = sum(gemv_bytes(M, N, K) for _, K, N in LLAMA3_8B_PROJ)
     value = step_bytes / (ms_step * 1e-3) / 1e9
+    del graphs
 
     # roofline of the dominant kernel: plain GEMV launches at the gate/up shape
     K, N = 4096, 14336
@@ -159,37 +310,41 @@ def main():
         for packed, absmax in roof_w:
             ops.nf4_linear(x_roof, packed, absmax, N, BLOCK)
 
-    roof_pass()
-    torch.cuda.synchronize()
-    rg = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(stream):
-        with torch.cuda.graph(rg, stream=stream):
-            roof_pass()
+    rg = _capture(roof_pass, stream)
     reps = 10
-    rg.replay()
-    torch.cuda.synchronize()
-    t0.record(cur)
-    for _ in range(reps):
-        rg.replay()
-    t1.record(cur)
-    torch.cuda.synchronize()
-    launches = reps * len(roof_w)
-    us_launch = t0.elapsed_time(t1) * 1e3 / launches
+    with _Range(f"rq-roofline nf4_gemv_kernel M={M} K={K} N={N}"):
+        us_launch = _time_graph(rg, reps) * 1e3 / len(roof_w)
     kb = kernel_bytes(M, N, K)
     achieved = kb / (us_launch * 1e-6) / 1e9
+    del rg
+    print(f"bench: decode {ms_step * 1e3:.1f} us/step, {value:.0f} GB/s; gate/up GEMV {us_launch:.2f} us",
+          file=sys.stderr, flush=True)
+
+    gemm = None
+    if not args.no_gemm:
+        del layers
+        torch.cuda.empty_cache()
+        gemm = bench_gemm(dev, stream)
+        print(f"bench: GEMM fwd {gemm['fwd_tflops']} TF/s, dX {gemm['dx_tflops']} TF/s", file=sys.stderr,
+              flush=True)
+        layer0 = make_layer(dev, 1000)
+    else:
+        layer0 = layers[0]
 
     cpu = None
     if not args.no_cpu:
-        layer_cpu = {nm: tuple(t.cpu() if torch.is_tensor(t) else t for t in v) for nm, v in layers[0].items()}
+        layer_cpu = {nm: tuple(t.cpu() if torch.is_tensor(t) else t for t in v) for nm, v in layer0.items()}
         xs_cpu = {k: v.cpu() for k, v in xs.items()}
         dt, n = cpu_baseline(layer_cpu, xs_cpu)
         cpu = {"value": round(step_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
                "kind": "port",
-               "sample": f"{n} decode step(s) of the same 7-projection layer (M={M}, LoRA r={RANK}) through "
-                         f"the oracle's torch CPU restatement; {dt * 1e3:.1f} ms/step"}
+               "sample": f"{n} decode step(s) of one 7-projection Llama-3-8B layer (M={M}, LoRA r={RANK}) "
+                         f"through the oracle's torch CPU restatement of dequantize_int4 -> .to(bf16) -> "
+                         f"F.linear + LoRA; {dt * 1e3:.1f} ms/step"}
 
+    traffic = MEASURED_TRAFFIC.get(("nf4_gemv_kernel", M, K, N))
     rec = {
-        "metric": "NF4 dequant-GEMV GB/s + GEMM TFLOP/s (% roofline), Llama-3-8B proj shapes",
+        "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -205,12 +360,13 @@ def main():
                                f"M={M}, LoRA r={RANK} fused, block {BLOCK} fp32 absmax",
                    "tokens": M, "layer_copies": n_copies, "step_bytes": step_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "nf4_gemv_kernel", "shape": f"M={M} K={K} N={N}",
                      "bytes_per_launch": kb, "us_per_launch": round(us_launch, 3)},
+        "gemm": gemm,
         "cpu_baseline": cpu,
     }
-    print(json.dumps(rec))
+    print(json.dumps(rec), flush=True)
 
 
 if __name__ == "__main__":

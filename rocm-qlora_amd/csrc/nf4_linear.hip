@@ -38,23 +38,26 @@ namespace rq {
 // becomes RND(T[code] * scale) through the LDS pair table.
 //
 // Grid (G, S), 1024 threads: workgroup (g, s) owns K split s (at most 16
-// segments) and visits 16-row tiles g, g + G, ...  Wave w always covers
-// segment w of the split, so its activation operands stay in registers.
-// Every load goes out as raw bits and is converted only where it is used,
-// and every prefetch is unconditional (past the workgroup's last tile it
-// reads one shared address), so the in-order load counter stays exact and
-// the math of tile j runs while the next tile's loads are in flight.  Each
-// tile ends with one barrier: the 16 partial tiles are summed in a fixed
-// order through LDS (so results are deterministic) and finished from LDS --
-// the tile's LoRA B rows and bias were fetched with its weights, one value
-// per thread.
+// segments; S > 1 only when K > 4096) and the NT <= 4 tiles g, g + G, ...,
+// g + (NT - 1) G.  The kernel is straight-line: every wave issues the loads
+// of all its tiles before it computes any (NT x 2 KiB per wave), and no
+// loaded value is carried around a loop, so the compiler's in-order load
+// counting is exact and each tile's math waits only for that tile's data.
+// Epilogue operands (the tiles' LoRA B rows, bias, RND(u)) are fetched before
+// the weights and staged in LDS once.  One barrier publishes the 16 wave
+// partials of every tile; they are summed in a fixed order (deterministic
+// results) and finished by one thread per output.
 // ---------------------------------------------------------------------------
 constexpr int kGemvThreads = 1024;
 constexpr int kGemvWaves = kGemvThreads / 64;
 constexpr int kSegK = 256;
-constexpr int kGemvMaxFusedRank = kGemvThreads / 16;  // B values of a tile, one per thread
+constexpr int kGemvMaxNT = 4;          // tiles per workgroup
+constexpr int kGemvMaxFusedRank = 64;  // LoRA rank the in-kernel epilogue stages
 constexpr int kGemvMaxUSplits = 16;
-constexpr int kGemvDepth = 2;  // tiles whose loads are in flight per wave
+constexpr int kGemvLutQwords = 256 * 32;  // 64 KiB: code byte -> fp32 (T[lo], T[hi]), 32 copies
+// Word 3 of a raw (stride 0) buffer resource on gfx9-family GPUs, gfx950
+// included: 32-bit data, bounds checked against num_records.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 
 struct GemvArgs {
   const uint16_t* x;
@@ -69,6 +72,8 @@ struct GemvArgs {
   float* ws;               // [S, M, N] partials when !direct
 };
 
+// One tile's loads for one lane: loads A and B (raw code bits) and the
+// scales of chunks q and q + 4 of row n.
 template <class Scale>
 struct GemvTileLoads {
   u32x4 a, b;
@@ -81,64 +86,33 @@ struct GemvLane {
   bool live;    // the wave has a segment of this split
 };
 
-// tile < 0 marks a prefetch past the workgroup's last tile: every lane then
-// reads one shared 16-byte address (and scale 0), which keeps the number of
-// loads static -- so the in-order load counter stays exact across the loop --
-// at the cost of a single cache line.
+// Loads of one tile for one lane.  The packed weights are read through a
+// buffer resource whose range is the weight matrix, so rows past N (a tile
+// past the end, or the rows of a last, partial tile) read as zero codes
+// without a bounds test, and chunks past K in a last, partial segment read
+// codes of the next row (or zeros) that meet zero activations.  Offsets are
+// 32-bit (the host keeps the packed weights under 2 GiB).  The loads are
+// issued on every path, branch-free, so each wave issues the same loads in
+// the same order and the compiler's in-order load counting stays exact.
 template <class Scale>
 __device__ __forceinline__ void gemv_issue_tile(GemvTileLoads<Scale>& L, const GemvArgs& a, const Scale& scale,
-                                                int64_t tile, const GemvLane& w) {
-  if (tile < 0) {
-    L.a = *reinterpret_cast<const u32x4*>(a.packed);
-    L.b = L.a;
-    L.s1 = scale.load(0);
-    L.s2 = L.s1;
-    return;
-  }
-  const int64_t half_k = a.K >> 1;
-  const int64_t r0 = tile * 16;
-  int64_t rowA = r0 + (w.n16 & 7), rowB = r0 + 8 + (w.n16 & 7), rowS = r0 + w.n16;
-  rowA = rowA < a.N ? rowA : a.N - 1;  // dead rows re-read a live row; never stored
-  rowB = rowB < a.N ? rowB : a.N - 1;
-  rowS = rowS < a.N ? rowS : a.N - 1;
-  const int cA = w.q + (w.n16 >= 8 ? 4 : 0), cB = w.q + (w.n16 < 8 ? 4 : 0);
-  const int64_t sk = w.seg * kSegK;
-  // chunks past K (a last, partial segment) re-read the row's last chunk
-  int64_t kA = sk + 32 * cA, kB = sk + 32 * cB;
-  kA = kA < a.K ? kA : a.K - 32;
-  kB = kB < a.K ? kB : a.K - 32;
-  L.a = *reinterpret_cast<const u32x4*>(a.packed + rowA * half_k + (kA >> 1));
-  L.b = *reinterpret_cast<const u32x4*>(a.packed + rowB * half_k + (kB >> 1));
-  int64_t k1 = sk + 32 * w.q, k2 = k1 + 128;
-  k1 = k1 < a.K ? k1 : a.K - 1;
-  k2 = k2 < a.K ? k2 : a.K - 1;
-  L.s1 = scale.load(rowS * a.blocks_per_row + (k1 >> a.bs_log2));
-  L.s2 = scale.load(rowS * a.blocks_per_row + (k2 >> a.bs_log2));
-}
-
-// LoRA B and bias of one tile as raw bits: thread t holds B[tile row t / 64,
-// t % 64] (rank <= 64) and, for t < 16, bias[tile row t].
-struct GemvEpiLoads {
-  Raw16x2 lb, bias;
-};
-
-__device__ __forceinline__ void gemv_issue_epi(GemvEpiLoads& E, const GemvArgs& a, const LinearEpi& e,
-                                               int64_t tile, int tid) {
-  // always the same loads: without LoRA or bias, or past the last tile, they
-  // read x[0] instead
-  const bool past = tile < 0;
-  tile = past ? 0 : tile;
-  int64_t bn = tile * 16 + (tid >> 6);
-  bn = bn < a.N ? bn : a.N - 1;
-  const int j = tid & 63;
-  const bool has_b = e.rank > 0 && !past;
-  E.lb = load_raw(has_b ? e.lora_b : static_cast<const void*>(a.x),
-                  has_b ? bn * e.ld_lora_b + (j < e.rank ? j : 0) : 0, has_b ? e.lora_dt : RQ_DTYPE_BF16);
-  int64_t cn = tile * 16 + (tid & 15);
-  cn = cn < a.N ? cn : a.N - 1;
-  const bool has_bias = e.bias != nullptr && !past;
-  E.bias = load_raw(has_bias ? e.bias : static_cast<const void*>(a.x), has_bias ? cn : 0,
-                    has_bias ? e.bias_dt : RQ_DTYPE_BF16);
+                                                __amdgpu_buffer_rsrc_t wres, uint32_t tile, const GemvLane& w) {
+  const uint32_t half_k = uint32_t(a.K >> 1);
+  const uint32_t r0 = tile * 16u, n7 = uint32_t(w.n16 & 7);
+  const uint32_t cA = uint32_t(w.q) + (w.n16 >= 8 ? 4u : 0u), cB = uint32_t(w.q) + (w.n16 < 8 ? 4u : 0u);
+  const uint32_t sb = uint32_t(w.seg) * (kSegK / 2);
+  L.a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, (r0 + n7) * half_k + sb + 16u * cA, 0, 0));
+  L.b = __builtin_bit_cast(u32x4,
+                           __builtin_amdgcn_raw_buffer_load_b128(wres, (r0 + 8u + n7) * half_k + sb + 16u * cB, 0, 0));
+  uint32_t srow = r0 + uint32_t(w.n16);
+  srow = srow < uint32_t(a.N) ? srow : uint32_t(a.N) - 1u;
+  const uint32_t kmax = uint32_t(a.K) - 1u;
+  uint32_t k1 = uint32_t(w.seg) * kSegK + 32u * uint32_t(w.q), k2 = k1 + 128u;
+  k1 = k1 < kmax ? k1 : kmax;
+  k2 = k2 < kmax ? k2 : kmax;
+  const uint32_t sr = srow * uint32_t(a.blocks_per_row);
+  L.s1 = scale.load(int64_t(sr + (k1 >> a.bs_log2)));
+  L.s2 = scale.load(int64_t(sr + (k2 >> a.bs_log2)));
 }
 
 __device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
@@ -165,83 +139,48 @@ __device__ __forceinline__ f32x4 gemv_tile(const GemvTileLoads<Scale>& L, const 
   return acc;
 }
 
-// LDS staging of one tile: 16 wave partials [16][16 m][16 n], RND(B)
-// [16][rank], RND(bias) [16].
-struct GemvStage {
-  float* part;
-  float* lb;
-  float* bias;
-};
+// The code book as fp32 bits (for the table fill).
+__device__ const uint32_t kNF4BitsDev[16] = {
+    kNF4Bits[0], kNF4Bits[1], kNF4Bits[2],  kNF4Bits[3],  kNF4Bits[4],  kNF4Bits[5],  kNF4Bits[6],  kNF4Bits[7],
+    kNF4Bits[8], kNF4Bits[9], kNF4Bits[10], kNF4Bits[11], kNF4Bits[12], kNF4Bits[13], kNF4Bits[14], kNF4Bits[15]};
 
-template <int XT>
-__device__ __forceinline__ void gemv_publish(const f32x4& acc, const GemvEpiLoads& E, const GemvStage& st,
-                                             const GemvArgs& a, const LinearEpi& e, int wave, int q, int n16,
-                                             int tid) {
+// Fill of the fp32 pair table by 1024 threads: entry e (a code byte) holds
+// (T[e & 15], T[e >> 4]); copy c at qword e * 32 + c (lane l reads copy
+// l % 32: a ds_read_b64 serves 32 lanes per cycle, which hit 32 distinct
+// bank pairs).  Thread t writes copies 8 (t % 4) .. + 7 of entry t / 4.
+__device__ __forceinline__ void fill_gemv_lut(u32x2* lut, uint32_t t_even, uint32_t t_odd, int tid) {
+  u32x4* dst = reinterpret_cast<u32x4*>(lut + (tid >> 2) * 32 + 8 * (tid & 3));
 #pragma unroll
-  for (int r = 0; r < 4; ++r) st.part[(wave * 16 + 4 * q + r) * 16 + n16] = acc[r];
-  if (a.direct) {
-    const int j = tid & 63;
-    if (j < e.rank) st.lb[(tid >> 6) * e.rank + j] = round_x<XT>(raw_to_f32(E.lb, e.lora_dt));
-    if (tid < 16) st.bias[tid] = e.bias ? round_x<XT>(raw_to_f32(E.bias, e.bias_dt)) : 0.0f;
-  }
+  for (int i = 0; i < 4; ++i) dst[i] = u32x4{t_even, t_odd, t_even, t_odd};
 }
 
-template <int XT>
-__device__ __forceinline__ void gemv_finish(const GemvArgs& a, const LinearEpi& e, const GemvStage& st,
-                                            const float* us, int64_t tile, int s, int tid) {
-  if (tid >= 256) return;
-  const int m = tid >> 4, nn = tid & 15;
-  const int64_t n = tile * 16 + nn;
-  if (m >= a.M || n >= a.N) return;
-  float p[kGemvWaves];
-#pragma unroll
-  for (int w = 0; w < kGemvWaves; ++w) p[w] = st.part[(w * 16 + m) * 16 + nn];
-  float v = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kGemvWaves; ++w) v = __fadd_rn(v, p[w]);
-  if (!a.direct) {
-    a.ws[(int64_t(s) * a.M + m) * a.N + n] = v;
-    return;
-  }
-  if (e.bias) v = __fadd_rn(v, st.bias[nn]);
-  v = round_x<XT>(v);
-  if (e.rank > 0) {
-    float l = 0.0f;
-    for (int j0 = 0; j0 < e.rank; j0 += 8) {
-      float uu[8], bb[8];
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        const bool ok = j0 + jj < e.rank;
-        uu[jj] = ok ? us[m * e.rank + j0 + jj] : 0.0f;
-        bb[jj] = ok ? st.lb[nn * e.rank + j0 + jj] : 0.0f;
-      }
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) l = __fmaf_rn(uu[jj], bb[jj], l);
-    }
-    l = round_x<XT>(__fmul_rn(round_x<XT>(l), e.scaling));
-    v = round_x<XT>(__fadd_rn(v, l));
-  }
-  static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
+// Workgroup barrier for LDS only: this wave's LDS accesses are complete,
+// then s_barrier.  (__syncthreads() may also wait for every outstanding
+// global load, which would serialize the prefetched tiles.)
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Dynamic LDS of the GEMV: wave partials [NT][16 waves][M][16], RND(B) of the
+// tiles' rows [NT * 16][64], RND(bias) [NT * 16], RND(u) [M][64] (fp32).
+__host__ __device__ inline size_t gemv_lds_floats(int nt, int64_t M, bool lora) {
+  return size_t(nt) * kGemvWaves * M * 16 + (lora ? size_t(nt) * 16 * kGemvMaxFusedRank : 0) + size_t(nt) * 16 +
+         (lora ? size_t(M) * kGemvMaxFusedRank : 0);
 }
 
-template <int XT, class Scale>
+template <int XT, class Scale, int NT>
 __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(GemvArgs a, Scale scale, LinearEpi e) {
   // The table is the kernel's only static LDS array, so it sits at address
   // 0 and every lookup's base folds into the instruction's offset field.
-  __shared__ u32x2 lut[kF32PairLutQwords];
+  __shared__ u32x2 lut[kGemvLutQwords];
   extern __shared__ uint32_t smem[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int M = int(a.M);
   const int rank = (a.direct && e.rank > 0) ? e.rank : 0;  // LoRA staging only when fused here
-  // dynamic LDS: 2 tile stages, then RND(u)
-  const int stage_floats = kGemvWaves * 256 + 16 * rank + 16;
-  GemvStage st[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    float* base = reinterpret_cast<float*>(smem) + i * stage_floats;
-    st[i] = GemvStage{base, base + kGemvWaves * 256, base + kGemvWaves * 256 + 16 * rank};
-  }
-  float* us = reinterpret_cast<float*>(smem) + 2 * stage_floats;  // [16][rank]
+  constexpr int RP = kGemvMaxFusedRank;                    // staging pitch
+  float* part = reinterpret_cast<float*>(smem);
+  float* lbs = part + NT * kGemvWaves * M * 16;
+  float* bss = lbs + (rank > 0 ? NT * 16 * RP : 0);
+  float* us = bss + NT * 16;
 
   GemvLane w;
   w.n16 = lane & 15;
@@ -251,88 +190,151 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(GemvArgs a, Scal
   const int64_t sg0 = (nsegs * s) / a.S, sg1 = (nsegs * (s + 1)) / a.S;
   w.live = sg0 + wave < sg1;
   w.seg = w.live ? sg0 + wave : sg0;  // a wave without a segment re-reads one; its activations are zero
-  const int64_t n_tiles = (a.N + 15) / 16;
-  const int64_t step = gridDim.x;
-  const int64_t first = blockIdx.x;
-  const int64_t n_mine = first < n_tiles ? (n_tiles - 1 - first) / step + 1 : 0;
-  auto tile_at = [&](int64_t j) -> int64_t { return j < n_mine ? first + j * step : -1; };
-  if (n_mine == 0) return;
+  const uint32_t n_tiles = uint32_t((a.N + 15) / 16);
+  // tiles g, g + G, g + 2G, ...: at any moment the workgroups' loads are
+  // spread over the whole weight matrix
+  auto tile_idx = [&](int t) -> uint32_t { return blockIdx.x + uint32_t(t) * gridDim.x; };
+  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(a.packed), 0, int(uint32_t(a.N) * uint32_t(a.K >> 1)), kBufferRsrcWord3);
 
-  // 1. activation operands (stationary): step st -> k = seg * 256 + 128
-  //    (st / 4) + 32 q + 8 (st % 4); zero past M, past K and for a wave
-  //    without a segment.  2. the RND(u) partials.  3. the first two tiles.
-  u32x4 xraw[8];
-  const bool mlive = w.n16 < a.M && w.live;
-  {
-    const uint16_t* xrow = a.x + (w.n16 < a.M ? w.n16 : 0) * a.ldx;
+  // 1. Loads the weights do not depend on, issued first so that staging them
+  //    waits only for them: the table entry this thread writes, the tiles'
+  //    LoRA B values (value i of thread t is row t / 64 + 16 i, rank t % 64
+  //    of the [NT * 16][64] staging block), the bias, the RND(u) partials
+  //    (waves m < M) and the activation operands.
+  const uint32_t t_even = kNF4BitsDev[(tid >> 2) & 15], t_odd = kNF4BitsDev[tid >> 6];
+  Raw16x2 lbr[NT];
+  const int lj = tid & (RP - 1);
+  if (rank > 0) {
 #pragma unroll
-    for (int stp = 0; stp < 8; ++stp) {
-      int64_t k = w.seg * kSegK + 128 * (stp >> 2) + 32 * w.q + 8 * (stp & 3);
-      k = k < a.K ? k : 0;
-      xraw[stp] = load_x8(xrow + k, a.xvec);
+    for (int i = 0; i < NT; ++i) {
+      const int rr = (tid >> 6) + 16 * i;
+      uint32_t bn = tile_idx(rr >> 4) * 16u + uint32_t(rr & 15);
+      bn = bn < uint32_t(a.N) ? bn : uint32_t(a.N) - 1u;
+      const int j = lj < rank ? lj : 0;
+      lbr[i] = load_raw(e.lora_b, int64_t(bn) * e.ld_lora_b + j, e.lora_dt);
     }
   }
-  // RND(u) partials: thread t < 16 rank sums u[split][t / rank][t % rank]
-  // (every address clamped into the buffer, so the loads are unconditional)
+  const bool has_bias = a.direct && e.bias != nullptr;
+  Raw16x2 br;
+  if (has_bias) {
+    const int cb = tid & (NT * 16 - 1);
+    uint32_t cn = tile_idx(cb >> 4) * 16u + uint32_t(cb & 15);
+    cn = cn < uint32_t(a.N) ? cn : uint32_t(a.N) - 1u;
+    br = load_raw(e.bias, int64_t(cn), e.bias_dt);
+  }
   float up[kGemvMaxUSplits];
-  const bool has_u = a.direct && rank > 0;
-  {
-    const int u_idx = (has_u && tid < 16 * rank) ? tid : 0;
-    const int64_t u_m0 = has_u ? u_idx / rank : 0;
-    const int64_t u_m = u_m0 < a.M ? u_m0 : a.M - 1;
-    const int u_j = has_u ? u_idx % rank : 0;
+  const int um = wave;  // RND(u) row m is staged by wave m
+  const bool stage_u = rank > 0 && um < M;
+  if (stage_u) {
+    const uint32_t u_idx = uint32_t(um * rank + (lj < rank ? lj : 0));
+    const uint32_t u_stride = uint32_t(M * rank);
+    const int ns = e.u_splits;
 #pragma unroll
-    for (int k = 0; k < kGemvMaxUSplits; ++k) up[k] = 0.0f;
-    if (has_u) {
+    for (int k = 0; k < kGemvMaxUSplits; ++k) up[k] = e.u[(k < ns ? uint32_t(k) : 0u) * u_stride + u_idx];
+  }
+  // activations: step c covers x[token][seg * 256 + 128 (c / 4) + 32 q + 8
+  // (c % 4) ...]; a token past M, a k past K and a wave without a segment
+  // read zeros
+  u32x4 xa[8];
+  const bool mlive = w.n16 < M && w.live;
+  if (a.xvec) {
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(a.x), 0, int(uint32_t(M - 1) * uint32_t(a.ldx) * 2u + uint32_t(a.K) * 2u),
+        kBufferRsrcWord3);
+    const uint32_t xrow = uint32_t(w.n16) * uint32_t(a.ldx) * 2u;
 #pragma unroll
-      for (int k = 0; k < kGemvMaxUSplits; ++k) {
-        const int kk = k < e.u_splits ? k : 0;
-        up[k] = e.u[(int64_t(kk) * a.M + u_m) * rank + u_j];
-      }
+    for (int c = 0; c < 8; ++c) {
+      const uint32_t k = uint32_t(w.seg) * kSegK + 128u * (c >> 2) + 32u * uint32_t(w.q) + 8u * (c & 3);
+      const uint32_t off = (mlive && k < uint32_t(a.K)) ? xrow + 2u * k : 0xFFFFFFF0u;
+      xa[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0));
+    }
+  } else {
+    const uint16_t* xrow = a.x + (w.n16 < M ? w.n16 : 0) * a.ldx;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      int64_t k = w.seg * kSegK + 128 * (c >> 2) + 32 * w.q + 8 * (c & 3);
+      const bool live = mlive && k < a.K;
+      k = k < a.K ? k : 0;
+      const u32x4 v = load_x8(xrow + k, false);
+      xa[c] = live ? v : u32x4{0u, 0u, 0u, 0u};
     }
   }
-  constexpr int D = kGemvDepth;
-  GemvTileLoads<Scale> buf[D];
-  GemvEpiLoads ebuf[2];  // the epilogue values run two tiles ahead
-#pragma unroll
-  for (int i = 0; i < D; ++i) gemv_issue_tile(buf[i], a, scale, tile_at(i), w);
-  gemv_issue_epi(ebuf[0], a, e, tile_at(0), tid);
-  gemv_issue_epi(ebuf[1], a, e, tile_at(1), tid);
 
-  u32x4 xa[8];
+  // 2. every tile's weights and scales
+  GemvTileLoads<Scale> buf[NT];
 #pragma unroll
-  for (int stp = 0; stp < 8; ++stp) {
-    const int64_t k = w.seg * kSegK + 128 * (stp >> 2) + 32 * w.q + 8 * (stp & 3);
-    xa[stp] = (mlive && k < a.K) ? xraw[stp] : u32x4{0u, 0u, 0u, 0u};
+  for (int t = 0; t < NT; ++t) gemv_issue_tile(buf[t], a, scale, wres, tile_idx(t), w);
+
+  // 3. the table and the epilogue operands into LDS (these wait for the
+  //    loads of step 1 only)
+  fill_gemv_lut(lut, t_even, t_odd, tid);
+  if (rank > 0) {
+#pragma unroll
+    for (int i = 0; i < NT; ++i)
+      lbs[tid + 1024 * i] = lj < rank ? round_x<XT>(raw_to_f32(lbr[i], e.lora_dt)) : 0.0f;
   }
-  fill_f32pair_lut<kGemvThreads>(lut, tid);
-  if (has_u && tid < 16 * rank) {
+  if (a.direct && tid < NT * 16) bss[tid] = has_bias ? round_x<XT>(raw_to_f32(br, e.bias_dt)) : 0.0f;
+  if (stage_u) {
     float sum = 0.0f;
 #pragma unroll
     for (int k = 0; k < kGemvMaxUSplits; ++k)
       if (k < e.u_splits) sum = __fadd_rn(sum, up[k]);
-    us[tid] = (tid / rank) < a.M ? round_x<XT>(sum) : 0.0f;
+    us[tid] = lj < rank ? round_x<XT>(sum) : 0.0f;
   }
-  __syncthreads();
+  lds_barrier();
 
+  // 4. the tiles, each as soon as its loads have landed; partials to LDS
   const uint32_t lane_off = uint32_t(lane & 31) * 8u;
-  // D tiles per iteration so the ring index is static; the refill D tiles
-  // ahead is unconditional
-  for (int64_t j = 0; j < n_mine; j += D) {
 #pragma unroll
-    for (int i = 0; i < D; ++i) {
-      if (j + i >= n_mine) break;
-      const f32x4 acc = gemv_tile<XT>(buf[i], scale, xa, lut, lane_off, w.n16);
-      gemv_issue_tile(buf[i], a, scale, tile_at(j + i + D), w);
-      // consecutive tiles alternate LDS stages and epilogue buffers
-      const GemvStage& sg = ((j + i) & 1) ? st[1] : st[0];
-      GemvEpiLoads& eb = ((j + i) & 1) ? ebuf[1] : ebuf[0];
-      gemv_publish<XT>(acc, eb, sg, a, e, wave, w.q, w.n16, tid);
-      gemv_issue_epi(eb, a, e, tile_at(j + i + 2), tid);
-      __syncthreads();
-      gemv_finish<XT>(a, e, sg, us, tile_at(j + i), s, tid);
+  for (int t = 0; t < NT; ++t) {
+    const f32x4 acc = gemv_tile<XT>(buf[t], scale, xa, lut, lane_off, w.n16);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * w.q + r;
+      if (m < M) part[((t * kGemvWaves + wave) * M + m) * 16 + w.n16] = acc[r];
     }
   }
+  lds_barrier();
+
+  // 5. one thread per output (tile t = tid / 256, row m, column nn): the 16 wave
+  //    partials in wave order, then bias, LoRA, rounding -- or the fp32 sum
+  //    to the split-K workspace
+  const int t = tid >> 8, m = (tid >> 4) & 15, nn = tid & 15;
+  if (t >= NT || m >= M) return;
+  const uint32_t tile = tile_idx(t);
+  const int64_t n = int64_t(tile) * 16 + nn;
+  if (tile >= n_tiles || n >= a.N) return;
+  float p[kGemvWaves];
+#pragma unroll
+  for (int ww = 0; ww < kGemvWaves; ++ww) p[ww] = part[((t * kGemvWaves + ww) * M + m) * 16 + nn];
+  float v = 0.0f;
+#pragma unroll
+  for (int ww = 0; ww < kGemvWaves; ++ww) v = __fadd_rn(v, p[ww]);
+  if (!a.direct) {
+    a.ws[(int64_t(s) * a.M + m) * a.N + n] = v;
+    return;
+  }
+  if (e.bias) v = __fadd_rn(v, bss[t * 16 + nn]);
+  v = round_x<XT>(v);
+  if (rank > 0) {
+    const float* brow = lbs + (t * 16 + nn) * RP;
+    const float* urow = us + m * RP;
+    float l = 0.0f;
+    for (int j0 = 0; j0 < rank; j0 += 8) {
+      float uu[8], bb[8];
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) {
+        uu[jj] = urow[j0 + jj];  // zero past rank
+        bb[jj] = brow[j0 + jj];
+      }
+#pragma unroll
+      for (int jj = 0; jj < 8; ++jj) l = __fmaf_rn(uu[jj], bb[jj], l);
+    }
+    l = round_x<XT>(__fmul_rn(round_x<XT>(l), e.scaling));
+    v = round_x<XT>(__fadd_rn(v, l));
+  }
+  static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
 }
 
 // Split-K finisher (and the LoRA epilogue for any M): y = finish(sum_s
@@ -454,23 +456,23 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus) {
   const int64_t tiles = (N + 15) / 16;
   p.nw = kGemvWaves;
   p.RT = 1;
-  int S = int((nsegs + kGemvWaves - 1) / kGemvWaves);
-  while (S < 8 && tiles * S < cus && nsegs >= 2 * S * (kGemvWaves / 2)) S *= 2;
+  // one segment per wave: K splits only past 16 segments (K > 4096)
+  const int S = int((nsegs + kGemvWaves - 1) / kGemvWaves);
   p.S = S;
+  // tiles per workgroup: enough that one round of workgroups covers the
+  // chip's compute units, at most kGemvMaxNT
+  int64_t nt = (tiles * S + cus - 1) / (cus > 0 ? cus : 1);
+  nt = nt < 1 ? 1 : (nt > kGemvMaxNT ? kGemvMaxNT : nt);
+  p.NT = nt > 2 ? 4 : int(nt);
+  p.grid = int((tiles + p.NT - 1) / p.NT);
   p.u_splits = 0;
   if (rank > 0) {
     const int64_t steps_per_wg = 4 * kLoraUStepsPerWave;
     p.u_splits = int((K / 32 + steps_per_wg - 1) / steps_per_wg);
   }
-  // the fused epilogue stages one B value per thread and sums <= 16 u splits
+  // the fused epilogue stages the tiles' B rows (rank <= 64), <= 16 u splits
   p.direct = S == 1 && rank <= kGemvMaxFusedRank && p.u_splits <= kGemvMaxUSplits;
-  const int64_t r = p.direct && rank > 0 ? rank : 0;
-  // dynamic part only (the 64 KiB table is static): 2 tile stages + RND(u)
-  p.lds_bytes = (size_t(2) * (kGemvWaves * 256 + 16 * r + 16) + 16 * r) * 4;
-  int per_cu = int((160 * 1024) / (p.lds_bytes + size_t(kF32PairLutQwords) * 8));
-  per_cu = per_cu < 1 ? 1 : per_cu;
-  const int64_t slots = int64_t(cus) * per_cu / S;
-  p.grid = int(tiles < slots ? tiles : (slots > 0 ? slots : 1));
+  p.lds_bytes = gemv_lds_floats(p.NT, M, p.direct && rank > 0) * 4;  // dynamic part (the 64 KiB table is static)
   p.ws_bytes = p.direct ? 0 : size_t(S) * M * N * 4;
   p.u_offset = (p.ws_bytes + 255) & ~size_t(255);
   if (rank > 0) p.ws_bytes = p.u_offset + size_t(p.u_splits) * M * rank * 4;
@@ -484,6 +486,22 @@ static int launch_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t str
   const bool avec = aligned(L.lora_a, 16);
   lora_u_kernel<XT><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(L.lora_x), L.ld_lora_x, xvec,
                                               L.lora_a, L.lora_dtype, avec, L.M, L.K, int(L.rank), ks, up);
+  return rq_check_launch();
+}
+
+template <int XT, class Scale, int NT>
+static int launch_gemv_nt(const GemvArgs& a, GemvPlan p, Scale scale, const LinearEpi& e, hipStream_t stream) {
+  p.grid = int(((a.N + 15) / 16 + NT - 1) / NT);
+  auto kern = nf4_gemv_kernel<XT, Scale, NT>;
+  static bool attr_set = false;  // one flag per instantiation
+  if (!attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024 - kGemvLutQwords * 8) != hipSuccess)
+      return RQ_ERR_HIP;
+    attr_set = true;
+  }
+  dim3 grid(unsigned(p.grid), unsigned(p.S));
+  kern<<<grid, kGemvThreads, p.lds_bytes, stream>>>(a, scale, e);
   return rq_check_launch();
 }
 
@@ -503,17 +521,15 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.direct = p.direct;
   a.xvec = aligned(L.x, 16) && (L.ldx % 8 == 0);
   a.ws = ws;
-  auto kern = nf4_gemv_kernel<XT, Scale>;
-  static bool attr_set = false;  // one flag per instantiation
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024 - kF32PairLutQwords * 8) != hipSuccess)
-      return RQ_ERR_HIP;
-    attr_set = true;
+  // double quantization keeps two loads per scale: at most 2 tiles per
+  // workgroup stay within the registers
+  if (p.NT == 1) return launch_gemv_nt<XT, Scale, 1>(a, p, scale, e, stream);
+  if constexpr (Scale::kLoads > 1) {
+    return launch_gemv_nt<XT, Scale, 2>(a, p, scale, e, stream);
+  } else {
+    if (p.NT == 2) return launch_gemv_nt<XT, Scale, 2>(a, p, scale, e, stream);
+    return launch_gemv_nt<XT, Scale, 4>(a, p, scale, e, stream);
   }
-  dim3 grid(unsigned(p.grid), unsigned(p.S));
-  kern<<<grid, kGemvThreads, p.lds_bytes, stream>>>(a, scale, e);
-  return rq_check_launch();
 }
 
 template <int XT>
@@ -595,6 +611,8 @@ int gemv_workspace(const LinearArgs& L, size_t* bytes) {
 }
 
 int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  // the GEMV addresses the packed weights with 32-bit byte offsets
+  if (L.N * (L.K / 2) > int64_t(INT32_MAX) - 256) return RQ_ERR_UNSUPPORTED;
   const GemvPlan p = plan_gemv(L.M, L.N, L.K, L.rank, device_cus());
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
   if (workspace && !aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;

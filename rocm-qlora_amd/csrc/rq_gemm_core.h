@@ -274,24 +274,29 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a, Prod
   // barrier.  Four steps per iteration index every register set statically;
   // the loop has a single exit, so the accumulators stay in place.  Steps
   // past the end wrap around K (in bounds; their results are never used).
-#define RQ_GEMM_STEP(J, P)                                                                                     \
+  // In the loop, each step's last vector-memory loads are the kLoads weight
+  // loads, whose registers later steps consume; the barrier leaves them in
+  // flight.  In the tail the weight loads feed nothing, so the compiler drops
+  // them, and the barrier must wait for every load (the activations of the
+  // next step would otherwise be read before they land).
+#define RQ_GEMM_STEP(J, P, WAIT)                                                                               \
   do {                                                                                                         \
     gemm_step<XT, Prod>(acc, xring + ((P) & 1) * kXStepBytes, wtile + ((P) & 1) * kWTileBytes, i32, q, a, xo,  \
                         ks((J) + 1), xring_addr + (((P) + 1) & 1) * kXStepBytes, prod, wl[((P) + 1) & 3], wl[P], \
                         ks((J) + kWDepth), wtile + (((P) + 1) & 1) * kWTileBytes);                             \
-    step_barrier<Prod::kLoads>();                                                                              \
+    step_barrier<WAIT>();                                                                                      \
   } while (0)
   int64_t j = 0;
   for (; j + 4 <= nk; j += 4) {
-    RQ_GEMM_STEP(j, 0);
-    RQ_GEMM_STEP(j + 1, 1);
-    RQ_GEMM_STEP(j + 2, 2);
-    RQ_GEMM_STEP(j + 3, 3);
+    RQ_GEMM_STEP(j, 0, Prod::kLoads);
+    RQ_GEMM_STEP(j + 1, 1, Prod::kLoads);
+    RQ_GEMM_STEP(j + 2, 2, Prod::kLoads);
+    RQ_GEMM_STEP(j + 3, 3, Prod::kLoads);
   }
   const int64_t rem = nk - j;
-  if (rem > 0) RQ_GEMM_STEP(j, 0);
-  if (rem > 1) RQ_GEMM_STEP(j + 1, 1);
-  if (rem > 2) RQ_GEMM_STEP(j + 2, 2);
+  if (rem > 0) RQ_GEMM_STEP(j, 0, 0);
+  if (rem > 1) RQ_GEMM_STEP(j + 1, 1, 0);
+  if (rem > 2) RQ_GEMM_STEP(j + 2, 2, 0);
 #undef RQ_GEMM_STEP
   wait_vmcnt<0>();  // nothing may still be landing in LDS when the epilogue reuses it
 

@@ -54,7 +54,7 @@ struct LinearEpi {
 };
 
 struct GemvPlan {
-  int nw, S, RT, grid, u_splits;
+  int nw, S, RT, NT, grid, u_splits;
   bool direct;
   size_t lds_bytes, ws_bytes, u_offset;
 };

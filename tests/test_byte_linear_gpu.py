@@ -149,3 +149,25 @@ def test_fp8_variants(dev, dtype, M):
     y = ops.fp8_linear(x.to(dev), wc, ws, bias.to(dev))
     ref = R.fp8_linear(x, w, bias)
     _check(y, ref)
+
+
+@pytest.mark.parametrize("K", [320, 384, 448])
+def test_byte_k_step_tails(dev, K):
+    """INT8 and FP8 MFMA paths (M > 16) with K / 64 = 5, 6, 7 k-steps: three
+    calls in a row each within tolerance and bitwise equal to each other."""
+    N, M = 384, 300
+    w = _weights(N, K, seed=K)
+    x = _x(M, K, torch.bfloat16, seed=K + 1)
+    q, s = quantize_int8(w.to(dev), per_channel=True)
+    ys = [ops.int8_linear(x.to(dev), q, s, N, block_size=0) for _ in range(3)]
+    ref = R.int8_linear(x, q.cpu(), s.cpu())
+    for y in ys:
+        _check(y, ref)
+        assert torch.equal(y.view(torch.int16), ys[0].view(torch.int16))
+    wb = w.to(torch.bfloat16)
+    wc, ws = ops.fp8_quantize(wb.to(dev))
+    fs = [ops.fp8_linear(x.to(dev), wc, ws) for _ in range(3)]
+    fref = R.fp8_linear(x, wb)
+    for y in fs:
+        _check(y, fref)
+        assert torch.equal(y.view(torch.int16), fs[0].view(torch.int16))

@@ -85,6 +85,24 @@ def test_dx_variants(dev, dtype, case):
     _check(dx, ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N", [320, 384, 448])
+@pytest.mark.parametrize("lora", [False, True])
+def test_dx_k_step_tails(dev, dtype, N, lora):
+    """Reduction over N = 5, 6, 7 k-steps: three calls in a row each equal
+    the oracle and each other bit for bit (regression: a tail step read its
+    activations before they had landed)."""
+    K, M = 512, 300
+    w, dy, a, b = _inputs(N, K, M, dtype, seed=N + 5, rank=16)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    kw = dict(lora_a=a.to(dev), lora_b=b.to(dev), scaling=2.0) if lora else {}
+    dxs = [ops.nf4_linear_dx(dy.to(dev), packed, absmax, K, 64, **kw) for _ in range(3)]
+    ref = R.nf4_dx(dy, packed.cpu(), absmax.cpu(), N, K, a if lora else None, b if lora else None, 2.0, 64)
+    for dx in dxs:
+        _check(dx, ref)
+        assert torch.equal(dx.view(torch.int16), dxs[0].view(torch.int16))
+
+
 def test_dx_double_quant(dev):
     N, K, M = 1024, 2048, 512
     w, dy, a, b = _inputs(N, K, M, torch.bfloat16, seed=29)

@@ -98,6 +98,26 @@ def test_gemm_variants(dev, dtype, case):
     _check(y, ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("K", [320, 384, 448])
+@pytest.mark.parametrize("lora", [False, True])
+def test_gemm_k_step_tails(dev, dtype, K, lora):
+    """K / 64 = 5, 6, 7 k-steps (1, 2, 3 past the loop's groups of four):
+    three calls in a row each equal the oracle and each other bit for bit
+    (a tail step once read its activations before they had landed, which
+    only a repeated call exposed)."""
+    N, M = 384, 300
+    w, x, a, b, _ = _inputs(N, K, M, dtype, seed=K + 1, rank=16)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    kw = dict(lora_a=a.to(dev), lora_b=b.to(dev), scaling=2.0) if lora else {}
+    ys = [ops.nf4_linear(x.to(dev), packed, absmax, N, 64, **kw) for _ in range(3)]
+    ref = R.nf4_lora_linear(x, packed.cpu(), absmax.cpu(), None, a if lora else None, b if lora else None, 2.0,
+                            N, 64)
+    for y in ys:
+        _check(y, ref)
+        assert torch.equal(y.view(torch.int16), ys[0].view(torch.int16))
+
+
 def test_gemm_double_quant(dev):
     N, K, M = 1024, 2048, 512
     w, x, a, b, _ = _inputs(N, K, M, torch.bfloat16, seed=23)

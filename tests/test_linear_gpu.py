@@ -87,6 +87,24 @@ def test_gemv_variants(dev, dtype, case):
     _check(y, ref)
 
 
+@pytest.mark.parametrize("N,K,M,rank", [
+    (8235, 512, 3, 64),     # 4 tiles per workgroup, the last workgroup with a tile past N, partial tile
+    (4800, 512, 16, 16),    # 2 tiles per workgroup, all 16 activation rows
+    (14336, 4096, 16, 64),  # 4 tiles per workgroup at M = 16 and rank 64 (largest LDS staging)
+    (4800, 4160, 2, 16),    # K split in two with a partial last segment (split-K finisher)
+])
+def test_gemv_tiling_cases(dev, N, K, M, rank):
+    """Tiles per workgroup 1, 2 and 4, dead tiles, K splits: bias + LoRA."""
+    print(f"gemv tiling N={N} K={K} M={M} r={rank}", flush=True)
+    w, x, a, b, bvec = _inputs(N, K, M, torch.bfloat16, seed=N + K, rank=rank, bias=True)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, bias=bvec.to(dev), lora_a=a.to(dev), lora_b=b.to(dev),
+                       scaling=0.25)
+    wf = R.dequantize_int4(packed.cpu(), absmax.cpu(), 64)
+    ref = R.lora_forward(x, R.quant_linear_forward(x, wf, bvec, N, K), a, b, 0.25)
+    _check(y, ref)
+
+
 def test_gemv_double_quant(dev):
     N, K, M = 2048, 4096, 3
     w, x, a, b, _ = _inputs(N, K, M, torch.bfloat16, seed=21)
