@@ -11,7 +11,8 @@ same torch ops in the same order, so dtype promotion (bf16 absmax, bf16
 division, fp32 distances, fp32 products) and rounding match the reference.
 
 Pinning (what checks these functions against something other than
-themselves) is listed in oracle/README.md and enforced by tests/test_oracle_*.py:
+themselves), enforced by tests/test_oracle_codec.py and
+tests/test_oracle_linear.py:
   * quantize_int4 / dequantize_int4: bit-level C restatement that decides by
     brute-force argmin and rounds by nearest-candidate search
     (oracle/codec_ref.c), known-answer blocks, exhaustive decision check.
@@ -19,7 +20,14 @@ themselves) is listed in oracle/README.md and enforced by tests/test_oracle_*.py
     nearest-fnuz rounding; torch's fnuz cast checked against it.
   * quantize_int8 / dequantize_int8: C restatement; range invariants.
   * fp8_quantize_tensor: C fnuz restatement; absmax element -> code 0x7F.
-  * linear / lora / fp8 linears: float64 references within stated tolerances.
+  * quant_linear_forward / lora_forward / nf4_lora_linear: one-hot rows pick
+    weight columns, bias and the s * B A[:, k] adapter term exactly.
+  * nf4_dx: float64 dY W + s dY B A.
+  * lora_linear_grads: float64 central differences of sum(dY * y).
+  * int8_linear: float64 x (q s)^T and linearity in the row scale.
+  * fp8_linear: decode-then-matmul with each scale applied once (exact), and
+    closeness to the unquantized product.
+No function of this module is left without such a check.
 """
 from __future__ import annotations
 

@@ -1,0 +1,111 @@
+"""Pins the oracle's linear compositions (oracle/qlora_ref.py:
+quant_linear_forward, lora_forward, nf4_lora_linear, nf4_dx, int8_linear,
+fp8_linear, lora_linear_grads) against closed forms and float64 finite
+differences, chosen so that a dropped term, a wrong sign, a transposed
+operand or a misplaced scaling fails one of them.  CPU only."""
+import math
+
+import pytest
+import torch
+
+from oracle import qlora_ref as R
+
+
+def _lora(N, K, r, seed):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.empty(r, K)
+    torch.nn.init.kaiming_uniform_(a, a=math.sqrt(5), generator=g)
+    b = torch.randn(N, r, generator=g) * 0.1
+    return a, b
+
+
+def test_one_hot_rows_pick_weight_columns_bias_and_adapter():
+    """x = e_k: base = W[:, k] + bias; the adapter adds s * B @ A[:, k]."""
+    N, K, r, s = 96, 128, 8, 0.75
+    g = torch.Generator().manual_seed(1)
+    w = torch.randn(N, K, generator=g) * 0.02
+    packed, absmax = R.quantize_int4(w, 64)
+    wf = R.dequantize_int4(packed, absmax, 64)[:N * K].view(N, K)
+    bias = torch.randn(N, generator=g)
+    a, b = _lora(N, K, r, 2)
+    ks = torch.tensor([0, 5, 127])
+    x = torch.zeros(3, K)
+    x[torch.arange(3), ks] = 1.0
+    base = R.quant_linear_forward(x, wf.reshape(-1), bias, N, K)
+    assert torch.equal(base, (wf[:, ks] + bias[:, None]).T)
+    y = R.nf4_lora_linear(x, packed, absmax, bias, a, b, s, N, 64)
+    expect = base + s * (b @ a[:, ks]).T
+    assert torch.allclose(y, expect, rtol=1e-6, atol=1e-7)
+    assert torch.equal(R.lora_forward(x, base, a, torch.zeros_like(b), s), base)
+
+
+def test_nf4_dx_is_the_transposed_product():
+    """dX[m, k] = sum_n dY[m, n] W[n, k] + s sum_n dY[m, n] (B A)[n, k], in float64."""
+    N, K, r, s = 64, 192, 4, 1.5
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(N, K, generator=g) * 0.02
+    packed, absmax = R.quantize_int4(w, 64)
+    wf = R.dequantize_int4(packed, absmax, 64)[:N * K].view(N, K).double()
+    a, b = _lora(N, K, r, 4)
+    dy = torch.randn(5, N, generator=g)
+    dx = R.nf4_dx(dy, packed, absmax, N, K, a, b, s, 64).double()
+    expect = dy.double() @ wf + s * dy.double() @ (b.double() @ a.double())
+    assert torch.allclose(dx, expect, rtol=1e-5, atol=1e-6)
+
+
+def test_lora_grads_match_finite_differences():
+    """Gradients of L = sum(dY * y) for y = x W^T + b + s (x A^T) B^T, by
+    central differences in float64 on a tiny case."""
+    N, K, r, M, s = 6, 8, 3, 2, 0.5
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(M, K, generator=g, dtype=torch.float64)
+    w = torch.randn(N, K, generator=g, dtype=torch.float64) * 0.3
+    bias = torch.randn(N, generator=g, dtype=torch.float64)
+    a = torch.randn(r, K, generator=g, dtype=torch.float64)
+    b = torch.randn(N, r, generator=g, dtype=torch.float64)
+    dy = torch.randn(M, N, generator=g, dtype=torch.float64)
+    _, dx, da, db = R.lora_linear_grads(x, w.reshape(-1), bias, a, b, s, dy)
+
+    def loss(xx, aa, bb):
+        y = xx @ w.T + bias + s * (xx @ aa.T) @ bb.T
+        return float((dy * y).sum())
+
+    h = 1e-6
+    for t, grad, which in ((x, dx, 0), (a, da, 1), (b, db, 2)):
+        num = torch.zeros_like(t)
+        for i in range(t.numel()):
+            tp, tm = t.clone(), t.clone()
+            tp.view(-1)[i] += h
+            tm.view(-1)[i] -= h
+            args_p = [x, a, b]
+            args_m = [x, a, b]
+            args_p[which], args_m[which] = tp, tm
+            num.view(-1)[i] = (loss(*args_p) - loss(*args_m)) / (2 * h)
+        assert torch.allclose(grad.double(), num, rtol=1e-6, atol=1e-8), which
+
+
+def test_int8_linear_per_row_scales():
+    """Row-absmax INT8: y = x (q * s[:, None])^T; a row scale multiplies its output column."""
+    g = torch.Generator().manual_seed(6)
+    w = torch.randn(40, 64, generator=g) * 0.02
+    q, s = R.quantize_int8(w, per_channel=True)
+    x = torch.randn(3, 64, generator=g)
+    y = R.int8_linear(x, q, s)
+    assert torch.allclose(y.double(), x.double() @ (q.double() * s.double()[:, None]).T, rtol=1e-5, atol=1e-7)
+    y2 = R.int8_linear(x, q, s * 2)
+    assert torch.allclose(y2, 2 * y, rtol=1e-6, atol=1e-7)
+
+
+def test_fp8_linear_is_decode_then_matmul_with_both_scales():
+    """y = (x8 * sx) @ (w8 * sw)^T + bias, the scales applied once each."""
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(4, 32, generator=g).to(torch.bfloat16)
+    w = (torch.randn(16, 32, generator=g) * 0.05).to(torch.bfloat16)
+    bias = torch.randn(16, generator=g).to(torch.bfloat16)
+    y = R.fp8_linear(x, w, bias)
+    x8, sx = R.fp8_quantize_tensor(x)
+    w8, sw = R.fp8_quantize_tensor(w)
+    core = (x8.double() * float(sx)) @ (w8.double() * float(sw)).T
+    assert torch.allclose(y.double(), (core.to(torch.bfloat16) + bias).double(), rtol=0, atol=0)
+    # and close to the unquantized product (e4m3 keeps ~3 bits)
+    assert torch.allclose(y.float(), (x.float() @ w.float().T + bias.float()), rtol=0.15, atol=0.15)
