@@ -24,6 +24,8 @@ Also reported:
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m M] [--no-gemm] [--no-cpu]
     python bench.py --summarize-profile DIR   # per-kernel, per-grid rocprofv3 kernel-trace table
+    python bench.py --counters                # short eager run for rocprofv3 --pmc passes
+    python bench.py --summarize-counters DIR [DIR ...]   # HBM bytes per launch from those passes
 """
 import argparse
 import csv
@@ -52,8 +54,10 @@ GEMM_M, GEMM_RANK, GEMM_ALPHA = 2048, 64, 16
 
 # HBM traffic of the roofline kernel per launch, measured with rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE and scaled by the same counters' reading for a copy
-# kernel of known size; keyed by (kernel, M, K, N).  None where not measured.
-MEASURED_TRAFFIC = {}
+# kernel of known size (factors 0.5 for FETCH_SIZE, 1.0 for WRITE_SIZE on a
+# 512 MiB device copy); keyed by (kernel, M, K, N).  None where not measured.
+MEASURED_TRAFFIC = {("nf4_gemv_kernel", 1, 4096, 14336): 33331494}
+COPY_BYTES = 512 << 20         # calibration copy: 512 MiB read + 512 MiB written
 
 
 def gemv_bytes(M, N, K, rank=RANK, scale_bytes=4):
@@ -246,6 +250,78 @@ def summarize_profile(path):
                       f"{sum(ds):>10.1f}")
 
 
+def run_counters(reps=4):
+    """Eager launches for counter collection: one plain device copy of
+    COPY_BYTES (calibration: its FETCH_SIZE / WRITE_SIZE readings against the
+    bytes it must move), then the roofline GEMV (M=1, K=4096, N=14336, no
+    LoRA) over the gate and up weights of six layer copies, `reps` rounds."""
+    import torch
+    from rocm_qlora import ops
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    src = torch.randint(0, 255, (COPY_BYTES,), dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    K, N = 4096, 14336
+    weights = []
+    for c in range(6):
+        layer = make_layer(dev, 1000 + c)
+        weights += [(layer[nm][0], layer[nm][1]) for nm in ("gate", "up")]
+        del layer
+    x = torch.randn(1, K, device=dev).to(torch.bfloat16)
+    for _ in range(reps):
+        for packed, absmax in weights:
+            ops.nf4_linear(x, packed, absmax, N, BLOCK)
+    torch.cuda.synchronize()
+    print(f"counters: copy {COPY_BYTES} B, {reps * len(weights)} nf4_gemv_kernel launches M=1 K={K} N={N}",
+          flush=True)
+
+
+def summarize_counters(paths):
+    """Per-kernel mean of each counter over the dispatches in rocprofv3 CSV
+    counter files (`-f csv`), and the GEMV's HBM bytes per launch: FETCH_SIZE
+    and WRITE_SIZE (KiB per dispatch) divided by what the same counter reads
+    per byte for the calibration copy."""
+    files = []
+    for p in paths:
+        files += glob.glob(os.path.join(p, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        sys.exit(f"no *counter_collection.csv under {paths}")
+    per = {}   # (kernel, counter) -> {dispatch: value}
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                key = (row["Kernel_Name"], row["Counter_Name"])
+                d = per.setdefault(key, {})
+                did = (f, row.get("Dispatch_Id", row.get("Correlation_Id")))
+                d[did] = d.get(did, 0.0) + float(row["Counter_Value"])
+    means = {}
+    for (kname, cname), d in per.items():
+        short = "copy" if "copy" in kname.lower() else ("nf4_gemv_kernel" if "nf4_gemv_kernel" in kname else None)
+        vals = list(d.values())
+        print(f"{_short(kname):<70} {cname:<12} n={len(vals):<4} mean={sum(vals) / len(vals):.1f}")
+        if short:
+            means.setdefault((short, cname), []).extend(vals)
+    M, K, N = 1, 4096, 14336
+    kb = kernel_bytes(M, N, K)
+    out = {}
+    for cname, expect in (("FETCH_SIZE", COPY_BYTES), ("WRITE_SIZE", COPY_BYTES)):
+        c = means.get(("copy", cname))
+        g = means.get(("nf4_gemv_kernel", cname))
+        if not c or not g:
+            continue
+        factor = (max(c) * 1024.0) / expect
+        gem = sum(g) / len(g) * 1024.0
+        out[cname] = gem / factor
+        print(f"{cname}: copy reads {max(c) * 1024.0 / 2**20:.1f} MiB for {expect / 2**20:.0f} MiB "
+              f"(factor {factor:.4f}); nf4_gemv_kernel {gem / 1e6:.3f} MB raw -> {gem / factor / 1e6:.3f} MB")
+    if len(out) == 2:
+        t = out["FETCH_SIZE"] + out["WRITE_SIZE"]
+        print(f"nf4_gemv_kernel M={M} K={K} N={N}: HBM traffic {t:.0f} B per launch "
+              f"(algorithmic {kb} B, ratio {t / kb:.3f})")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -255,9 +331,18 @@ def main():
     ap.add_argument("--no-gemm", action="store_true", help="skip the M=2048 GEMM section")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--summarize-profile", metavar="DIR", help="summarize a rocprofv3 CSV kernel trace and exit")
+    ap.add_argument("--counters", action="store_true", help="short eager run for rocprofv3 --pmc passes")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
+                    help="HBM bytes per launch from rocprofv3 --pmc CSV output and exit")
     args = ap.parse_args()
     if args.summarize_profile:
         summarize_profile(args.summarize_profile)
+        return
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
+        return
+    if args.counters:
+        run_counters()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path is built and measured on a single MI355X; "
