@@ -24,8 +24,16 @@ namespace rq {
 // Decode GEMV: y[M <= 16, N] = x[M, K] . W^T, W NF4 (block size a power of
 // two >= 64 dividing K, K % 64 == 0).
 //
-// HBM access: a "segment" is 256 k of a 16-row tile, 128 contiguous bytes per
-// row.  A wave reads it with two 1 KiB loads, 8 lanes x 16 B per row (full
+// Work units.  A tile is 16 rows of W; a segment is 256 k of a tile (128
+// contiguous code bytes per row); a unit (tile, segment) is 8 MFMA steps of
+// one wave.  Workgroup (g, s) of 16 waves owns tiles g, g + G, ..., g + (TS -
+// 1) G and the segments of K split s.  The host assigns the units to the
+// waves (a table in the kernel arguments; at most 4 units per wave) so that
+// every wave has work for any K: one segment per wave when K = 4096, several
+// tiles per wave for shorter K, several segments of one tile per wave for
+// longer K.
+//
+// HBM access of a unit: two 1 KiB loads, 8 lanes x 16 B per row (full
 // 128-byte lines; narrower per-row pieces cost HBM efficiency):
 //   load A: lane (n = l % 16, q = l / 16) reads row n % 8,     chunk q + 4 [n >= 8]
 //   load B: lane (n, q)                   reads row 8 + n % 8, chunk q + 4 [n < 8]
@@ -35,84 +43,192 @@ namespace rq {
 // layout (lane l = row l % 16, k group l / 16) with no LDS round trip.
 // Steps 0-3 take X1's dwords, steps 4-7 X2's; the activation operand (A,
 // rows = tokens, zero past M) uses the same k order.  Each dword of codes
-// becomes RND(T[code] * scale) through the LDS pair table.
+// becomes RND(T[code] * scale) through the LDS pair table.  Every address is
+// a per-lane constant plus a wave-uniform unit offset, so a unit's loads cost
+// a few adds.
 //
-// Grid (G, S), 1024 threads: workgroup (g, s) owns K split s (at most 16
-// segments; S > 1 only when K > 4096) and the NT <= 4 tiles g, g + G, ...,
-// g + (NT - 1) G.  The kernel is straight-line: every wave issues the loads
-// of all its tiles before it computes any (NT x 2 KiB per wave), and no
-// loaded value is carried around a loop, so the compiler's in-order load
-// counting is exact and each tile's math waits only for that tile's data.
-// Epilogue operands (the tiles' LoRA B rows, bias, RND(u)) are fetched before
-// the weights and staged in LDS once.  One barrier publishes the 16 wave
-// partials of every tile; they are summed in a fixed order (deterministic
-// results) and finished by one thread per output.
+// Schedule.  The code is straight-line: the units are unrolled, no load sits
+// under a branch and no loaded value is carried around a loop, so the
+// compiler's in-order load counting is exact and each unit waits only for
+// its own data.
+//   1. The activations: when M x K fits a 32 KiB stage, the workgroup reads
+//      x once (16-byte loads, at most two per thread) into LDS; otherwise each
+//      wave reads its own segment's operands (its units then share one
+//      segment).
+//   2. The first unit's weights and scales.
+//   3. The byte table (built from constants, no loads) and the activation
+//      stage; one barrier.
+//   4. The epilogue operands (the tiles' LoRA B rows, bias, RND(u) partials),
+//      kept as raw bits until the end.
+//   5. Per unit: issue the next unit's loads, then dequantize and multiply
+//      this one; the 16 x M partial goes to LDS, indexed by (tile, segment).
+//   6. The epilogue operands into LDS, one barrier; one thread per output sums
+//      its tile's segment partials in segment order (deterministic), adds the
+//      bias and the LoRA term, rounds and stores -- or writes the fp32 sum of
+//      its K split to the workspace for the split-K finisher.
 // ---------------------------------------------------------------------------
 constexpr int kGemvThreads = 1024;
 constexpr int kGemvWaves = kGemvThreads / 64;
 constexpr int kSegK = 256;
-constexpr int kGemvMaxNT = 4;          // tiles per workgroup
+constexpr int kGemvMaxU = 4;           // units per wave
+constexpr int kGemvMaxTS = 4;          // tiles per workgroup
 constexpr int kGemvMaxFusedRank = 64;  // LoRA rank the in-kernel epilogue stages
 constexpr int kGemvMaxUSplits = 16;
+constexpr int kGemvXStageBytes = 32 * 1024;
 constexpr int kGemvLutQwords = 256 * 32;  // 64 KiB: code byte -> fp32 (T[lo], T[hi]), 32 copies
+constexpr int kGemvLdsBudget = 160 * 1024 - kGemvLutQwords * 8;
+constexpr uint8_t kGemvNoUnit = 0xFF;
 // Word 3 of a raw (stride 0) buffer resource on gfx9-family GPUs, gfx950
 // included: 32-bit data, bounds checked against num_records.
 constexpr int kBufferRsrcWord3 = 0x00020000;
+// A buffer offset past every range this file builds: the load returns zero.
+constexpr uint32_t kOobOffset = 0xFFFFFFF0u;
 
 struct GemvArgs {
   const uint16_t* x;
-  int64_t ldx;
+  int ldx;                 // activation row stride (elements)
   const uint8_t* packed;
-  int64_t M, N, K;
-  int64_t blocks_per_row;  // K / block_size
+  int M, N, K;
+  int bpr;                 // scale blocks per row, K / block_size
   int bs_log2;             // log2(block_size)
-  int S;                   // K splits (gridDim.y)
+  int nseg;                // segments per K split
+  int TS;                  // tiles per workgroup
+  int xstage;              // activations staged in LDS
+  int kpad;                // LDS activation row pitch (elements, nseg * S * 256)
+  int xchunks;             // 16-byte activation chunks staged, M * kpad / 8
+  uint32_t xrow_magic;     // ceil(2^32 / (kpad / 8)): row of chunk c = mulhi(c, magic)
   bool direct;             // epilogue in this kernel (else fp32 partials to ws)
-  bool xvec;
+  bool xvec;               // x rows 16-byte aligned (vector loads)
   float* ws;               // [S, M, N] partials when !direct
+  uint8_t unit_t[kGemvWaves][kGemvMaxU];  // tile slot of unit u of wave w (kGemvNoUnit: none)
+  uint8_t unit_s[kGemvWaves][kGemvMaxU];  // segment (within the split) of unit u of wave w
 };
 
-// One tile's loads for one lane: loads A and B (raw code bits) and the
-// scales of chunks q and q + 4 of row n.
+__host__ __device__ inline int gemv_part_floats(int TS, int nseg, int M) { return TS * nseg * M * 16; }
+
+// Dynamic LDS of the GEMV (bytes): segment partials [TS][nseg][M][16], the
+// activation stage [M][kpad] (16-bit), RND(B) of the tiles' rows [TS * 16][64],
+// RND(bias) [TS * 16], RND(u) [M][64] (fp32).
+__host__ __device__ inline size_t gemv_lds_bytes(int TS, int nseg, int M, bool xstage, int kpad, bool lora) {
+  size_t b = size_t(gemv_part_floats(TS, nseg, M)) * 4;
+  if (xstage) b += size_t(M) * kpad * 2;
+  b += (lora ? size_t(TS) * 16 * kGemvMaxFusedRank * 4 : 0) + size_t(TS) * 16 * 4;
+  b += lora ? size_t(M) * kGemvMaxFusedRank * 4 : 0;
+  return b;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), kBufferRsrcWord3);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return uint32_t(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return uint32_t(__builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0));
+}
+// One element of a runtime float dtype (fp32 or 16-bit) as raw bits.
+__device__ __forceinline__ uint32_t buf_load_elem(__amdgpu_buffer_rsrc_t r, uint32_t idx, bool live, int dt) {
+  if (dt == RQ_DTYPE_F32) return buf_load4(r, live ? idx * 4u : kOobOffset);
+  return buf_load2(r, live ? idx * 2u : kOobOffset);
+}
+__device__ __forceinline__ float raw_elem_to_f32(uint32_t raw, int dt) {
+  return dt == RQ_DTYPE_F32 ? u2f(raw) : (dt == RQ_DTYPE_BF16 ? bf16_to_f32(uint16_t(raw)) : f16_to_f32(uint16_t(raw)));
+}
+
+// Per-unit scale loads through buffer resources: the scale of the block
+// holding k1 (steps 0-3) and k2 = k1 + 128 (steps 4-7) of the lane's row.
 template <class Scale>
-struct GemvTileLoads {
-  u32x4 a, b;
-  typename Scale::Raw s1, s2;
+struct GemvScale;
+
+template <int SDT>
+struct GemvScale<ScaleAbsmax<SDT>> {
+  typedef uint32_t Raw;
+  __amdgpu_buffer_rsrc_t r;
+  __device__ GemvScale(const ScaleAbsmax<SDT>& s, uint32_t nblocks) {
+    r = buffer_rsrc(s.p, nblocks * (SDT == RQ_DTYPE_F32 ? 4u : 2u));
+  }
+  __device__ __forceinline__ Raw load(uint32_t b, bool live) const {
+    if constexpr (SDT == RQ_DTYPE_F32) return buf_load4(r, live ? b * 4u : kOobOffset);
+    else return buf_load2(r, live ? b * 2u : kOobOffset);
+  }
+  __device__ __forceinline__ float value(Raw v) const {
+    if constexpr (SDT == RQ_DTYPE_F32) return u2f(v);
+    else if constexpr (SDT == RQ_DTYPE_BF16) return bf16_to_f32(uint16_t(v));
+    else return f16_to_f32(uint16_t(v));
+  }
 };
 
+template <int SDT>
+struct GemvScale<ScaleDQ<SDT>> {
+  struct Raw {
+    uint32_t code, hi;
+  };
+  __amdgpu_buffer_rsrc_t rc, rs;
+  int fmt, sh;
+  uint32_t bs2;
+  __device__ GemvScale(const ScaleDQ<SDT>& s, uint32_t nblocks) {
+    rc = buffer_rsrc(s.c2, nblocks);
+    const uint32_t ngroups = s.bs2_shift >= 0 ? ((nblocks + (1u << s.bs2_shift) - 1u) >> s.bs2_shift)
+                                              : uint32_t((int64_t(nblocks) + s.bs2 - 1) / s.bs2);
+    rs = buffer_rsrc(s.c2s, ngroups * (SDT == RQ_DTYPE_F32 ? 4u : 2u));
+    fmt = s.fmt;
+    sh = s.bs2_shift;
+    bs2 = uint32_t(s.bs2);
+  }
+  __device__ __forceinline__ Raw load(uint32_t b, bool live) const {
+    const uint32_t g = sh >= 0 ? (b >> sh) : b / bs2;
+    Raw v;
+    v.code = buf_load1(rc, live ? b : kOobOffset);
+    if constexpr (SDT == RQ_DTYPE_F32) v.hi = buf_load4(rs, live ? g * 4u : kOobOffset);
+    else v.hi = buf_load2(rs, live ? g * 2u : kOobOffset);
+    return v;
+  }
+  __device__ __forceinline__ float value(Raw v) const {
+    float hi;
+    if constexpr (SDT == RQ_DTYPE_F32) hi = u2f(v.hi);
+    else if constexpr (SDT == RQ_DTYPE_BF16) hi = bf16_to_f32(uint16_t(v.hi));
+    else hi = f16_to_f32(uint16_t(v.hi));
+    const uint8_t c = uint8_t(v.code);
+    const float lo = fmt == RQ_C2_FP8_E4M3FNUZ ? fnuz_to_f32(c) : __fdiv_rn(float(int8_t(c)), 127.0f);
+    return __fmul_rn(lo, hi);
+  }
+};
+
+// One unit's loads for one lane: loads A and B (raw code bits) and the
+// scales of steps 0-3 and 4-7.
+template <class Scale>
+struct GemvUnit {
+  u32x4 a, b;
+  typename GemvScale<Scale>::Raw s1, s2;
+};
+
+// Per-lane constants of the unit loads.
 struct GemvLane {
   int n16, q;
-  int64_t seg;  // this wave's segment
-  bool live;    // the wave has a segment of this split
+  uint32_t offA, offB;   // byte offset of loads A / B within a tile row block, segment 0
+  uint32_t sb1, sb2;     // scale block offset of k1 / k2 within segment 0 of the lane's row
 };
 
-// Loads of one tile for one lane.  The packed weights are read through a
-// buffer resource whose range is the weight matrix, so rows past N (a tile
-// past the end, or the rows of a last, partial tile) read as zero codes
-// without a bounds test, and chunks past K in a last, partial segment read
-// codes of the next row (or zeros) that meet zero activations.  Offsets are
-// 32-bit (the host keeps the packed weights under 2 GiB).  The loads are
-// issued on every path, branch-free, so each wave issues the same loads in
-// the same order and the compiler's in-order load counting stays exact.
 template <class Scale>
-__device__ __forceinline__ void gemv_issue_tile(GemvTileLoads<Scale>& L, const GemvArgs& a, const Scale& scale,
-                                                __amdgpu_buffer_rsrc_t wres, uint32_t tile, const GemvLane& w) {
-  const uint32_t half_k = uint32_t(a.K >> 1);
-  const uint32_t r0 = tile * 16u, n7 = uint32_t(w.n16 & 7);
-  const uint32_t cA = uint32_t(w.q) + (w.n16 >= 8 ? 4u : 0u), cB = uint32_t(w.q) + (w.n16 < 8 ? 4u : 0u);
-  const uint32_t sb = uint32_t(w.seg) * (kSegK / 2);
-  L.a = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wres, (r0 + n7) * half_k + sb + 16u * cA, 0, 0));
-  L.b = __builtin_bit_cast(u32x4,
-                           __builtin_amdgcn_raw_buffer_load_b128(wres, (r0 + 8u + n7) * half_k + sb + 16u * cB, 0, 0));
-  uint32_t srow = r0 + uint32_t(w.n16);
-  srow = srow < uint32_t(a.N) ? srow : uint32_t(a.N) - 1u;
-  const uint32_t kmax = uint32_t(a.K) - 1u;
-  uint32_t k1 = uint32_t(w.seg) * kSegK + 32u * uint32_t(w.q), k2 = k1 + 128u;
-  k1 = k1 < kmax ? k1 : kmax;
-  k2 = k2 < kmax ? k2 : kmax;
-  const uint32_t sr = srow * uint32_t(a.blocks_per_row);
-  L.s1 = scale.load(int64_t(sr + (k1 >> a.bs_log2)));
-  L.s2 = scale.load(int64_t(sr + (k2 >> a.bs_log2)));
+__device__ __forceinline__ void gemv_issue(GemvUnit<Scale>& U, const GemvArgs& a, const GemvScale<Scale>& sc,
+                                           __amdgpu_buffer_rsrc_t wres, const GemvLane& ln, uint32_t tile,
+                                           uint32_t seg, bool live) {
+  const uint32_t half_k = uint32_t(a.K) >> 1;
+  const uint32_t base = tile * 16u * half_k + seg * (kSegK / 2);
+  U.a = buf_load16(wres, live ? base + ln.offA : kOobOffset);
+  U.b = buf_load16(wres, live ? base + ln.offB : kOobOffset);
+  // scale block of k = seg * 256 + c (c < 256): (seg * 256 + c) >> bs_log2
+  const uint32_t row = tile * 16u + uint32_t(ln.n16);
+  const uint32_t sseg = a.bs_log2 <= 8 ? (seg << (8 - a.bs_log2)) : (seg >> (a.bs_log2 - 8));
+  const uint32_t b0 = row * uint32_t(a.bpr) + sseg;
+  U.s1 = sc.load(b0 + ln.sb1, live);
+  U.s2 = sc.load(b0 + ln.sb2, live);
 }
 
 __device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
@@ -120,13 +236,13 @@ __device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
 }
 
 template <int XT, class Scale>
-__device__ __forceinline__ f32x4 gemv_tile(const GemvTileLoads<Scale>& L, const Scale& scale, const u32x4 (&xa)[8],
-                                           const u32x2* lut, uint32_t lane_off, int n16) {
+__device__ __forceinline__ f32x4 gemv_tile(const GemvUnit<Scale>& U, const GemvScale<Scale>& sc,
+                                           const u32x4 (&xa)[8], const u32x2* lut, uint32_t lane_off, int n16) {
   const bool lo = n16 < 8;
-  const u32x4 X1 = lo ? L.a : L.b;
-  const u32x4 Y = lo ? L.b : L.a;
+  const u32x4 X1 = lo ? U.a : U.b;
+  const u32x4 Y = lo ? U.b : U.a;
   const u32x4 X2 = u32x4{row_ror8(Y.x), row_ror8(Y.y), row_ror8(Y.z), row_ror8(Y.w)};
-  const float s1 = scale.value(L.s1), s2 = scale.value(L.s2);
+  const float s1 = sc.value(U.s1), s2 = sc.value(U.s2);
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   acc = mfma16x16x32<XT>(xa[0], expand8_scaled<XT>(lut, X1.x, lane_off, s1), acc);
   acc = mfma16x16x32<XT>(xa[1], expand8_scaled<XT>(lut, X1.y, lane_off, s1), acc);
@@ -139,180 +255,228 @@ __device__ __forceinline__ f32x4 gemv_tile(const GemvTileLoads<Scale>& L, const 
   return acc;
 }
 
-// The code book as fp32 bits (for the table fill).
-__device__ const uint32_t kNF4BitsDev[16] = {
-    kNF4Bits[0], kNF4Bits[1], kNF4Bits[2],  kNF4Bits[3],  kNF4Bits[4],  kNF4Bits[5],  kNF4Bits[6],  kNF4Bits[7],
-    kNF4Bits[8], kNF4Bits[9], kNF4Bits[10], kNF4Bits[11], kNF4Bits[12], kNF4Bits[13], kNF4Bits[14], kNF4Bits[15]};
-
-// Fill of the fp32 pair table by 1024 threads: entry e (a code byte) holds
-// (T[e & 15], T[e >> 4]); copy c at qword e * 32 + c (lane l reads copy
-// l % 32: a ds_read_b64 serves 32 lanes per cycle, which hit 32 distinct
-// bank pairs).  Thread t writes copies 8 (t % 4) .. + 7 of entry t / 4.
-__device__ __forceinline__ void fill_gemv_lut(u32x2* lut, uint32_t t_even, uint32_t t_odd, int tid) {
-  u32x4* dst = reinterpret_cast<u32x4*>(lut + (tid >> 2) * 32 + 8 * (tid & 3));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) dst[i] = u32x4{t_even, t_odd, t_even, t_odd};
-}
-
 // Workgroup barrier for LDS only: this wave's LDS accesses are complete,
 // then s_barrier.  (__syncthreads() may also wait for every outstanding
-// global load, which would serialize the prefetched tiles.)
+// global load, which would serialize the prefetched units.)
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Dynamic LDS of the GEMV: wave partials [NT][16 waves][M][16], RND(B) of the
-// tiles' rows [NT * 16][64], RND(bias) [NT * 16], RND(u) [M][64] (fp32).
-__host__ __device__ inline size_t gemv_lds_floats(int nt, int64_t M, bool lora) {
-  return size_t(nt) * kGemvWaves * M * 16 + (lora ? size_t(nt) * 16 * kGemvMaxFusedRank : 0) + size_t(nt) * 16 +
-         (lora ? size_t(M) * kGemvMaxFusedRank : 0);
-}
-
-template <int XT, class Scale, int NT>
-__global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(GemvArgs a, Scale scale, LinearEpi e) {
+template <int XT, class Scale, int U>
+__global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
+void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   // The table is the kernel's only static LDS array, so it sits at address
   // 0 and every lookup's base folds into the instruction's offset field.
   __shared__ u32x2 lut[kGemvLutQwords];
   extern __shared__ uint32_t smem[];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int M = int(a.M);
+  const int M = a.M, TS = a.TS, nseg = a.nseg;
   const int rank = (a.direct && e.rank > 0) ? e.rank : 0;  // LoRA staging only when fused here
   constexpr int RP = kGemvMaxFusedRank;                    // staging pitch
   float* part = reinterpret_cast<float*>(smem);
-  float* lbs = part + NT * kGemvWaves * M * 16;
-  float* bss = lbs + (rank > 0 ? NT * 16 * RP : 0);
-  float* us = bss + NT * 16;
+  uint16_t* xs = reinterpret_cast<uint16_t*>(part + gemv_part_floats(TS, nseg, M));
+  float* lbs = reinterpret_cast<float*>(xs + (a.xstage ? M * a.kpad : 0));
+  float* bss = lbs + (rank > 0 ? TS * 16 * RP : 0);
+  float* us = bss + TS * 16;
 
-  GemvLane w;
-  w.n16 = lane & 15;
-  w.q = lane >> 4;
-  const int s = blockIdx.y;
-  const int64_t nsegs = (a.K + kSegK - 1) / kSegK;
-  const int64_t sg0 = (nsegs * s) / a.S, sg1 = (nsegs * (s + 1)) / a.S;
-  w.live = sg0 + wave < sg1;
-  w.seg = w.live ? sg0 + wave : sg0;  // a wave without a segment re-reads one; its activations are zero
+  GemvLane ln;
+  ln.n16 = lane & 15;
+  ln.q = lane >> 4;
+  {
+    const uint32_t half_k = uint32_t(a.K) >> 1, n7 = uint32_t(ln.n16 & 7);
+    const uint32_t cA = uint32_t(ln.q) + (ln.n16 >= 8 ? 4u : 0u), cB = uint32_t(ln.q) + (ln.n16 < 8 ? 4u : 0u);
+    ln.offA = n7 * half_k + 16u * cA;
+    ln.offB = (8u + n7) * half_k + 16u * cB;
+    // block offsets of k1 = 32 q and k2 = 128 + 32 q within a segment (zero
+    // when a block spans whole segments)
+    ln.sb1 = a.bs_log2 <= 8 ? (32u * uint32_t(ln.q)) >> a.bs_log2 : 0u;
+    ln.sb2 = a.bs_log2 <= 8 ? (128u + 32u * uint32_t(ln.q)) >> a.bs_log2 : 0u;
+  }
+  const uint32_t seg0 = blockIdx.y * uint32_t(nseg);  // first segment of this K split
   const uint32_t n_tiles = uint32_t((a.N + 15) / 16);
-  // tiles g, g + G, g + 2G, ...: at any moment the workgroups' loads are
-  // spread over the whole weight matrix
-  auto tile_idx = [&](int t) -> uint32_t { return blockIdx.x + uint32_t(t) * gridDim.x; };
-  const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<uint8_t*>(a.packed), 0, int(uint32_t(a.N) * uint32_t(a.K >> 1)), kBufferRsrcWord3);
+  // tiles g, g + G, ...: at any moment the workgroups' loads are spread over
+  // the whole weight matrix
+  auto tile_of = [&](int t) -> uint32_t { return blockIdx.x + uint32_t(t) * gridDim.x; };
+  const __amdgpu_buffer_rsrc_t wres = buffer_rsrc(a.packed, uint32_t(a.N) * (uint32_t(a.K) >> 1));
+  const GemvScale<Scale> sc(scale_src, uint32_t(a.N) * uint32_t(a.bpr));
+  // this wave's units (wave-uniform; one dword of the table per wave, the
+  // host writes segment 0 for a missing unit)
+  const uint32_t tword = reinterpret_cast<const uint32_t*>(&a.unit_t[0][0])[wave];
+  const uint32_t sword = reinterpret_cast<const uint32_t*>(&a.unit_s[0][0])[wave];
+  int ut[U], useg[U];
+  bool ulive[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = int((tword >> (8 * u)) & 0xFFu);
+    ulive[u] = t != kGemvNoUnit;
+    ut[u] = ulive[u] ? t : 0;
+    useg[u] = int((sword >> (8 * u)) & 0xFFu);
+  }
+  const __amdgpu_buffer_rsrc_t xres =
+      buffer_rsrc(a.x, uint32_t(M - 1) * uint32_t(a.ldx) * 2u + uint32_t(a.K) * 2u);
 
-  // 1. Loads the weights do not depend on, issued first so that staging them
-  //    waits only for them: the table entry this thread writes, the tiles'
-  //    LoRA B values (value i of thread t is row t / 64 + 16 i, rank t % 64
-  //    of the [NT * 16][64] staging block), the bias, the RND(u) partials
-  //    (waves m < M) and the activation operands.
-  const uint32_t t_even = kNF4BitsDev[(tid >> 2) & 15], t_odd = kNF4BitsDev[tid >> 6];
-  Raw16x2 lbr[NT];
+  // 1. activations into the LDS stage (chunk c = 8 consecutive k of one row)
+  u32x4 xst[2];
+  if (a.xstage) {
+    const uint32_t cpr = uint32_t(a.kpad) >> 3;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t c = uint32_t(tid) + 1024u * uint32_t(i);
+      const uint32_t m = __umulhi(c, a.xrow_magic);
+      const uint32_t k = 8u * (c - m * cpr);
+      const bool live = c < uint32_t(a.xchunks) && k < uint32_t(a.K);
+      xst[i] = buf_load16(xres, live ? (m * uint32_t(a.ldx) + k) * 2u : kOobOffset);
+    }
+  }
+
+  // 2. the first unit's weights and scales
+  GemvUnit<Scale> L[U];
+  gemv_issue(L[0], a, sc, wres, ln, tile_of(ut[0]), seg0 + uint32_t(useg[0]), ulive[0]);
+
+  // 1'. without the stage, this wave's own activation operands (its units
+  //     share one segment): step c covers k = seg * 256 + 128 (c / 4) + 32 q +
+  //     8 (c % 4) of token n16; a token past M or a k past K reads zeros
+  u32x4 xa[8];
+  if (!a.xstage) {
+    const uint32_t sg = seg0 + uint32_t(useg[0]);
+    const bool mlive = ln.n16 < M && ulive[0];
+    if (a.xvec) {
+      const uint32_t xrow = uint32_t(ln.n16) * uint32_t(a.ldx) * 2u;
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t k = sg * kSegK + 128u * (c >> 2) + 32u * uint32_t(ln.q) + 8u * (c & 3);
+        xa[c] = buf_load16(xres, (mlive && k < uint32_t(a.K)) ? xrow + 2u * k : kOobOffset);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const uint32_t k = sg * kSegK + 128u * (c >> 2) + 32u * uint32_t(ln.q) + 8u * (c & 3);
+        const bool live = mlive && k < uint32_t(a.K);
+        const uint32_t base = (uint32_t(ln.n16 < M ? ln.n16 : 0) * uint32_t(a.ldx) + (live ? k : 0u)) * 2u;
+        uint32_t w[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          w[h] = buf_load2(xres, live ? base + 4u * h : kOobOffset) |
+                 (buf_load2(xres, live ? base + 4u * h + 2u : kOobOffset) << 16);
+        xa[c] = u32x4{w[0], w[1], w[2], w[3]};
+      }
+    }
+  }
+
+  // 3. the table and the activation stage
+  fill_f32pair_lut<kGemvThreads>(lut, tid);
+  if (a.xstage) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t c = uint32_t(tid) + 1024u * uint32_t(i);
+      if (c < uint32_t(a.xchunks)) *reinterpret_cast<u32x4*>(xs + 8u * c) = xst[i];
+    }
+  }
+  lds_barrier();
+
+  // 4. epilogue operands, raw: LoRA B values (value t of thread tid is row
+  //    tid / 64 of tile slot t, rank tid % 64), the bias, the RND(u) partials
+  //    (waves m < M)
+  uint32_t lbr[kGemvMaxTS], br = 0u, up[kGemvMaxUSplits];
+#pragma unroll
+  for (int t = 0; t < kGemvMaxTS; ++t) lbr[t] = 0u;
+#pragma unroll
+  for (int k = 0; k < kGemvMaxUSplits; ++k) up[k] = 0u;
   const int lj = tid & (RP - 1);
   if (rank > 0) {
+    const __amdgpu_buffer_rsrc_t bres = buffer_rsrc(e.lora_b, uint32_t(a.N) * uint32_t(e.ld_lora_b) *
+                                                                   (e.lora_dt == RQ_DTYPE_F32 ? 4u : 2u));
 #pragma unroll
-    for (int i = 0; i < NT; ++i) {
-      const int rr = (tid >> 6) + 16 * i;
-      uint32_t bn = tile_idx(rr >> 4) * 16u + uint32_t(rr & 15);
-      bn = bn < uint32_t(a.N) ? bn : uint32_t(a.N) - 1u;
-      const int j = lj < rank ? lj : 0;
-      lbr[i] = load_raw(e.lora_b, int64_t(bn) * e.ld_lora_b + j, e.lora_dt);
+    for (int t = 0; t < kGemvMaxTS; ++t) {
+      const uint32_t bn = tile_of(t) * 16u + uint32_t(tid >> 6);
+      const bool live = t < TS && lj < rank && bn < uint32_t(a.N);
+      lbr[t] = buf_load_elem(bres, bn * uint32_t(e.ld_lora_b) + uint32_t(lj), live, e.lora_dt);
     }
   }
   const bool has_bias = a.direct && e.bias != nullptr;
-  Raw16x2 br;
   if (has_bias) {
-    const int cb = tid & (NT * 16 - 1);
-    uint32_t cn = tile_idx(cb >> 4) * 16u + uint32_t(cb & 15);
-    cn = cn < uint32_t(a.N) ? cn : uint32_t(a.N) - 1u;
-    br = load_raw(e.bias, int64_t(cn), e.bias_dt);
+    const __amdgpu_buffer_rsrc_t bres = buffer_rsrc(e.bias, uint32_t(a.N) * (e.bias_dt == RQ_DTYPE_F32 ? 4u : 2u));
+    const int cb = tid & (kGemvMaxTS * 16 - 1);
+    const uint32_t cn = tile_of(cb >> 4) * 16u + uint32_t(cb & 15);
+    br = buf_load_elem(bres, cn, (cb >> 4) < TS && cn < uint32_t(a.N), e.bias_dt);
   }
-  float up[kGemvMaxUSplits];
-  const int um = wave;  // RND(u) row m is staged by wave m
-  const bool stage_u = rank > 0 && um < M;
+  const bool stage_u = rank > 0 && wave < M;
   if (stage_u) {
-    const uint32_t u_idx = uint32_t(um * rank + (lj < rank ? lj : 0));
-    const uint32_t u_stride = uint32_t(M * rank);
-    const int ns = e.u_splits;
+    const uint32_t ns = uint32_t(e.u_splits), stride = uint32_t(M) * uint32_t(rank);
+    const __amdgpu_buffer_rsrc_t ures = buffer_rsrc(e.u, ns * stride * 4u);
+    const uint32_t u_idx = uint32_t(wave) * uint32_t(rank) + uint32_t(lj);
 #pragma unroll
-    for (int k = 0; k < kGemvMaxUSplits; ++k) up[k] = e.u[(k < ns ? uint32_t(k) : 0u) * u_stride + u_idx];
+    for (int k = 0; k < kGemvMaxUSplits; ++k)
+      up[k] = buf_load4(ures, (uint32_t(k) < ns && lj < rank) ? (uint32_t(k) * stride + u_idx) * 4u : kOobOffset);
   }
-  // activations: step c covers x[token][seg * 256 + 128 (c / 4) + 32 q + 8
-  // (c % 4) ...]; a token past M, a k past K and a wave without a segment
-  // read zeros
-  u32x4 xa[8];
-  const bool mlive = w.n16 < M && w.live;
-  if (a.xvec) {
-    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(a.x), 0, int(uint32_t(M - 1) * uint32_t(a.ldx) * 2u + uint32_t(a.K) * 2u),
-        kBufferRsrcWord3);
-    const uint32_t xrow = uint32_t(w.n16) * uint32_t(a.ldx) * 2u;
+
+  // 5. the units, each as soon as its loads have landed; partials to LDS
+  const uint32_t lane_off = uint32_t(lane & 31) * 8u;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const uint32_t k = uint32_t(w.seg) * kSegK + 128u * (c >> 2) + 32u * uint32_t(w.q) + 8u * (c & 3);
-      const uint32_t off = (mlive && k < uint32_t(a.K)) ? xrow + 2u * k : 0xFFFFFFF0u;
-      xa[c] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xres, off, 0, 0));
-    }
-  } else {
-    const uint16_t* xrow = a.x + (w.n16 < M ? w.n16 : 0) * a.ldx;
+  for (int u = 0; u < U; ++u) {
+    if (u + 1 < U) gemv_issue(L[u + 1], a, sc, wres, ln, tile_of(ut[u + 1]), seg0 + uint32_t(useg[u + 1]), ulive[u + 1]);
+    if (ulive[u]) {
+      if (a.xstage) {
+        if (ln.n16 < M) {
+          const uint16_t* xrow = xs + ln.n16 * a.kpad + (seg0 + uint32_t(useg[u])) * kSegK + 32 * ln.q;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      int64_t k = w.seg * kSegK + 128 * (c >> 2) + 32 * w.q + 8 * (c & 3);
-      const bool live = mlive && k < a.K;
-      k = k < a.K ? k : 0;
-      const u32x4 v = load_x8(xrow + k, false);
-      xa[c] = live ? v : u32x4{0u, 0u, 0u, 0u};
+          for (int c = 0; c < 8; ++c) xa[c] = *reinterpret_cast<const u32x4*>(xrow + 128 * (c >> 2) + 8 * (c & 3));
+        } else {
+#pragma unroll
+          for (int c = 0; c < 8; ++c) xa[c] = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+      const f32x4 acc = gemv_tile<XT>(L[u], sc, xa, lut, lane_off, ln.n16);
+      float* pp = part + (ut[u] * nseg + useg[u]) * M * 16 + ln.n16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 4 * ln.q + r;
+        if (m < M) pp[m * 16] = acc[r];
+      }
     }
   }
 
-  // 2. every tile's weights and scales
-  GemvTileLoads<Scale> buf[NT];
+  // 6. epilogue operands into LDS, then one thread per output (tile slot
+  //    t = tid / 256, row m, column nn).  The empty asm marks the raw values
+  //    as changed here, so that no use of them (which waits for its load)
+  //    is scheduled into the unit loop above.
 #pragma unroll
-  for (int t = 0; t < NT; ++t) gemv_issue_tile(buf[t], a, scale, wres, tile_idx(t), w);
-
-  // 3. the table and the epilogue operands into LDS (these wait for the
-  //    loads of step 1 only)
-  fill_gemv_lut(lut, t_even, t_odd, tid);
+  for (int t = 0; t < kGemvMaxTS; ++t) asm volatile("" : "+v"(lbr[t]));
+  asm volatile("" : "+v"(br));
+#pragma unroll
+  for (int k = 0; k < kGemvMaxUSplits; ++k) asm volatile("" : "+v"(up[k]));
   if (rank > 0) {
 #pragma unroll
-    for (int i = 0; i < NT; ++i)
-      lbs[tid + 1024 * i] = lj < rank ? round_x<XT>(raw_to_f32(lbr[i], e.lora_dt)) : 0.0f;
+    for (int t = 0; t < kGemvMaxTS; ++t)
+      if (t < TS) lbs[tid + 1024 * t] = lj < rank ? round_x<XT>(raw_elem_to_f32(lbr[t], e.lora_dt)) : 0.0f;
   }
-  if (a.direct && tid < NT * 16) bss[tid] = has_bias ? round_x<XT>(raw_to_f32(br, e.bias_dt)) : 0.0f;
+  if (a.direct && tid < TS * 16) bss[tid] = has_bias ? round_x<XT>(raw_elem_to_f32(br, e.bias_dt)) : 0.0f;
   if (stage_u) {
     float sum = 0.0f;
 #pragma unroll
     for (int k = 0; k < kGemvMaxUSplits; ++k)
-      if (k < e.u_splits) sum = __fadd_rn(sum, up[k]);
+      if (k < e.u_splits) sum = __fadd_rn(sum, u2f(up[k]));
     us[tid] = lj < rank ? round_x<XT>(sum) : 0.0f;
   }
   lds_barrier();
 
-  // 4. the tiles, each as soon as its loads have landed; partials to LDS
-  const uint32_t lane_off = uint32_t(lane & 31) * 8u;
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const f32x4 acc = gemv_tile<XT>(buf[t], scale, xa, lut, lane_off, w.n16);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 4 * w.q + r;
-      if (m < M) part[((t * kGemvWaves + wave) * M + m) * 16 + w.n16] = acc[r];
-    }
-  }
-  lds_barrier();
-
-  // 5. one thread per output (tile t = tid / 256, row m, column nn): the 16 wave
-  //    partials in wave order, then bias, LoRA, rounding -- or the fp32 sum
-  //    to the split-K workspace
   const int t = tid >> 8, m = (tid >> 4) & 15, nn = tid & 15;
-  if (t >= NT || m >= M) return;
-  const uint32_t tile = tile_idx(t);
+  if (t >= TS || m >= M) return;
+  const uint32_t tile = tile_of(t);
   const int64_t n = int64_t(tile) * 16 + nn;
   if (tile >= n_tiles || n >= a.N) return;
-  float p[kGemvWaves];
-#pragma unroll
-  for (int ww = 0; ww < kGemvWaves; ++ww) p[ww] = part[((t * kGemvWaves + ww) * M + m) * 16 + nn];
+  const float* pp = part + t * nseg * M * 16 + m * 16 + nn;
   float v = 0.0f;
+  int sgi = 0;
+  for (; sgi + 8 <= nseg; sgi += 8) {
+    float p[8];
 #pragma unroll
-  for (int ww = 0; ww < kGemvWaves; ++ww) v = __fadd_rn(v, p[ww]);
+    for (int j = 0; j < 8; ++j) p[j] = pp[(sgi + j) * M * 16];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v = __fadd_rn(v, p[j]);
+  }
+  for (; sgi < nseg; ++sgi) v = __fadd_rn(v, pp[sgi * M * 16]);
   if (!a.direct) {
-    a.ws[(int64_t(s) * a.M + m) * a.N + n] = v;
+    a.ws[(int64_t(blockIdx.y) * a.M + m) * a.N + n] = v;
     return;
   }
   if (e.bias) v = __fadd_rn(v, bss[t * 16 + nn]);
@@ -336,6 +500,7 @@ __global__ __launch_bounds__(kGemvThreads) void nf4_gemv_kernel(GemvArgs a, Scal
   }
   static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
 }
+
 
 // Split-K finisher (and the LoRA epilogue for any M): y = finish(sum_s
 // ws[s]).  Workgroup = 256 columns x 16 activation rows; B values are read 8
@@ -450,34 +615,85 @@ __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus) {
+// Work plan of the GEMV: K splits, tiles per workgroup, units per wave, the
+// unit table, the activation stage, and the workspace layout.
+GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool xvec) {
   GemvPlan p{};
-  const int64_t nsegs = (K + kSegK - 1) / kSegK;
+  const int nsegs = int((K + kSegK - 1) / kSegK);
   const int64_t tiles = (N + 15) / 16;
-  p.nw = kGemvWaves;
-  p.RT = 1;
-  // one segment per wave: K splits only past 16 segments (K > 4096)
-  const int S = int((nsegs + kGemvWaves - 1) / kGemvWaves);
-  p.S = S;
-  // tiles per workgroup: enough that one round of workgroups covers the
-  // chip's compute units, at most kGemvMaxNT
-  int64_t nt = (tiles * S + cus - 1) / (cus > 0 ? cus : 1);
-  nt = nt < 1 ? 1 : (nt > kGemvMaxNT ? kGemvMaxNT : nt);
-  p.NT = nt > 2 ? 4 : int(nt);
-  p.grid = int((tiles + p.NT - 1) / p.NT);
+  const int64_t ncu = cus > 0 ? cus : 1;
   p.u_splits = 0;
   if (rank > 0) {
     const int64_t steps_per_wg = 4 * kLoraUStepsPerWave;
-    p.u_splits = int((K / 32 + steps_per_wg - 1) / steps_per_wg);
+    const int64_t ks = (K / 32 + steps_per_wg - 1) / steps_per_wg;
+    p.u_splits = int(ks < kGemvMaxUSplits ? ks : kGemvMaxUSplits);
   }
-  // the fused epilogue stages the tiles' B rows (rank <= 64), <= 16 u splits
-  p.direct = S == 1 && rank <= kGemvMaxFusedRank && p.u_splits <= kGemvMaxUSplits;
-  p.lds_bytes = gemv_lds_floats(p.NT, M, p.direct && rank > 0) * 4;  // dynamic part (the 64 KiB table is static)
-  p.ws_bytes = p.direct ? 0 : size_t(S) * M * N * 4;
+  const bool lora_fusable = rank <= kGemvMaxFusedRank;
+  for (int stage = 1; stage >= 0; --stage) {
+    const bool xstage = stage != 0;
+    if (xstage && !xvec) continue;
+    // segments one workgroup covers: 4 per wave with the stage, else one
+    const int max_nseg = xstage ? kGemvWaves * kGemvMaxU : kGemvWaves;
+    const int S = (nsegs + max_nseg - 1) / max_nseg;
+    const int nseg = (nsegs + S - 1) / S;
+    if (xstage && M * int64_t(nseg) * S * kSegK * 2 > kGemvXStageBytes) continue;
+    const int R = kGemvWaves / nseg;  // tile slots per round without the stage
+    const int ts_cap = xstage ? (kGemvWaves * kGemvMaxU) / nseg : kGemvMaxU * R;
+    const bool direct = S == 1 && lora_fusable;
+    int best = 0;
+    int64_t best_cost = 0;
+    for (int TS = 1; TS <= kGemvMaxTS && TS <= ts_cap; ++TS) {
+      const int U = xstage ? (TS * nseg + kGemvWaves - 1) / kGemvWaves : (TS + R - 1) / R;
+      if (U != 1 && U != 2 && U != 4) continue;
+      const int kpad = nseg * S * kSegK;
+      if (gemv_lds_bytes(TS, nseg, int(M), xstage, kpad, direct && rank > 0) > size_t(kGemvLdsBudget)) continue;
+      // tiles a compute unit works through one after another
+      const int64_t grid = (tiles + TS - 1) / TS;
+      const int64_t cost = ((grid * S + ncu - 1) / ncu) * TS;
+      if (best == 0 || cost <= best_cost) {
+        best = TS;
+        best_cost = cost;
+      }
+    }
+    if (best == 0) continue;
+    p.S = S;
+    p.nseg = nseg;
+    p.TS = best;
+    p.xstage = xstage;
+    p.kpad = nseg * S * kSegK;
+    p.U = xstage ? (best * nseg + kGemvWaves - 1) / kGemvWaves : (best + R - 1) / R;
+    p.grid = int((tiles + best - 1) / best);
+    p.direct = direct;
+    for (int w = 0; w < kGemvWaves; ++w)
+      for (int u = 0; u < kGemvMaxU; ++u) {
+        p.unit_t[w][u] = kGemvNoUnit;
+        p.unit_s[w][u] = 0;
+        if (u >= p.U) continue;
+        if (xstage) {
+          const int i = w + kGemvWaves * u;
+          if (i < best * nseg) {
+            p.unit_t[w][u] = uint8_t(i / nseg);
+            p.unit_s[w][u] = uint8_t(i % nseg);
+          }
+        } else if (w < R * nseg) {
+          const int t = w / nseg + u * R;
+          if (t < best) {
+            p.unit_t[w][u] = uint8_t(t);
+            p.unit_s[w][u] = uint8_t(w % nseg);
+          }
+        }
+      }
+    break;
+  }
+  p.lds_bytes = gemv_lds_bytes(p.TS, p.nseg, int(M), p.xstage, p.kpad, p.direct && rank > 0);
+  p.ws_bytes = p.direct ? 0 : size_t(p.S) * M * N * 4;
   p.u_offset = (p.ws_bytes + 255) & ~size_t(255);
   if (rank > 0) p.ws_bytes = p.u_offset + size_t(p.u_splits) * M * rank * 4;
   return p;
 }
+
+// x rows 16-byte aligned: the GEMV reads activations with 16-byte loads.
+static bool gemv_xvec(const LinearArgs& L) { return aligned(L.x, 16) && L.ldx % 8 == 0; }
 
 template <int XT>
 static int launch_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream) {
@@ -489,14 +705,13 @@ static int launch_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t str
   return rq_check_launch();
 }
 
-template <int XT, class Scale, int NT>
-static int launch_gemv_nt(const GemvArgs& a, GemvPlan p, Scale scale, const LinearEpi& e, hipStream_t stream) {
-  p.grid = int(((a.N + 15) / 16 + NT - 1) / NT);
-  auto kern = nf4_gemv_kernel<XT, Scale, NT>;
+template <int XT, class Scale, int U>
+static int launch_gemv_u(const GemvArgs& a, const GemvPlan& p, Scale scale, const LinearEpi& e, hipStream_t stream) {
+  auto kern = nf4_gemv_kernel<XT, Scale, U>;
   static bool attr_set = false;  // one flag per instantiation
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            160 * 1024 - kGemvLutQwords * 8) != hipSuccess)
+                            kGemvLdsBudget) != hipSuccess)
       return RQ_ERR_HIP;
     attr_set = true;
   }
@@ -508,27 +723,34 @@ static int launch_gemv_nt(const GemvArgs& a, GemvPlan p, Scale scale, const Line
 template <int XT, class Scale>
 static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, const LinearEpi& e,
                          float* ws, hipStream_t stream) {
-  GemvArgs a;
+  GemvArgs a{};
   a.x = static_cast<const uint16_t*>(L.x);
-  a.ldx = L.ldx;
+  a.ldx = int(L.ldx);
   a.packed = L.w_packed;
-  a.M = L.M;
-  a.N = L.N;
-  a.K = L.K;
-  a.blocks_per_row = L.K / L.block_size;
+  a.M = int(L.M);
+  a.N = int(L.N);
+  a.K = int(L.K);
+  a.bpr = int(L.K / L.block_size);
   a.bs_log2 = pow2_shift(L.block_size);
-  a.S = p.S;
+  a.nseg = p.nseg;
+  a.TS = p.TS;
+  a.xstage = p.xstage ? 1 : 0;
+  a.kpad = p.kpad;
+  const uint32_t cpr = uint32_t(p.kpad / 8);
+  a.xchunks = int(L.M * p.kpad / 8);
+  a.xrow_magic = uint32_t(((uint64_t(1) << 32) + cpr - 1) / cpr);
   a.direct = p.direct;
-  a.xvec = aligned(L.x, 16) && (L.ldx % 8 == 0);
+  a.xvec = gemv_xvec(L);
   a.ws = ws;
-  // double quantization keeps two loads per scale: at most 2 tiles per
-  // workgroup stay within the registers
-  if (p.NT == 1) return launch_gemv_nt<XT, Scale, 1>(a, p, scale, e, stream);
-  if constexpr (Scale::kLoads > 1) {
-    return launch_gemv_nt<XT, Scale, 2>(a, p, scale, e, stream);
-  } else {
-    if (p.NT == 2) return launch_gemv_nt<XT, Scale, 2>(a, p, scale, e, stream);
-    return launch_gemv_nt<XT, Scale, 4>(a, p, scale, e, stream);
+  for (int w = 0; w < kGemvWaves; ++w)
+    for (int u = 0; u < kGemvMaxU; ++u) {
+      a.unit_t[w][u] = p.unit_t[w][u];
+      a.unit_s[w][u] = p.unit_s[w][u];
+    }
+  switch (p.U) {
+    case 1: return launch_gemv_u<XT, Scale, 1>(a, p, scale, e, stream);
+    case 2: return launch_gemv_u<XT, Scale, 2>(a, p, scale, e, stream);
+    default: return launch_gemv_u<XT, Scale, 4>(a, p, scale, e, stream);
   }
 }
 
@@ -605,15 +827,21 @@ int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream) {
 }
 
 int gemv_workspace(const LinearArgs& L, size_t* bytes) {
-  GemvPlan p = plan_gemv(L.M, L.N, L.K, L.rank, device_cus());
-  *bytes = p.ws_bytes;
+  // the plan depends on the activations' alignment, unknown here: the larger
+  // of the two
+  const GemvPlan p0 = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), false);
+  const GemvPlan p1 = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), true);
+  *bytes = p0.ws_bytes > p1.ws_bytes ? p0.ws_bytes : p1.ws_bytes;
   return RQ_OK;
 }
 
 int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream) {
   // the GEMV addresses the packed weights with 32-bit byte offsets
   if (L.N * (L.K / 2) > int64_t(INT32_MAX) - 256) return RQ_ERR_UNSUPPORTED;
-  const GemvPlan p = plan_gemv(L.M, L.N, L.K, L.rank, device_cus());
+  // ... and the activations, LoRA B and bias with 32-bit offsets too
+  if ((L.M - 1) * L.ldx + L.K > (int64_t(1) << 29)) return RQ_ERR_UNSUPPORTED;
+  if (L.rank > 0 && L.N * L.ld_lora_b > (int64_t(1) << 29)) return RQ_ERR_UNSUPPORTED;
+  const GemvPlan p = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), gemv_xvec(L));
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
   if (workspace && !aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;
   float* ws = static_cast<float*>(workspace);
