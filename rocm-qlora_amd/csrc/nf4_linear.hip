@@ -51,18 +51,19 @@ namespace rq {
 // under a branch and no loaded value is carried around a loop, so the
 // compiler's in-order load counting is exact and each unit waits only for
 // its own data.
-//   1. The activations: when M x K fits a 32 KiB stage, the workgroup reads
-//      x once (16-byte loads, at most two per thread) into LDS; otherwise each
-//      wave reads its own segment's operands (its units then share one
-//      segment).
-//   2. The first unit's weights and scales.
-//   3. The byte table (built from constants, no loads) and the activation
-//      stage; one barrier.
-//   4. The epilogue operands (the tiles' LoRA B rows, bias, RND(u) partials),
+//   1. The first unit's loads: its activations (M <= 2 and 16-byte aligned
+//      rows: the M x 256 values of the unit's segment, one 16-byte load per
+//      lane; otherwise the wave's MFMA operands directly, eight
+//      16-byte loads, and all of the wave's units share one segment), then its
+//      weights and scales.
+//   2. The byte table (built from constants, no loads); one barrier.
+//   3. The epilogue operands (the tiles' LoRA B rows, bias, RND(u) partials),
 //      kept as raw bits until the end.
-//   5. Per unit: issue the next unit's loads, then dequantize and multiply
-//      this one; the 16 x M partial goes to LDS, indexed by (tile, segment).
-//   6. The epilogue operands into LDS, one barrier; one thread per output sums
+//   4. Per unit: issue the next unit's loads; put the unit's activations
+//      through the wave's own LDS slice into the MFMA layout (no barrier: the
+//      wave writes and reads its slice itself); dequantize and multiply; the
+//      16 x M partial goes to LDS, indexed by (tile, segment).
+//   5. The epilogue operands into LDS, one barrier; one thread per output sums
 //      its tile's segment partials in segment order (deterministic), adds the
 //      bias and the LoRA term, rounds and stores -- or writes the fp32 sum of
 //      its K split to the workspace for the split-K finisher.
@@ -74,7 +75,7 @@ constexpr int kGemvMaxU = 4;           // units per wave
 constexpr int kGemvMaxTS = 4;          // tiles per workgroup
 constexpr int kGemvMaxFusedRank = 64;  // LoRA rank the in-kernel epilogue stages
 constexpr int kGemvMaxUSplits = 16;
-constexpr int kGemvXStageBytes = 32 * 1024;
+constexpr int kGemvXSliceMaxM = 2;  // activation rows through the per-wave LDS slice
 constexpr int kGemvLutQwords = 256 * 32;  // 64 KiB: code byte -> fp32 (T[lo], T[hi]), 32 copies
 constexpr int kGemvLdsBudget = 160 * 1024 - kGemvLutQwords * 8;
 constexpr uint8_t kGemvNoUnit = 0xFF;
@@ -93,12 +94,9 @@ struct GemvArgs {
   int bs_log2;             // log2(block_size)
   int nseg;                // segments per K split
   int TS;                  // tiles per workgroup
-  int xstage;              // activations staged in LDS
-  int kpad;                // LDS activation row pitch (elements, nseg * S * 256)
-  int xchunks;             // 16-byte activation chunks staged, M * kpad / 8
-  uint32_t xrow_magic;     // ceil(2^32 / (kpad / 8)): row of chunk c = mulhi(c, magic)
   bool direct;             // epilogue in this kernel (else fp32 partials to ws)
   bool xvec;               // x rows 16-byte aligned (vector loads)
+  int bvec_log2;           // LoRA B rows read as 16-byte chunks, 2^bvec_log2 per row (-1: by element)
   float* ws;               // [S, M, N] partials when !direct
   uint8_t unit_t[kGemvWaves][kGemvMaxU];  // tile slot of unit u of wave w (kGemvNoUnit: none)
   uint8_t unit_s[kGemvWaves][kGemvMaxU];  // segment (within the split) of unit u of wave w
@@ -107,11 +105,14 @@ struct GemvArgs {
 __host__ __device__ inline int gemv_part_floats(int TS, int nseg, int M) { return TS * nseg * M * 16; }
 
 // Dynamic LDS of the GEMV (bytes): segment partials [TS][nseg][M][16], the
-// activation stage [M][kpad] (16-bit), RND(B) of the tiles' rows [TS * 16][64],
-// RND(bias) [TS * 16], RND(u) [M][64] (fp32).
-__host__ __device__ inline size_t gemv_lds_bytes(int TS, int nseg, int M, bool xstage, int kpad, bool lora) {
+// waves' scale slices [16][64][16 bytes] (gathered absmax), the waves'
+// activation slices [16][M][256] (16-bit), RND(B) of the tiles' rows
+// [TS * 16][64], RND(bias) [TS * 16], RND(u) [M][64] (fp32).
+constexpr int kGemvScaleSliceBytes = 64 * 16;
+__host__ __device__ inline size_t gemv_lds_bytes(int TS, int nseg, int M, bool gather, bool xslice, bool lora) {
   size_t b = size_t(gemv_part_floats(TS, nseg, M)) * 4;
-  if (xstage) b += size_t(M) * kpad * 2;
+  if (gather) b += size_t(kGemvWaves) * kGemvScaleSliceBytes;
+  if (xslice) b += size_t(kGemvWaves) * M * kSegK * 2;
   b += (lora ? size_t(TS) * 16 * kGemvMaxFusedRank * 4 : 0) + size_t(TS) * 16 * 4;
   b += lora ? size_t(M) * kGemvMaxFusedRank * 4 : 0;
   return b;
@@ -132,42 +133,71 @@ __device__ __forceinline__ uint32_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t
 __device__ __forceinline__ uint32_t buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return uint32_t(__builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0));
 }
-// One element of a runtime float dtype (fp32 or 16-bit) as raw bits.
-__device__ __forceinline__ uint32_t buf_load_elem(__amdgpu_buffer_rsrc_t r, uint32_t idx, bool live, int dt) {
-  if (dt == RQ_DTYPE_F32) return buf_load4(r, live ? idx * 4u : kOobOffset);
-  return buf_load2(r, live ? idx * 2u : kOobOffset);
+// One element of a runtime float dtype (fp32 or 16-bit) as raw bits: both
+// widths are issued, the unused one out of range, so that no load sits under
+// a branch; elem_to_f32 picks and converts at the point of use.
+struct RawElem {
+  uint32_t w4, w2;
+};
+__device__ __forceinline__ RawElem buf_load_elem(__amdgpu_buffer_rsrc_t r, uint32_t idx, bool live, int dt) {
+  const bool f32 = dt == RQ_DTYPE_F32;
+  RawElem v;
+  v.w4 = buf_load4(r, live && f32 ? idx * 4u : kOobOffset);
+  v.w2 = buf_load2(r, live && !f32 ? idx * 2u : kOobOffset);
+  return v;
 }
-__device__ __forceinline__ float raw_elem_to_f32(uint32_t raw, int dt) {
-  return dt == RQ_DTYPE_F32 ? u2f(raw) : (dt == RQ_DTYPE_BF16 ? bf16_to_f32(uint16_t(raw)) : f16_to_f32(uint16_t(raw)));
+__device__ __forceinline__ float elem_to_f32(const RawElem& v, int dt) {
+  return dt == RQ_DTYPE_F32 ? u2f(v.w4) : (dt == RQ_DTYPE_BF16 ? bf16_to_f32(uint16_t(v.w2)) : f16_to_f32(uint16_t(v.w2)));
 }
 
-// Per-unit scale loads through buffer resources: the scale of the block
-// holding k1 (steps 0-3) and k2 = k1 + 128 (steps 4-7) of the lane's row.
+// Per-unit scale loads through buffer resources: the scales of the blocks
+// holding k1 (steps 0-3) and k2 = k1 + 128 (steps 4-7) of the lane's row,
+// given as block indices b1 and b2 (a past-the-end index reads zero).
 template <class Scale>
 struct GemvScale;
 
+// Absmax scales are gathered once per wave: lane (u, r) = (l / 16, l % 16)
+// loads the scales of row r of unit u's tile for unit u's segment (at most
+// four blocks: 16 bytes of fp32, 8 of 16-bit values) and the wave puts them
+// through its own LDS slice; unit u's lanes then read their two blocks there.
 template <int SDT>
 struct GemvScale<ScaleAbsmax<SDT>> {
-  typedef uint32_t Raw;
+  static constexpr bool kGather = true;
+  static constexpr uint32_t kBytes = SDT == RQ_DTYPE_F32 ? 4u : 2u;
+  struct Pair {};
   __amdgpu_buffer_rsrc_t r;
-  __device__ GemvScale(const ScaleAbsmax<SDT>& s, uint32_t nblocks) {
-    r = buffer_rsrc(s.p, nblocks * (SDT == RQ_DTYPE_F32 ? 4u : 2u));
+  __device__ GemvScale(const ScaleAbsmax<SDT>& s, uint32_t nblocks) { r = buffer_rsrc(s.p, nblocks * kBytes); }
+  // the four blocks from block b on (a past-the-end b reads zeros)
+  __device__ __forceinline__ u32x4 gather(uint32_t b) const {
+    if constexpr (SDT == RQ_DTYPE_F32) return buf_load16(r, b * 4u);
+    else {
+      const u32x2 v = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, b * 2u, 0, 0));
+      return u32x4{v.x, v.y, 0u, 0u};
+    }
   }
-  __device__ __forceinline__ Raw load(uint32_t b, bool live) const {
-    if constexpr (SDT == RQ_DTYPE_F32) return buf_load4(r, live ? b * 4u : kOobOffset);
-    else return buf_load2(r, live ? b * 2u : kOobOffset);
+  // block c (0..3) of a gathered row
+  __device__ __forceinline__ float value(const uint32_t* row, uint32_t c) const {
+    if constexpr (SDT == RQ_DTYPE_F32) return u2f(row[c]);
+    else {
+      const uint16_t h = reinterpret_cast<const uint16_t*>(row)[c];
+      if constexpr (SDT == RQ_DTYPE_BF16) return bf16_to_f32(h);
+      else return f16_to_f32(h);
+    }
   }
-  __device__ __forceinline__ float value(Raw v) const {
-    if constexpr (SDT == RQ_DTYPE_F32) return u2f(v);
-    else if constexpr (SDT == RQ_DTYPE_BF16) return bf16_to_f32(uint16_t(v));
-    else return f16_to_f32(uint16_t(v));
-  }
+  __device__ __forceinline__ Pair load(uint32_t, uint32_t) const { return Pair{}; }
+  __device__ __forceinline__ void hold(const Pair&) const {}
+  __device__ __forceinline__ float v1(const Pair&) const { return 0.0f; }
+  __device__ __forceinline__ float v2(const Pair&) const { return 0.0f; }
 };
 
 template <int SDT>
 struct GemvScale<ScaleDQ<SDT>> {
+  static constexpr bool kGather = false;
   struct Raw {
     uint32_t code, hi;
+  };
+  struct Pair {
+    Raw s1, s2;
   };
   __amdgpu_buffer_rsrc_t rc, rs;
   int fmt, sh;
@@ -181,15 +211,17 @@ struct GemvScale<ScaleDQ<SDT>> {
     sh = s.bs2_shift;
     bs2 = uint32_t(s.bs2);
   }
-  __device__ __forceinline__ Raw load(uint32_t b, bool live) const {
-    const uint32_t g = sh >= 0 ? (b >> sh) : b / bs2;
+  __device__ __forceinline__ Raw load1(uint32_t b) const {
+    // a missing unit's block (from kDeadBlock on) reads code 0 and scale 0
+    const uint32_t g = b >= 0x20000000u ? b : (sh >= 0 ? (b >> sh) : b / bs2);
     Raw v;
-    v.code = buf_load1(rc, live ? b : kOobOffset);
-    if constexpr (SDT == RQ_DTYPE_F32) v.hi = buf_load4(rs, live ? g * 4u : kOobOffset);
-    else v.hi = buf_load2(rs, live ? g * 2u : kOobOffset);
+    v.code = buf_load1(rc, b);
+    if constexpr (SDT == RQ_DTYPE_F32) v.hi = buf_load4(rs, g * 4u);
+    else v.hi = buf_load2(rs, g * 2u);
     return v;
   }
-  __device__ __forceinline__ float value(Raw v) const {
+  __device__ __forceinline__ Pair load(uint32_t b1, uint32_t b2) const { return Pair{load1(b1), load1(b2)}; }
+  __device__ __forceinline__ float value(const Raw& v) const {
     float hi;
     if constexpr (SDT == RQ_DTYPE_F32) hi = u2f(v.hi);
     else if constexpr (SDT == RQ_DTYPE_BF16) hi = bf16_to_f32(uint16_t(v.hi));
@@ -198,37 +230,61 @@ struct GemvScale<ScaleDQ<SDT>> {
     const float lo = fmt == RQ_C2_FP8_E4M3FNUZ ? fnuz_to_f32(c) : __fdiv_rn(float(int8_t(c)), 127.0f);
     return __fmul_rn(lo, hi);
   }
+  __device__ __forceinline__ float v1(const Pair& p) const { return value(p.s1); }
+  __device__ __forceinline__ float v2(const Pair& p) const { return value(p.s2); }
+  __device__ __forceinline__ void hold(const Pair&) const {}
 };
 
 // One unit's loads for one lane: loads A and B (raw code bits) and the
 // scales of steps 0-3 and 4-7.
 template <class Scale>
 struct GemvUnit {
+  u32x4 xc;  // activation chunk (slice mode)
   u32x4 a, b;
-  typename GemvScale<Scale>::Raw s1, s2;
+  typename GemvScale<Scale>::Pair sp;
 };
 
 // Per-lane constants of the unit loads.
 struct GemvLane {
   int n16, q;
-  uint32_t offA, offB;   // byte offset of loads A / B within a tile row block, segment 0
-  uint32_t sb1, sb2;     // scale block offset of k1 / k2 within segment 0 of the lane's row
+  uint32_t offA, offB;   // byte offsets of loads A / B within a tile's rows, segment 0
+  uint32_t sb1, sb2;     // scale block offsets of k1 / k2 from the tile's first block row, segment 0
+  uint32_t c1, c2;       // block of k1 / k2 among a segment's (gathered) blocks
+  uint32_t xoff;         // byte offset of the lane's activation chunk, segment 0 (slice mode)
+  uint32_t xk;           // k of that chunk within a segment
 };
 
-template <class Scale>
+// Wave-uniform bases that put every lane offset past the end of its buffer,
+// so the loads of a missing unit read zeros without a per-lane select: a
+// byte offset base (buffers here stay under 2^31 bytes) and a scale block
+// index base (times 4 bytes still 2^31, with no wrap; scale arrays stay under
+// 2^28 bytes since the packed weights stay under 2^31).
+constexpr uint32_t kDeadBase = 0x80000000u;
+constexpr uint32_t kDeadBlock = 0x20000000u;
+
+template <int XM, class Scale>
 __device__ __forceinline__ void gemv_issue(GemvUnit<Scale>& U, const GemvArgs& a, const GemvScale<Scale>& sc,
-                                           __amdgpu_buffer_rsrc_t wres, const GemvLane& ln, uint32_t tile,
-                                           uint32_t seg, bool live) {
+                                           __amdgpu_buffer_rsrc_t wres, __amdgpu_buffer_rsrc_t xres,
+                                           const GemvLane& ln, uint32_t tile, uint32_t seg, bool live) {
+  if constexpr (XM == 1) {
+    // lane c: row c / 32, k = seg * 256 + 8 (c % 32); issued first, so that
+    // waiting for it never waits for the weights.  A row past M reads past
+    // the end of x; a k past K (a last, partial segment) must not read the
+    // next row.
+    const bool kin = seg * kSegK + ln.xk < uint32_t(a.K);
+    const uint32_t xb = live ? seg * (kSegK * 2u) : kDeadBase;
+    U.xc = buf_load16(xres, kin ? xb + ln.xoff : kDeadBase);
+  }
   const uint32_t half_k = uint32_t(a.K) >> 1;
-  const uint32_t base = tile * 16u * half_k + seg * (kSegK / 2);
-  U.a = buf_load16(wres, live ? base + ln.offA : kOobOffset);
-  U.b = buf_load16(wres, live ? base + ln.offB : kOobOffset);
+  const uint32_t wb = live ? tile * 16u * half_k + seg * (kSegK / 2) : kDeadBase;
+  U.a = buf_load16(wres, wb + ln.offA);
+  U.b = buf_load16(wres, wb + ln.offB);
   // scale block of k = seg * 256 + c (c < 256): (seg * 256 + c) >> bs_log2
-  const uint32_t row = tile * 16u + uint32_t(ln.n16);
   const uint32_t sseg = a.bs_log2 <= 8 ? (seg << (8 - a.bs_log2)) : (seg >> (a.bs_log2 - 8));
-  const uint32_t b0 = row * uint32_t(a.bpr) + sseg;
-  U.s1 = sc.load(b0 + ln.sb1, live);
-  U.s2 = sc.load(b0 + ln.sb2, live);
+  if constexpr (!GemvScale<Scale>::kGather) {
+    const uint32_t sb = live ? tile * 16u * uint32_t(a.bpr) + sseg : kDeadBlock;
+    U.sp = sc.load(sb + ln.sb1, sb + ln.sb2);
+  }
 }
 
 __device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
@@ -236,13 +292,12 @@ __device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
 }
 
 template <int XT, class Scale>
-__device__ __forceinline__ f32x4 gemv_tile(const GemvUnit<Scale>& U, const GemvScale<Scale>& sc,
-                                           const u32x4 (&xa)[8], const u32x2* lut, uint32_t lane_off, int n16) {
+__device__ __forceinline__ f32x4 gemv_tile(const GemvUnit<Scale>& U, float s1, float s2, const u32x4 (&xa)[8],
+                                           const u32x2* lut, uint32_t lane_off, int n16) {
   const bool lo = n16 < 8;
   const u32x4 X1 = lo ? U.a : U.b;
   const u32x4 Y = lo ? U.b : U.a;
   const u32x4 X2 = u32x4{row_ror8(Y.x), row_ror8(Y.y), row_ror8(Y.z), row_ror8(Y.w)};
-  const float s1 = sc.value(U.s1), s2 = sc.value(U.s2);
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   acc = mfma16x16x32<XT>(xa[0], expand8_scaled<XT>(lut, X1.x, lane_off, s1), acc);
   acc = mfma16x16x32<XT>(xa[1], expand8_scaled<XT>(lut, X1.y, lane_off, s1), acc);
@@ -260,7 +315,7 @@ __device__ __forceinline__ f32x4 gemv_tile(const GemvUnit<Scale>& U, const GemvS
 // global load, which would serialize the prefetched units.)
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <int XT, class Scale, int U>
+template <int XT, class Scale, int U, int XM>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   // The table is the kernel's only static LDS array, so it sits at address
@@ -272,9 +327,15 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   const int M = a.M, TS = a.TS, nseg = a.nseg;
   const int rank = (a.direct && e.rank > 0) ? e.rank : 0;  // LoRA staging only when fused here
   constexpr int RP = kGemvMaxFusedRank;                    // staging pitch
+  constexpr bool kGather = GemvScale<Scale>::kGather;
   float* part = reinterpret_cast<float*>(smem);
-  uint16_t* xs = reinterpret_cast<uint16_t*>(part + gemv_part_floats(TS, nseg, M));
-  float* lbs = reinterpret_cast<float*>(xs + (a.xstage ? M * a.kpad : 0));
+  // this wave's scale slice [64][4] (gathered absmax)
+  uint32_t* gs = reinterpret_cast<uint32_t*>(part + gemv_part_floats(TS, nseg, M)) + wave * (kGemvScaleSliceBytes / 4);
+  uint16_t* xs0 = reinterpret_cast<uint16_t*>(reinterpret_cast<uint32_t*>(part + gemv_part_floats(TS, nseg, M)) +
+                                              (kGather ? kGemvWaves * (kGemvScaleSliceBytes / 4) : 0));
+  // this wave's activation slice [M][256] (slice mode)
+  uint16_t* xs = xs0 + wave * M * kSegK;
+  float* lbs = reinterpret_cast<float*>(xs0 + (XM == 1 ? kGemvWaves * M * kSegK : 0));
   float* bss = lbs + (rank > 0 ? TS * 16 * RP : 0);
   float* us = bss + TS * 16;
 
@@ -287,9 +348,15 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     ln.offA = n7 * half_k + 16u * cA;
     ln.offB = (8u + n7) * half_k + 16u * cB;
     // block offsets of k1 = 32 q and k2 = 128 + 32 q within a segment (zero
-    // when a block spans whole segments)
-    ln.sb1 = a.bs_log2 <= 8 ? (32u * uint32_t(ln.q)) >> a.bs_log2 : 0u;
-    ln.sb2 = a.bs_log2 <= 8 ? (128u + 32u * uint32_t(ln.q)) >> a.bs_log2 : 0u;
+    // when a block spans whole segments), from the tile's first row
+    const uint32_t rowb = uint32_t(ln.n16) * uint32_t(a.bpr);
+    ln.sb1 = rowb + (a.bs_log2 <= 8 ? (32u * uint32_t(ln.q)) >> a.bs_log2 : 0u);
+    ln.sb2 = rowb + (a.bs_log2 <= 8 ? (128u + 32u * uint32_t(ln.q)) >> a.bs_log2 : 0u);
+    ln.c1 = a.bs_log2 <= 8 ? (32u * uint32_t(ln.q)) >> a.bs_log2 : 0u;
+    ln.c2 = a.bs_log2 <= 8 ? (128u + 32u * uint32_t(ln.q)) >> a.bs_log2 : 0u;
+    const uint32_t c = uint32_t(lane);
+    ln.xk = 8u * (c & 31u);
+    ln.xoff = ((c >> 5) * uint32_t(a.ldx) + ln.xk) * 2u;
   }
   const uint32_t seg0 = blockIdx.y * uint32_t(nseg);  // first segment of this K split
   const uint32_t n_tiles = uint32_t((a.N + 15) / 16);
@@ -314,29 +381,38 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   const __amdgpu_buffer_rsrc_t xres =
       buffer_rsrc(a.x, uint32_t(M - 1) * uint32_t(a.ldx) * 2u + uint32_t(a.K) * 2u);
 
-  // 1. activations into the LDS stage (chunk c = 8 consecutive k of one row)
-  u32x4 xst[2];
-  if (a.xstage) {
-    const uint32_t cpr = uint32_t(a.kpad) >> 3;
+  // 1. the first unit's loads; without the slice, this wave's own
+  //    activation operands (its units share one segment): step c covers k =
+  //    seg * 256 + 128 (c / 4) + 32 q + 8 (c % 4) of token n16; a token past M
+  //    or a k past K reads zeros
+  // units in flight ahead of the one being computed (two measured slower:
+  // the extra bytes in flight only lengthened the loaded latency)
+  constexpr int D = 1;
+  // the gathered scales first: lane (u, r) = (lane / 16, lane % 16) takes
+  // row r of unit u's tile, from unit u's segment's first block on
+  u32x4 gsv = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (kGather) {
+    const int gu = lane >> 4;
+    int gt = ut[0], gseg = useg[0];
+    bool glive = ulive[0];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t c = uint32_t(tid) + 1024u * uint32_t(i);
-      const uint32_t m = __umulhi(c, a.xrow_magic);
-      const uint32_t k = 8u * (c - m * cpr);
-      const bool live = c < uint32_t(a.xchunks) && k < uint32_t(a.K);
-      xst[i] = buf_load16(xres, live ? (m * uint32_t(a.ldx) + k) * 2u : kOobOffset);
-    }
+    for (int u = 1; u < U; ++u)
+      if (gu == u) {
+        gt = ut[u];
+        gseg = useg[u];
+        glive = ulive[u];
+      }
+    const uint32_t sg = seg0 + uint32_t(gseg);
+    const uint32_t first = a.bs_log2 <= 8 ? (sg << (8 - a.bs_log2)) : (sg >> (a.bs_log2 - 8));
+    const uint32_t blk = (tile_of(gt) * 16u + uint32_t(ln.n16)) * uint32_t(a.bpr) + first;
+    gsv = sc.gather(glive && gu < U ? blk : kDeadBlock);
   }
-
-  // 2. the first unit's weights and scales
   GemvUnit<Scale> L[U];
-  gemv_issue(L[0], a, sc, wres, ln, tile_of(ut[0]), seg0 + uint32_t(useg[0]), ulive[0]);
-
-  // 1'. without the stage, this wave's own activation operands (its units
-  //     share one segment): step c covers k = seg * 256 + 128 (c / 4) + 32 q +
-  //     8 (c % 4) of token n16; a token past M or a k past K reads zeros
+#pragma unroll
+  for (int u = 0; u < D; ++u)
+    gemv_issue<XM>(L[u], a, sc, wres, xres, ln, tile_of(ut[u]), seg0 + uint32_t(useg[u]), ulive[u]);
   u32x4 xa[8];
-  if (!a.xstage) {
+  if constexpr (XM == 0) {
     const uint32_t sg = seg0 + uint32_t(useg[0]);
     const bool mlive = ln.n16 < M && ulive[0];
     if (a.xvec) {
@@ -362,38 +438,34 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
   }
 
-  // 3. the table and the activation stage
+  // 2. the table
   fill_f32pair_lut<kGemvThreads>(lut, tid);
-  if (a.xstage) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t c = uint32_t(tid) + 1024u * uint32_t(i);
-      if (c < uint32_t(a.xchunks)) *reinterpret_cast<u32x4*>(xs + 8u * c) = xst[i];
-    }
-  }
   lds_barrier();
 
-  // 4. epilogue operands, raw: LoRA B values (value t of thread tid is row
+  // 3. epilogue operands, raw: LoRA B values (value t of thread tid is row
   //    tid / 64 of tile slot t, rank tid % 64), the bias, the RND(u) partials
   //    (waves m < M)
-  uint32_t lbr[kGemvMaxTS], br = 0u, up[kGemvMaxUSplits];
-#pragma unroll
-  for (int t = 0; t < kGemvMaxTS; ++t) lbr[t] = 0u;
+  RawElem br = RawElem{0u, 0u};
+  u32x4 bvr = u32x4{0u, 0u, 0u, 0u};
+  uint32_t up[kGemvMaxUSplits];
 #pragma unroll
   for (int k = 0; k < kGemvMaxUSplits; ++k) up[k] = 0u;
   const int lj = tid & (RP - 1);
-  if (rank > 0) {
-    const __amdgpu_buffer_rsrc_t bres = buffer_rsrc(e.lora_b, uint32_t(a.N) * uint32_t(e.ld_lora_b) *
-                                                                   (e.lora_dt == RQ_DTYPE_F32 ? 4u : 2u));
-#pragma unroll
-    for (int t = 0; t < kGemvMaxTS; ++t) {
-      const uint32_t bn = tile_of(t) * 16u + uint32_t(tid >> 6);
-      const bool live = t < TS && lj < rank && bn < uint32_t(a.N);
-      lbr[t] = buf_load_elem(bres, bn * uint32_t(e.ld_lora_b) + uint32_t(lj), live, e.lora_dt);
-    }
+  const uint32_t bbytes = e.lora_dt == RQ_DTYPE_F32 ? 4u : 2u;
+  // LoRA B rows as 16-byte chunks (the host fuses LoRA only for such rows):
+  // thread tid < TS * 16 * 2^cl takes chunk tid % 2^cl of row (tid >> cl) % 16
+  // of tile slot tid >> (4 + cl)
+  const int cl = rank > 0 ? a.bvec_log2 : 0;
+  const int bt = tid >> (4 + cl), br_row = (tid >> cl) & 15, bc = tid & ((1 << cl) - 1);
+  const bool bvec_live = rank > 0 && tid < (TS * 16 << cl);
+  if (rank > 0 && wave * 64 < (TS * 16 << cl)) {
+    const __amdgpu_buffer_rsrc_t bres = buffer_rsrc(e.lora_b, uint32_t(a.N) * uint32_t(e.ld_lora_b) * bbytes);
+    const uint32_t bn = tile_of(bt) * 16u + uint32_t(br_row);
+    const bool live = bvec_live && bn < uint32_t(a.N);
+    bvr = buf_load16(bres, live ? bn * uint32_t(e.ld_lora_b) * bbytes + 16u * uint32_t(bc) : kOobOffset);
   }
   const bool has_bias = a.direct && e.bias != nullptr;
-  if (has_bias) {
+  if (has_bias && wave == 0) {
     const __amdgpu_buffer_rsrc_t bres = buffer_rsrc(e.bias, uint32_t(a.N) * (e.bias_dt == RQ_DTYPE_F32 ? 4u : 2u));
     const int cb = tid & (kGemvMaxTS * 16 - 1);
     const uint32_t cn = tile_of(cb >> 4) * 16u + uint32_t(cb & 15);
@@ -409,15 +481,22 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
       up[k] = buf_load4(ures, (uint32_t(k) < ns && lj < rank) ? (uint32_t(k) * stride + u_idx) * 4u : kOobOffset);
   }
 
-  // 5. the units, each as soon as its loads have landed; partials to LDS
+  // 4. the units, each as soon as its loads have landed; partials to LDS
   const uint32_t lane_off = uint32_t(lane & 31) * 8u;
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    if (u + 1 < U) gemv_issue(L[u + 1], a, sc, wres, ln, tile_of(ut[u + 1]), seg0 + uint32_t(useg[u + 1]), ulive[u + 1]);
+    if (u + D < U)
+      gemv_issue<XM>(L[u + D], a, sc, wres, xres, ln, tile_of(ut[u + D]), seg0 + uint32_t(useg[u + D]), ulive[u + D]);
+    if constexpr (kGather) {
+      if (u == 0) *reinterpret_cast<u32x4*>(gs + 4 * lane) = gsv;
+    }
     if (ulive[u]) {
-      if (a.xstage) {
+      if constexpr (XM == 1) {
+        // the unit's activations through this wave's slice: lane c wrote
+        // row c / 32, k 8 (c % 32); token n16 < M reads its MFMA operands
+        if (lane < 32 * M) *reinterpret_cast<u32x4*>(xs + 8 * lane) = L[u].xc;
         if (ln.n16 < M) {
-          const uint16_t* xrow = xs + ln.n16 * a.kpad + (seg0 + uint32_t(useg[u])) * kSegK + 32 * ln.q;
+          const uint16_t* xrow = xs + ln.n16 * kSegK + 32 * ln.q;
 #pragma unroll
           for (int c = 0; c < 8; ++c) xa[c] = *reinterpret_cast<const u32x4*>(xrow + 128 * (c >> 2) + 8 * (c & 3));
         } else {
@@ -425,7 +504,17 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
           for (int c = 0; c < 8; ++c) xa[c] = u32x4{0u, 0u, 0u, 0u};
         }
       }
-      const f32x4 acc = gemv_tile<XT>(L[u], sc, xa, lut, lane_off, ln.n16);
+      float s1, s2;
+      if constexpr (kGather) {
+        const uint32_t* grow = gs + 4 * (16 * u + ln.n16);
+        s1 = sc.value(grow, ln.c1);
+        s2 = sc.value(grow, ln.c2);
+      } else {
+        sc.hold(L[u].sp);
+        s1 = sc.v1(L[u].sp);
+        s2 = sc.v2(L[u].sp);
+      }
+      const f32x4 acc = gemv_tile<XT>(L[u], s1, s2, xa, lut, lane_off, ln.n16);
       float* pp = part + (ut[u] * nseg + useg[u]) * M * 16 + ln.n16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -435,21 +524,29 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
   }
 
-  // 6. epilogue operands into LDS, then one thread per output (tile slot
+  // 5. epilogue operands into LDS, then one thread per output (tile slot
   //    t = tid / 256, row m, column nn).  The empty asm marks the raw values
   //    as changed here, so that no use of them (which waits for its load)
   //    is scheduled into the unit loop above.
-#pragma unroll
-  for (int t = 0; t < kGemvMaxTS; ++t) asm volatile("" : "+v"(lbr[t]));
-  asm volatile("" : "+v"(br));
+  asm volatile("" : "+v"(br.w4), "+v"(br.w2));
+  asm volatile("" : "+v"(bvr));
 #pragma unroll
   for (int k = 0; k < kGemvMaxUSplits; ++k) asm volatile("" : "+v"(up[k]));
-  if (rank > 0) {
+  if (bvec_live) {
+    float* dst = lbs + (bt * 16 + br_row) * RP + bc * int(16u / bbytes);
+    if (e.lora_dt == RQ_DTYPE_F32) {
 #pragma unroll
-    for (int t = 0; t < kGemvMaxTS; ++t)
-      if (t < TS) lbs[tid + 1024 * t] = lj < rank ? round_x<XT>(raw_elem_to_f32(lbr[t], e.lora_dt)) : 0.0f;
+      for (int i = 0; i < 4; ++i) dst[i] = round_x<XT>(u2f(bvr[i]));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t lo = uint16_t(bvr[i]), hi = uint16_t(bvr[i] >> 16);
+        dst[2 * i] = round_x<XT>(e.lora_dt == RQ_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo));
+        dst[2 * i + 1] = round_x<XT>(e.lora_dt == RQ_DTYPE_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi));
+      }
+    }
   }
-  if (a.direct && tid < TS * 16) bss[tid] = has_bias ? round_x<XT>(raw_elem_to_f32(br, e.bias_dt)) : 0.0f;
+  if (a.direct && tid < TS * 16) bss[tid] = has_bias ? round_x<XT>(elem_to_f32(br, e.bias_dt)) : 0.0f;
   if (stage_u) {
     float sum = 0.0f;
 #pragma unroll
@@ -489,18 +586,18 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
       float uu[8], bb[8];
 #pragma unroll
       for (int jj = 0; jj < 8; ++jj) {
-        uu[jj] = urow[j0 + jj];  // zero past rank
+        uu[jj] = urow[j0 + jj];
         bb[jj] = brow[j0 + jj];
       }
 #pragma unroll
-      for (int jj = 0; jj < 8; ++jj) l = __fmaf_rn(uu[jj], bb[jj], l);
+      for (int jj = 0; jj < 8; ++jj)
+        if (j0 + jj < rank) l = __fmaf_rn(uu[jj], bb[jj], l);
     }
     l = round_x<XT>(__fmul_rn(round_x<XT>(l), e.scaling));
     v = round_x<XT>(__fadd_rn(v, l));
   }
   static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
 }
-
 
 // Split-K finisher (and the LoRA epilogue for any M): y = finish(sum_s
 // ws[s]).  Workgroup = 256 columns x 16 activation rows; B values are read 8
@@ -617,7 +714,8 @@ __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------
 // Work plan of the GEMV: K splits, tiles per workgroup, units per wave, the
 // unit table, the activation stage, and the workspace layout.
-GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool xvec) {
+GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool xvec, bool gather,
+                   bool lora_vec) {
   GemvPlan p{};
   const int nsegs = int((K + kSegK - 1) / kSegK);
   const int64_t tiles = (N + 15) / 16;
@@ -628,25 +726,24 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     const int64_t ks = (K / 32 + steps_per_wg - 1) / steps_per_wg;
     p.u_splits = int(ks < kGemvMaxUSplits ? ks : kGemvMaxUSplits);
   }
-  const bool lora_fusable = rank <= kGemvMaxFusedRank;
-  for (int stage = 1; stage >= 0; --stage) {
-    const bool xstage = stage != 0;
-    if (xstage && !xvec) continue;
-    // segments one workgroup covers: 4 per wave with the stage, else one
-    const int max_nseg = xstage ? kGemvWaves * kGemvMaxU : kGemvWaves;
+  const bool lora_fusable = rank <= 0 || (rank <= kGemvMaxFusedRank && lora_vec);
+  for (int slice = 1; slice >= 0; --slice) {
+    // activations through the waves' LDS slices: any unit to any wave
+    const bool xslice = slice != 0;
+    if (xslice && !(xvec && M <= kGemvXSliceMaxM)) continue;
+    // segments one workgroup covers: 4 per wave with the slices, else one
+    const int max_nseg = xslice ? kGemvWaves * kGemvMaxU : kGemvWaves;
     const int S = (nsegs + max_nseg - 1) / max_nseg;
     const int nseg = (nsegs + S - 1) / S;
-    if (xstage && M * int64_t(nseg) * S * kSegK * 2 > kGemvXStageBytes) continue;
-    const int R = kGemvWaves / nseg;  // tile slots per round without the stage
-    const int ts_cap = xstage ? (kGemvWaves * kGemvMaxU) / nseg : kGemvMaxU * R;
+    const int R = kGemvWaves / nseg;  // tile slots per round without the slices
+    const int ts_cap = xslice ? (kGemvWaves * kGemvMaxU) / nseg : kGemvMaxU * R;
     const bool direct = S == 1 && lora_fusable;
     int best = 0;
     int64_t best_cost = 0;
     for (int TS = 1; TS <= kGemvMaxTS && TS <= ts_cap; ++TS) {
-      const int U = xstage ? (TS * nseg + kGemvWaves - 1) / kGemvWaves : (TS + R - 1) / R;
+      const int U = xslice ? (TS * nseg + kGemvWaves - 1) / kGemvWaves : (TS + R - 1) / R;
       if (U != 1 && U != 2 && U != 4) continue;
-      const int kpad = nseg * S * kSegK;
-      if (gemv_lds_bytes(TS, nseg, int(M), xstage, kpad, direct && rank > 0) > size_t(kGemvLdsBudget)) continue;
+      if (gemv_lds_bytes(TS, nseg, int(M), gather, xslice, direct && rank > 0) > size_t(kGemvLdsBudget)) continue;
       // tiles a compute unit works through one after another
       const int64_t grid = (tiles + TS - 1) / TS;
       const int64_t cost = ((grid * S + ncu - 1) / ncu) * TS;
@@ -659,9 +756,8 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     p.S = S;
     p.nseg = nseg;
     p.TS = best;
-    p.xstage = xstage;
-    p.kpad = nseg * S * kSegK;
-    p.U = xstage ? (best * nseg + kGemvWaves - 1) / kGemvWaves : (best + R - 1) / R;
+    p.xslice = xslice;
+    p.U = xslice ? (best * nseg + kGemvWaves - 1) / kGemvWaves : (best + R - 1) / R;
     p.grid = int((tiles + best - 1) / best);
     p.direct = direct;
     for (int w = 0; w < kGemvWaves; ++w)
@@ -669,7 +765,7 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
         p.unit_t[w][u] = kGemvNoUnit;
         p.unit_s[w][u] = 0;
         if (u >= p.U) continue;
-        if (xstage) {
+        if (xslice) {
           const int i = w + kGemvWaves * u;
           if (i < best * nseg) {
             p.unit_t[w][u] = uint8_t(i / nseg);
@@ -685,7 +781,7 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
       }
     break;
   }
-  p.lds_bytes = gemv_lds_bytes(p.TS, p.nseg, int(M), p.xstage, p.kpad, p.direct && rank > 0);
+  p.lds_bytes = gemv_lds_bytes(p.TS, p.nseg, int(M), gather, p.xslice, p.direct && rank > 0);
   p.ws_bytes = p.direct ? 0 : size_t(p.S) * M * N * 4;
   p.u_offset = (p.ws_bytes + 255) & ~size_t(255);
   if (rank > 0) p.ws_bytes = p.u_offset + size_t(p.u_splits) * M * rank * 4;
@@ -694,6 +790,19 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
 
 // x rows 16-byte aligned: the GEMV reads activations with 16-byte loads.
 static bool gemv_xvec(const LinearArgs& L) { return aligned(L.x, 16) && L.ldx % 8 == 0; }
+
+// log2 of the 16-byte chunks per LoRA B row when the GEMV epilogue can read
+// the rows that way (aligned rows of a power of two of whole chunks), else -1:
+// the LoRA term then goes to the split-K finisher.
+static int gemv_bvec_log2(const LinearArgs& L) {
+  if (L.rank <= 0) return -1;
+  const int64_t bb = L.lora_dtype == RQ_DTYPE_F32 ? 4 : 2;
+  const int64_t cpr = L.rank * bb / 16;
+  if (!aligned(L.lora_b, 16) || (L.ld_lora_b * bb) % 16 != 0 || (L.rank * bb) % 16 != 0 || cpr <= 0 ||
+      (cpr & (cpr - 1)) != 0)
+    return -1;
+  return pow2_shift(cpr);
+}
 
 template <int XT>
 static int launch_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream) {
@@ -705,9 +814,9 @@ static int launch_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t str
   return rq_check_launch();
 }
 
-template <int XT, class Scale, int U>
+template <int XT, class Scale, int U, int XM>
 static int launch_gemv_u(const GemvArgs& a, const GemvPlan& p, Scale scale, const LinearEpi& e, hipStream_t stream) {
-  auto kern = nf4_gemv_kernel<XT, Scale, U>;
+  auto kern = nf4_gemv_kernel<XT, Scale, U, XM>;
   static bool attr_set = false;  // one flag per instantiation
   if (!attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -734,23 +843,26 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.bs_log2 = pow2_shift(L.block_size);
   a.nseg = p.nseg;
   a.TS = p.TS;
-  a.xstage = p.xstage ? 1 : 0;
-  a.kpad = p.kpad;
-  const uint32_t cpr = uint32_t(p.kpad / 8);
-  a.xchunks = int(L.M * p.kpad / 8);
-  a.xrow_magic = uint32_t(((uint64_t(1) << 32) + cpr - 1) / cpr);
   a.direct = p.direct;
   a.xvec = gemv_xvec(L);
+  a.bvec_log2 = gemv_bvec_log2(L);
   a.ws = ws;
   for (int w = 0; w < kGemvWaves; ++w)
     for (int u = 0; u < kGemvMaxU; ++u) {
       a.unit_t[w][u] = p.unit_t[w][u];
       a.unit_s[w][u] = p.unit_s[w][u];
     }
+  if (p.xslice) {
+    switch (p.U) {
+      case 1: return launch_gemv_u<XT, Scale, 1, 1>(a, p, scale, e, stream);
+      case 2: return launch_gemv_u<XT, Scale, 2, 1>(a, p, scale, e, stream);
+      default: return launch_gemv_u<XT, Scale, 4, 1>(a, p, scale, e, stream);
+    }
+  }
   switch (p.U) {
-    case 1: return launch_gemv_u<XT, Scale, 1>(a, p, scale, e, stream);
-    case 2: return launch_gemv_u<XT, Scale, 2>(a, p, scale, e, stream);
-    default: return launch_gemv_u<XT, Scale, 4>(a, p, scale, e, stream);
+    case 1: return launch_gemv_u<XT, Scale, 1, 0>(a, p, scale, e, stream);
+    case 2: return launch_gemv_u<XT, Scale, 2, 0>(a, p, scale, e, stream);
+    default: return launch_gemv_u<XT, Scale, 4, 0>(a, p, scale, e, stream);
   }
 }
 
@@ -829,19 +941,20 @@ int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream) {
 int gemv_workspace(const LinearArgs& L, size_t* bytes) {
   // the plan depends on the activations' alignment, unknown here: the larger
   // of the two
-  const GemvPlan p0 = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), false);
-  const GemvPlan p1 = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), true);
+  const GemvPlan p0 = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), false, false, false);
+  const GemvPlan p1 = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), true, false, false);
   *bytes = p0.ws_bytes > p1.ws_bytes ? p0.ws_bytes : p1.ws_bytes;
   return RQ_OK;
 }
 
 int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream) {
   // the GEMV addresses the packed weights with 32-bit byte offsets
-  if (L.N * (L.K / 2) > int64_t(INT32_MAX) - 256) return RQ_ERR_UNSUPPORTED;
+  if (L.N * (L.K / 2) > int64_t(INT32_MAX) - 256 || L.K >= (int64_t(1) << 27)) return RQ_ERR_UNSUPPORTED;
   // ... and the activations, LoRA B and bias with 32-bit offsets too
   if ((L.M - 1) * L.ldx + L.K > (int64_t(1) << 29)) return RQ_ERR_UNSUPPORTED;
   if (L.rank > 0 && L.N * L.ld_lora_b > (int64_t(1) << 29)) return RQ_ERR_UNSUPPORTED;
-  const GemvPlan p = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), gemv_xvec(L));
+  const GemvPlan p = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), gemv_xvec(L), L.c2 == nullptr,
+                               gemv_bvec_log2(L) >= 0);
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
   if (workspace && !aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;
   float* ws = static_cast<float*>(workspace);

@@ -54,13 +54,14 @@ struct LinearEpi {
 };
 
 struct GemvPlan {
-  int S, TS, U, nseg, grid, u_splits, kpad;
-  bool direct, xstage;
+  int S, TS, U, nseg, grid, u_splits;
+  bool direct, xslice;
   size_t lds_bytes, ws_bytes, u_offset;
   uint8_t unit_t[16][4], unit_s[16][4];  // (tile slot, segment) of unit u of wave w; 0xFF: none
 };
 
-GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool xvec);
+GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool xvec, bool gather,
+                   bool lora_vec);
 int validate_linear(const LinearArgs& L);
 LinearEpi make_epi(const LinearArgs& L, float* u_parts, int u_splits);
 int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream);

@@ -97,12 +97,18 @@ __device__ __forceinline__ uint32_t nf4_bits(int i) {
   return v;
 }
 
+// The high nibbles a wave writes are the same in all its lanes and its low
+// nibbles take two values (lanes 0-31, 32-63), so the code-book selections
+// run on wave-uniform values (scalar ops) and one per-lane select remains.
 template <int NT>
 __device__ __forceinline__ void fill_f32pair_lut(u32x2* lut, int tid) {
   static_assert(NT == 512 || NT == 1024, "table fill expects 512 or 1024 threads");
   constexpr int kPer = 16 / (NT / 512);
-  const int c = tid & 31, lo = (tid >> 5) & 15, j0 = (tid >> 9) * kPer;
-  const uint32_t lo_bits = nf4_bits(lo);
+  const int c = tid & 31, lo = (tid >> 5) & 15;
+  const int lo0 = __builtin_amdgcn_readfirstlane((tid >> 5) & 15);  // lanes 0-31; lanes 32-63 hold lo0 + 1
+  const int j0 = __builtin_amdgcn_readfirstlane(tid >> 9) * kPer;
+  const uint32_t b0 = nf4_bits(lo0), b1 = nf4_bits((lo0 + 1) & 15);
+  const uint32_t lo_bits = lo == lo0 ? b0 : b1;
 #pragma unroll
   for (int j = 0; j < kPer; ++j) lut[(lo + 16 * (j0 + j)) * 32 + c] = u32x2{lo_bits, nf4_bits(j0 + j)};
 }
