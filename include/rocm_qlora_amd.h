@@ -52,6 +52,12 @@ int rq_version(void);
 /* Target architecture the code objects were built for ("gfx950"). */
 const char* rq_build_arch(void);
 
+/* Identifier of the graph capture active on `stream`, 0 when none (no
+ * counterpart in the reference: for callers that keep one rq_nf4_linear
+ * workspace per captured graph, since a graph's replays reuse the
+ * workspace it was captured with). */
+int rq_stream_capture_id(hipStream_t stream, uint64_t* id);
+
 /* ------------------------------------------------------------------------
  * NF4 codec
  * ------------------------------------------------------------------------ */
@@ -118,7 +124,14 @@ int rq_int8_dequantize(const int8_t* q, const void* scales, int scales_dtype,
  * ------------------------------------------------------------------------ */
 
 /* Bytes of device workspace rq_nf4_linear needs for these sizes (0 when
- * none).  The caller allocates it (256-byte aligned) and passes it in. */
+ * none).  The caller allocates it (256-byte aligned) and passes it in.  Its
+ * first RQ_LINEAR_SYNC_BYTES are a synchronization area of the decode GEMV
+ * (a count and the LoRA down-projection's partials, exchanged between the
+ * workgroups of one launch): it must be zero before the workspace's first
+ * use, and every call leaves it zero once its kernels have finished, so a
+ * workspace is reused as it is by calls ordered on one stream.  Calls that
+ * may overlap need workspaces of their own. */
+#define RQ_LINEAR_SYNC_BYTES 65792
 int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, int64_t N, int64_t rank,
                                  int64_t* bytes);
 
@@ -145,6 +158,13 @@ int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   int64_t ld_lora_b, int lora_dtype, int64_t rank, float scaling,
                   void* y, int64_t ldy, void* workspace, int64_t workspace_bytes,
                   hipStream_t stream);
+
+/* Test hook, no counterpart in the reference: how many times a decode-GEMV
+ * workgroup polls for the workgroups that compute the LoRA down-projection
+ * inside the same launch before it computes the down-projection itself
+ * (the same sums in the same order).  0 forces that path.  Returns the
+ * previous value. */
+uint32_t rq_set_gemv_spin_limit(uint32_t polls);
 
 /* Bytes of device workspace rq_nf4_linear_dx needs (0 when none). */
 int rq_nf4_linear_dx_workspace_size(int dy_dtype, int64_t M, int64_t N, int64_t K, int64_t rank,

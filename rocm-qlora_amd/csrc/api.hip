@@ -18,3 +18,12 @@ extern "C" const char* rq_status_string(int status) {
 extern "C" int rq_version(void) { return 100; }
 
 extern "C" const char* rq_build_arch(void) { return "gfx950"; }
+
+extern "C" int rq_stream_capture_id(hipStream_t stream, uint64_t* id) {
+  if (!id) return RQ_ERR_NULL_POINTER;
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long cid = 0;
+  if (hipStreamGetCaptureInfo(stream, &status, &cid) != hipSuccess) return RQ_ERR_HIP;
+  *id = status == hipStreamCaptureStatusActive ? uint64_t(cid) : 0;
+  return RQ_OK;
+}

@@ -13,6 +13,8 @@
 // The weight operand is RND(T[code] * scale), the very value the reference's
 // dequantize_int4 + .to(x.dtype) produces (fp32 product, one RNE rounding);
 // only the order of the fp32 sums differs from the CPU GEMM.
+#include <algorithm>
+
 #include "rq_mfma.h"
 #include "rq_launch.h"
 #include "rq_linear.h"
@@ -98,6 +100,20 @@ struct GemvArgs {
   bool xvec;               // x rows 16-byte aligned (vector loads)
   int bvec_log2;           // LoRA B rows read as 16-byte chunks, 2^bvec_log2 per row (-1: by element)
   float* ws;               // [S, M, N] partials when !direct
+  // LoRA down-projection inside this launch (jt > 0): workgroup j < jt
+  // computes the fp32 partials of ranks [16 (j / u_splits), +16) over K split
+  // j % u_splits (the layout lora_u_kernel writes) into ubits, +0.0 stored
+  // as -0.0 so that 0 means "not written yet"; the tile workgroups (from jt
+  // on) poll their partials until none is 0.  Every workgroup then counts
+  // itself in *done; the last one clears ubits and *done, so both are zero
+  // again once the launch is over.
+  int jt;
+  uint32_t spin_limit;     // polls before a tile workgroup computes u itself
+  uint32_t* done;          // workgroups past their use of ubits
+  uint32_t* ubits;         // [u_splits, M, rank] partials as fp32 bits
+  const uint16_t* lora_x;
+  int ld_lora_x;
+  const void* lora_a;      // [rank, K]
   uint8_t unit_t[kGemvWaves][kGemvMaxU];  // tile slot of unit u of wave w (kGemvNoUnit: none)
   uint8_t unit_s[kGemvWaves][kGemvMaxU];  // segment (within the split) of unit u of wave w
 };
@@ -315,6 +331,81 @@ __device__ __forceinline__ f32x4 gemv_tile(const GemvUnit<Scale>& U, float s1, f
 // global load, which would serialize the prefetched units.)
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Polls of the ready counter before a tile workgroup gives up waiting for the
+// producers and computes u itself.  The producers have the lowest workgroup
+// indices and never wait, so they are dispatched first and finish; the bound
+// keeps the wait finite when the device is shared with other work.
+constexpr uint32_t kGemvSpinLimit = 1u << 16;
+
+// One LoRA down-projection job of the GEMV launch: the fp32 partial sums
+// x[m, k] RND(A[16 p + jj, k]) over the k of split s of `splits` (32-k steps
+// [S s / splits, S (s + 1) / splits)), the steps dealt to the 16 waves in
+// contiguous runs, four in flight at once, then the wave partials summed in
+// wave order through `red` (16 KiB of LDS).  Returns the sum for (m, jj) =
+// (tid / 16, tid % 16) in threads tid < 16 M.  Ends with red read: the
+// caller synchronizes before red is written again.
+template <int XT>
+__device__ __forceinline__ float lora_u_job(const GemvArgs& a, const LinearEpi& e, int p, int s, int splits, int tid,
+                                            int wave, float* red) {
+  const int lane = tid & 63, i16 = lane & 15, q = lane >> 4;
+  const int M = a.M, rank = e.rank;
+  const uint32_t K = uint32_t(a.K), nsteps = K / 32u;
+  const uint32_t j0 = nsteps * uint32_t(s) / uint32_t(splits), j1 = nsteps * uint32_t(s + 1) / uint32_t(splits);
+  const uint32_t s0 = j0 + (j1 - j0) * uint32_t(wave) / 16u, s1 = j0 + (j1 - j0) * uint32_t(wave + 1) / 16u;
+  const bool mlive = i16 < M;
+  const uint32_t j = uint32_t(16 * p + i16);
+  const bool jlive = j < uint32_t(rank);
+  const bool f32 = e.lora_dt == RQ_DTYPE_F32;
+  const uint32_t ab = f32 ? 4u : 2u;
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.lora_x, uint32_t(M - 1) * uint32_t(a.ld_lora_x) * 2u + K * 2u);
+  const __amdgpu_buffer_rsrc_t ar = buffer_rsrc(a.lora_a, uint32_t(rank) * K * ab);
+  const uint32_t xrow = uint32_t(i16) * uint32_t(a.ld_lora_x) * 2u, arow = j * K * ab;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (uint32_t b0 = s0; b0 < s1; b0 += 4) {
+    u32x4 xv[4], a0[4], a1[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const bool live = b0 + uint32_t(t) < s1;
+      const uint32_t k = 32u * (b0 + uint32_t(t)) + 8u * uint32_t(q);
+      xv[t] = buf_load16(xr, live && mlive ? xrow + 2u * k : kOobOffset);
+      // fp32 A: two 16-byte pieces of 4 values; 16-bit A: one piece of 8
+      a0[t] = buf_load16(ar, live && jlive ? arow + ab * k : kOobOffset);
+      a1[t] = buf_load16(ar, live && jlive && f32 ? arow + 4u * k + 16u : kOobOffset);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      // RND(A) in the activation dtype (lora_layer.py:67's A.to(x.dtype))
+      const u32x4 bop = f32 ? u32x4{cvt_pk<XT>(u2f(a0[t].x), u2f(a0[t].y)), cvt_pk<XT>(u2f(a0[t].z), u2f(a0[t].w)),
+                                    cvt_pk<XT>(u2f(a1[t].x), u2f(a1[t].y)), cvt_pk<XT>(u2f(a1[t].z), u2f(a1[t].w))}
+                            : a0[t];
+      acc = mfma16x16x32<XT>(xv[t], bop, acc);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = 4 * q + r;
+    if (m < M) red[(wave * 16 + m) * 16 + i16] = acc[r];
+  }
+  lds_barrier();
+  float v = 0.0f;
+  if (tid < M * 16) {
+#pragma unroll
+    for (int w = 0; w < kGemvWaves; ++w) v = __fadd_rn(v, red[w * 256 + tid]);
+  }
+  return v;
+}
+
+// Wave 0 of a workgroup that has counted itself in *done (old: the count
+// before it): the launch's last workgroup clears the partials and the count
+// for the next launch (every other workgroup is past its use of them).
+__device__ __forceinline__ void gemv_last_clears(const GemvArgs& a, const LinearEpi& e, int lane, uint32_t old) {
+  if (old != gridDim.x - 1u) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const uint32_t n = uint32_t(e.u_splits) * uint32_t(a.M) * uint32_t(e.rank);
+  for (uint32_t i = uint32_t(lane); i < n; i += 64u) a.ubits[i] = 0u;
+  if (lane == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <int XT, class Scale, int U, int XM>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
@@ -325,6 +416,28 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int M = a.M, TS = a.TS, nseg = a.nseg;
+  if (int(blockIdx.x) < a.jt) {
+    // a LoRA down-projection job: partials to ubits (device-coherent
+    // stores), then count this workgroup once they have all completed
+    const int j = blockIdx.x, ns = e.u_splits;
+    const float v = lora_u_job<XT>(a, e, j / ns, j % ns, ns, tid, wave, reinterpret_cast<float*>(smem));
+    const int jj = 16 * (j / ns) + (tid & 15);
+    if (tid < M * 16 && jj < e.rank) {
+      const uint32_t bits = f2u(v);
+      __hip_atomic_store(&a.ubits[((j % ns) * M + (tid >> 4)) * e.rank + jj], bits != 0u ? bits : 0x80000000u,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    }
+    __syncthreads();
+    if (wave == 0) {
+      uint32_t old = 0u;
+      if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      gemv_last_clears(a, e, lane, __builtin_amdgcn_readfirstlane(old));
+    }
+    return;
+  }
+  const bool fused = a.jt > 0;
+  const uint32_t g = blockIdx.x - uint32_t(a.jt), G = gridDim.x - uint32_t(a.jt);  // this tile workgroup, their number
   const int rank = (a.direct && e.rank > 0) ? e.rank : 0;  // LoRA staging only when fused here
   constexpr int RP = kGemvMaxFusedRank;                    // staging pitch
   constexpr bool kGather = GemvScale<Scale>::kGather;
@@ -338,6 +451,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   float* lbs = reinterpret_cast<float*>(xs0 + (XM == 1 ? kGemvWaves * M * kSegK : 0));
   float* bss = lbs + (rank > 0 ? TS * 16 * RP : 0);
   float* us = bss + TS * 16;
+  uint32_t* flag = reinterpret_cast<uint32_t*>(us + M * RP);  // in-launch LoRA: set when u is computed here
 
   GemvLane ln;
   ln.n16 = lane & 15;
@@ -362,7 +476,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   const uint32_t n_tiles = uint32_t((a.N + 15) / 16);
   // tiles g, g + G, ...: at any moment the workgroups' loads are spread over
   // the whole weight matrix
-  auto tile_of = [&](int t) -> uint32_t { return blockIdx.x + uint32_t(t) * gridDim.x; };
+  auto tile_of = [&](int t) -> uint32_t { return g + uint32_t(t) * G; };
   const __amdgpu_buffer_rsrc_t wres = buffer_rsrc(a.packed, uint32_t(a.N) * (uint32_t(a.K) >> 1));
   const GemvScale<Scale> sc(scale_src, uint32_t(a.N) * uint32_t(a.bpr));
   // this wave's units (wave-uniform; one dword of the table per wave, the
@@ -440,6 +554,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
 
   // 2. the table
   fill_f32pair_lut<kGemvThreads>(lut, tid);
+  if (fused && tid == 0) *flag = 0u;
   lds_barrier();
 
   // 3. epilogue operands, raw: LoRA B values (value t of thread tid is row
@@ -472,14 +587,15 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     br = buf_load_elem(bres, cn, (cb >> 4) < TS && cn < uint32_t(a.N), e.bias_dt);
   }
   const bool stage_u = rank > 0 && wave < M;
-  if (stage_u) {
+  auto load_u_partials = [&]() {
     const uint32_t ns = uint32_t(e.u_splits), stride = uint32_t(M) * uint32_t(rank);
     const __amdgpu_buffer_rsrc_t ures = buffer_rsrc(e.u, ns * stride * 4u);
     const uint32_t u_idx = uint32_t(wave) * uint32_t(rank) + uint32_t(lj);
 #pragma unroll
     for (int k = 0; k < kGemvMaxUSplits; ++k)
       up[k] = buf_load4(ures, (uint32_t(k) < ns && lj < rank) ? (uint32_t(k) * stride + u_idx) * 4u : kOobOffset);
-  }
+  };
+  if (stage_u && !fused) load_u_partials();
 
   // 4. the units, each as soon as its loads have landed; partials to LDS
   const uint32_t lane_off = uint32_t(lane & 31) * 8u;
@@ -524,7 +640,55 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
   }
 
-  // 5. epilogue operands into LDS, then one thread per output (tile slot
+  // 5. with the LoRA down-projection in this launch: the waves m < M poll
+  //    their partials (device-coherent loads) until none reads 0 -- a
+  //    bounded poll -- and thread 0 counts the workgroup past its use of
+  //    them.  A workgroup in which a poll gave up runs every job itself, in
+  //    the producers' order (the same sums), in the table's LDS, which the
+  //    unit loop no longer reads.
+  float* ufl = reinterpret_cast<float*>(lut) + kGemvWaves * 256;  // [M][RP] sums, own u only
+  uint32_t self_u = 0u, done_old = 0u;
+  if (fused) {
+    if (stage_u && lj < rank) {
+      const uint32_t ns = uint32_t(e.u_splits), stride = uint32_t(M) * uint32_t(rank);
+      const uint32_t u_idx = uint32_t(wave) * uint32_t(rank) + uint32_t(lj);
+      bool ok = false;
+      for (uint32_t i = 0;; ++i) {
+        // all the loads of a poll in flight together: no branch between
+        // them (a split past ns reads split 0 again and is not checked)
+#pragma unroll
+        for (int k = 0; k < kGemvMaxUSplits; ++k)
+          up[k] = __hip_atomic_load(&a.ubits[(uint32_t(k) < ns ? uint32_t(k) * stride : 0u) + u_idx],
+                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t missing = 0u;
+#pragma unroll
+        for (int k = 0; k < kGemvMaxUSplits; ++k) missing |= uint32_t(up[k] == 0u) & uint32_t(uint32_t(k) < ns);
+        ok = missing == 0u;
+        if (ok || i >= a.spin_limit) break;
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (!ok) *flag = 1u;
+    }
+    lds_barrier();
+    self_u = __builtin_amdgcn_readfirstlane(*flag);
+    if (tid == 0) done_old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (self_u) {
+      float* red = reinterpret_cast<float*>(lut);
+      const int ns = e.u_splits;
+      for (int pg = 0; pg < (rank + 15) / 16; ++pg) {
+        float sum = 0.0f;
+        for (int sp = 0; sp < ns; ++sp) {
+          sum = __fadd_rn(sum, lora_u_job<XT>(a, e, pg, sp, ns, tid, wave, red));
+          lds_barrier();
+        }
+        const int jj = 16 * pg + (tid & 15);
+        if (tid < M * 16 && jj < rank) ufl[(tid >> 4) * RP + jj] = sum;
+      }
+      lds_barrier();
+    }
+  }
+
+  // 6. epilogue operands into LDS, then one thread per output (tile slot
   //    t = tid / 256, row m, column nn).  The empty asm marks the raw values
   //    as changed here, so that no use of them (which waits for its load)
   //    is scheduled into the unit loop above.
@@ -552,51 +716,58 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
 #pragma unroll
     for (int k = 0; k < kGemvMaxUSplits; ++k)
       if (k < e.u_splits) sum = __fadd_rn(sum, u2f(up[k]));
+    if (self_u) sum = ufl[wave * RP + lj];
     us[tid] = lj < rank ? round_x<XT>(sum) : 0.0f;
   }
   lds_barrier();
 
-  const int t = tid >> 8, m = (tid >> 4) & 15, nn = tid & 15;
-  if (t >= TS || m >= M) return;
-  const uint32_t tile = tile_of(t);
-  const int64_t n = int64_t(tile) * 16 + nn;
-  if (tile >= n_tiles || n >= a.N) return;
-  const float* pp = part + t * nseg * M * 16 + m * 16 + nn;
-  float v = 0.0f;
-  int sgi = 0;
-  for (; sgi + 8 <= nseg; sgi += 8) {
-    float p[8];
+  // 7. the outputs, then (in-launch LoRA) wave 0 learns whether this was
+  //    the launch's last workgroup to count itself
+  auto finish = [&]() {
+    const int t = tid >> 8, m = (tid >> 4) & 15, nn = tid & 15;
+    if (t >= TS || m >= M) return;
+    const uint32_t tile = tile_of(t);
+    const int64_t n = int64_t(tile) * 16 + nn;
+    if (tile >= n_tiles || n >= a.N) return;
+    const float* pp = part + t * nseg * M * 16 + m * 16 + nn;
+    float v = 0.0f;
+    int sgi = 0;
+    for (; sgi + 8 <= nseg; sgi += 8) {
+      float p[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) p[j] = pp[(sgi + j) * M * 16];
+      for (int j = 0; j < 8; ++j) p[j] = pp[(sgi + j) * M * 16];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v = __fadd_rn(v, p[j]);
-  }
-  for (; sgi < nseg; ++sgi) v = __fadd_rn(v, pp[sgi * M * 16]);
-  if (!a.direct) {
-    a.ws[(int64_t(blockIdx.y) * a.M + m) * a.N + n] = v;
-    return;
-  }
-  if (e.bias) v = __fadd_rn(v, bss[t * 16 + nn]);
-  v = round_x<XT>(v);
-  if (rank > 0) {
-    const float* brow = lbs + (t * 16 + nn) * RP;
-    const float* urow = us + m * RP;
-    float l = 0.0f;
-    for (int j0 = 0; j0 < rank; j0 += 8) {
-      float uu[8], bb[8];
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj) {
-        uu[jj] = urow[j0 + jj];
-        bb[jj] = brow[j0 + jj];
-      }
-#pragma unroll
-      for (int jj = 0; jj < 8; ++jj)
-        if (j0 + jj < rank) l = __fmaf_rn(uu[jj], bb[jj], l);
+      for (int j = 0; j < 8; ++j) v = __fadd_rn(v, p[j]);
     }
-    l = round_x<XT>(__fmul_rn(round_x<XT>(l), e.scaling));
-    v = round_x<XT>(__fadd_rn(v, l));
-  }
-  static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
+    for (; sgi < nseg; ++sgi) v = __fadd_rn(v, pp[sgi * M * 16]);
+    if (!a.direct) {
+      a.ws[(int64_t(blockIdx.y) * a.M + m) * a.N + n] = v;
+      return;
+    }
+    if (e.bias) v = __fadd_rn(v, bss[t * 16 + nn]);
+    v = round_x<XT>(v);
+    if (rank > 0) {
+      const float* brow = lbs + (t * 16 + nn) * RP;
+      const float* urow = us + m * RP;
+      float l = 0.0f;
+      for (int j0 = 0; j0 < rank; j0 += 8) {
+        float uu[8], bb[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          uu[jj] = urow[j0 + jj];
+          bb[jj] = brow[j0 + jj];
+        }
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          if (j0 + jj < rank) l = __fmaf_rn(uu[jj], bb[jj], l);
+      }
+      l = round_x<XT>(__fmul_rn(round_x<XT>(l), e.scaling));
+      v = round_x<XT>(__fadd_rn(v, l));
+    }
+    static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
+  };
+  finish();
+  if (fused && wave == 0) gemv_last_clears(a, e, lane, __builtin_amdgcn_readfirstlane(done_old));
 }
 
 // Split-K finisher (and the LoRA epilogue for any M): y = finish(sum_s
@@ -712,10 +883,18 @@ __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict_
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+static uint32_t gemv_spin_limit = kGemvSpinLimit;
+
+uint32_t set_gemv_spin_limit(uint32_t polls) {
+  const uint32_t old = gemv_spin_limit;
+  gemv_spin_limit = polls;
+  return old;
+}
+
 // Work plan of the GEMV: K splits, tiles per workgroup, units per wave, the
 // unit table, the activation stage, and the workspace layout.
 GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool xvec, bool gather,
-                   bool lora_vec) {
+                   bool lora_vec, bool lora_prod) {
   GemvPlan p{};
   const int nsegs = int((K + kSegK - 1) / kSegK);
   const int64_t tiles = (N + 15) / 16;
@@ -727,6 +906,9 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     p.u_splits = int(ks < kGemvMaxUSplits ? ks : kGemvMaxUSplits);
   }
   const bool lora_fusable = rank <= 0 || (rank <= kGemvMaxFusedRank && lora_vec);
+  // K splits of the down-projection when it runs inside the GEMV launch:
+  // about 1024 k per producer workgroup
+  const int fused_splits = int(std::min<int64_t>((K + 1023) / 1024, kGemvMaxUSplits));
   for (int slice = 1; slice >= 0; --slice) {
     // activations through the waves' LDS slices: any unit to any wave
     const bool xslice = slice != 0;
@@ -738,21 +920,36 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     const int R = kGemvWaves / nseg;  // tile slots per round without the slices
     const int ts_cap = xslice ? (kGemvWaves * kGemvMaxU) / nseg : kGemvMaxU * R;
     const bool direct = S == 1 && lora_fusable;
-    int best = 0;
+    // the down-projection's producer workgroups need compute units the tile
+    // workgroups leave free (else the last tiles would start only after the
+    // producers end): the first pass looks for such a plan, the second runs
+    // the down-projection as its own kernel
+    const bool prod_fits = size_t(M) * rank * fused_splits * 4 <= kLinearSyncBytes - kLinearCountBytes;
+    const int jt = (direct && rank > 0 && lora_prod && prod_fits) ? int((rank + 15) / 16) * fused_splits : 0;
+    int best = 0, best_jt = 0;
     int64_t best_cost = 0;
-    for (int TS = 1; TS <= kGemvMaxTS && TS <= ts_cap; ++TS) {
-      const int U = xslice ? (TS * nseg + kGemvWaves - 1) / kGemvWaves : (TS + R - 1) / R;
-      if (U != 1 && U != 2 && U != 4) continue;
-      if (gemv_lds_bytes(TS, nseg, int(M), gather, xslice, direct && rank > 0) > size_t(kGemvLdsBudget)) continue;
-      // tiles a compute unit works through one after another
-      const int64_t grid = (tiles + TS - 1) / TS;
-      const int64_t cost = ((grid * S + ncu - 1) / ncu) * TS;
-      if (best == 0 || cost <= best_cost) {
-        best = TS;
-        best_cost = cost;
+    for (int pass = jt > 0 ? 0 : 1; pass < 2 && best == 0; ++pass) {
+      const int pj = pass == 0 ? jt : 0;
+      for (int TS = 1; TS <= kGemvMaxTS && TS <= ts_cap; ++TS) {
+        const int U = xslice ? (TS * nseg + kGemvWaves - 1) / kGemvWaves : (TS + R - 1) / R;
+        if (U != 1 && U != 2 && U != 4) continue;
+        if (gemv_lds_bytes(TS, nseg, int(M), gather, xslice, direct && rank > 0) + (pj > 0 ? 16 : 0) >
+            size_t(kGemvLdsBudget))
+          continue;
+        // tiles a compute unit works through one after another
+        const int64_t grid = (tiles + TS - 1) / TS;
+        if (pj > 0 && grid * S + pj > ncu) continue;
+        const int64_t cost = ((grid * S + ncu - 1) / ncu) * TS;
+        if (best == 0 || cost <= best_cost) {
+          best = TS;
+          best_cost = cost;
+          best_jt = pj;
+        }
       }
     }
     if (best == 0) continue;
+    p.jt = best_jt;
+    if (p.jt > 0) p.u_splits = fused_splits;
     p.S = S;
     p.nseg = nseg;
     p.TS = best;
@@ -782,9 +979,18 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     break;
   }
   p.lds_bytes = gemv_lds_bytes(p.TS, p.nseg, int(M), gather, p.xslice, p.direct && rank > 0);
-  p.ws_bytes = p.direct ? 0 : size_t(p.S) * M * N * 4;
-  p.u_offset = (p.ws_bytes + 255) & ~size_t(255);
-  if (rank > 0) p.ws_bytes = p.u_offset + size_t(p.u_splits) * M * rank * 4;
+  if (p.jt > 0) {
+    // the wait flag after RND(u); the producers' 16 KiB wave partials
+    p.lds_bytes += 16;
+    if (p.lds_bytes < size_t(kGemvWaves) * 256 * 4) p.lds_bytes = size_t(kGemvWaves) * 256 * 4;
+  }
+  // workspace: the synchronization area (the in-launch down-projection's
+  // count and partials, left zero by every launch), the split-K partials,
+  // the partials of lora_u_kernel
+  const size_t parts = p.direct ? 0 : size_t(p.S) * M * N * 4;
+  const size_t uparts = (rank > 0 && p.jt == 0) ? size_t(p.u_splits) * M * rank * 4 : 0;
+  p.u_offset = kLinearSyncBytes + ((parts + 255) & ~size_t(255));
+  p.ws_bytes = p.jt > 0 ? kLinearSyncBytes : (parts + uparts > 0 ? p.u_offset + uparts : 0);
   return p;
 }
 
@@ -824,14 +1030,14 @@ static int launch_gemv_u(const GemvArgs& a, const GemvPlan& p, Scale scale, cons
       return RQ_ERR_HIP;
     attr_set = true;
   }
-  dim3 grid(unsigned(p.grid), unsigned(p.S));
+  dim3 grid(unsigned(p.grid + p.jt), unsigned(p.S));
   kern<<<grid, kGemvThreads, p.lds_bytes, stream>>>(a, scale, e);
   return rq_check_launch();
 }
 
 template <int XT, class Scale>
 static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, const LinearEpi& e,
-                         float* ws, hipStream_t stream) {
+                         float* ws, void* sync, hipStream_t stream) {
   GemvArgs a{};
   a.x = static_cast<const uint16_t*>(L.x);
   a.ldx = int(L.ldx);
@@ -846,6 +1052,13 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.direct = p.direct;
   a.xvec = gemv_xvec(L);
   a.bvec_log2 = gemv_bvec_log2(L);
+  a.jt = p.jt;
+  a.spin_limit = gemv_spin_limit;
+  a.done = static_cast<uint32_t*>(sync);
+  a.ubits = reinterpret_cast<uint32_t*>(static_cast<char*>(sync) + kLinearCountBytes);
+  a.lora_x = static_cast<const uint16_t*>(L.lora_x);
+  a.ld_lora_x = int(L.ld_lora_x);
+  a.lora_a = L.lora_a;
   a.ws = ws;
   for (int w = 0; w < kGemvWaves; ++w)
     for (int u = 0; u < kGemvMaxU; ++u) {
@@ -867,22 +1080,23 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
 }
 
 template <int XT>
-static int run_gemv(const LinearArgs& L, const GemvPlan& p, const LinearEpi& e, float* ws, hipStream_t stream) {
+static int run_gemv(const LinearArgs& L, const GemvPlan& p, const LinearEpi& e, float* ws, void* sync,
+                    hipStream_t stream) {
   if (L.c2) {
     const int sh = pow2_shift(L.block2);
     switch (L.absmax_dtype) {
       case RQ_DTYPE_F32:
-        return launch_gemv_t<XT>(L, p, ScaleDQ<RQ_DTYPE_F32>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, ws, stream);
+        return launch_gemv_t<XT>(L, p, ScaleDQ<RQ_DTYPE_F32>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, ws, sync, stream);
       case RQ_DTYPE_BF16:
-        return launch_gemv_t<XT>(L, p, ScaleDQ<RQ_DTYPE_BF16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, ws, stream);
+        return launch_gemv_t<XT>(L, p, ScaleDQ<RQ_DTYPE_BF16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, ws, sync, stream);
       default:
-        return launch_gemv_t<XT>(L, p, ScaleDQ<RQ_DTYPE_F16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, ws, stream);
+        return launch_gemv_t<XT>(L, p, ScaleDQ<RQ_DTYPE_F16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, ws, sync, stream);
     }
   }
   switch (L.absmax_dtype) {
-    case RQ_DTYPE_F32: return launch_gemv_t<XT>(L, p, ScaleAbsmax<RQ_DTYPE_F32>{L.absmax}, e, ws, stream);
-    case RQ_DTYPE_BF16: return launch_gemv_t<XT>(L, p, ScaleAbsmax<RQ_DTYPE_BF16>{L.absmax}, e, ws, stream);
-    default: return launch_gemv_t<XT>(L, p, ScaleAbsmax<RQ_DTYPE_F16>{L.absmax}, e, ws, stream);
+    case RQ_DTYPE_F32: return launch_gemv_t<XT>(L, p, ScaleAbsmax<RQ_DTYPE_F32>{L.absmax}, e, ws, sync, stream);
+    case RQ_DTYPE_BF16: return launch_gemv_t<XT>(L, p, ScaleAbsmax<RQ_DTYPE_BF16>{L.absmax}, e, ws, sync, stream);
+    default: return launch_gemv_t<XT>(L, p, ScaleAbsmax<RQ_DTYPE_F16>{L.absmax}, e, ws, sync, stream);
   }
 }
 
@@ -941,9 +1155,12 @@ int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream) {
 int gemv_workspace(const LinearArgs& L, size_t* bytes) {
   // the plan depends on the activations' alignment, unknown here: the larger
   // of the two
-  const GemvPlan p0 = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), false, false, false);
-  const GemvPlan p1 = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), true, false, false);
-  *bytes = p0.ws_bytes > p1.ws_bytes ? p0.ws_bytes : p1.ws_bytes;
+  size_t b = 0;
+  for (int c = 0; c < 8; ++c) {
+    const GemvPlan p = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), c & 1, false, c & 2, c & 4);
+    b = std::max(b, p.ws_bytes);
+  }
+  *bytes = b;
   return RQ_OK;
 }
 
@@ -953,17 +1170,21 @@ int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   // ... and the activations, LoRA B and bias with 32-bit offsets too
   if ((L.M - 1) * L.ldx + L.K > (int64_t(1) << 29)) return RQ_ERR_UNSUPPORTED;
   if (L.rank > 0 && L.N * L.ld_lora_b > (int64_t(1) << 29)) return RQ_ERR_UNSUPPORTED;
+  // the down-projection runs inside the GEMV launch when the x rows and A
+  // are 16-byte aligned (its producers read both 16 bytes at a time)
+  const bool lora_prod = L.rank > 0 && aligned(L.lora_x, 16) && L.ld_lora_x % 8 == 0 && aligned(L.lora_a, 16);
   const GemvPlan p = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), gemv_xvec(L), L.c2 == nullptr,
-                               gemv_bvec_log2(L) >= 0);
+                               gemv_bvec_log2(L) >= 0, lora_prod);
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
   if (workspace && !aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;
-  float* ws = static_cast<float*>(workspace);
-  float* up = L.rank > 0 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.u_offset) : nullptr;
+  char* wsb = static_cast<char*>(workspace);
+  float* ws = p.direct ? nullptr : reinterpret_cast<float*>(wsb + kLinearSyncBytes);
+  float* up = L.rank > 0 ? reinterpret_cast<float*>(wsb + p.u_offset) : nullptr;
   int st;
-  if (L.rank > 0 && (st = run_lora_u(L, p.u_splits, up, stream)) != RQ_OK) return st;
+  if (L.rank > 0 && p.jt == 0 && (st = run_lora_u(L, p.u_splits, up, stream)) != RQ_OK) return st;
   const LinearEpi e = make_epi(L, up, p.u_splits);
-  if (L.x_dtype == RQ_DTYPE_BF16) st = run_gemv<RQ_DTYPE_BF16>(L, p, e, ws, stream);
-  else st = run_gemv<RQ_DTYPE_F16>(L, p, e, ws, stream);
+  if (L.x_dtype == RQ_DTYPE_BF16) st = run_gemv<RQ_DTYPE_BF16>(L, p, e, ws, workspace, stream);
+  else st = run_gemv<RQ_DTYPE_F16>(L, p, e, ws, workspace, stream);
   if (st != RQ_OK || p.direct) return st;
   if (L.x_dtype == RQ_DTYPE_BF16) return launch_splitk_epilogue<RQ_DTYPE_BF16>(L, p, e, ws, stream);
   return launch_splitk_epilogue<RQ_DTYPE_F16>(L, p, e, ws, stream);
@@ -996,6 +1217,8 @@ static LinearArgs pack_linear_args(const void* x, int x_dtype, int64_t M, int64_
   return L;
 }
 
+extern "C" uint32_t rq_set_gemv_spin_limit(uint32_t polls) { return set_gemv_spin_limit(polls); }
+
 extern "C" int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, int64_t N, int64_t rank,
                                             int64_t* bytes) {
   if (!bytes) return RQ_ERR_NULL_POINTER;
@@ -1005,6 +1228,7 @@ extern "C" int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, i
   LinearArgs L{};
   L.x_dtype = x_dtype; L.M = M; L.K = K; L.N = N; L.rank = rank;
   int st = M <= kGemvMaxM ? gemv_workspace(L, &b) : gemm_workspace(L, &b);
+  if (M > kGemvMaxM && b > 0) b += kLinearSyncBytes;
   *bytes = int64_t(b);
   return st;
 }
@@ -1023,5 +1247,8 @@ extern "C" int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, i
   if (st != RQ_OK || M == 0) return st;
   if (workspace_bytes < 0) return RQ_ERR_BAD_SHAPE;
   if (M <= kGemvMaxM) return run_nf4_gemv(L, workspace, size_t(workspace_bytes), stream);
-  return run_nf4_gemm(L, workspace, size_t(workspace_bytes), stream);
+  // the GEMM's workspace follows the synchronization words
+  return run_nf4_gemm(L, workspace ? static_cast<char*>(workspace) + kLinearSyncBytes : nullptr,
+                      size_t(workspace_bytes) > kLinearSyncBytes ? size_t(workspace_bytes) - kLinearSyncBytes : 0,
+                      stream);
 }

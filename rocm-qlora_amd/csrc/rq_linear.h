@@ -12,6 +12,14 @@ namespace rq {
 // the MFMA GEMM.
 constexpr int64_t kGemvMaxM = 16;
 
+// rq_nf4_linear's workspace starts with RQ_LINEAR_SYNC_BYTES of
+// synchronization area: zero before a call, zero again once its kernels are
+// done.  The decode GEMV's in-launch LoRA down-projection keeps its count in
+// the first kLinearCountBytes and its partials after them; the GEMM and the
+// split-K partials start after the area.
+constexpr size_t kLinearSyncBytes = RQ_LINEAR_SYNC_BYTES;
+constexpr size_t kLinearCountBytes = 256;
+
 // Unpacked arguments of rq_nf4_linear (see include/rocm_qlora_amd.h).
 struct LinearArgs {
   const void* x;
@@ -55,13 +63,18 @@ struct LinearEpi {
 
 struct GemvPlan {
   int S, TS, U, nseg, grid, u_splits;
+  int jt;  // LoRA down-projection workgroups inside the launch (0: lora_u_kernel)
   bool direct, xslice;
   size_t lds_bytes, ws_bytes, u_offset;
   uint8_t unit_t[16][4], unit_s[16][4];  // (tile slot, segment) of unit u of wave w; 0xFF: none
 };
 
 GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool xvec, bool gather,
-                   bool lora_vec);
+                   bool lora_vec, bool lora_prod);
+// Polls of the GEMV's wait for its LoRA producers before a workgroup computes
+// the down-projection itself (a test hook: 0 forces that path).  Returns the
+// previous value.
+uint32_t set_gemv_spin_limit(uint32_t polls);
 int validate_linear(const LinearArgs& L);
 LinearEpi make_epi(const LinearArgs& L, float* u_parts, int u_splits);
 int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream);

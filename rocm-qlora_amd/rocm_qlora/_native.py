@@ -40,6 +40,8 @@ SIGNATURES = {
                       _P, _I32,                              # bias, dtype
                       _P, _I64, _P, _P, _I64, _I32, _I64, _F32,  # lora x, ld, A, B, ldB, dtype, rank, scaling
                       _P, _I64, _P, _I64, _P],               # y, ldy, workspace, bytes, stream
+    "rq_set_gemv_spin_limit": [ctypes.c_uint32],
+    "rq_stream_capture_id": [_P, _P],
     "rq_nf4_linear_dx_workspace_size": [_I32, _I64, _I64, _I64, _I64, _P],
     "rq_nf4_linear_dx": [_P, _I32, _I64, _I64, _I64,         # dy, dtype, M, N, lddy
                          _P, _I64, _I64, _P, _I32,           # packed, K, block, absmax, dtype
@@ -56,7 +58,8 @@ SIGNATURES = {
                       _P, _I64, _P, _P, _I32,                # codes, N, w scale, bias, dtype
                       _P, _I64, _P, _I64, _P],               # y, ldy, workspace, bytes, stream
 }
-_RESTYPE = {"rq_status_string": ctypes.c_char_p, "rq_build_arch": ctypes.c_char_p}
+_RESTYPE = {"rq_status_string": ctypes.c_char_p, "rq_build_arch": ctypes.c_char_p,
+            "rq_set_gemv_spin_limit": ctypes.c_uint32}
 
 _lib: Optional[ctypes.CDLL] = None
 _lock = threading.Lock()
@@ -103,6 +106,20 @@ def call(name: str, *args) -> None:
     status = getattr(load(), name)(*args)
     if status != 0:
         raise RuntimeError(f"{name} failed: {status_string(status)} (status {status})")
+
+
+def set_gemv_spin_limit(polls: int) -> int:
+    """Test hook: polls of the decode GEMV's wait for its in-launch LoRA
+    down-projection before a workgroup computes it itself (0 forces that).
+    Returns the previous value."""
+    return int(load().rq_set_gemv_spin_limit(polls))
+
+
+def capture_id(device: torch.device) -> int:
+    """Identifier of the graph capture active on the current stream (0: none)."""
+    cid = ctypes.c_uint64(0)
+    call("rq_stream_capture_id", stream_handle(device), ctypes.byref(cid))
+    return int(cid.value)
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -28,13 +28,69 @@ def _rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
     return t2, (t2.stride(0) if t2.shape[0] > 1 else K)
 
 
+# rq_nf4_linear's workspace per (device, stream): its first
+# RQ_LINEAR_SYNC_BYTES (include/rocm_qlora_amd.h) are a synchronization area
+# that must be zero before a call and is zero again after it, so one buffer,
+# its area zeroed once, serves every call ordered on the stream.  It grows
+# by reallocation; a dropped buffer returns to torch's caching allocator,
+# which reuses it only after the work already queued on the stream.
+#
+# A graph capture gets a buffer of its own, shared by the calls it captures
+# and reused by every replay: a spare that eager calls zeroed beforehand (so
+# the graph records no fill), or, when no spare is large enough, one from
+# the graph's memory pool zeroed by a fill kernel recorded in the graph.  A
+# spare given to a capture is held for the life of the process (the graph's
+# replays may come at any time).
+LINEAR_SYNC_BYTES = 65792
+_LINEAR_WS: dict = {}
+_CAPTURE_WS: dict = {}
+_SPARES: dict = {}
+_HELD_BY_GRAPHS: list = []
+_N_SPARES = 2
+_WS_MIN_BYTES = 1 << 20
+
+
+def _zeroed_area(nbytes: int, dev) -> torch.Tensor:
+    ws = torch.empty(max(nbytes, _WS_MIN_BYTES), dtype=torch.uint8, device=dev)
+    ws[:LINEAR_SYNC_BYTES].zero_()
+    return ws
+
+
 def _workspace(x_dtype: torch.dtype, M: int, K: int, N: int, rank: int, dev) -> Optional[torch.Tensor]:
     import ctypes
     nbytes = ctypes.c_int64(0)
     nat.call("rq_nf4_linear_workspace_size", nat.dtype_code(x_dtype), M, K, N, rank, ctypes.byref(nbytes))
-    if nbytes.value == 0:
+    need = nbytes.value
+    if need == 0:
         return None
-    return torch.empty(nbytes.value, dtype=torch.uint8, device=dev)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if torch.cuda.is_current_stream_capturing():
+        cid = nat.capture_id(dev)
+        ws = _CAPTURE_WS.get(idx)
+        if ws is None or ws[0] != cid or ws[1].numel() < need:
+            spares = _SPARES.get(idx, [])
+            fit = next((i for i, b in enumerate(spares) if b.numel() >= need), None)
+            if fit is not None:
+                buf = spares.pop(fit)
+                _HELD_BY_GRAPHS.append(buf)
+            else:
+                buf = _zeroed_area(need, dev)  # stays in the graph's pool
+            ws = (cid, buf)
+            _CAPTURE_WS[idx] = ws
+        return ws[1]
+    key = (idx, torch.cuda.current_stream(dev).cuda_stream)
+    ws = _LINEAR_WS.get(key)
+    if ws is None or ws.numel() < need:
+        ws = _zeroed_area(max(need, 2 * ws.numel() if ws is not None else 0), dev)
+        _LINEAR_WS[key] = ws
+    spares = _SPARES.setdefault(idx, [])
+    if len(spares) < _N_SPARES or any(b.numel() < need for b in spares):
+        spares[:] = [b for b in spares if b.numel() >= need]
+        while len(spares) < _N_SPARES:
+            spares.append(_zeroed_area(need, dev))
+        # a capture on another stream may take a spare: its fill must be done
+        torch.cuda.synchronize(dev)
+    return ws
 
 
 def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optional[torch.Tensor],

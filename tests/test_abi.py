@@ -30,6 +30,25 @@ def test_python_signatures_cover_header():
     assert set(declared_symbols()) <= set(nat.SIGNATURES)
 
 
+def test_linear_sync_area_size_matches_header():
+    from rocm_qlora import ops
+    m = re.search(r"#define RQ_LINEAR_SYNC_BYTES (\d+)", HEADER.read_text())
+    assert m and int(m.group(1)) == ops.LINEAR_SYNC_BYTES
+
+
+def test_linear_workspace_holds_sync_area():
+    """A GEMV with LoRA needs at least the synchronization area; a GEMM that
+    needs workspace gets it after the area."""
+    from rocm_qlora import ops
+    nb = ctypes.c_int64(0)
+    nat.call("rq_nf4_linear_workspace_size", nat.DTYPE_BF16, 1, 4096, 4096, 16, ctypes.byref(nb))
+    assert nb.value >= ops.LINEAR_SYNC_BYTES
+    nat.call("rq_nf4_linear_workspace_size", nat.DTYPE_BF16, 1, 4096, 4096, 0, ctypes.byref(nb))
+    assert nb.value == 0
+    nat.call("rq_nf4_linear_workspace_size", nat.DTYPE_BF16, 2048, 4096, 4096, 64, ctypes.byref(nb))
+    assert nb.value > ops.LINEAR_SYNC_BYTES
+
+
 def test_status_strings_and_version():
     assert nat.status_string(0) == "ok"
     assert "dtype" in nat.status_string(2)

@@ -1,0 +1,188 @@
+"""The decode GEMV with the LoRA down-projection u = x A^T computed inside the
+same launch (producer workgroups hand their partials to the tile workgroups
+through the workspace's zeroed synchronization area).  Checked against the oracle's
+QuantLinear.forward + LoRALinear.forward (quant_linear.py:182-197,
+lora_layer.py:60-70) at rtol = atol = 1e-2 in the activation dtype, and
+against the library's own other paths bit for bit:
+
+- calls in a row on one stream (the counters return to zero after each);
+- the workgroups' own computation of u when the producers' report is not
+  awaited (polls forced to 0), which must give the same bits;
+- replays of a captured HIP graph with new inputs, against eager calls;
+- operands the producers cannot read 16 bytes at a time, which run the
+  down-projection as its own kernel.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import qlora_ref as R
+from rocm_qlora import _native as nat
+from rocm_qlora import ops
+from rocm_qlora.quantization import quantize_int4
+
+pytestmark = pytest.mark.gpu
+
+RTOL = ATOL = 1e-2
+
+
+def _layer(N, K, rank, seed, dev, lora_dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(N, K, generator=g) * 0.02
+    a = torch.empty(rank, K)
+    torch.nn.init.kaiming_uniform_(a, a=math.sqrt(5), generator=g)
+    b = torch.randn(N, rank, generator=g) * 0.01
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    return packed, absmax, a.to(lora_dtype), b.to(lora_dtype)
+
+
+def _x(M, K, seed, dtype=torch.bfloat16):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(M, K, generator=g).to(dtype)
+
+
+def _check(got, ref):
+    got = got.cpu().float()
+    ref = ref.float()
+    assert got.shape == ref.shape
+    err = (got - ref).abs()
+    bad = err > ATOL + RTOL * ref.abs()
+    assert not bad.any(), f"{int(bad.sum())} of {bad.numel()} outside tol; max err {float(err.max()):.4g}"
+
+
+def _sync_words_zero(dev):
+    torch.cuda.synchronize(dev)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(dev).cuda_stream)
+    ws = ops._LINEAR_WS.get(key)
+    assert ws is not None
+    assert int(ws[:ops.LINEAR_SYNC_BYTES].cpu().count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("K,N,M,rank", [
+    (4096, 4096, 1, 16),     # q / o: two tiles per workgroup leave room for the producers
+    (4096, 14336, 1, 16),    # gate / up
+    (4096, 1024, 2, 16),     # k / v
+    (4096, 4096, 5, 8),      # activations as register operands
+    (4096, 1024, 16, 64),    # four rank groups x four K splits of producers
+    (1024, 512, 3, 32),
+])
+def test_calls_in_a_row(dev, K, N, M, rank):
+    print(f"in-launch lora K={K} N={N} M={M} rank={rank}", flush=True)
+    packed, absmax, a, b = _layer(N, K, rank, seed=K + N + rank, dev=dev)
+    ad, bd = a.to(dev), b.to(dev)
+    for i in range(3):
+        x = _x(M, K, seed=100 * i + M)
+        y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0)
+        ref = R.nf4_lora_linear(x, packed.cpu(), absmax.cpu(), None, a, b, 2.0, N, 64)
+        _check(y, ref)
+    _sync_words_zero(dev)
+
+
+@pytest.mark.parametrize("K,N,M,rank,lora_dtype", [
+    (4096, 4096, 1, 16, torch.float32),
+    (4096, 1024, 4, 64, torch.float32),
+    (2048, 768, 2, 16, torch.bfloat16),
+])
+def test_workgroups_own_u_same_bits(dev, K, N, M, rank, lora_dtype):
+    """Polls forced to 0: every tile workgroup computes u itself, job by job
+    in the producers' order, so y is bit-identical to the awaited path."""
+    print(f"own-u K={K} N={N} M={M} rank={rank} {lora_dtype}", flush=True)
+    packed, absmax, a, b = _layer(N, K, rank, seed=7 + K, dev=dev, lora_dtype=lora_dtype)
+    x = _x(M, K, seed=3).to(dev)
+    ad, bd = a.to(dev), b.to(dev)
+    y0 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
+    old = nat.set_gemv_spin_limit(0)
+    try:
+        y1 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
+        y2 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
+    finally:
+        nat.set_gemv_spin_limit(old)
+    y3 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
+    assert torch.equal(y0, y1) and torch.equal(y0, y2) and torch.equal(y0, y3)
+    _sync_words_zero(dev)
+    ref = R.nf4_lora_linear(x.cpu(), packed.cpu(), absmax.cpu(), None, a, b, 0.5, N, 64)
+    _check(y1, ref)
+
+
+def test_graph_replays_match_eager(dev):
+    K, N, M, rank = 4096, 4096, 1, 16
+    packed, absmax, a, b = _layer(N, K, rank, seed=11, dev=dev)
+    ad, bd = a.to(dev), b.to(dev)
+    xs = torch.zeros(M, K, dtype=torch.bfloat16, device=dev)
+    side = torch.cuda.Stream(dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for _ in range(2):  # warm the allocator and the kernels outside the capture
+            ops.nf4_linear(xs, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0)
+    torch.cuda.current_stream(dev).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ys = ops.nf4_linear(xs, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0)
+    for i in range(4):
+        x = _x(M, K, seed=50 + i).to(dev)
+        xs.copy_(x)
+        graph.replay()
+        got = ys.clone()
+        torch.cuda.synchronize(dev)
+        want = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0)
+        torch.cuda.synchronize(dev)
+        assert torch.equal(got, want), f"replay {i} differs from the eager call"
+    _sync_words_zero(dev)
+
+
+def test_two_graphs_replayed_in_turn(dev):
+    """Two captures take workspaces of their own (spares zeroed by eager
+    calls beforehand); replays of either, in turn, match eager calls."""
+    K, M, rank = 4096, 2, 16
+    shapes = [(4096, 11), (14336, 12)]
+    layers = [(N,) + _layer(N, K, rank, seed=s, dev=dev) for N, s in shapes]
+    xs = torch.zeros(M, K, dtype=torch.bfloat16, device=dev)
+    side = torch.cuda.Stream(dev)
+    graphs, outs, operands = [], [], []
+    for N, packed, absmax, a, b in layers:
+        ad, bd = a.to(dev), b.to(dev)
+        operands.append((ad, bd))  # a graph does not keep its inputs alive
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            ops.nf4_linear(xs, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0)
+        torch.cuda.current_stream(dev).wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(ops.nf4_linear(xs, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0))
+        graphs.append(g)
+    for i in range(6):
+        j = i % 2
+        N, packed, absmax, a, b = layers[j]
+        x = _x(M, K, seed=70 + i).to(dev)
+        xs.copy_(x)
+        graphs[j].replay()
+        got = outs[j].clone()
+        want = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=a.to(dev), lora_b=b.to(dev), scaling=2.0)
+        torch.cuda.synchronize(dev)
+        assert torch.equal(got, want), f"replay {i} of graph {j} differs from the eager call"
+
+
+@pytest.mark.parametrize("case", ["lora_x_offset", "a_offset", "bf16_a_offset"])
+def test_unaligned_operands_run_separate_kernel(dev, case):
+    K, N, M, rank = 1024, 1024, 2, 16
+    lora_dtype = torch.bfloat16 if case == "bf16_a_offset" else torch.float32
+    packed, absmax, a, b = _layer(N, K, rank, seed=21, dev=dev, lora_dtype=lora_dtype)
+    x = _x(M, K, seed=5)
+    xl = _x(M, K, seed=6)
+    if case == "lora_x_offset":
+        # rows 8 bytes off a 16-byte boundary
+        buf = torch.zeros(M * K + 4, dtype=torch.bfloat16, device=dev)
+        xld = buf[4:].view(M, K)
+        xld.copy_(xl.to(dev))
+        ad = a.to(dev)
+    else:
+        xld = xl.to(dev)
+        buf = torch.zeros(rank * K + 2, dtype=lora_dtype, device=dev)
+        ad = buf[2:].view(rank, K)
+        ad.copy_(a.to(dev))
+    y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=ad, lora_b=b.to(dev), scaling=2.0, lora_x=xld)
+    base = R.quant_linear_forward(x, R.dequantize_int4(packed.cpu(), absmax.cpu(), 64), None, N, K)
+    ref = R.lora_forward(xl, base, a, b, 2.0)
+    _check(y, ref)
