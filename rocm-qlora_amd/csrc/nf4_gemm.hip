@@ -41,6 +41,7 @@
 // share activation row slices, which then stay in that XCD's L2, and their
 // k loops start staggered so that only one of them misses on each slice.
 #include "rq_gemm_core.h"
+#include "rq_gemm8.h"
 
 namespace rq {
 
@@ -194,6 +195,36 @@ struct DxProducer {
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+template <int XT, class Scale>
+static int launch_fwd8(const GemmArgs& a, const ProducerParams& pp, Scale scale, const GemmEpi& e,
+                       hipStream_t stream) {
+  const unsigned grid = unsigned(int64_t(a.tiles_m) * a.tiles_n);
+  nf4_gemm8_kernel<XT, Fwd8Producer<XT, Scale>, Scale><<<grid, kGemm8Threads, 0, stream>>>(a, pp, scale, e);
+  return rq_check_launch();
+}
+
+// The forward GEMM on the eight-wave core, by scale format.
+template <int XT>
+static int run_fwd8(const GemmArgs& a, const ProducerParams& pp, const LinearArgs& L, const GemmEpi& e,
+                    hipStream_t stream) {
+  if (L.c2) {
+    const int sh = pow2_shift(L.block2);
+    switch (L.absmax_dtype) {
+      case RQ_DTYPE_F32:
+        return launch_fwd8<XT>(a, pp, ScaleDQ<RQ_DTYPE_F32>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, stream);
+      case RQ_DTYPE_BF16:
+        return launch_fwd8<XT>(a, pp, ScaleDQ<RQ_DTYPE_BF16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, stream);
+      default:
+        return launch_fwd8<XT>(a, pp, ScaleDQ<RQ_DTYPE_F16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, stream);
+    }
+  }
+  switch (L.absmax_dtype) {
+    case RQ_DTYPE_F32: return launch_fwd8<XT>(a, pp, ScaleAbsmax<RQ_DTYPE_F32>{L.absmax}, e, stream);
+    case RQ_DTYPE_BF16: return launch_fwd8<XT>(a, pp, ScaleAbsmax<RQ_DTYPE_BF16>{L.absmax}, e, stream);
+    default: return launch_fwd8<XT>(a, pp, ScaleAbsmax<RQ_DTYPE_F16>{L.absmax}, e, stream);
+  }
+}
+
 int gemm_workspace(const LinearArgs& L, size_t* bytes) {
   *bytes = plan_gemm(L.M, L.N, L.K, L.rank, device_cus()).ws_bytes;
   return RQ_OK;
@@ -239,11 +270,8 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   a.tiles_n = p.tiles_n;
   a.xcd_map = p.xcd_map;
   ProducerParams pp{L.w_packed, L.K / 2, L.N, L.K / L.block_size, pow2_shift(L.block_size)};
-  if (L.x_dtype == RQ_DTYPE_BF16)
-    return run_core<RQ_DTYPE_BF16, FwdProducer>(a, pp, L.absmax, L.absmax_dtype, L.c2, L.c2_format, L.block2, e,
-                                                stream);
-  return run_core<RQ_DTYPE_F16, FwdProducer>(a, pp, L.absmax, L.absmax_dtype, L.c2, L.c2_format, L.block2, e,
-                                             stream);
+  if (L.x_dtype == RQ_DTYPE_BF16) return run_fwd8<RQ_DTYPE_BF16>(a, pp, L, e, stream);
+  return run_fwd8<RQ_DTYPE_F16>(a, pp, L, e, stream);
 }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,314 @@
+// Eight-wave variant of the NF4 MFMA GEMM core for gfx950 (the forward
+// GEMM): the same 256 x 128 workgroup tile, LDS layout and k loop as
+// nf4_gemm_kernel, split over 512 threads, two waves per SIMD.  Wave w owns
+// rows 64 (w % 4) .. +63 and columns 64 (w / 4) .. +63 of the tile as 2 x 2
+// blocks of v_mfma_f32_32x32x16_{bf16,f16}.  With one wave per SIMD the
+// matrix core waits whenever that wave waits (LDS reads, table lookups,
+// barrier); a second wave per SIMD issues its MFMAs in those gaps.
+//
+// The two waves of a row slice (w and w + 4) each bring half of the slice's
+// activation rows into the ring; the step barrier, which already waits for
+// every wave's activation loads, makes both halves visible to both.
+#pragma once
+
+#include "rq_gemm_core.h"
+
+namespace rq {
+
+constexpr int kGemm8Threads = 512;
+constexpr int kGemm8MB = 2;  // 32-row blocks per wave
+constexpr int kGemm8NB = 2;  // 32-column blocks per wave
+
+// Forward producer for 512 threads: thread t dequantizes tile row t / 4,
+// codes 16 (t % 4) .. +16 of the step (8 packed bytes, 2 pieces of 8 codes).
+// A wave's 16-byte stores cover 16 rows, 4 chunks each; with the tile
+// swizzle any 16 consecutive lanes hit 16 distinct 16-byte bank groups.
+template <int XT, class Scale>
+struct Fwd8Producer {
+  static constexpr int kLoads = 1 + Scale::kLoads;
+  struct Regs {
+    u32x2 w;
+    typename Scale::Raw s;
+  };
+  struct Step {
+    float sc;
+    uint32_t taddr[2][4];
+    u32x2 lk[2][4];
+    uint32_t r[4];
+  };
+  ProducerParams P;
+  Scale scale;
+  const u32x2* lut;
+  uint32_t lane_off, tile_row, quarter, wrow;
+  int64_t wn;
+
+  __device__ __forceinline__ void init(const ProducerParams& p, const Scale& sc, const u32x2* l, int tid,
+                                       int64_t col0) {
+    P = p;
+    scale = sc;
+    lut = l;
+    lane_off = uint32_t(tid & 31) * 8u;
+    tile_row = uint32_t(tid >> 2);
+    quarter = uint32_t(tid & 3);
+    wn = col0 + tile_row;
+    wn = wn < P.rows ? wn : P.rows - 1;  // rows past N re-read a live row; never stored
+    wrow = uint32_t(wn * P.row_bytes + 8 * quarter);  // the host keeps the weights under 4 GiB
+  }
+  __device__ __forceinline__ void issue(Regs& R, int64_t kstep) const {
+    R.w = *reinterpret_cast<const u32x2*>(P.packed + (wrow + uint32_t(kstep) * 32u));
+    R.s = scale.load(wn * P.blocks_per_row + ((kstep * kGemmBK) >> P.bs_log2));
+  }
+  __device__ __forceinline__ void prep(Step& S, const Regs& R) const {
+    S.sc = scale.value(R.s);
+    const uint32_t words[2] = {R.w.x, R.w.y};
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int h = 0; h < 4; ++h) S.taddr[p][h] = lut_addr(words[p], lane_off, h);
+  }
+  __device__ __forceinline__ void lookup(Step& S, int p) const {
+#pragma unroll
+    for (int h = 0; h < 4; ++h) S.lk[p][h] = lut_read(lut, S.taddr[p][h]);
+  }
+  __device__ __forceinline__ void finish(Step& S, int p, int hh, uint8_t* tile) const {
+#pragma unroll
+    for (int h = 2 * hh; h < 2 * hh + 2; ++h)
+      S.r[h] = cvt_pk<XT>(__fmul_rn(u2f(S.lk[p][h].x), S.sc), __fmul_rn(u2f(S.lk[p][h].y), S.sc));
+    if (hh == 1)
+      *reinterpret_cast<u32x4*>(tile + swz(tile_row, 2u * quarter + uint32_t(p))) =
+          u32x4{S.r[0], S.r[1], S.r[2], S.r[3]};
+  }
+};
+
+// One 64-k step of a wave's 64 x 64 block.  Sub-step s (k = 16 s + 8 q + e)
+// runs four MFMAs; between them: the operand reads of sub-step s + 1, this
+// wave's four direct-to-LDS activation loads of step j + 1 (s = 0, 1), the
+// table lookups of the next weight tile's two pieces (s = 0, 1) and their
+// scale-multiply, rounding and stores (s = 1, 2); after the last sub-step,
+// the packed weights of step j + 4.
+template <int XT, class Prod>
+__device__ __forceinline__ void gemm8_step(f32x16 (&acc)[kGemm8MB][kGemm8NB], const uint8_t* xr,
+                                           const uint8_t* wt, int i32, int q, uint32_t col_base,
+                                           const GemmArgs& a, const uint32_t (&xo)[4], int64_t kx, uint32_t xdst,
+                                           const Prod& prod, const typename Prod::Regs& wq,
+                                           typename Prod::Regs& wl_fill, int64_t kfill, uint8_t* wdst) {
+  typename Prod::Step S;
+  prod.prep(S, wq);
+  auto read_ops = [&](u32x4 (&xa)[kGemm8MB], u32x4 (&b)[kGemm8NB], int s) {
+    const uint32_t c = uint32_t(2 * s + q);
+#pragma unroll
+    for (int mb = 0; mb < kGemm8MB; ++mb)
+      xa[mb] = *reinterpret_cast<const u32x4*>(xr + swz(uint32_t(32 * mb + i32), c));
+#pragma unroll
+    for (int nb = 0; nb < kGemm8NB; ++nb)
+      b[nb] = *reinterpret_cast<const u32x4*>(wt + swz(col_base + uint32_t(32 * nb + i32), c));
+  };
+  u32x4 xa[kGemm8MB], b[kGemm8NB], xan[kGemm8MB], bn[kGemm8NB];
+  read_ops(xa, b, 0);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (s < 3) read_ops(xan, bn, s + 1);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < kGemm8MB * kGemm8NB; ++i) {
+      const int nb = i / kGemm8MB, mb = i % kGemm8MB;
+      acc[mb][nb] = mfma32x32x16<XT>(xa[mb], b[nb], acc[mb][nb]);
+      if (i == 0 && s < 2) {
+#pragma unroll
+        for (int t = 2 * s; t < 2 * s + 2; ++t) dma16(a.x, (xo[t] + uint32_t(kx) * kGemmBK) * 2u, xdst + t * 1024);
+      } else if (i == 1 && s < 2) {
+        prod.lookup(S, s);
+      } else if (i >= 2 && (s == 1 || s == 2)) {
+        prod.finish(S, s - 1, i - 2, wdst);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (s < 3) {
+#pragma unroll
+      for (int mb = 0; mb < kGemm8MB; ++mb) xa[mb] = xan[mb];
+#pragma unroll
+      for (int nb = 0; nb < kGemm8NB; ++nb) b[nb] = bn[nb];
+    }
+  }
+  prod.issue(wl_fill, kfill);
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int XT, class Prod, class Scale>
+__global__ __launch_bounds__(kGemm8Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
+  u32x2* lut = reinterpret_cast<u32x2*>(lds);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int rb = wave & 3, ch = wave >> 2;  // row slice, column half
+  const int i32 = lane & 31, q = lane >> 5;
+
+  // tile of this workgroup (the numbering of nf4_gemm_kernel)
+  const int64_t T = int64_t(a.tiles_m) * a.tiles_n;
+  const int64_t g = blockIdx.x;
+  const int64_t t = a.xcd_map ? (g % 8) * (T / 8) + g / 8 : g;
+  const int64_t mt = t / a.tiles_n, nt = t % a.tiles_n;
+  const int64_t m0 = mt * kGemmBM, n0 = nt * kGemmBN;
+  const int64_t m0w = m0 + 64 * rb;
+  const int64_t nk = a.K / kGemmBK;
+
+  // Activation DMA lanes: this wave loads rows 32 ch .. +31 of its slice;
+  // instruction tt covers rows 32 ch + 8 tt + lane / 8, chunk (lane % 8) ^
+  // ((r / 2) & 7) of each.
+  uint32_t xo[4];
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) {
+    const int r = 32 * ch + 8 * tt + (lane >> 3);
+    int64_t m = m0w + r;
+    m = m < a.M ? m : a.M - 1;  // rows past M re-read a live row; never stored
+    xo[tt] = uint32_t(m * a.ldx + 8 * ((lane & 7) ^ ((r >> 1) & 7)));
+  }
+  uint8_t* xring = lds + kXRingOff + rb * kXWaveBytes;  // + (step & 1) * kXStepBytes
+  const uint32_t xring_addr = __builtin_amdgcn_readfirstlane(uint32_t(kXRingOff + rb * kXWaveBytes + ch * 4096));
+  uint8_t* wtile = lds + kWTileOff;  // + (step & 1) * kWTileBytes
+  const uint32_t col_base = uint32_t(64 * ch);
+  Prod prod;
+  prod.init(pp, scale, lut, tid, n0);
+
+  const int nk32 = __builtin_amdgcn_readfirstlane(int(nk));
+  const int k_off = __builtin_amdgcn_readfirstlane(int((((nt + 4 * mt) & 31) * nk) >> 5));
+  auto ks = [&](int64_t j) -> int64_t {
+    int v = int(j) + k_off;
+    v = v >= nk32 ? v - nk32 : v;
+    v = v >= nk32 ? v - nk32 : v;
+    return v;
+  };
+
+  // prologue: activations of step 0, packed weights of steps 0..3, the
+  // table, and step 0's weight tile
+#pragma unroll
+  for (int tt = 0; tt < 4; ++tt) dma16(a.x, (xo[tt] + uint32_t(ks(0)) * kGemmBK) * 2u, xring_addr + tt * 1024);
+  typename Prod::Regs wl[kWDepth];
+#pragma unroll
+  for (int d = 0; d < kWDepth; ++d) prod.issue(wl[d], ks(d));
+  fill_f32pair_lut<kGemm8Threads>(lut, tid);
+  __syncthreads();
+  {
+    typename Prod::Step S;
+    prod.prep(S, wl[0]);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      prod.lookup(S, p);
+      prod.finish(S, p, 0, wtile);
+      prod.finish(S, p, 1, wtile);
+    }
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+
+  f32x16 acc[kGemm8MB][kGemm8NB];
+#pragma unroll
+  for (int mb = 0; mb < kGemm8MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < kGemm8NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
+
+  // The k loop of nf4_gemm_kernel: step j computes on slot j % 2, loads
+  // activations j + 1 into the other slot, dequantizes step j + 1 into the
+  // other weight tile, loads the packed weights of step j + 4; the barrier
+  // leaves only those trailing weight loads in flight (in the tail, where
+  // they feed nothing and are dropped, it waits for every load).
+#define RQ_GEMM8_STEP(J, P, WAIT)                                                                              \
+  do {                                                                                                         \
+    gemm8_step<XT, Prod>(acc, xring + ((P) & 1) * kXStepBytes, wtile + ((P) & 1) * kWTileBytes, i32, q,       \
+                         col_base, a, xo, ks((J) + 1), xring_addr + (((P) + 1) & 1) * kXStepBytes, prod,      \
+                         wl[((P) + 1) & 3], wl[P], ks((J) + kWDepth), wtile + (((P) + 1) & 1) * kWTileBytes); \
+    step_barrier<WAIT>();                                                                                      \
+  } while (0)
+  int64_t j = 0;
+  for (; j + 4 <= nk; j += 4) {
+    RQ_GEMM8_STEP(j, 0, Prod::kLoads);
+    RQ_GEMM8_STEP(j + 1, 1, Prod::kLoads);
+    RQ_GEMM8_STEP(j + 2, 2, Prod::kLoads);
+    RQ_GEMM8_STEP(j + 3, 3, Prod::kLoads);
+  }
+  const int64_t rem = nk - j;
+  if (rem > 0) RQ_GEMM8_STEP(j, 0, 0);
+  if (rem > 1) RQ_GEMM8_STEP(j + 1, 1, 0);
+  if (rem > 2) RQ_GEMM8_STEP(j + 2, 2, 0);
+#undef RQ_GEMM8_STEP
+  wait_vmcnt<0>();  // nothing may still be landing in LDS when the epilogue reuses it
+
+  // ---- epilogue: the one of nf4_gemm_kernel on this wave's 64 x 64 block
+  const int rank = e.rank;
+  f32x16 lo[kGemm8MB][kGemm8NB];
+#pragma unroll
+  for (int mb = 0; mb < kGemm8MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < kGemm8NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) lo[mb][nb][r] = 0.0f;
+  if (rank > 0) {
+    constexpr int kP = 72;  // staging pitch in elements
+    uint16_t* us = reinterpret_cast<uint16_t*>(lds);  // [256][kP]
+    uint16_t* bs = us + kGemmBM * kP;                 // [128][kP]
+    for (int j0 = 0; j0 < e.rank16; j0 += 64) {
+      const int w8 = (e.rank16 - j0 < 64 ? e.rank16 - j0 : 64) / 8;  // 16-byte chunks per row
+      __syncthreads();  // the tiles, ring and table (first chunk) or the last chunk's operands are free
+      for (int idx = tid; idx < kGemmBM * w8; idx += kGemm8Threads) {
+        const int r = idx / w8, c = idx - r * w8;
+        int64_t m = m0 + r;
+        m = m < a.M ? m : a.M - 1;
+        *reinterpret_cast<u32x4*>(us + r * kP + 8 * c) =
+            *reinterpret_cast<const u32x4*>(e.u + m * e.rank16 + j0 + 8 * c);
+      }
+      for (int idx = tid; idx < kGemmBN * w8; idx += kGemm8Threads) {
+        const int r = idx / w8, c = idx - r * w8;
+        int64_t n = n0 + r;
+        n = n < a.N ? n : a.N - 1;
+        *reinterpret_cast<u32x4*>(bs + r * kP + 8 * c) =
+            *reinterpret_cast<const u32x4*>(e.bl + n * e.rank16 + j0 + 8 * c);
+      }
+      __syncthreads();
+      for (int s = 0; s < w8 / 2; ++s) {
+        u32x4 ua[kGemm8MB];
+#pragma unroll
+        for (int mb = 0; mb < kGemm8MB; ++mb)
+          ua[mb] = *reinterpret_cast<const u32x4*>(us + (64 * rb + 32 * mb + i32) * kP + 16 * s + 8 * q);
+#pragma unroll
+        for (int nb = 0; nb < kGemm8NB; ++nb) {
+          const u32x4 ub =
+              *reinterpret_cast<const u32x4*>(bs + (64 * ch + 32 * nb + i32) * kP + 16 * s + 8 * q);
+#pragma unroll
+          for (int mb = 0; mb < kGemm8MB; ++mb) lo[mb][nb] = mfma32x32x16<XT>(ua[mb], ub, lo[mb][nb]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int nb = 0; nb < kGemm8NB; ++nb) {
+    const int64_t n = n0 + 64 * ch + 32 * nb + i32;
+    if (n >= a.N) continue;
+    const float bias = e.bias ? round_x<XT>(load_as_f32(e.bias, n, e.bias_dt)) : 0.0f;
+    const float post = e.post_a ? __fmul_rn(*e.post_a, *e.post_b) : 1.0f;
+#pragma unroll
+    for (int mb = 0; mb < kGemm8MB; ++mb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0w + 32 * mb + 8 * (r >> 2) + 4 * q + (r & 3);
+        if (m >= a.M) continue;
+        float v = acc[mb][nb][r];
+        if (e.post_a) {
+          v = round_x<XT>(__fmul_rn(v, post));
+          if (e.bias) v = round_x<XT>(__fadd_rn(v, bias));
+        } else {
+          if (e.bias) v = __fadd_rn(v, bias);
+          v = round_x<XT>(v);
+        }
+        if (rank > 0)
+          v = round_x<XT>(__fadd_rn(v, round_x<XT>(__fmul_rn(round_x<XT>(lo[mb][nb][r]), e.scaling))));
+        e.y[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
+      }
+    }
+  }
+}
+
+}  // namespace rq
