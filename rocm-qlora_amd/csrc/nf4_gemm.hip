@@ -10,19 +10,20 @@
 // come from the LoRA operand kernels of rq_lora.hip).
 //
 // The core multiplies activation rows (x, or dY) by a weight operand tile
-// that a producer policy dequantizes into LDS: FwdProducer writes W rows
-// (output feature n, reduction k), DxProducer writes W^T rows (output
+// that a producer policy dequantizes into LDS: Fwd8Producer writes W rows
+// (output feature n, reduction k), Dx8Producer writes W^T rows (output
 // feature k, reduction n) by dequantizing a 64 x 128 block of W and storing
 // it transposed.  Below, "columns" are output features and "k" is the
 // reduction index of the core.
 //
-// Workgroup tile 256 tokens x 128 features, 4 waves; wave w owns rows
-// 64 w .. 64 w + 63 and all 128 columns as 2 x 4 blocks of
-// v_mfma_f32_32x32x16_{bf16,f16}.  K advances 64 per step -- one NF4 block
-// per weight row, one scale per row per step.  LDS (160 KiB, all of it):
+// Workgroup tile 256 tokens x 128 features, 8 waves (two per SIMD); wave w
+// owns rows 64 (w % 4) .. +63 and columns 64 (w / 4) .. +63 as 2 x 2 blocks
+// of v_mfma_f32_32x32x16_{bf16,f16} (rq_gemm8.h).  K advances 64 per step --
+// one NF4 block per weight row, one scale per row per step.  LDS (160 KiB,
+// all of it):
 //   [0, 64K)     the fp32 pair table for exact dequantization (address 0,
 //                so lookups fold their base into the instruction offset);
-//   [64K, 128K)  activation ring: 2 steps x 4 waves x 64 rows x 128 bytes;
+//   [64K, 128K)  activation ring: 2 steps x 4 row slices x 64 rows x 128 bytes;
 //   [128K, 160K) weight tiles: 2 steps x 128 rows x 128 bytes.
 // Both LDS layouts store 16-byte chunk c of row r at slot c ^ ((r / 2) & 7)
 // of the row: the LDS serves 16 lanes x 16 bytes (its 64 banks) per cycle,
@@ -32,11 +33,11 @@
 //   * Activations go from global memory straight into the ring with
 //     global_load_lds_dwordx4: each instruction moves 8 whole 128-byte rows
 //     (8 cache lines; loads that spread 32 rows over one instruction cost the
-//     vector L1 32 line lookups and stall the MFMA stream).  Each wave loads
-//     and reads only its own rows, so the ring needs no workgroup barrier.
-//   * Packed weights (16 bytes per thread per step) and their scales sit in
-//     registers four steps ahead; each step dequantizes the next step's tile
-//     through the pair table into the other weight tile.
+//     vector L1 32 line lookups and stall the MFMA stream).  The two waves of
+//     a row slice each load half of its rows.
+//   * Packed weights and their scales sit in registers four steps ahead;
+//     each step dequantizes the next step's tile through the pair table into
+//     the other weight tile.
 // Tiles are numbered so that the workgroups of one XCD (workgroup id mod 8)
 // share activation row slices, which then stay in that XCD's L2, and their
 // k loops start staggered so that only one of them misses on each slice.
@@ -45,86 +46,26 @@
 
 namespace rq {
 
-// Forward: tile row = output feature n, 64 reduction k per step.  Thread t
-// dequantizes row t / 2, codes 32 (t % 2) .. +32 of the step (16 packed
-// bytes, 4 pieces of 8 codes).
+// dX on the eight-wave core (512 threads): thread t dequantizes rows n = 64
+// kstep + 2 (t % 32) + i (i = 0, 1: piece i) at layer columns col0 + 8 (t /
+// 32) .. +8, and stores the 2 x 8 block transposed: for each of its 8 k, the
+// pair {n, n + 1} as one 4-byte store.  32 consecutive lanes cover one k
+// row's 64 n (128 bytes); the other 32 lanes of the wave (the next column
+// group) store their rows in swapped pair order, so the two halves of a
+// wave hit different row parities (bank halves).
 template <int XT, class Scale>
-struct FwdProducer {
-  static constexpr int kLoads = 1 + Scale::kLoads;
+struct Dx8Producer {
+  static constexpr int kLoads = 2 * (1 + Scale::kLoads);
   struct Regs {
-    u32x4 w;
-    typename Scale::Raw s;
+    uint32_t w[2];
+    typename Scale::Raw s[2];
   };
   struct Step {
-    float sc;
-    uint32_t taddr[4][4];
+    float sc[2];
+    uint32_t taddr[2][4];
     u32x2 lk[2][4];
-    uint32_t r[4];
-  };
-  ProducerParams P;
-  Scale scale;
-  const u32x2* lut;
-  uint32_t lane_off, tile_row, half, wrow;
-  int64_t wn;
-
-  __device__ __forceinline__ void init(const ProducerParams& p, const Scale& sc, const u32x2* l, int tid,
-                                       int64_t col0) {
-    P = p;
-    scale = sc;
-    lut = l;
-    lane_off = uint32_t(tid & 31) * 8u;
-    tile_row = uint32_t(tid >> 1);
-    half = uint32_t(tid & 1);
-    wn = col0 + tile_row;
-    wn = wn < P.rows ? wn : P.rows - 1;  // rows past N re-read a live row; never stored
-    wrow = uint32_t(wn * P.row_bytes + 16 * half);  // the host keeps the weights under 4 GiB
-  }
-  __device__ __forceinline__ void issue(Regs& R, int64_t kstep) const {
-    R.w = *reinterpret_cast<const u32x4*>(P.packed + (wrow + uint32_t(kstep) * 32u));
-    R.s = scale.load(wn * P.blocks_per_row + ((kstep * kGemmBK) >> P.bs_log2));
-  }
-  __device__ __forceinline__ void prep(Step& S, const Regs& R) const {
-    S.sc = scale.value(R.s);
-    const uint32_t words[4] = {R.w.x, R.w.y, R.w.z, R.w.w};
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-#pragma unroll
-      for (int h = 0; h < 4; ++h) S.taddr[p][h] = lut_addr(words[p], lane_off, h);
-  }
-  __device__ __forceinline__ void lookup(Step& S, int p) const {
-#pragma unroll
-    for (int h = 0; h < 4; ++h) S.lk[p & 1][h] = lut_read(lut, S.taddr[p][h]);
-  }
-  __device__ __forceinline__ void finish(Step& S, int p, int hh, uint8_t* tile) const {
-#pragma unroll
-    for (int h = 2 * hh; h < 2 * hh + 2; ++h)
-      S.r[h] = cvt_pk<XT>(__fmul_rn(u2f(S.lk[p & 1][h].x), S.sc), __fmul_rn(u2f(S.lk[p & 1][h].y), S.sc));
-    if (hh == 1)
-      *reinterpret_cast<u32x4*>(tile + swz(tile_row, 4u * half + uint32_t(p))) = u32x4{S.r[0], S.r[1], S.r[2], S.r[3]};
-  }
-};
-
-// dX: tile row = layer input feature k (output column of dX), 64 reduction
-// n (layer output features) per step.  Thread t dequantizes rows
-// n = 64 kstep + 4 (t % 16) + i (i = 0..3, piece i) at layer columns
-// col0 + 8 (t / 16) .. +8 (one packed dword per row) and stores the 4 x 8
-// block transposed: for each of its 8 k, the 4 n values as one 8-byte
-// store.  16 consecutive lanes cover one k row's 64 n (all 128 bytes);
-// odd-numbered column groups store their rows in swapped pair order so that
-// the two groups served together hit different row parities (bank halves).
-template <int XT, class Scale>
-struct DxProducer {
-  static constexpr int kLoads = 4 * (1 + Scale::kLoads);
-  struct Regs {
-    uint32_t w[4];
-    typename Scale::Raw s[4];
-  };
-  struct Step {
-    float sc[4];
-    uint32_t taddr[4][4];
-    u32x2 lk[2][4];
-    float v[8];       // piece 0 / 2 products, waiting for their partner
-    uint32_t pr[2][8];  // {n, n + 1} pairs of pieces (0, 1) and (2, 3)
+    float v[8];       // piece 0 products (row n), waiting for their partner
+    uint32_t pr[8];   // {n, n + 1} pairs by k
   };
   ProducerParams P;
   Scale scale;
@@ -138,8 +79,8 @@ struct DxProducer {
     scale = sc;
     lut = l;
     lane_off = uint32_t(tid & 31) * 8u;
-    rg = uint32_t(tid & 15);
-    dcol = uint32_t(tid >> 4);
+    rg = uint32_t(tid & 31);
+    dcol = uint32_t(tid >> 5);
     swap = dcol & 1u;
     const int64_t layer_k = P.row_bytes * 2;
     kcol = col0 + 8 * dcol;
@@ -148,15 +89,15 @@ struct DxProducer {
   }
   __device__ __forceinline__ void issue(Regs& R, int64_t kstep) const {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int64_t n = kstep * kGemmBK + 4 * rg + i;
+    for (int i = 0; i < 2; ++i) {
+      const int64_t n = kstep * kGemmBK + 2 * rg + i;
       R.w[i] = *reinterpret_cast<const uint32_t*>(P.packed + (uint32_t(n * P.row_bytes) + boff));
       R.s[i] = scale.load(n * P.blocks_per_row + (kcol >> P.bs_log2));
     }
   }
   __device__ __forceinline__ void prep(Step& S, const Regs& R) const {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 2; ++i) {
       S.sc[i] = scale.value(R.s[i]);
 #pragma unroll
       for (int h = 0; h < 4; ++h) S.taddr[i][h] = lut_addr(R.w[i], lane_off, h);
@@ -164,29 +105,30 @@ struct DxProducer {
   }
   __device__ __forceinline__ void lookup(Step& S, int p) const {
 #pragma unroll
-    for (int h = 0; h < 4; ++h) S.lk[p & 1][h] = lut_read(lut, S.taddr[p][h]);
+    for (int h = 0; h < 4; ++h) S.lk[p][h] = lut_read(lut, S.taddr[p][h]);
   }
   __device__ __forceinline__ void finish(Step& S, int p, int hh, uint8_t* tile) const {
 #pragma unroll
     for (int h = 2 * hh; h < 2 * hh + 2; ++h) {
-      const float a = __fmul_rn(u2f(S.lk[p & 1][h].x), S.sc[p]);  // k = 2h
-      const float b = __fmul_rn(u2f(S.lk[p & 1][h].y), S.sc[p]);  // k = 2h + 1
-      if ((p & 1) == 0) {
+      const float a = __fmul_rn(u2f(S.lk[p][h].x), S.sc[p]);  // k = 2h
+      const float b = __fmul_rn(u2f(S.lk[p][h].y), S.sc[p]);  // k = 2h + 1
+      if (p == 0) {
         S.v[2 * h] = a;
         S.v[2 * h + 1] = b;
       } else {
-        S.pr[p >> 1][2 * h] = cvt_pk<XT>(S.v[2 * h], a);
-        S.pr[p >> 1][2 * h + 1] = cvt_pk<XT>(S.v[2 * h + 1], b);
+        S.pr[2 * h] = cvt_pk<XT>(S.v[2 * h], a);
+        S.pr[2 * h + 1] = cvt_pk<XT>(S.v[2 * h + 1], b);
       }
     }
-    if (p == 3 && hh == 1) {
+    if (p == 1 && hh == 1) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int e0 = e ^ 1;
-        const uint32_t lo = swap ? S.pr[0][e0] : S.pr[0][e];
-        const uint32_t hi = swap ? S.pr[1][e0] : S.pr[1][e];
-        const uint32_t krow = 8u * dcol + (uint32_t(e) ^ swap);
-        *reinterpret_cast<u32x2*>(tile + swz(krow, rg >> 1) + ((rg & 1u) << 3)) = u32x2{lo, hi};
+        // the values as rvalues: a conditional on the array elements would
+        // select an address, and the array would live in scratch memory
+        const uint32_t ke = uint32_t(e) ^ swap;
+        const uint32_t own = S.pr[e], partner = S.pr[e ^ 1];
+        const uint32_t val = swap ? partner : own;
+        *reinterpret_cast<uint32_t*>(tile + swz(8u * dcol + ke, rg >> 2) + ((rg & 3u) << 2)) = val;
       }
     }
   }
@@ -195,33 +137,34 @@ struct DxProducer {
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-template <int XT, class Scale>
-static int launch_fwd8(const GemmArgs& a, const ProducerParams& pp, Scale scale, const GemmEpi& e,
-                       hipStream_t stream) {
+template <int XT, template <int, class> class ProdT, class Scale>
+static int launch_core8(const GemmArgs& a, const ProducerParams& pp, Scale scale, const GemmEpi& e,
+                        hipStream_t stream) {
   const unsigned grid = unsigned(int64_t(a.tiles_m) * a.tiles_n);
-  nf4_gemm8_kernel<XT, Fwd8Producer<XT, Scale>, Scale><<<grid, kGemm8Threads, 0, stream>>>(a, pp, scale, e);
+  nf4_gemm8_kernel<XT, ProdT<XT, Scale>, Scale><<<grid, kGemm8Threads, 0, stream>>>(a, pp, scale, e);
   return rq_check_launch();
 }
 
-// The forward GEMM on the eight-wave core, by scale format.
-template <int XT>
-static int run_fwd8(const GemmArgs& a, const ProducerParams& pp, const LinearArgs& L, const GemmEpi& e,
-                    hipStream_t stream) {
-  if (L.c2) {
-    const int sh = pow2_shift(L.block2);
-    switch (L.absmax_dtype) {
+// The eight-wave core with producer ProdT, by scale format: absmax of its
+// dtype, or double quantization (c2 codes of c2_format with c2_scales).
+template <int XT, template <int, class> class ProdT>
+static int run_core8(const GemmArgs& a, const ProducerParams& pp, const void* absmax, int absmax_dtype,
+                     const uint8_t* c2, int c2_format, int64_t block2, const GemmEpi& e, hipStream_t stream) {
+  if (c2) {
+    const int sh = pow2_shift(block2);
+    switch (absmax_dtype) {
       case RQ_DTYPE_F32:
-        return launch_fwd8<XT>(a, pp, ScaleDQ<RQ_DTYPE_F32>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, stream);
+        return launch_core8<XT, ProdT>(a, pp, ScaleDQ<RQ_DTYPE_F32>{c2, absmax, c2_format, sh, block2}, e, stream);
       case RQ_DTYPE_BF16:
-        return launch_fwd8<XT>(a, pp, ScaleDQ<RQ_DTYPE_BF16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, stream);
+        return launch_core8<XT, ProdT>(a, pp, ScaleDQ<RQ_DTYPE_BF16>{c2, absmax, c2_format, sh, block2}, e, stream);
       default:
-        return launch_fwd8<XT>(a, pp, ScaleDQ<RQ_DTYPE_F16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, e, stream);
+        return launch_core8<XT, ProdT>(a, pp, ScaleDQ<RQ_DTYPE_F16>{c2, absmax, c2_format, sh, block2}, e, stream);
     }
   }
-  switch (L.absmax_dtype) {
-    case RQ_DTYPE_F32: return launch_fwd8<XT>(a, pp, ScaleAbsmax<RQ_DTYPE_F32>{L.absmax}, e, stream);
-    case RQ_DTYPE_BF16: return launch_fwd8<XT>(a, pp, ScaleAbsmax<RQ_DTYPE_BF16>{L.absmax}, e, stream);
-    default: return launch_fwd8<XT>(a, pp, ScaleAbsmax<RQ_DTYPE_F16>{L.absmax}, e, stream);
+  switch (absmax_dtype) {
+    case RQ_DTYPE_F32: return launch_core8<XT, ProdT>(a, pp, ScaleAbsmax<RQ_DTYPE_F32>{absmax}, e, stream);
+    case RQ_DTYPE_BF16: return launch_core8<XT, ProdT>(a, pp, ScaleAbsmax<RQ_DTYPE_BF16>{absmax}, e, stream);
+    default: return launch_core8<XT, ProdT>(a, pp, ScaleAbsmax<RQ_DTYPE_F16>{absmax}, e, stream);
   }
 }
 
@@ -270,8 +213,11 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   a.tiles_n = p.tiles_n;
   a.xcd_map = p.xcd_map;
   ProducerParams pp{L.w_packed, L.K / 2, L.N, L.K / L.block_size, pow2_shift(L.block_size)};
-  if (L.x_dtype == RQ_DTYPE_BF16) return run_fwd8<RQ_DTYPE_BF16>(a, pp, L, e, stream);
-  return run_fwd8<RQ_DTYPE_F16>(a, pp, L, e, stream);
+  if (L.x_dtype == RQ_DTYPE_BF16)
+    return run_core8<RQ_DTYPE_BF16, Fwd8Producer>(a, pp, L.absmax, L.absmax_dtype, L.c2, L.c2_format, L.block2, e,
+                                                  stream);
+  return run_core8<RQ_DTYPE_F16, Fwd8Producer>(a, pp, L.absmax, L.absmax_dtype, L.c2, L.c2_format, L.block2, e,
+                                               stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -345,10 +291,10 @@ int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t st
   a.xcd_map = p.xcd_map;
   ProducerParams pp{D.w_packed, D.K / 2, D.N, D.K / D.block_size, pow2_shift(D.block_size)};
   if (D.dy_dtype == RQ_DTYPE_BF16)
-    return run_core<RQ_DTYPE_BF16, DxProducer>(a, pp, D.absmax, D.absmax_dtype, D.c2, D.c2_format, D.block2, e,
-                                               stream);
-  return run_core<RQ_DTYPE_F16, DxProducer>(a, pp, D.absmax, D.absmax_dtype, D.c2, D.c2_format, D.block2, e,
-                                            stream);
+    return run_core8<RQ_DTYPE_BF16, Dx8Producer>(a, pp, D.absmax, D.absmax_dtype, D.c2, D.c2_format, D.block2, e,
+                                                 stream);
+  return run_core8<RQ_DTYPE_F16, Dx8Producer>(a, pp, D.absmax, D.absmax_dtype, D.c2, D.c2_format, D.block2, e,
+                                              stream);
 }
 
 }  // namespace rq
