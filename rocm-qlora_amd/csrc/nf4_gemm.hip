@@ -140,7 +140,7 @@ struct Dx8Producer {
 template <int XT, template <int, class> class ProdT, class Scale>
 static int launch_core8(const GemmArgs& a, const ProducerParams& pp, Scale scale, const GemmEpi& e,
                         hipStream_t stream) {
-  const unsigned grid = unsigned(int64_t(a.tiles_m) * a.tiles_n);
+  const unsigned grid = unsigned(int64_t(a.tiles_m) * a.tiles_n * a.splits);
   nf4_gemm8_kernel<XT, ProdT<XT, Scale>, Scale><<<grid, kGemm8Threads, 0, stream>>>(a, pp, scale, e);
   return rq_check_launch();
 }
@@ -169,15 +169,19 @@ static int run_core8(const GemmArgs& a, const ProducerParams& pp, const void* ab
 }
 
 int gemm_workspace(const LinearArgs& L, size_t* bytes) {
-  *bytes = plan_gemm(L.M, L.N, L.K, L.rank, device_cus()).ws_bytes;
+  *bytes = plan_gemm(L.M, L.N, L.K, L.rank, device_cus(), true).ws_bytes;
   return RQ_OK;
 }
 
-int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream) {
+int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t* tile_cnt, size_t n_cnt,
+                 hipStream_t stream) {
   // the activation operands are loaded 16 bytes at a time
   if (!aligned(L.x, 16) || L.ldx % 8 != 0) return RQ_ERR_BAD_ALIGNMENT;
   if (!offsets_fit(L.M, L.ldx, L.N, L.K)) return RQ_ERR_UNSUPPORTED;
-  const GemmPlan p = plan_gemm(L.M, L.N, L.K, L.rank, device_cus());
+  // K splits need the zeroed tile counts
+  GemmPlan p = plan_gemm(L.M, L.N, L.K, L.rank, device_cus(), true);
+  if (p.splits > 1 && (!tile_cnt || size_t(p.tiles_m) * p.tiles_n > n_cnt))
+    p = plan_gemm(L.M, L.N, L.K, L.rank, device_cus(), false);
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
   if (workspace && !aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;
   GemmEpi e{};
@@ -212,6 +216,9 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
   a.xcd_map = p.xcd_map;
+  a.splits = p.splits;
+  a.part = p.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.part_offset) : nullptr;
+  a.tile_cnt = tile_cnt;
   ProducerParams pp{L.w_packed, L.K / 2, L.N, L.K / L.block_size, pow2_shift(L.block_size)};
   if (L.x_dtype == RQ_DTYPE_BF16)
     return run_core8<RQ_DTYPE_BF16, Fwd8Producer>(a, pp, L.absmax, L.absmax_dtype, L.c2, L.c2_format, L.block2, e,
@@ -289,6 +296,7 @@ int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t st
   a.tiles_m = p.tiles_m;
   a.tiles_n = p.tiles_n;
   a.xcd_map = p.xcd_map;
+  a.splits = 1;
   ProducerParams pp{D.w_packed, D.K / 2, D.N, D.K / D.block_size, pow2_shift(D.block_size)};
   if (D.dy_dtype == RQ_DTYPE_BF16)
     return run_core8<RQ_DTYPE_BF16, Dx8Producer>(a, pp, D.absmax, D.absmax_dtype, D.c2, D.c2_format, D.block2, e,

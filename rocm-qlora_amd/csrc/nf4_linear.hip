@@ -1247,8 +1247,11 @@ extern "C" int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, i
   if (st != RQ_OK || M == 0) return st;
   if (workspace_bytes < 0) return RQ_ERR_BAD_SHAPE;
   if (M <= kGemvMaxM) return run_nf4_gemv(L, workspace, size_t(workspace_bytes), stream);
-  // the GEMM's workspace follows the synchronization words
-  return run_nf4_gemm(L, workspace ? static_cast<char*>(workspace) + kLinearSyncBytes : nullptr,
-                      size_t(workspace_bytes) > kLinearSyncBytes ? size_t(workspace_bytes) - kLinearSyncBytes : 0,
-                      stream);
+  // the GEMM's workspace follows the synchronization area, whose zeroed
+  // words past the count block serve as its K splits' tile counters
+  const bool area = workspace && size_t(workspace_bytes) >= kLinearSyncBytes;
+  return run_nf4_gemm(L, area ? static_cast<char*>(workspace) + kLinearSyncBytes : nullptr,
+                      area ? size_t(workspace_bytes) - kLinearSyncBytes : 0,
+                      area ? reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kLinearCountBytes) : nullptr,
+                      (kLinearSyncBytes - kLinearCountBytes) / 4, stream);
 }

@@ -145,14 +145,18 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   const int rb = wave & 3, ch = wave >> 2;  // row slice, column half
   const int i32 = lane & 31, q = lane >> 5;
 
-  // tile of this workgroup (the numbering of nf4_gemm_kernel)
+  // tile and K split of this workgroup (the tile numbering of
+  // nf4_gemm_kernel; with T % 8 == 0 every split of a tile sits on its XCD)
   const int64_t T = int64_t(a.tiles_m) * a.tiles_n;
-  const int64_t g = blockIdx.x;
+  const int split = int(blockIdx.x / T);
+  const int64_t g = blockIdx.x - int64_t(split) * T;
   const int64_t t = a.xcd_map ? (g % 8) * (T / 8) + g / 8 : g;
   const int64_t mt = t / a.tiles_n, nt = t % a.tiles_n;
   const int64_t m0 = mt * kGemmBM, n0 = nt * kGemmBN;
   const int64_t m0w = m0 + 64 * rb;
-  const int64_t nk = a.K / kGemmBK;
+  const int64_t nk_all = a.K / kGemmBK;
+  const int64_t kbeg = nk_all * split / a.splits;
+  const int64_t nk = nk_all * (split + 1) / a.splits - kbeg;  // steps of this split
 
   // Activation DMA lanes: this wave loads rows 32 ch .. +31 of its slice;
   // instruction tt covers rows 32 ch + 8 tt + lane / 8, chunk (lane % 8) ^
@@ -174,11 +178,12 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
 
   const int nk32 = __builtin_amdgcn_readfirstlane(int(nk));
   const int k_off = __builtin_amdgcn_readfirstlane(int((((nt + 4 * mt) & 31) * nk) >> 5));
+  const int kb32 = __builtin_amdgcn_readfirstlane(int(kbeg));
   auto ks = [&](int64_t j) -> int64_t {
     int v = int(j) + k_off;
     v = v >= nk32 ? v - nk32 : v;
     v = v >= nk32 ? v - nk32 : v;
-    return v;
+    return kb32 + v;
   };
 
   // prologue: activations of step 0, packed weights of steps 0..3, the
@@ -236,6 +241,61 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   if (rem > 2) RQ_GEMM8_STEP(j + 2, 2, 0);
 #undef RQ_GEMM8_STEP
   wait_vmcnt<0>();  // nothing may still be landing in LDS when the epilogue reuses it
+
+  // ---- K splits: every split stores its tile; the last to count itself
+  // sums all of them in split order (the same sums whichever split is last).
+  // The partials move by device-coherent stores and loads, so that no cache
+  // write-back or invalidation is needed: each thread waits for its stores
+  // to complete before the workgroup counts itself.
+  if (a.splits > 1) {
+    constexpr int kTileFloats = kGemm8Threads * 64;
+    float* mine = a.part + (int64_t(split) * T + t) * kTileFloats + tid;
+#pragma unroll
+    for (int mb = 0; mb < kGemm8MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < kGemm8NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          __hip_atomic_store(&mine[((mb * kGemm8NB + nb) * 16 + r) * kGemm8Threads], acc[mb][nb][r],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    uint32_t* flag = reinterpret_cast<uint32_t*>(lds);  // the table's LDS is free now
+    if (tid == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(&a.tile_cnt[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old == uint32_t(a.splits - 1);
+      if (last) __hip_atomic_store(&a.tile_cnt[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = last ? 1u : 0u;
+    }
+    __syncthreads();
+    const uint32_t last = __builtin_amdgcn_readfirstlane(*flag);
+    __syncthreads();  // every wave has read the flag before the LDS is reused
+    if (!last) return;
+    // a block's 16 values of every split in flight together (a split past
+    // `splits` re-reads split 0 and is not added)
+    float* base = a.part + t * kTileFloats + tid;
+#pragma unroll
+    for (int mb = 0; mb < kGemm8MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < kGemm8NB; ++nb) {
+        float o[kGemmMaxSplits][16];
+#pragma unroll
+        for (int sp = 0; sp < kGemmMaxSplits; ++sp)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            o[sp][r] = __hip_atomic_load(&base[int64_t(sp < a.splits ? sp : 0) * T * kTileFloats +
+                                               ((mb * kGemm8NB + nb) * 16 + r) * kGemm8Threads],
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = 0.0f;
+#pragma unroll
+          for (int sp = 0; sp < kGemmMaxSplits; ++sp)
+            if (sp < a.splits) v = __fadd_rn(v, sp == split ? acc[mb][nb][r] : o[sp][r]);
+          acc[mb][nb][r] = v;
+        }
+      }
+  }
 
   // ---- epilogue: the one of nf4_gemm_kernel on this wave's 64 x 64 block
   const int rank = e.rank;

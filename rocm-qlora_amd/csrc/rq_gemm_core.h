@@ -27,6 +27,7 @@ constexpr int kXRingOff = kLutBytes;
 constexpr int kWTileOff = kXRingOff + 2 * kXStepBytes;
 constexpr int kGemmLds = kWTileOff + 2 * kWTileBytes;  // 160 KiB
 constexpr int kWDepth = 4;                           // packed-weight prefetch distance in steps
+constexpr int kGemmMaxSplits = 4;                    // K splits of the eight-wave core
 static_assert(kGemmLds == 160 * 1024, "LDS plan");
 
 // Core problem: out[M, N] = act[M, K] . op[N, K]^T (+ epilogue).
@@ -36,6 +37,13 @@ struct GemmArgs {
   int64_t M, N, K;    // rows, output columns, reduction length
   int tiles_m, tiles_n;
   bool xcd_map;       // tiles of one row slice on one XCD
+  // K splits (eight-wave core only): workgroup g takes tile g % T and split
+  // g / T; each split stores its fp32 tile to part and counts itself in
+  // tile_cnt[tile] (zero before the launch); the last one of a tile sums the
+  // splits in split order, runs the epilogue and sets the count back to 0.
+  int splits;
+  float* part;         // [splits][T][64 x 512] fp32
+  uint32_t* tile_cnt;  // [T]
 };
 
 struct GemmEpi {
@@ -382,6 +390,8 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a, Prod
 struct GemmPlan {
   int tiles_m, tiles_n;
   bool xcd_map;
+  int splits;
+  size_t part_offset;
   int rank16;
   LoraRowsPlan lr;
   size_t u16_offset, bl16_offset, ws_bytes;
@@ -390,12 +400,18 @@ struct GemmPlan {
 // M activation rows, N output columns, K reduction; the LoRA operands are
 // u [M][r16] (product of activations with an [r][K] matrix) and bl
 // [N][r16].  Workspace: [lora_rows partials][RND(S) r x K][u16][bl16].
-inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus) {
+inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool split_ok = false) {
   GemmPlan p{};
   p.tiles_m = int((M + kGemmBM - 1) / kGemmBM);
   p.tiles_n = int((N + kGemmBN - 1) / kGemmBN);
   const int64_t T = int64_t(p.tiles_m) * p.tiles_n;
   p.xcd_map = T % 8 == 0;
+  // K splits while the tiles leave half the compute units idle (at least
+  // 8 steps of 64 k per split)
+  p.splits = 1;
+  if (split_ok)
+    while (p.splits < kGemmMaxSplits && T * p.splits * 2 <= cus && K / kGemmBK / (p.splits * 2) >= 8)
+      p.splits *= 2;
   p.rank16 = int((rank + 15) & ~int64_t(15));
   p.ws_bytes = 0;
   if (rank > 0) {
@@ -404,6 +420,8 @@ inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus
     p.bl16_offset = p.u16_offset + ((size_t(M) * p.rank16 * 2 + 255) & ~size_t(255));
     p.ws_bytes = p.bl16_offset + size_t(N) * p.rank16 * 2;
   }
+  p.part_offset = (p.ws_bytes + 255) & ~size_t(255);
+  if (p.splits > 1) p.ws_bytes = p.part_offset + size_t(p.splits) * T * kGemmBM * kGemmBN * 4;
   return p;
 }
 

@@ -81,7 +81,10 @@ int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream);
 int gemv_workspace(const LinearArgs& L, size_t* bytes);
 int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream);
 int gemm_workspace(const LinearArgs& L, size_t* bytes);
-int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream);
+// tile_cnt: n_cnt zeroed counters the GEMM's K splits use (and leave zero);
+// without them the GEMM runs unsplit.
+int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t* tile_cnt, size_t n_cnt,
+                 hipStream_t stream);
 
 // Unpacked arguments of rq_nf4_linear_dx (see include/rocm_qlora_amd.h).
 struct DxArgs {

@@ -165,3 +165,33 @@ def test_gemm_weight_operand_bit_exact(dev, dtype, dq):
         wf = R.dequantize_int4(packed.cpu(), absmax.cpu(), 64)[:N * K].reshape(N, K)
     ref = wf.to(dtype)[:, ks].T
     assert torch.equal(y.cpu().view(torch.int16), ref.contiguous().view(torch.int16))
+
+
+def test_gemm_k_splits_and_shared_workspace(dev):
+    """Shapes with few tiles run as K splits whose last split of each tile sums
+    the others (tile counters in the workspace's zeroed synchronization area).
+    Calls of split GEMMs, an unsplit GEMM and a decode GEMV with in-launch
+    LoRA share one workspace in a row; each matches the oracle, repeated
+    calls give the same bits, and the area is zero again afterwards."""
+    K, rank = 2048, 16
+    cases = [(1024, 512), (768, 2048), (2048, 2048), (1024, 3)]
+    layers = {}
+    for N, M in cases:
+        if N not in layers:
+            w, _, a, b, _ = _inputs(N, K, 1, torch.bfloat16, seed=N, rank=rank)
+            packed, absmax = quantize_int4(w.to(dev), 64)
+            layers[N] = (packed, absmax, a, b)
+    for rep in range(2):
+        for i, (N, M) in enumerate(cases):
+            packed, absmax, a, b = layers[N]
+            x = _inputs(N, K, M, torch.bfloat16, seed=100 + i)[1]
+            print(f"k-split case N={N} M={M} rep={rep}", flush=True)
+            y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=a.to(dev), lora_b=b.to(dev), scaling=0.5)
+            y2 = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=a.to(dev), lora_b=b.to(dev), scaling=0.5)
+            assert torch.equal(y, y2)
+            ref = R.nf4_lora_linear(x, packed.cpu(), absmax.cpu(), None, a, b, 0.5, N, 64)
+            _check(y, ref)
+    torch.cuda.synchronize(dev)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(dev).cuda_stream)
+    assert int(ops._LINEAR_WS[key][:ops.LINEAR_SYNC_BYTES].cpu().count_nonzero()) == 0
