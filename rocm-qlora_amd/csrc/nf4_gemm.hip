@@ -140,7 +140,8 @@ struct Dx8Producer {
 template <int XT, template <int, class> class ProdT, class Scale>
 static int launch_core8(const GemmArgs& a, const ProducerParams& pp, Scale scale, const GemmEpi& e,
                         hipStream_t stream) {
-  const unsigned grid = unsigned(int64_t(a.tiles_m) * a.tiles_n * a.splits);
+  const int64_t T = int64_t(a.tiles_m) * a.tiles_n;
+  const unsigned grid = unsigned(a.xcd_map ? 8 * (a.lf + (T / 8 - a.lf) * a.splits) : T);
   nf4_gemm8_kernel<XT, ProdT<XT, Scale>, Scale><<<grid, kGemm8Threads, 0, stream>>>(a, pp, scale, e);
   return rq_check_launch();
 }
@@ -180,7 +181,7 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t
   if (!offsets_fit(L.M, L.ldx, L.N, L.K)) return RQ_ERR_UNSUPPORTED;
   // K splits need the zeroed tile counts
   GemmPlan p = plan_gemm(L.M, L.N, L.K, L.rank, device_cus(), true);
-  if (p.splits > 1 && (!tile_cnt || size_t(p.tiles_m) * p.tiles_n > n_cnt))
+  if (p.splits > 1 && (!tile_cnt || size_t(8) * p.lt > n_cnt))
     p = plan_gemm(L.M, L.N, L.K, L.rank, device_cus(), false);
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
   if (workspace && !aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;
@@ -201,11 +202,14 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t
                            L.lora_dtype, L.K, 1, e.rank, false, 1.0f, p.lr, reinterpret_cast<float*>(ws),
                            reinterpret_cast<uint16_t*>(ws + p.lr.part_bytes), u16, p.rank16, stream);
     if (st != RQ_OK) return st;
-    // RND(B), B [N][r] with row stride ld_lora_b
-    st = run_lora_round(L.x_dtype, L.lora_b, L.lora_dtype, L.ld_lora_b, 1, L.N, e.rank, p.rank16, bl16, stream);
-    if (st != RQ_OK) return st;
+    // RND(B), B [N][r] with row stride ld_lora_b, rounded as the epilogue stages it
     e.u = u16;
     e.bl = bl16;
+    e.braw = L.lora_b;
+    e.b_dt = L.lora_dtype;
+    e.b_sn = L.ld_lora_b;
+    e.b_sj = 1;
+    e.b_vec = aligned(L.lora_b, 16) && (L.lora_dtype != RQ_DTYPE_F32 || L.ld_lora_b % 4 == 0);
   }
   GemmArgs a{};
   a.x = static_cast<const uint16_t*>(L.x);
@@ -217,6 +221,7 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t
   a.tiles_n = p.tiles_n;
   a.xcd_map = p.xcd_map;
   a.splits = p.splits;
+  a.lf = p.lf;
   a.part = p.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + p.part_offset) : nullptr;
   a.tile_cnt = tile_cnt;
   ProducerParams pp{L.w_packed, L.K / 2, L.N, L.K / L.block_size, pow2_shift(L.block_size)};
@@ -281,11 +286,14 @@ int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t st
                        D.ld_lora_b, int(rank), true, D.scaling, p.lr, reinterpret_cast<float*>(ws),
                        reinterpret_cast<uint16_t*>(ws + p.lr.part_bytes), g16, p.rank16, stream);
     if (st != RQ_OK) return st;
-    // RND(A^T) [K][r]: element (k, j) = A[j][k], A [r][K] row-major
-    st = run_lora_round(D.dy_dtype, D.lora_a, D.lora_dtype, 1, D.K, D.K, int(rank), p.rank16, at16, stream);
-    if (st != RQ_OK) return st;
+    // RND(A^T) [K][r]: element (k, j) = A[j][k], A [r][K] row-major, rounded
+    // as the epilogue stages it
     e.u = g16;
     e.bl = at16;
+    e.braw = D.lora_a;
+    e.b_dt = D.lora_dtype;
+    e.b_sn = 1;
+    e.b_sj = D.K;
   }
   GemmArgs a{};
   a.x = static_cast<const uint16_t*>(D.dy);
@@ -297,6 +305,7 @@ int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t st
   a.tiles_n = p.tiles_n;
   a.xcd_map = p.xcd_map;
   a.splits = 1;
+  a.lf = p.tiles_m * p.tiles_n / 8;
   ProducerParams pp{D.w_packed, D.K / 2, D.N, D.K / D.block_size, pow2_shift(D.block_size)};
   if (D.dy_dtype == RQ_DTYPE_BF16)
     return run_core8<RQ_DTYPE_BF16, Dx8Producer>(a, pp, D.absmax, D.absmax_dtype, D.c2, D.c2_format, D.block2, e,

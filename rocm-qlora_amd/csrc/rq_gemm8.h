@@ -145,18 +145,34 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   const int rb = wave & 3, ch = wave >> 2;  // row slice, column half
   const int i32 = lane & 31, q = lane >> 5;
 
-  // tile and K split of this workgroup (the tile numbering of
-  // nf4_gemm_kernel; with T % 8 == 0 every split of a tile sits on its XCD)
+  // tile and K split of this workgroup: the tile numbering of
+  // nf4_gemm_kernel (XCD x = g % 8 takes tiles x T/8 .. +T/8), its first lf
+  // tiles whole, the rest as `splits` workgroups each (split tile ti of the
+  // launch); every split of a tile sits on the tile's XCD
   const int64_t T = int64_t(a.tiles_m) * a.tiles_n;
-  const int split = int(blockIdx.x / T);
-  const int64_t g = blockIdx.x - int64_t(split) * T;
-  const int64_t t = a.xcd_map ? (g % 8) * (T / 8) + g / 8 : g;
+  const int64_t g = blockIdx.x;
+  int64_t t, ti = 0;
+  int split = 0, nsplit = 1;
+  if (a.xcd_map) {
+    const int64_t x = g % 8, jw = g / 8, L = T / 8;
+    if (jw < a.lf) {
+      t = x * L + jw;
+    } else {
+      const int64_t lt = L - a.lf, jj = jw - a.lf;
+      split = int(jj / lt);
+      nsplit = a.splits;
+      t = x * L + a.lf + jj % lt;
+      ti = x * lt + jj % lt;
+    }
+  } else {
+    t = g;
+  }
   const int64_t mt = t / a.tiles_n, nt = t % a.tiles_n;
   const int64_t m0 = mt * kGemmBM, n0 = nt * kGemmBN;
   const int64_t m0w = m0 + 64 * rb;
   const int64_t nk_all = a.K / kGemmBK;
-  const int64_t kbeg = nk_all * split / a.splits;
-  const int64_t nk = nk_all * (split + 1) / a.splits - kbeg;  // steps of this split
+  const int64_t kbeg = nk_all * split / nsplit;
+  const int64_t nk = nk_all * (split + 1) / nsplit - kbeg;  // steps of this split
 
   // Activation DMA lanes: this wave loads rows 32 ch .. +31 of its slice;
   // instruction tt covers rows 32 ch + 8 tt + lane / 8, chunk (lane % 8) ^
@@ -247,9 +263,10 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   // The partials move by device-coherent stores and loads, so that no cache
   // write-back or invalidation is needed: each thread waits for its stores
   // to complete before the workgroup counts itself.
-  if (a.splits > 1) {
+  if (nsplit > 1) {
     constexpr int kTileFloats = kGemm8Threads * 64;
-    float* mine = a.part + (int64_t(split) * T + t) * kTileFloats + tid;
+    const int64_t n_split_tiles = 8 * (T / 8 - a.lf);
+    float* mine = a.part + (int64_t(split) * n_split_tiles + ti) * kTileFloats + tid;
 #pragma unroll
     for (int mb = 0; mb < kGemm8MB; ++mb)
 #pragma unroll
@@ -262,9 +279,9 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
     __syncthreads();
     uint32_t* flag = reinterpret_cast<uint32_t*>(lds);  // the table's LDS is free now
     if (tid == 0) {
-      const uint32_t old = __hip_atomic_fetch_add(&a.tile_cnt[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const bool last = old == uint32_t(a.splits - 1);
-      if (last) __hip_atomic_store(&a.tile_cnt[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t old = __hip_atomic_fetch_add(&a.tile_cnt[ti], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old == uint32_t(nsplit - 1);
+      if (last) __hip_atomic_store(&a.tile_cnt[ti], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       *flag = last ? 1u : 0u;
     }
     __syncthreads();
@@ -273,7 +290,7 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
     if (!last) return;
     // a block's 16 values of every split in flight together (a split past
     // `splits` re-reads split 0 and is not added)
-    float* base = a.part + t * kTileFloats + tid;
+    float* base = a.part + ti * kTileFloats + tid;
 #pragma unroll
     for (int mb = 0; mb < kGemm8MB; ++mb)
 #pragma unroll
@@ -283,7 +300,7 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
         for (int sp = 0; sp < kGemmMaxSplits; ++sp)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            o[sp][r] = __hip_atomic_load(&base[int64_t(sp < a.splits ? sp : 0) * T * kTileFloats +
+            o[sp][r] = __hip_atomic_load(&base[int64_t(sp < nsplit ? sp : 0) * n_split_tiles * kTileFloats +
                                                ((mb * kGemm8NB + nb) * 16 + r) * kGemm8Threads],
                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
@@ -291,7 +308,7 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
           float v = 0.0f;
 #pragma unroll
           for (int sp = 0; sp < kGemmMaxSplits; ++sp)
-            if (sp < a.splits) v = __fadd_rn(v, sp == split ? acc[mb][nb][r] : o[sp][r]);
+            if (sp < nsplit) v = __fadd_rn(v, sp == split ? acc[mb][nb][r] : o[sp][r]);
           acc[mb][nb][r] = v;
         }
       }
@@ -324,8 +341,12 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
         const int r = idx / w8, c = idx - r * w8;
         int64_t n = n0 + r;
         n = n < a.N ? n : a.N - 1;
-        *reinterpret_cast<u32x4*>(bs + r * kP + 8 * c) =
-            *reinterpret_cast<const u32x4*>(e.bl + n * e.rank16 + j0 + 8 * c);
+        const int j = j0 + 8 * c;
+        u32x4 v;
+        if (!e.braw) v = *reinterpret_cast<const u32x4*>(e.bl + n * e.rank16 + j);
+        else if (e.b_sj == 1) v = load_a8_masked<XT>(e.braw, e.b_dt, n * e.b_sn + j, e.rank - j, e.b_vec);
+        else v = load_a8_strided<XT>(e.braw, e.b_dt, n * e.b_sn + j * e.b_sj, e.b_sj, e.rank - j);
+        *reinterpret_cast<u32x4*>(bs + r * kP + 8 * c) = v;
       }
       __syncthreads();
       for (int s = 0; s < w8 / 2; ++s) {

@@ -37,13 +37,16 @@ struct GemmArgs {
   int64_t M, N, K;    // rows, output columns, reduction length
   int tiles_m, tiles_n;
   bool xcd_map;       // tiles of one row slice on one XCD
-  // K splits (eight-wave core only): workgroup g takes tile g % T and split
-  // g / T; each split stores its fp32 tile to part and counts itself in
-  // tile_cnt[tile] (zero before the launch); the last one of a tile sums the
-  // splits in split order, runs the epilogue and sets the count back to 0.
+  // K splits of the last wave's tiles (eight-wave core, xcd_map only).  Of
+  // the T / 8 tiles of an XCD, the first lf run whole; the other lt =
+  // T / 8 - lf run as `splits` workgroups each, over K ranges of equal
+  // length.  Each split stores its fp32 tile to part and counts itself in
+  // tile_cnt (zero before the launch); the last one of a tile sums the splits
+  // in split order, runs the epilogue and sets the count back to 0.
   int splits;
-  float* part;         // [splits][T][64 x 512] fp32
-  uint32_t* tile_cnt;  // [T]
+  int lf;
+  float* part;         // [splits][8 lt][64 x 512] fp32
+  uint32_t* tile_cnt;  // [8 lt]
 };
 
 struct GemmEpi {
@@ -52,6 +55,13 @@ struct GemmEpi {
   int rank, rank16;      // LoRA rank and rank rounded up to 16
   const uint16_t* u;     // RND(u) [M][rank16] (dX: RND(g)), zero padded
   const uint16_t* bl;    // RND(B) [N][rank16] (dX: RND(A^T)), zero padded
+  // eight-wave core: the bl operand read as it is -- element (n, j) at
+  // braw[n * b_sn + j * b_sj], of b_dt -- and rounded while staged, in place
+  // of bl (nullptr: bl)
+  const void* braw;
+  int b_dt;
+  int64_t b_sn, b_sj;
+  bool b_vec;            // b_sj == 1 and braw rows 16-byte aligned (fp32 vector loads)
   float scaling;         // 1 for dX
   // FP8: y = RND(RND(acc * (*post_a) * (*post_b)) + RND(bias)) (the scaled
   // product is rounded before the bias is added); nullptr otherwise
@@ -390,7 +400,7 @@ __global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a, Prod
 struct GemmPlan {
   int tiles_m, tiles_n;
   bool xcd_map;
-  int splits;
+  int splits, lf, lt;  // see GemmArgs; lt = split tiles per XCD
   size_t part_offset;
   int rank16;
   LoraRowsPlan lr;
@@ -406,12 +416,23 @@ inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus
   p.tiles_n = int((N + kGemmBN - 1) / kGemmBN);
   const int64_t T = int64_t(p.tiles_m) * p.tiles_n;
   p.xcd_map = T % 8 == 0;
-  // K splits while the tiles leave half the compute units idle (at least
-  // 8 steps of 64 k per split)
+  // The tiles of an XCD past its last whole wave (cus / 8 workgroups per
+  // XCD) run as K splits while the split tiles still fit in one wave (at
+  // least 8 steps of 64 k per split).
   p.splits = 1;
-  if (split_ok)
-    while (p.splits < kGemmMaxSplits && T * p.splits * 2 <= cus && K / kGemmBK / (p.splits * 2) >= 8)
-      p.splits *= 2;
+  p.lf = int(T / 8);
+  p.lt = 0;
+  if (split_ok && p.xcd_map) {
+    const int64_t L = T / 8, c8 = cus / 8 > 0 ? cus / 8 : 1;
+    const int64_t lf = (L / c8) * c8, lt = L - lf;
+    int s = 1;
+    while (lt > 0 && s < kGemmMaxSplits && lt * s * 2 <= c8 && K / kGemmBK / (s * 2) >= 8) s *= 2;
+    if (s > 1) {
+      p.splits = s;
+      p.lf = int(lf);
+      p.lt = int(lt);
+    }
+  }
   p.rank16 = int((rank + 15) & ~int64_t(15));
   p.ws_bytes = 0;
   if (rank > 0) {
@@ -421,7 +442,7 @@ inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus
     p.ws_bytes = p.bl16_offset + size_t(N) * p.rank16 * 2;
   }
   p.part_offset = (p.ws_bytes + 255) & ~size_t(255);
-  if (p.splits > 1) p.ws_bytes = p.part_offset + size_t(p.splits) * T * kGemmBM * kGemmBN * 4;
+  if (p.splits > 1) p.ws_bytes = p.part_offset + size_t(p.splits) * 8 * p.lt * kGemmBM * kGemmBN * 4;
   return p;
 }
 

@@ -156,6 +156,31 @@ __device__ __forceinline__ u32x4 load_a8(const void* p, int dt, int64_t off, boo
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
+// 8 consecutive values p[off + e] (e < n_live, zeros past), rounded to the
+// activation dtype; the vector path when all 8 are live.
+template <int XT>
+__device__ __forceinline__ u32x4 load_a8_masked(const void* p, int dt, int64_t off, int n_live, bool vec32) {
+  if (n_live >= 8) return load_a8<XT>(p, dt, off, true, vec32);
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w[j] = cvt_pk<XT>(2 * j < n_live ? load_as_f32(p, off + 2 * j, dt) : 0.0f,
+                      2 * j + 1 < n_live ? load_as_f32(p, off + 2 * j + 1, dt) : 0.0f);
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
+// 8 values p[off + e * stride] (e < n_live, zeros past), rounded to the
+// activation dtype.
+template <int XT>
+__device__ __forceinline__ u32x4 load_a8_strided(const void* p, int dt, int64_t off, int64_t stride, int n_live) {
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w[j] = cvt_pk<XT>(2 * j < n_live ? load_as_f32(p, off + (2 * j) * stride, dt) : 0.0f,
+                      2 * j + 1 < n_live ? load_as_f32(p, off + (2 * j + 1) * stride, dt) : 0.0f);
+  return u32x4{w[0], w[1], w[2], w[3]};
+}
+
 // ---------------------------------------------------------------------------
 // Host helpers
 // ---------------------------------------------------------------------------

@@ -33,7 +33,8 @@ constexpr int kLoraSPitch = kLoraChunkK + 8;
 template <int XT, bool PRESCALE>
 __global__ __launch_bounds__(256) void lora_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
                                                         int64_t K, const uint16_t* __restrict__ s16, int R,
-                                                        float prescale, int64_t k_per_split,
+                                                        const void* __restrict__ sraw, int sdt, int64_t ldsr,
+                                                        bool svec, float prescale, int64_t k_per_split,
                                                         float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) uint16_t ss[kLoraRowsR * kLoraSPitch];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -66,8 +67,10 @@ __global__ __launch_bounds__(256) void lora_rows_kernel(const uint16_t* __restri
       const int jj = tid / 32 + 8 * i, c = tid % 32;
       const int j = j0 + jj;
       if (c < c16) {
-        const u32x4 v = j < R ? *reinterpret_cast<const u32x4*>(s16 + int64_t(j) * K + kc + 8 * c)
-                              : u32x4{0u, 0u, 0u, 0u};
+        // RND(S) from the rounded copy, or from S itself (rows of stride ldsr)
+        const u32x4 v = j >= R ? u32x4{0u, 0u, 0u, 0u}
+                        : sraw ? load_a8<XT>(sraw, sdt, int64_t(j) * ldsr + kc + 8 * c, true, svec)
+                               : *reinterpret_cast<const u32x4*>(s16 + int64_t(j) * K + kc + 8 * c);
         *reinterpret_cast<u32x4*>(ss + jj * kLoraSPitch + 8 * c) = v;
       }
     }
@@ -197,10 +200,12 @@ LoraRowsPlan plan_lora_rows(int64_t M, int64_t K, int64_t R, int cus) {
 
 template <int XT, bool PRESCALE>
 static int launch_rows_t(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const uint16_t* s16, int R,
-                         float prescale, const LoraRowsPlan& p, float* part, hipStream_t stream) {
+                         const void* sraw, int sdt, int64_t ldsr, bool svec, float prescale, const LoraRowsPlan& p,
+                         float* part, hipStream_t stream) {
   dim3 grid(unsigned((M + kLoraRowsM - 1) / kLoraRowsM), unsigned((R + kLoraRowsR - 1) / kLoraRowsR),
             unsigned(p.splits));
-  lora_rows_kernel<XT, PRESCALE><<<grid, 256, 0, stream>>>(x, ldx, M, K, s16, R, prescale, p.k_per_split, part);
+  lora_rows_kernel<XT, PRESCALE><<<grid, 256, 0, stream>>>(x, ldx, M, K, s16, R, sraw, sdt, ldsr, svec, prescale,
+                                                           p.k_per_split, part);
   return rq_check_launch();
 }
 
@@ -208,15 +213,23 @@ int run_lora_rows(int xt, const uint16_t* x, int64_t ldx, int64_t M, int64_t K, 
                   int64_t s_j, int64_t s_k, int R, bool prescale, float scale, const LoraRowsPlan& p, float* part,
                   uint16_t* s16, uint16_t* out, int R16, hipStream_t stream) {
   if (!aligned(x, 16) || ldx % 8 != 0 || K % 64 != 0) return RQ_ERR_BAD_ALIGNMENT;
-  // RND(S) as a contiguous [R][K] 16-bit copy: S[j][k] = s[j * s_j + k * s_k]
-  int st = run_lora_round(xt, s, s_dt, s_j, s_k, R, int(K), int(K), s16, stream);
-  if (st != RQ_OK) return st;
+  // S with contiguous rows is rounded as it is staged; otherwise RND(S) is
+  // first gathered into a contiguous [R][K] 16-bit copy: S[j][k] = s[j * s_j + k * s_k]
+  int st = RQ_OK;
+  const bool direct = s_k == 1;
+  const bool svec = direct && aligned(s, 16) && (s_dt != RQ_DTYPE_F32 || s_j % 4 == 0);
+  if (!direct && (st = run_lora_round(xt, s, s_dt, s_j, s_k, R, int(K), int(K), s16, stream)) != RQ_OK) return st;
+  const void* sraw = direct ? s : nullptr;
   if (xt == RQ_DTYPE_BF16)
-    st = prescale ? launch_rows_t<RQ_DTYPE_BF16, true>(x, ldx, M, K, s16, R, scale, p, part, stream)
-                  : launch_rows_t<RQ_DTYPE_BF16, false>(x, ldx, M, K, s16, R, scale, p, part, stream);
+    st = prescale ? launch_rows_t<RQ_DTYPE_BF16, true>(x, ldx, M, K, s16, R, sraw, s_dt, s_j, svec, scale, p, part,
+                                                       stream)
+                  : launch_rows_t<RQ_DTYPE_BF16, false>(x, ldx, M, K, s16, R, sraw, s_dt, s_j, svec, scale, p, part,
+                                                        stream);
   else
-    st = prescale ? launch_rows_t<RQ_DTYPE_F16, true>(x, ldx, M, K, s16, R, scale, p, part, stream)
-                  : launch_rows_t<RQ_DTYPE_F16, false>(x, ldx, M, K, s16, R, scale, p, part, stream);
+    st = prescale ? launch_rows_t<RQ_DTYPE_F16, true>(x, ldx, M, K, s16, R, sraw, s_dt, s_j, svec, scale, p, part,
+                                                      stream)
+                  : launch_rows_t<RQ_DTYPE_F16, false>(x, ldx, M, K, s16, R, sraw, s_dt, s_j, svec, scale, p, part,
+                                                       stream);
   if (st != RQ_OK) return st;
   const unsigned blocks = unsigned((M * (R16 / 8) + 255) / 256);
   if (xt == RQ_DTYPE_BF16)
