@@ -188,7 +188,11 @@ LoraRowsPlan plan_lora_rows(int64_t M, int64_t K, int64_t R, int cus) {
   LoraRowsPlan p{};
   const int64_t tiles = ((M + kLoraRowsM - 1) / kLoraRowsM) * ((R + kLoraRowsR - 1) / kLoraRowsR);
   const int64_t steps = K / 64;
+  // enough splits to fill the compute units, and at most 8 steps (two LDS
+  // chunks) per split: a workgroup's chunks run one after another
   int64_t ks = (cus + tiles - 1) / tiles;
+  const int64_t ks_len = (steps + 7) / 8;
+  ks = ks < ks_len ? ks_len : ks;
   ks = ks < 1 ? 1 : (ks > steps ? steps : ks);
   const int64_t steps_per = (steps + ks - 1) / ks;
   p.k_per_split = steps_per * 64;
