@@ -18,11 +18,19 @@ Also reported:
   gemm          the prefill/training shapes: the same seven projections at
                 M = 2048 tokens with LoRA r = 64, alpha = 16, forward and dX
                 backward, TFLOP/s and fraction of the 2.5 PFLOP/s bf16 MFMA peak.
+  codec         NF4 + double quantization of an 11008x4096 bf16 weight (N(0,0.02)
+                with 0.1 % outliers at +-8 sigma, blocks 64 / 256): quantize ->
+                pack -> double-quantize the absmax, and double-dequantize ->
+                bf16; algorithmic bytes / time vs 8 TB/s.
+  byte_linears  INT8 (per-row absmax) and FP8 (e4m3fnuz, per-tensor scales)
+                linears at the Llama-3-70B MLP shape 8192 -> 28672, M = 1
+                (HBM: bytes / time, two weight copies rotating) and M = 512,
+                4096 (TFLOP/s against the bf16 MFMA peak).
   cpu_baseline  the oracle's restatement of the reference's CPU path
                 (dequantize_int4 -> .to(bf16) -> F.linear + LoRA) over a bounded
                 sample of the same decode step on the host cores.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m M] [--no-gemm] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--m M] [--no-gemm] [--no-extra] [--no-cpu]
     python bench.py --summarize-profile DIR   # per-kernel, per-grid rocprofv3 kernel-trace table
     python bench.py --counters                # short eager run for rocprofv3 --pmc passes
     python bench.py --summarize-counters DIR [DIR ...]   # HBM bytes per launch from those passes
@@ -203,6 +211,89 @@ def bench_gemm(dev, stream):
             "peak_tflops": BF16_PEAK_TFLOPS, "per_shape": per}
 
 
+def bench_codec(dev, stream):
+    """NF4 + double quantization of the down-projection weight (11008 x 4096
+    bf16, 0.1 % outliers at +-8 sigma), blocks 64 / 256, 10 graph replays
+    each way.  Algorithmic bytes (each way): 2 numel (bf16 W) + numel / 2
+    (packed) + numel / 64 (c2 codes) + 4 numel / 16384 (c2 scales)."""
+    import torch
+    from rocm_qlora.quantization import quantize_int4
+    from rocm_qlora.quantization.double_quant import dq_quantize_absmax, dq_dequantize_to
+    N, K = 11008, 4096
+    numel = N * K
+    g = torch.Generator(device=dev).manual_seed(5)
+    w = torch.randn(N, K, generator=g, device=dev) * 0.02
+    n_out = numel // 1000
+    idx = torch.randperm(numel, generator=g, device=dev)[:n_out]
+    sign = torch.randint(0, 2, (n_out,), generator=g, device=dev).float() * 2 - 1
+    w.view(-1)[idx] = sign * 0.16
+    w = w.to(torch.bfloat16)
+    state = {}
+
+    def encode():
+        packed, c1 = quantize_int4(w, 64)
+        c2, c2s = dq_quantize_absmax(c1, 256, True)
+        state.update(packed=packed, c2=c2, c2s=c2s)
+
+    encode()
+    ge = _capture(encode, stream)
+    packed, c2, c2s = state["packed"], state["c2"], state["c2s"]
+    gd = _capture(lambda: dq_dequantize_to(packed, c2, c2s, 64, 256, True, torch.bfloat16, numel), stream)
+    nbytes = 2 * numel + numel // 2 + numel // 64 + 4 * numel // 16384
+    with _Range(f"rq-codec encode {N}x{K}"):
+        ms_e = _time_graph(ge, 10)
+    with _Range(f"rq-codec decode {N}x{K}"):
+        ms_d = _time_graph(gd, 10)
+    del ge, gd
+    enc, dec = nbytes / ms_e / 1e6, nbytes / ms_d / 1e6
+    return {"workload": f"NF4 + double quantization (blocks 64/256, fp8 c2) of a {N}x{K} bf16 weight with "
+                        f"0.1% outliers at +-8 sigma",
+            "bytes": nbytes, "encode_us": round(ms_e * 1e3, 2), "encode_gbs": round(enc, 1),
+            "encode_frac": round(enc / HBM_PEAK_GBS, 4), "decode_us": round(ms_d * 1e3, 2),
+            "decode_gbs": round(dec, 1), "decode_frac": round(dec / HBM_PEAK_GBS, 4)}
+
+
+def bench_byte_linears(dev, stream):
+    """INT8 per-row-absmax and FP8 (e4m3fnuz) linears at 8192 -> 28672 with
+    bf16 activations N(0,1), weights N(0,0.02); M = 1 rotates two weight
+    copies (470 MB each kind, past the MALL), M = 512 and 4096 one copy."""
+    import torch
+    from rocm_qlora import ops
+    from rocm_qlora.quantization import quantize_int8
+    K, N = 8192, 28672
+    g = torch.Generator(device=dev).manual_seed(9)
+    int8_w, fp8_w = [], []
+    for c in range(2):
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        int8_w.append(quantize_int8(w, per_channel=True))
+        fp8_w.append(ops.fp8_quantize(w))
+        del w
+    out = {}
+    for M in (1, 512, 4096):
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        copies = 2 if M == 1 else 1
+        for kind in ("int8", "fp8"):
+            if kind == "int8":
+                fn = lambda: [ops.int8_linear(x, q, s, N) for q, s in int8_w[:copies]]
+            else:
+                fn = lambda: [ops.fp8_linear(x, cw, sc) for cw, sc in fp8_w[:copies]]
+            gr = _capture(fn, stream)
+            with _Range(f"rq-{kind}-linear M={M} K={K} N={N}"):
+                us = _time_graph(gr, 10) * 1e3 / copies
+            del gr
+            if M == 1:
+                nb = N * K + 4 * N + 2 * M * K + 2 * M * N
+                gbs = nb / us / 1e3
+                out[f"{kind}_m{M}"] = {"us": round(us, 2), "gbs": round(gbs, 1),
+                                        "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm"}
+            else:
+                tf = 2 * M * N * K / us / 1e6
+                out[f"{kind}_m{M}"] = {"us": round(us, 2), "tflops": round(tf, 1),
+                                        "frac": round(tf / BF16_PEAK_TFLOPS, 4), "bound": "bf16 mfma"}
+        del x
+    return {"workload": f"INT8 per-row and FP8 per-tensor linears, K={K} N={N}, bf16 activations", **out}
+
+
 def _short(name, n=70):
     return name if len(name) <= n else name[:n - 3] + "..."
 
@@ -330,6 +421,7 @@ def main():
     ap.add_argument("--m", type=int, default=1, help="decode tokens per step (activation rows)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the M=2048 GEMM section")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the codec and INT8/FP8 sections")
     ap.add_argument("--summarize-profile", metavar="DIR", help="summarize a rocprofv3 CSV kernel trace and exit")
     ap.add_argument("--counters", action="store_true", help="short eager run for rocprofv3 --pmc passes")
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
@@ -416,6 +508,17 @@ def main():
     else:
         layer0 = layers[0]
 
+    codec = byte = None
+    if not args.no_extra:
+        codec = bench_codec(dev, stream)
+        print(f"bench: codec encode {codec['encode_gbs']} GB/s, decode {codec['decode_gbs']} GB/s",
+              file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        byte = bench_byte_linears(dev, stream)
+        print("bench: byte linears " + ", ".join(f"{k} {v['us']} us" for k, v in byte.items()
+                                                  if isinstance(v, dict)), file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu:
         layer_cpu = {nm: tuple(t.cpu() if torch.is_tensor(t) else t for t in v) for nm, v in layer0.items()}
@@ -449,6 +552,8 @@ def main():
                      "kernel": "nf4_gemv_kernel", "shape": f"M={M} K={K} N={N}",
                      "bytes_per_launch": kb, "us_per_launch": round(us_launch, 3)},
         "gemm": gemm,
+        "codec": codec,
+        "byte_linears": byte,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)
