@@ -17,6 +17,7 @@
 // M > 16 runs the shared MFMA core (rq_gemm_core.h) with a byte-weight
 // producer; M <= 16 runs byte_gemv_kernel, a weight-streaming MFMA GEMV.
 #include "rq_gemm_core.h"
+#include "rq_gemm8.h"
 
 namespace rq {
 
@@ -64,60 +65,54 @@ struct ScaleNone {
   __device__ __forceinline__ float value(Raw) const { return 1.0f; }
 };
 
-// Forward producer for byte weights: tile row = output feature n, 64
-// reduction k per step = 64 weight bytes per row.  Thread t decodes row
-// t / 2, bytes 32 (t % 2) .. +32 of the step (piece p = bytes 8p .. 8p + 7).
+// Forward producer for byte weights (512 threads): tile row = output feature
+// n, 64 reduction k per step = 64 weight bytes per row.  Thread t decodes
+// row t / 4, bytes 16 (t % 4) .. +16 of the step (piece p = bytes 8p .. 8p + 7).
 template <int XT, class Scale, bool FP8>
-struct ByteProducer {
-  static constexpr int kLoads = 2 + Scale::kLoads;
+struct Byte8Producer {
+  static constexpr int kLoads = 1 + Scale::kLoads;
   struct Regs {
-    u32x4 w[2];
+    u32x4 w;
     typename Scale::Raw s;
   };
   struct Step {
     float sc;
-    u32x4 w[2];
+    u32x4 w;
     uint32_t r[4];
   };
   ProducerParams P;
   Scale scale;
-  uint32_t tile_row, half, wrow;
+  uint32_t tile_row, quarter, wrow;
   int64_t wn;
 
   __device__ __forceinline__ void init(const ProducerParams& p, const Scale& sc, const u32x2*, int tid,
                                        int64_t col0) {
     P = p;
     scale = sc;
-    tile_row = uint32_t(tid >> 1);
-    half = uint32_t(tid & 1);
+    tile_row = uint32_t(tid >> 2);
+    quarter = uint32_t(tid & 3);
     wn = col0 + tile_row;
     wn = wn < P.rows ? wn : P.rows - 1;  // rows past N re-read a live row; never stored
-    wrow = uint32_t(wn * P.row_bytes + 32 * half);  // the host keeps the weights under 4 GiB
+    wrow = uint32_t(wn * P.row_bytes + 16 * quarter);  // the host keeps the weights under 4 GiB
   }
   __device__ __forceinline__ void issue(Regs& R, int64_t kstep) const {
-    const uint32_t off = wrow + uint32_t(kstep) * 64u;
-    R.w[0] = *reinterpret_cast<const u32x4*>(P.packed + off);
-    R.w[1] = *reinterpret_cast<const u32x4*>(P.packed + (off + 16u));
+    R.w = *reinterpret_cast<const u32x4*>(P.packed + (wrow + uint32_t(kstep) * 64u));
     R.s = scale.load(wn * P.blocks_per_row + ((kstep * kGemmBK) >> P.bs_log2));
   }
   __device__ __forceinline__ void prep(Step& S, const Regs& R) const {
-    // an (empty) use of the step's last-loaded words, so that the wait for
-    // these loads happens here, ahead of the step's direct-to-LDS loads
-    asm volatile("" ::"v"(R.w[1].w), "v"(R.w[0].x));
     S.sc = scale.value(R.s);
-    S.w[0] = R.w[0];
-    S.w[1] = R.w[1];
+    S.w = R.w;
   }
   __device__ __forceinline__ void lookup(Step&, int) const {}
   __device__ __forceinline__ void finish(Step& S, int p, int hh, uint8_t* tile) const {
-    const int d = 2 * p + hh;  // dword of this thread's 32 bytes
-    const u32x4& q = S.w[d >> 2];
-    const uint32_t word = (d & 3) == 0 ? q.x : (d & 3) == 1 ? q.y : (d & 3) == 2 ? q.z : q.w;
+    const int d = 2 * p + hh;  // dword of this thread's 16 bytes
+    const uint32_t word = d == 0 ? S.w.x : d == 1 ? S.w.y : d == 2 ? S.w.z : S.w.w;
     const uint2 pk = decode4_pk<XT, FP8>(word, S.sc);
     S.r[2 * hh] = pk.x;
     S.r[2 * hh + 1] = pk.y;
     if (hh == 1)
-      *reinterpret_cast<u32x4*>(tile + swz(tile_row, 4u * half + uint32_t(p))) = u32x4{S.r[0], S.r[1], S.r[2], S.r[3]};
+      *reinterpret_cast<u32x4*>(tile + swz(tile_row, 2u * quarter + uint32_t(p))) =
+          u32x4{S.r[0], S.r[1], S.r[2], S.r[3]};
   }
 };
 
@@ -347,13 +342,14 @@ static int launch_byte(const ByteLinearArgs& A, const uint16_t* xact, int64_t ld
   GemmArgs a{};
   a.x = xact; a.ldx = ldx; a.M = A.M; a.N = A.N; a.K = A.K;
   a.tiles_m = p.tiles_m; a.tiles_n = p.tiles_n; a.xcd_map = p.xcd_map;
+  a.splits = 1; a.lf = p.tiles_m * p.tiles_n / 8;
   GemmEpi e{};
   e.bias = A.bias; e.bias_dt = A.bias_dtype; e.scaling = 1.0f;
   e.post_a = post_a; e.post_b = post_b;
   e.y = static_cast<uint16_t*>(A.y); e.ldy = A.ldy;
   ProducerParams pp{A.w, A.K, A.N, bpr, bsl};
   const unsigned grid = unsigned(int64_t(p.tiles_m) * p.tiles_n);
-  nf4_gemm_kernel<XT, ByteProducer<XT, Scale, FP8>, Scale><<<grid, kGemmThreads, 0, stream>>>(a, pp, scale, e);
+  nf4_gemm8_kernel<XT, Byte8Producer<XT, Scale, FP8>, Scale><<<grid, kGemm8Threads, 0, stream>>>(a, pp, scale, e);
   return rq_check_launch();
 }
 

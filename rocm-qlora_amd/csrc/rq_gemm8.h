@@ -1,10 +1,10 @@
-// Eight-wave variant of the NF4 MFMA GEMM core for gfx950 (the forward
-// GEMM): the same 256 x 128 workgroup tile, LDS layout and k loop as
-// nf4_gemm_kernel, split over 512 threads, two waves per SIMD.  Wave w owns
-// rows 64 (w % 4) .. +63 and columns 64 (w / 4) .. +63 of the tile as 2 x 2
-// blocks of v_mfma_f32_32x32x16_{bf16,f16}.  With one wave per SIMD the
-// matrix core waits whenever that wave waits (LDS reads, table lookups,
-// barrier); a second wave per SIMD issues its MFMAs in those gaps.
+// The NF4/byte-weight MFMA GEMM kernel for gfx950 (forward GEMM, dX, INT8 /
+// FP8 linears, by producer policy): 256 x 128 workgroup tiles, 64-k steps,
+// 512 threads, two waves per SIMD.  Wave w owns rows 64 (w % 4) .. +63 and
+// columns 64 (w / 4) .. +63 of the tile as 2 x 2 blocks of
+// v_mfma_f32_32x32x16_{bf16,f16}.  With one wave per SIMD (a 64 x 128 block
+// each) the matrix core waited whenever that wave waited (LDS reads, table
+// lookups, barrier); a second wave per SIMD issues its MFMAs in those gaps.
 //
 // The two waves of a row slice (w and w + 4) each bring half of the slice's
 // activation rows into the ring; the step barrier, which already waits for
@@ -145,8 +145,8 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   const int rb = wave & 3, ch = wave >> 2;  // row slice, column half
   const int i32 = lane & 31, q = lane >> 5;
 
-  // tile and K split of this workgroup: the tile numbering of
-  // nf4_gemm_kernel (XCD x = g % 8 takes tiles x T/8 .. +T/8), its first lf
+  // tile and K split of this workgroup: with xcd_map, XCD x = g % 8 takes
+  // tiles x T/8 .. +T/8 (row slices whose activations stay in its L2), its first lf
   // tiles whole, the rest as `splits` workgroups each (split tile ti of the
   // launch); every split of a tile sits on the tile's XCD
   const int64_t T = int64_t(a.tiles_m) * a.tiles_n;
@@ -192,6 +192,10 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   Prod prod;
   prod.init(pp, scale, lut, tid, n0);
 
+  // Staggered start: step j covers k-step ks(j) = kbeg + (j + k_off) mod nk.
+  // Workgroups sharing an activation row slice (one XCD) and those sharing a
+  // weight tile start at different steps, so that one of them misses on each
+  // line and the rest find it in L2 or the MALL.
   const int nk32 = __builtin_amdgcn_readfirstlane(int(nk));
   const int k_off = __builtin_amdgcn_readfirstlane(int((((nt + 4 * mt) & 31) * nk) >> 5));
   const int kb32 = __builtin_amdgcn_readfirstlane(int(kbeg));
@@ -232,11 +236,16 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
 
-  // The k loop of nf4_gemm_kernel: step j computes on slot j % 2, loads
-  // activations j + 1 into the other slot, dequantizes step j + 1 into the
-  // other weight tile, loads the packed weights of step j + 4; the barrier
-  // leaves only those trailing weight loads in flight (in the tail, where
-  // they feed nothing and are dropped, it waits for every load).
+  // Step j: MFMAs on weight tile j % 2 and activation ring slot j % 2;
+  // direct-to-LDS loads of activations j + 1 into the other slot; step j + 1
+  // dequantized from wl[(j + 1) % 4] into the other weight tile; packed
+  // weights of step j + 4 into wl[j % 4]; then a barrier that waits for
+  // this wave's activation loads (all but the step's kLoads trailing weight
+  // loads).  Four steps per iteration index every register set statically;
+  // the loop has a single exit, so the accumulators stay in place.  Steps
+  // past the end wrap around the split's K range (in bounds; their results
+  // are never used).  In the tail the weight loads feed nothing, so the
+  // compiler drops them, and the barrier waits for every load.
 #define RQ_GEMM8_STEP(J, P, WAIT)                                                                              \
   do {                                                                                                         \
     gemm8_step<XT, Prod>(acc, xring + ((P) & 1) * kXStepBytes, wtile + ((P) & 1) * kWTileBytes, i32, q,       \
@@ -314,7 +323,10 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
       }
   }
 
-  // ---- epilogue: the one of nf4_gemm_kernel on this wave's 64 x 64 block
+  // ---- epilogue.  y = RND(RND(acc + RND(bias)) + RND(RND(lora) * scaling))
+  // with lora = RND(u) RND(B)^T accumulated by MFMA in chunks of 64 ranks,
+  // both operands staged into LDS (u rows and B rows of the tile, 144-byte
+  // pitch); FP8: y = RND(RND(acc * post_a * post_b) + RND(bias)).
   const int rank = e.rank;
   f32x16 lo[kGemm8MB][kGemm8NB];
 #pragma unroll

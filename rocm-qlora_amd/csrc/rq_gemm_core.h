@@ -1,9 +1,8 @@
-// The NF4/byte-weight MFMA GEMM core for gfx950, shared by the forward
-// GEMM, the dX backward and the INT8/FP8 linears: activation rows streamed
-// into a swizzled LDS ring by direct-to-LDS loads, a weight operand tile
-// produced each step by a producer policy (see the producer interface
-// below), 32x32x16 MFMAs, and the bias/LoRA/scale epilogue.  Layout and
-// schedule are described at gemm_step and nf4_gemm_kernel.
+// Shared pieces of the NF4/byte-weight MFMA GEMM for gfx950 (the forward
+// GEMM, the dX backward and the INT8/FP8 linears): tile and LDS layout
+// constants, kernel arguments, the swizzle, wait and direct-to-LDS helpers,
+// the producer interface, and the host-side plan.  The kernel itself is
+// nf4_gemm8_kernel (rq_gemm8.h).
 #pragma once
 #include "rq_mfma.h"
 #include "rq_launch.h"
@@ -13,21 +12,18 @@
 
 namespace rq {
 
-constexpr int kGemmThreads = 256;
 constexpr int kGemmBM = 256;
 constexpr int kGemmBN = 128;
 constexpr int kGemmBK = 64;
-constexpr int kGemmMB = 2;  // 32-row blocks per wave
-constexpr int kGemmNB = 4;  // 32-column blocks per wave
 constexpr int kLutBytes = kF32PairLutQwords * 8;     // 64 KiB
-constexpr int kXWaveBytes = 64 * 128;                // one wave's rows of one step
+constexpr int kXWaveBytes = 64 * 128;                // one 64-row slice of one step
 constexpr int kXStepBytes = 4 * kXWaveBytes;         // 32 KiB
 constexpr int kWTileBytes = kGemmBN * 128;           // 16 KiB
 constexpr int kXRingOff = kLutBytes;
 constexpr int kWTileOff = kXRingOff + 2 * kXStepBytes;
 constexpr int kGemmLds = kWTileOff + 2 * kWTileBytes;  // 160 KiB
 constexpr int kWDepth = 4;                           // packed-weight prefetch distance in steps
-constexpr int kGemmMaxSplits = 4;                    // K splits of the eight-wave core
+constexpr int kGemmMaxSplits = 4;                    // K splits of a tile
 static_assert(kGemmLds == 160 * 1024, "LDS plan");
 
 // Core problem: out[M, N] = act[M, K] . op[N, K]^T (+ epilogue).
@@ -125,7 +121,7 @@ __device__ __forceinline__ u32x2 lut_read(const u32x2* lut, uint32_t addr) {
 //                            addresses); called before the step's
 //                            direct-to-LDS loads, so that no later
 //                            instruction waits on a register load
-//   lookup(S, p)             table reads of piece p (p = 0..3)
+//   lookup(S, p)             table reads of piece p
 //   finish(S, p, h, tile)    half h of piece p's scale-multiply and rounding,
 //                            and its LDS stores into the operand tile
 // ---------------------------------------------------------------------------
@@ -136,263 +132,6 @@ struct ProducerParams {
   int64_t blocks_per_row;   // layer K / block_size
   int bs_log2;
 };
-
-// One 64-k step for a wave's 64 x 128 tile, software-pipelined by hand so
-// that the matrix cores never wait on the rest of the wave's work: an MFMA
-// keeps the core busy for 32 cycles, in which the wave can issue a few VALU,
-// LDS and vector-memory instructions, so that work is spread between the
-// MFMAs (in-order issue would otherwise leave the core idle while a batch of
-// it drains).  Sub-step s (k = 16 s + 8 q + e, eight MFMAs in four pairs):
-//   head:   activation and weight operand reads of sub-step s + 1;
-//   pair 0: (s < 2) four of the eight direct-to-LDS loads of step j + 1;
-//   pair 1: table lookups of piece s + 1 of the next step's weights;
-//   pair 2, 3: the two halves of piece s's scale-multiply, rounding and
-//           LDS stores into the other weight tile; after the last pair, the
-//           packed weights of step j + 4 (the last loads of the step, so the
-//           next step's activation wait leaves them in flight).
-// Scheduling fences pin each group.
-template <int XT, class Prod>
-__device__ __forceinline__ void gemm_step(f32x16 (&acc)[kGemmMB][kGemmNB], const uint8_t* xr, const uint8_t* wt,
-                                          int i32, int q, const GemmArgs& a, const uint32_t (&xo)[8],
-                                          int64_t kx, uint32_t xdst, const Prod& prod,
-                                          const typename Prod::Regs& wq, typename Prod::Regs& wl_fill,
-                                          int64_t kfill, uint8_t* wdst) {
-  typename Prod::Step S;
-  prod.prep(S, wq);
-  auto read_ops = [&](u32x4 (&xa)[kGemmMB], u32x4 (&b)[kGemmNB], int s) {
-    const uint32_t c = uint32_t(2 * s + q);
-#pragma unroll
-    for (int mb = 0; mb < kGemmMB; ++mb)
-      xa[mb] = *reinterpret_cast<const u32x4*>(xr + swz(uint32_t(32 * mb + i32), c));
-#pragma unroll
-    for (int nb = 0; nb < kGemmNB; ++nb)
-      b[nb] = *reinterpret_cast<const u32x4*>(wt + swz(uint32_t(32 * nb + i32), c));
-  };
-  u32x4 xa[kGemmMB], b[kGemmNB], xan[kGemmMB], bn[kGemmNB];
-  read_ops(xa, b, 0);
-  prod.lookup(S, 0);
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    if (s < 3) read_ops(xan, bn, s + 1);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int nb = 0; nb < kGemmNB; ++nb) {
-#pragma unroll
-      for (int mb = 0; mb < kGemmMB; ++mb) acc[mb][nb] = mfma32x32x16<XT>(xa[mb], b[nb], acc[mb][nb]);
-      if (nb == 0) {
-        if (s < 2) {
-#pragma unroll
-          for (int t = 4 * s; t < 4 * s + 4; ++t) dma16(a.x, (xo[t] + uint32_t(kx) * kGemmBK) * 2u, xdst + t * 1024);
-        }
-      } else if (nb == 1) {
-        if (s < 3) prod.lookup(S, s + 1);
-      } else {
-        prod.finish(S, s, nb - 2, wdst);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if (s < 3) {
-#pragma unroll
-      for (int mb = 0; mb < kGemmMB; ++mb) xa[mb] = xan[mb];
-#pragma unroll
-      for (int nb = 0; nb < kGemmNB; ++nb) b[nb] = bn[nb];
-    }
-  }
-  prod.issue(wl_fill, kfill);
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-template <int XT, class Prod, class Scale>
-__global__ __launch_bounds__(kGemmThreads) void nf4_gemm_kernel(GemmArgs a, ProducerParams pp, Scale scale,
-                                                                GemmEpi e) {
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kGemmLds];
-  u32x2* lut = reinterpret_cast<u32x2*>(lds);
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int i32 = lane & 31, q = lane >> 5;
-
-  // tile of this workgroup
-  const int64_t T = int64_t(a.tiles_m) * a.tiles_n;
-  const int64_t g = blockIdx.x;
-  const int64_t t = a.xcd_map ? (g % 8) * (T / 8) + g / 8 : g;
-  const int64_t mt = t / a.tiles_n, nt = t % a.tiles_n;
-  const int64_t m0 = mt * kGemmBM, n0 = nt * kGemmBN;
-  const int64_t m0w = m0 + 64 * wave;
-  const int64_t nk = a.K / kGemmBK;
-
-  // Activation DMA lanes: per instruction t, row r = 8t + lane / 8 of the
-  // wave, chunk (lane % 8) ^ ((r / 2) & 7); element offsets are 32-bit (the
-  // host keeps the activations under 4 GiB).
-  uint32_t xo[8];
-#pragma unroll
-  for (int tt = 0; tt < 8; ++tt) {
-    const int r = 8 * tt + (lane >> 3);
-    int64_t m = m0w + r;
-    m = m < a.M ? m : a.M - 1;  // rows past M re-read a live row; never stored
-    xo[tt] = uint32_t(m * a.ldx + 8 * ((lane & 7) ^ ((r >> 1) & 7)));
-  }
-  uint8_t* xring = lds + kXRingOff + wave * kXWaveBytes;  // + (step & 1) * kXStepBytes
-  const uint32_t xring_addr = __builtin_amdgcn_readfirstlane(uint32_t(kXRingOff + wave * kXWaveBytes));
-  uint8_t* wtile = lds + kWTileOff;                       // + (step & 1) * kWTileBytes
-  Prod prod;
-  prod.init(pp, scale, lut, tid, n0);
-
-  // Staggered start: step j covers k-step ks(j) = (j + k_off) mod nk.
-  // Workgroups sharing an activation row slice (one XCD) and those sharing a
-  // weight tile (one per XCD) start at different steps, so that one of them
-  // misses on each line and the rest find it in L2 or the MALL.
-  const int nk32 = __builtin_amdgcn_readfirstlane(int(nk));
-  const int k_off = __builtin_amdgcn_readfirstlane(int((((nt + 4 * mt) & 31) * nk) >> 5));
-  auto ks = [&](int64_t j) -> int64_t {
-    int v = int(j) + k_off;
-    v = v >= nk32 ? v - nk32 : v;
-    v = v >= nk32 ? v - nk32 : v;
-    return v;
-  };
-
-  // prologue: activations of step 0, packed weights of steps 0..3, the
-  // table, and step 0's weight tile
-  {
-#pragma unroll
-    for (int tt = 0; tt < 8; ++tt) dma16(a.x, (xo[tt] + uint32_t(ks(0)) * kGemmBK) * 2u, xring_addr + tt * 1024);
-  }
-  typename Prod::Regs wl[kWDepth];
-#pragma unroll
-  for (int d = 0; d < kWDepth; ++d) prod.issue(wl[d], ks(d));
-  fill_f32pair_lut<kGemmThreads * 2>(lut, tid);  // the 512-thread fill pattern, in two halves
-  fill_f32pair_lut<kGemmThreads * 2>(lut, tid + kGemmThreads);
-  __syncthreads();
-  {
-    typename Prod::Step S;
-    prod.prep(S, wl[0]);
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      prod.lookup(S, p);
-      prod.finish(S, p, 0, wtile);
-      prod.finish(S, p, 1, wtile);
-    }
-  }
-  wait_vmcnt<0>();
-  __syncthreads();
-
-  f32x16 acc[kGemmMB][kGemmNB];
-#pragma unroll
-  for (int mb = 0; mb < kGemmMB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < kGemmNB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
-
-  // Step j: MFMAs on weight tile j % 2 and activation ring slot j % 2;
-  // direct-to-LDS loads of activations j + 1 into slot (j + 1) % 2;
-  // dequantize step j + 1 from wl[(j + 1) % 4] into tile (j + 1) % 2;
-  // packed weights j + 4 into wl[j % 4]; then wait for this wave's
-  // activation loads (all but the step's kLoads trailing weight loads) and
-  // barrier.  Four steps per iteration index every register set statically;
-  // the loop has a single exit, so the accumulators stay in place.  Steps
-  // past the end wrap around K (in bounds; their results are never used).
-  // In the loop, each step's last vector-memory loads are the kLoads weight
-  // loads, whose registers later steps consume; the barrier leaves them in
-  // flight.  In the tail the weight loads feed nothing, so the compiler drops
-  // them, and the barrier must wait for every load (the activations of the
-  // next step would otherwise be read before they land).
-#define RQ_GEMM_STEP(J, P, WAIT)                                                                               \
-  do {                                                                                                         \
-    gemm_step<XT, Prod>(acc, xring + ((P) & 1) * kXStepBytes, wtile + ((P) & 1) * kWTileBytes, i32, q, a, xo,  \
-                        ks((J) + 1), xring_addr + (((P) + 1) & 1) * kXStepBytes, prod, wl[((P) + 1) & 3], wl[P], \
-                        ks((J) + kWDepth), wtile + (((P) + 1) & 1) * kWTileBytes);                             \
-    step_barrier<WAIT>();                                                                                      \
-  } while (0)
-  int64_t j = 0;
-  for (; j + 4 <= nk; j += 4) {
-    RQ_GEMM_STEP(j, 0, Prod::kLoads);
-    RQ_GEMM_STEP(j + 1, 1, Prod::kLoads);
-    RQ_GEMM_STEP(j + 2, 2, Prod::kLoads);
-    RQ_GEMM_STEP(j + 3, 3, Prod::kLoads);
-  }
-  const int64_t rem = nk - j;
-  if (rem > 0) RQ_GEMM_STEP(j, 0, 0);
-  if (rem > 1) RQ_GEMM_STEP(j + 1, 1, 0);
-  if (rem > 2) RQ_GEMM_STEP(j + 2, 2, 0);
-#undef RQ_GEMM_STEP
-  wait_vmcnt<0>();  // nothing may still be landing in LDS when the epilogue reuses it
-
-  // ---- epilogue.  y = RND(RND(acc + RND(bias)) + RND(RND(lora) * scaling))
-  // with lora = RND(u) RND(B)^T accumulated by MFMA in chunks of 64 ranks,
-  // both operands staged from their pre-rounded 16-bit copies into LDS
-  // (u rows of the tile, B rows of the tile, 144-byte pitch).
-  const int rank = e.rank;
-  f32x16 lo[kGemmMB][kGemmNB];
-#pragma unroll
-  for (int mb = 0; mb < kGemmMB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < kGemmNB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) lo[mb][nb][r] = 0.0f;
-  if (rank > 0) {
-    constexpr int kP = 72;  // staging pitch in elements
-    uint16_t* us = reinterpret_cast<uint16_t*>(lds);   // [256][kP]
-    uint16_t* bs = us + kGemmBM * kP;                  // [128][kP]
-    for (int j0 = 0; j0 < e.rank16; j0 += 64) {
-      const int w8 = (e.rank16 - j0 < 64 ? e.rank16 - j0 : 64) / 8;  // 16-byte chunks per row
-      __syncthreads();  // the tiles, ring and table (first chunk) or the last chunk's operands are free
-      for (int idx = tid; idx < kGemmBM * w8; idx += kGemmThreads) {
-        const int r = idx / w8, c = idx - r * w8;
-        int64_t m = m0 + r;
-        m = m < a.M ? m : a.M - 1;
-        *reinterpret_cast<u32x4*>(us + r * kP + 8 * c) =
-            *reinterpret_cast<const u32x4*>(e.u + m * e.rank16 + j0 + 8 * c);
-      }
-      for (int idx = tid; idx < kGemmBN * w8; idx += kGemmThreads) {
-        const int r = idx / w8, c = idx - r * w8;
-        int64_t n = n0 + r;
-        n = n < a.N ? n : a.N - 1;
-        *reinterpret_cast<u32x4*>(bs + r * kP + 8 * c) =
-            *reinterpret_cast<const u32x4*>(e.bl + n * e.rank16 + j0 + 8 * c);
-      }
-      __syncthreads();
-      for (int s = 0; s < w8 / 2; ++s) {
-        u32x4 ua[kGemmMB];
-#pragma unroll
-        for (int mb = 0; mb < kGemmMB; ++mb)
-          ua[mb] = *reinterpret_cast<const u32x4*>(us + (64 * wave + 32 * mb + i32) * kP + 16 * s + 8 * q);
-#pragma unroll
-        for (int nb = 0; nb < kGemmNB; ++nb) {
-          const u32x4 ub = *reinterpret_cast<const u32x4*>(bs + (32 * nb + i32) * kP + 16 * s + 8 * q);
-#pragma unroll
-          for (int mb = 0; mb < kGemmMB; ++mb) lo[mb][nb] = mfma32x32x16<XT>(ua[mb], ub, lo[mb][nb]);
-        }
-      }
-    }
-  }
-#pragma unroll
-  for (int nb = 0; nb < kGemmNB; ++nb) {
-    const int64_t n = n0 + 32 * nb + i32;
-    if (n >= a.N) continue;
-    const float bias = e.bias ? round_x<XT>(load_as_f32(e.bias, n, e.bias_dt)) : 0.0f;
-    const float post = e.post_a ? __fmul_rn(*e.post_a, *e.post_b) : 1.0f;
-#pragma unroll
-    for (int mb = 0; mb < kGemmMB; ++mb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0w + 32 * mb + 8 * (r >> 2) + 4 * q + (r & 3);
-        if (m >= a.M) continue;
-        float v = acc[mb][nb][r];
-        if (e.post_a) {
-          v = round_x<XT>(__fmul_rn(v, post));
-          if (e.bias) v = round_x<XT>(__fadd_rn(v, bias));
-        } else {
-          if (e.bias) v = __fadd_rn(v, bias);
-          v = round_x<XT>(v);
-        }
-        if (rank > 0)
-          v = round_x<XT>(__fadd_rn(v, round_x<XT>(__fmul_rn(round_x<XT>(lo[mb][nb][r]), e.scaling))));
-        e.y[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
-      }
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Host-side planning and launch (shared by the entry points)
@@ -446,37 +185,6 @@ inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus
   return p;
 }
 
-
-template <int XT, template <int, class> class ProdT, class Scale>
-static inline int launch_core(const GemmArgs& a, const ProducerParams& pp, Scale scale, const GemmEpi& e,
-                       hipStream_t stream) {
-  const unsigned grid = unsigned(int64_t(a.tiles_m) * a.tiles_n);
-  nf4_gemm_kernel<XT, ProdT<XT, Scale>, Scale><<<grid, kGemmThreads, 0, stream>>>(a, pp, scale, e);
-  return rq_check_launch();
-}
-
-// Scale provider by format: absmax of its dtype, or double quantization
-// (c2 codes of c2_format with c2_scales of their dtype).
-template <int XT, template <int, class> class ProdT>
-static inline int run_core(const GemmArgs& a, const ProducerParams& pp, const void* absmax, int absmax_dtype,
-                    const uint8_t* c2, int c2_format, int64_t block2, const GemmEpi& e, hipStream_t stream) {
-  if (c2) {
-    const int sh = pow2_shift(block2);
-    switch (absmax_dtype) {
-      case RQ_DTYPE_F32:
-        return launch_core<XT, ProdT>(a, pp, ScaleDQ<RQ_DTYPE_F32>{c2, absmax, c2_format, sh, block2}, e, stream);
-      case RQ_DTYPE_BF16:
-        return launch_core<XT, ProdT>(a, pp, ScaleDQ<RQ_DTYPE_BF16>{c2, absmax, c2_format, sh, block2}, e, stream);
-      default:
-        return launch_core<XT, ProdT>(a, pp, ScaleDQ<RQ_DTYPE_F16>{c2, absmax, c2_format, sh, block2}, e, stream);
-    }
-  }
-  switch (absmax_dtype) {
-    case RQ_DTYPE_F32: return launch_core<XT, ProdT>(a, pp, ScaleAbsmax<RQ_DTYPE_F32>{absmax}, e, stream);
-    case RQ_DTYPE_BF16: return launch_core<XT, ProdT>(a, pp, ScaleAbsmax<RQ_DTYPE_BF16>{absmax}, e, stream);
-    default: return launch_core<XT, ProdT>(a, pp, ScaleAbsmax<RQ_DTYPE_F16>{absmax}, e, stream);
-  }
-}
 
 inline bool offsets_fit(int64_t M, int64_t ld, int64_t N, int64_t K) {
   // activation and packed-weight loads use 32-bit byte offsets
