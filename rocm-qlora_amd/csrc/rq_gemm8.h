@@ -354,11 +354,9 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
         int64_t n = n0 + r;
         n = n < a.N ? n : a.N - 1;
         const int j = j0 + 8 * c;
-        u32x4 v;
-        if (!e.braw) v = *reinterpret_cast<const u32x4*>(e.bl + n * e.rank16 + j);
-        else if (e.b_sj == 1) v = load_a8_masked<XT>(e.braw, e.b_dt, n * e.b_sn + j, e.rank - j, e.b_vec);
-        else v = load_a8_strided<XT>(e.braw, e.b_dt, n * e.b_sn + j * e.b_sj, e.b_sj, e.rank - j);
-        *reinterpret_cast<u32x4*>(bs + r * kP + 8 * c) = v;
+        *reinterpret_cast<u32x4*>(bs + r * kP + 8 * c) =
+            e.b_sj == 1 ? load_a8_masked<XT>(e.braw, e.b_dt, n * e.b_sn + j, e.rank - j, e.b_vec)
+                        : load_a8_strided<XT>(e.braw, e.b_dt, n * e.b_sn + j * e.b_sj, e.b_sj, e.rank - j);
       }
       __syncthreads();
       for (int s = 0; s < w8 / 2; ++s) {

@@ -50,10 +50,9 @@ struct GemmEpi {
   int bias_dt;
   int rank, rank16;      // LoRA rank and rank rounded up to 16
   const uint16_t* u;     // RND(u) [M][rank16] (dX: RND(g)), zero padded
-  const uint16_t* bl;    // RND(B) [N][rank16] (dX: RND(A^T)), zero padded
-  // eight-wave core: the bl operand read as it is -- element (n, j) at
-  // braw[n * b_sn + j * b_sj], of b_dt -- and rounded while staged, in place
-  // of bl (nullptr: bl)
+  // the other LoRA operand, B [N][rank] (dX: A^T [K][rank]), read as it is --
+  // element (n, j) at braw[n * b_sn + j * b_sj], of b_dt -- and rounded to
+  // the activation dtype while the epilogue stages it
   const void* braw;
   int b_dt;
   int64_t b_sn, b_sj;
@@ -143,12 +142,12 @@ struct GemmPlan {
   size_t part_offset;
   int rank16;
   LoraRowsPlan lr;
-  size_t u16_offset, bl16_offset, ws_bytes;
+  size_t u16_offset, ws_bytes;
 };
 
-// M activation rows, N output columns, K reduction; the LoRA operands are
-// u [M][r16] (product of activations with an [r][K] matrix) and bl
-// [N][r16].  Workspace: [lora_rows partials][RND(S) r x K][u16][bl16].
+// M activation rows, N output columns, K reduction; the LoRA operand u
+// [M][r16] is the product of the activations with an [r][K] matrix.
+// Workspace: [lora_rows partials][RND(S) r x K][u16][K-split tiles].
 inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool split_ok = false) {
   GemmPlan p{};
   p.tiles_m = int((M + kGemmBM - 1) / kGemmBM);
@@ -177,8 +176,7 @@ inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus
   if (rank > 0) {
     p.lr = plan_lora_rows(M, K, rank, cus);
     p.u16_offset = p.lr.part_bytes + p.lr.s16_bytes;
-    p.bl16_offset = p.u16_offset + ((size_t(M) * p.rank16 * 2 + 255) & ~size_t(255));
-    p.ws_bytes = p.bl16_offset + size_t(N) * p.rank16 * 2;
+    p.ws_bytes = p.u16_offset + size_t(M) * p.rank16 * 2;
   }
   p.part_offset = (p.ws_bytes + 255) & ~size_t(255);
   if (p.splits > 1) p.ws_bytes = p.part_offset + size_t(p.splits) * 8 * p.lt * kGemmBM * kGemmBN * 4;

@@ -4,15 +4,17 @@
 //   forward  u = RND(xl . RND(A)^T)                   [M, r]
 //   backward g = RND(RND(dY * s) . RND(B))            [M, r] (lora_layer.py:67
 //            differentiated: dX += RND(g . RND(A)))
-// The kernels here produce those [rows, r16] 16-bit operands (r16 = r rounded
-// up to 16, zero padded) that the GEMM epilogues stage into LDS:
+// The kernels here produce u / g as [rows, r16] 16-bit operands (r16 = r
+// rounded up to 16, zero padded) that the GEMM epilogues stage into LDS:
 //   lora_rows_kernel     fp32 partial sums of a split-K MFMA product
-//                        X[rows, K] . RND(S)[r, K]^T, with RND(S) first
-//                        gathered (through strides, so B^T needs no copy)
-//                        into a contiguous 16-bit [r, K] scratch;
+//                        X[rows, K] . RND(S)[r, K]^T; S with contiguous rows
+//                        (A) is rounded as it is staged, S with strided rows
+//                        (B^T) is first gathered into a contiguous 16-bit
+//                        [r, K] scratch;
 //   lora_finish_kernel   sum of the partials, rounded;
-//   lora_round_kernel    RND of a strided [rows, r] matrix (B for the forward
-//                        epilogue, A^T for the dX epilogue).
+//   lora_round_kernel    RND of a strided matrix into a contiguous 16-bit
+//                        copy (B^T for the dX's lora_rows, whose rows are
+//                        strided in B).
 #include "rq_mfma.h"
 #include "rq_launch.h"
 #include "rq_linear.h"
