@@ -198,8 +198,8 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t
     uint16_t* u16 = reinterpret_cast<uint16_t*>(ws + p.u16_offset);
     // u = RND(xl . RND(A)^T), A [r][K] row-major (lora_layer.py:67)
     int st = run_lora_rows(L.x_dtype, static_cast<const uint16_t*>(L.lora_x), L.ld_lora_x, L.M, L.K, L.lora_a,
-                           L.lora_dtype, L.K, 1, e.rank, false, 1.0f, p.lr, reinterpret_cast<float*>(ws),
-                           reinterpret_cast<uint16_t*>(ws + p.lr.part_bytes), u16, p.rank16, stream);
+                           L.lora_dtype, L.K, 1, e.rank, false, 1.0f, p.lr, reinterpret_cast<float*>(ws), u16,
+                           p.rank16, stream);
     if (st != RQ_OK) return st;
     // RND(B), B [N][r] with row stride ld_lora_b, rounded as the epilogue stages it
     e.u = u16;
@@ -280,8 +280,8 @@ int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t st
     uint16_t* g16 = reinterpret_cast<uint16_t*>(ws + p.u16_offset);
     // g = RND(RND(dY * s) . RND(B)): S[j][n] = B[n][j]
     st = run_lora_rows(D.dy_dtype, static_cast<const uint16_t*>(D.dy), D.lddy, D.M, D.N, D.lora_b, D.lora_dtype, 1,
-                       D.ld_lora_b, int(rank), true, D.scaling, p.lr, reinterpret_cast<float*>(ws),
-                       reinterpret_cast<uint16_t*>(ws + p.lr.part_bytes), g16, p.rank16, stream);
+                       D.ld_lora_b, int(rank), true, D.scaling, p.lr, reinterpret_cast<float*>(ws), g16, p.rank16,
+                       stream);
     if (st != RQ_OK) return st;
     // RND(A^T) [K][r]: element (k, j) = A[j][k], A [r][K] row-major, rounded
     // as the epilogue stages it

@@ -147,7 +147,7 @@ struct GemmPlan {
 
 // M activation rows, N output columns, K reduction; the LoRA operand u
 // [M][r16] is the product of the activations with an [r][K] matrix.
-// Workspace: [lora_rows partials][RND(S) r x K][u16][K-split tiles].
+// Workspace: [lora_rows partials][u16][K-split tiles].
 inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool split_ok = false) {
   GemmPlan p{};
   p.tiles_m = int((M + kGemmBM - 1) / kGemmBM);
@@ -175,7 +175,7 @@ inline GemmPlan plan_gemm(int64_t M, int64_t N, int64_t K, int64_t rank, int cus
   p.ws_bytes = 0;
   if (rank > 0) {
     p.lr = plan_lora_rows(M, K, rank, cus);
-    p.u16_offset = p.lr.part_bytes + p.lr.s16_bytes;
+    p.u16_offset = p.lr.part_bytes;
     p.ws_bytes = p.u16_offset + size_t(M) * p.rank16 * 2;
   }
   p.part_offset = (p.ws_bytes + 255) & ~size_t(255);

@@ -10,22 +10,18 @@ namespace rq {
 
 struct LoraRowsPlan {
   int splits;           // K splits of lora_rows_kernel
+  int jb;               // 16-rank blocks per workgroup (1, 2 or 4)
   int64_t k_per_split;  // multiple of 64
   size_t part_bytes;    // fp32 partials [splits][M][R], 256-byte padded
-  size_t s16_bytes;     // RND(S) [R][K] 16-bit, 256-byte padded
 };
 
 LoraRowsPlan plan_lora_rows(int64_t M, int64_t K, int64_t R, int cus);
 
 // out[M][R16] = RND(sum_k RND(X[m,k] (* scale if prescale)) . RND(S[j,k]))
-// with S[j,k] at s[j * s_j + k * s_k]; part and s16 are the plan's scratch
-// (part_bytes and s16_bytes).  K must be a multiple of 64.
+// with S[j,k] at s[j * s_j + k * s_k], s_k == 1 or s_j == 1; part is the
+// plan's scratch (part_bytes).  K must be a multiple of 64.
 int run_lora_rows(int xt, const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const void* s, int s_dt,
                   int64_t s_j, int64_t s_k, int R, bool prescale, float scale, const LoraRowsPlan& p, float* part,
-                  uint16_t* s16, uint16_t* out, int R16, hipStream_t stream);
-
-// out[rows][R16] = RND(src[n * s_n + j * s_j]) (zero for j >= R).
-int run_lora_round(int xt, const void* src, int dt, int64_t s_n, int64_t s_j, int64_t rows, int R, int R16,
-                   uint16_t* out, hipStream_t stream);
+                  uint16_t* out, int R16, hipStream_t stream);
 
 }  // namespace rq

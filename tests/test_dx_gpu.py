@@ -60,13 +60,14 @@ def test_dx_llama3_shapes_bf16(dev, K, N):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", ["plain", "no_lora", "m1", "m5", "m17", "odd_m", "k_tail", "block128",
-                                  "rank16", "rank96", "rank256", "bf16_lora", "strided_dy", "n64"])
+                                  "rank8", "rank16", "rank24", "rank96", "rank256", "bf16_lora", "strided_dy",
+                                  "n64"])
 def test_dx_variants(dev, dtype, case):
     N, K, M = 512, 640, 300
     M = {"m1": 1, "m5": 5, "m17": 17, "odd_m": 777}.get(case, M)
     K = {"k_tail": 320}.get(case, K)
     N = {"n64": 64}.get(case, N)
-    rank = {"rank16": 16, "rank96": 96, "rank256": 256}.get(case, 64)
+    rank = {"rank8": 8, "rank16": 16, "rank24": 24, "rank96": 96, "rank256": 256}.get(case, 64)
     bs = 128 if case == "block128" else 64
     print(f"dx variant {case} {dtype}", flush=True)
     w, dy, a, b = _inputs(N, K, M, dtype, seed=13, rank=rank)

@@ -62,14 +62,15 @@ def test_gemm_llama3_shapes_bf16(dev, K, N):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", ["plain", "bias", "odd_n", "odd_m", "m17", "block128", "strided_x",
-                                  "dropout_x", "no_lora", "k64", "k320", "rank16", "rank96", "rank256",
+                                  "dropout_x", "no_lora", "k64", "k320", "rank8", "rank16", "rank24", "rank96",
+                                  "rank256",
                                   "bf16_lora", "tiles8"])
 def test_gemm_variants(dev, dtype, case):
     N, K, M = 640, 512, 300
     N = {"odd_n": 1000, "tiles8": 512}.get(case, N)
     M = {"odd_m": 777, "m17": 17, "tiles8": 512}.get(case, M)
     K = {"k64": 64, "k320": 320}.get(case, K)
-    rank = {"rank16": 16, "rank96": 96, "rank256": 256}.get(case, 64)
+    rank = {"rank8": 8, "rank16": 16, "rank24": 24, "rank96": 96, "rank256": 256}.get(case, 64)
     bs = 128 if case == "block128" else 64
     print(f"gemm variant {case} {dtype}", flush=True)
     w, x, a, b, bvec = _inputs(N, K, M, dtype, seed=11, rank=rank, bias=(case == "bias"))
