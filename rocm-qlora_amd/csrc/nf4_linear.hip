@@ -399,8 +399,9 @@ __device__ __forceinline__ float lora_u_job(const GemvArgs& a, const LinearEpi& 
 // before it): the launch's last workgroup clears the partials and the count
 // for the next launch (every other workgroup is past its use of them).
 __device__ __forceinline__ void gemv_last_clears(const GemvArgs& a, const LinearEpi& e, int lane, uint32_t old) {
+  // every other workgroup counted itself after its last access to ubits
+  // had completed; the clears below depend on the count's result
   if (old != gridDim.x - 1u) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   const uint32_t n = uint32_t(e.u_splits) * uint32_t(a.M) * uint32_t(e.rank);
   for (uint32_t i = uint32_t(lane); i < n; i += 64u) a.ubits[i] = 0u;
   if (lane == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -426,12 +427,15 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
       const uint32_t bits = f2u(v);
       __hip_atomic_store(&a.ubits[((j % ns) * M + (tid >> 4)) * e.rank + jj], bits != 0u ? bits : 0x80000000u,
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     }
+    // the device-coherent stores have completed before the count (their
+    // values are their own flags; an agent-scope release fence would write
+    // back the whole L2 instead)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (wave == 0) {
       uint32_t old = 0u;
-      if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       gemv_last_clears(a, e, lane, __builtin_amdgcn_readfirstlane(old));
     }
     return;
@@ -671,7 +675,10 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
     lds_barrier();
     self_u = __builtin_amdgcn_readfirstlane(*flag);
-    if (tid == 0) done_old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the count's result is needed only at the very end: an increment (the
+    // compiler's atomic optimizer rewrites fetch_add into a form that waits
+    // for the result at once) lets the epilogue run under its round trip
+    if (tid == 0) done_old = __builtin_amdgcn_atomic_inc32(a.done, 0xFFFFFFFFu, __ATOMIC_RELAXED, "agent");
     if (self_u) {
       float* red = reinterpret_cast<float*>(lut);
       const int ns = e.u_splits;
@@ -880,6 +887,21 @@ __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict_
   }
 }
 
+// The down-projection jobs of lora_u_job as a launch of their own, for a
+// GEMV whose tile workgroups leave no compute unit free: workgroup j runs job
+// j (ranks [16 (j / u_splits), +16), K split j % u_splits) and stores its
+// partials with plain stores in the layout lora_u_kernel writes, with the
+// bits the in-launch producers would give.
+template <int XT>
+__global__ __launch_bounds__(kGemvThreads) void lora_u_jobs_kernel(GemvArgs a, LinearEpi e, float* __restrict__ up) {
+  __shared__ float red[kGemvWaves * 256];
+  const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int j = blockIdx.x, ns = e.u_splits;
+  const float v = lora_u_job<XT>(a, e, j / ns, j % ns, ns, tid, wave, red);
+  const int jj = 16 * (j / ns) + (tid & 15);
+  if (tid < a.M * 16 && jj < e.rank) up[((j % ns) * a.M + (tid >> 4)) * e.rank + jj] = v;
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -900,15 +922,15 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
   const int64_t tiles = (N + 15) / 16;
   const int64_t ncu = cus > 0 ? cus : 1;
   p.u_splits = 0;
+  // K splits of the down-projection jobs (inside the GEMV launch or as
+  // lora_u_jobs_kernel): about 1024 k per job
+  const int fused_splits = int(std::min<int64_t>((K + 1023) / 1024, kGemvMaxUSplits));
   if (rank > 0) {
     const int64_t steps_per_wg = 4 * kLoraUStepsPerWave;
     const int64_t ks = (K / 32 + steps_per_wg - 1) / steps_per_wg;
-    p.u_splits = int(ks < kGemvMaxUSplits ? ks : kGemvMaxUSplits);
+    p.u_splits = lora_prod ? fused_splits : int(ks < kGemvMaxUSplits ? ks : kGemvMaxUSplits);
   }
   const bool lora_fusable = rank <= 0 || (rank <= kGemvMaxFusedRank && lora_vec);
-  // K splits of the down-projection when it runs inside the GEMV launch:
-  // about 1024 k per producer workgroup
-  const int fused_splits = int(std::min<int64_t>((K + 1023) / 1024, kGemvMaxUSplits));
   for (int slice = 1; slice >= 0; --slice) {
     // activations through the waves' LDS slices: any unit to any wave
     const bool xslice = slice != 0;
@@ -1017,6 +1039,19 @@ static int launch_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t str
   const bool avec = aligned(L.lora_a, 16);
   lora_u_kernel<XT><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(L.lora_x), L.ld_lora_x, xvec,
                                               L.lora_a, L.lora_dtype, avec, L.M, L.K, int(L.rank), ks, up);
+  return rq_check_launch();
+}
+
+template <int XT>
+static int launch_lora_u_jobs(const LinearArgs& L, const LinearEpi& e, float* up, hipStream_t stream) {
+  GemvArgs a{};
+  a.M = int(L.M);
+  a.K = int(L.K);
+  a.lora_x = static_cast<const uint16_t*>(L.lora_x);
+  a.ld_lora_x = int(L.ld_lora_x);
+  a.lora_a = L.lora_a;
+  const unsigned grid = unsigned((L.rank + 15) / 16) * unsigned(e.u_splits);
+  lora_u_jobs_kernel<XT><<<grid, kGemvThreads, 0, stream>>>(a, e, up);
   return rq_check_launch();
 }
 
@@ -1181,8 +1216,16 @@ int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   float* ws = p.direct ? nullptr : reinterpret_cast<float*>(wsb + kLinearSyncBytes);
   float* up = L.rank > 0 ? reinterpret_cast<float*>(wsb + p.u_offset) : nullptr;
   int st;
-  if (L.rank > 0 && p.jt == 0 && (st = run_lora_u(L, p.u_splits, up, stream)) != RQ_OK) return st;
   const LinearEpi e = make_epi(L, up, p.u_splits);
+  if (L.rank > 0 && p.jt == 0) {
+    if (lora_prod) {
+      st = L.x_dtype == RQ_DTYPE_BF16 ? launch_lora_u_jobs<RQ_DTYPE_BF16>(L, e, up, stream)
+                                      : launch_lora_u_jobs<RQ_DTYPE_F16>(L, e, up, stream);
+    } else {
+      st = run_lora_u(L, p.u_splits, up, stream);
+    }
+    if (st != RQ_OK) return st;
+  }
   if (L.x_dtype == RQ_DTYPE_BF16) st = run_gemv<RQ_DTYPE_BF16>(L, p, e, ws, workspace, stream);
   else st = run_gemv<RQ_DTYPE_F16>(L, p, e, ws, workspace, stream);
   if (st != RQ_OK || p.direct) return st;

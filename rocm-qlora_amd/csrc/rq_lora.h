@@ -11,6 +11,7 @@ namespace rq {
 struct LoraRowsPlan {
   int splits;           // K splits of lora_rows_kernel
   int jb;               // 16-rank blocks per workgroup (1, 2 or 4)
+  int waves;            // waves of 16 activation rows per workgroup (4 or 8)
   int64_t k_per_split;  // multiple of 64
   size_t part_bytes;    // fp32 partials [splits][M][R], 256-byte padded
 };

@@ -19,27 +19,28 @@
 
 namespace rq {
 
-constexpr int kLoraRowsM = 64;     // activation rows per workgroup (4 waves x 16)
 constexpr int kLoraChunkK = 256;   // k per LDS stage of S
 constexpr int kLoraSPitch = kLoraChunkK + 8;
 constexpr int kLoraMaxSplits = 16;
 
 // X[m, k] (16-bit, row stride ldx) times RND(S)[j, k] over k in this split's
-// range, for the 16 JB ranks j0 .. j0 + 16 JB - 1 of this workgroup, where
+// range, for the 16 W activation rows (W waves of 16) and the 16 JB ranks
+// j0 .. j0 + 16 JB - 1 of this workgroup, where
 // S[j][k] = s[j * s_j + k * s_k] (dtype sdt) and j < R (zeros past R).
 // s_rows: s_k == 1 (each rank's row contiguous); otherwise s_j == 1 and each
 // k holds the ranks contiguously, and the staging transposes them.
 // PRESCALE multiplies each x element by `prescale` and rounds it to XT
 // first.  Output: part[ks][m][j] fp32 for m < M, j < R.
-template <int XT, bool PRESCALE, int JB>
-__global__ __launch_bounds__(256) void lora_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
+template <int XT, bool PRESCALE, int JB, int W>
+__global__ __launch_bounds__(64 * W) void lora_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
                                                         int64_t K, const void* __restrict__ s, int sdt, int64_t s_j,
                                                         int64_t s_k, bool s_rows, bool svec, int R, float prescale,
                                                         int64_t k_per_split, float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) uint16_t ss[16 * JB * kLoraSPitch];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i16 = lane & 15, q4 = lane >> 4;
-  const int64_t m0 = int64_t(blockIdx.x) * kLoraRowsM;
+  constexpr int NT = 64 * W;
+  const int64_t m0 = int64_t(blockIdx.x) * 16 * W;
   const int j0 = blockIdx.y * 16 * JB;
   const int ks = blockIdx.z;
   const int64_t k0 = int64_t(ks) * k_per_split;
@@ -53,37 +54,43 @@ __global__ __launch_bounds__(256) void lora_rows_kernel(const uint16_t* __restri
   for (int64_t kc = k0; kc < k1; kc += kLoraChunkK) {
     const int len = int(k1 - kc < kLoraChunkK ? k1 - kc : kLoraChunkK);  // multiple of 64
     // this lane's activation fragments of the whole chunk, issued before the
-    // staging so that their latency overlaps it (steps past len re-read the
-    // chunk's first step: in bounds, unused)
+    // staging so that their latency overlaps it
     u32x4 xf[kLoraChunkK / 32];
 #pragma unroll
     for (int t = 0; t < kLoraChunkK / 32; ++t)
-      xf[t] = *reinterpret_cast<const u32x4*>(xr + kc + (32 * t < len ? 32 * t : 0) + 8 * q4);
+      if (32 * t < len) xf[t] = *reinterpret_cast<const u32x4*>(xr + kc + 32 * t + 8 * q4);
     __syncthreads();
     if (s_rows) {
-      // 16 JB ranks x len: thread tid takes chunk (tid % 32) of ranks tid / 32 + 8 i
-      const int c = tid % 32;
+      // 16 JB ranks x len in 16-byte chunks, CPR per rank: thread tid takes
+      // chunk tid % CPR of ranks tid / CPR + (NT / CPR) i
+      constexpr int CPR = kLoraChunkK / 8;
+      const int c = tid % CPR;
 #pragma unroll
-      for (int i = 0; i < 2 * JB; ++i) {
-        const int jj = tid / 32 + 8 * i, j = j0 + jj;
+      for (int i = 0; i < 16 * JB / (NT / CPR); ++i) {
+        const int jj = tid / CPR + (NT / CPR) * i, j = j0 + jj;
         if (8 * c < len) {
           const u32x4 v = load_a8<XT>(s, sdt, int64_t(j) * s_j + kc + 8 * c, j < R, svec);
           *reinterpret_cast<u32x4*>(ss + jj * kLoraSPitch + 8 * c) = v;
         }
       }
     } else {
-      // len k x 16 JB ranks: thread tid takes k = tid, ranks 8 i .. 8 i + 7
-      // (eight contiguous values, stored down one LDS column)
-      if (tid < len) {
+      // len k x 16 JB ranks: thread tid takes k = tid % 256, ranks 8 i ..
+      // 8 i + 7 for i = tid / 256 + (NT / 256) n (eight contiguous values,
+      // stored down one LDS column)
+      static_assert(kLoraChunkK == 256 && NT % 256 == 0, "one k of the chunk per thread");
+      const int kk = tid % 256;
+      if (kk < len) {
 #pragma unroll
-        for (int i = 0; i < 2 * JB; ++i) {
+        for (int n = 0; n < (2 * JB + NT / 256 - 1) / (NT / 256); ++n) {
+          const int i = tid / 256 + (NT / 256) * n;
+          if (i >= 2 * JB) break;
           const int j = j0 + 8 * i;
-          const u32x4 v = j < R ? load_a8_masked<XT>(s, sdt, (kc + tid) * s_k + j, R - j, svec)
+          const u32x4 v = j < R ? load_a8_masked<XT>(s, sdt, (kc + kk) * s_k + j, R - j, svec)
                                 : u32x4{0u, 0u, 0u, 0u};
           const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            ss[(8 * i + e) * kLoraSPitch + tid] = uint16_t(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
+            ss[(8 * i + e) * kLoraSPitch + kk] = uint16_t(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xFFFFu);
         }
       }
     }
@@ -169,7 +176,11 @@ LoraRowsPlan plan_lora_rows(int64_t M, int64_t K, int64_t R, int cus) {
   LoraRowsPlan p{};
   const int64_t r16 = (R + 15) / 16 * 16;
   p.jb = r16 <= 16 ? 1 : (r16 <= 32 ? 2 : 4);
-  const int64_t tiles = ((M + kLoraRowsM - 1) / kLoraRowsM) * ((r16 + 16 * p.jb - 1) / (16 * p.jb));
+  // 128 activation rows per workgroup with 64 ranks (each rank block read
+  // for twice the rows), else 64
+  p.waves = p.jb == 4 ? 8 : 4;
+  const int64_t rows = 16 * p.waves;
+  const int64_t tiles = ((M + rows - 1) / rows) * ((r16 + 16 * p.jb - 1) / (16 * p.jb));
   const int64_t steps = K / 64;
   // about two workgroups per compute unit, at most 8 steps (two LDS chunks)
   // per split and at least 2 unless that leaves too many splits for the
@@ -187,13 +198,12 @@ LoraRowsPlan plan_lora_rows(int64_t M, int64_t K, int64_t R, int cus) {
   return p;
 }
 
-template <int XT, bool PRESCALE, int JB>
+template <int XT, bool PRESCALE, int JB, int W>
 static void launch_rows_jb(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const void* s, int sdt,
                            int64_t s_j, int64_t s_k, bool s_rows, bool svec, int R, float prescale,
                            const LoraRowsPlan& p, float* part, hipStream_t stream) {
-  dim3 grid(unsigned((M + kLoraRowsM - 1) / kLoraRowsM), unsigned((R + 16 * JB - 1) / (16 * JB)),
-            unsigned(p.splits));
-  lora_rows_kernel<XT, PRESCALE, JB><<<grid, 256, 0, stream>>>(x, ldx, M, K, s, sdt, s_j, s_k, s_rows, svec, R,
+  dim3 grid(unsigned((M + 16 * W - 1) / (16 * W)), unsigned((R + 16 * JB - 1) / (16 * JB)), unsigned(p.splits));
+  lora_rows_kernel<XT, PRESCALE, JB, W><<<grid, 64 * W, 0, stream>>>(x, ldx, M, K, s, sdt, s_j, s_k, s_rows, svec, R,
                                                                prescale, p.k_per_split, part);
 }
 
@@ -202,11 +212,11 @@ static void launch_rows_t(const uint16_t* x, int64_t ldx, int64_t M, int64_t K, 
                           int64_t s_k, bool s_rows, bool svec, int R, float prescale, const LoraRowsPlan& p,
                           float* part, hipStream_t stream) {
   if (p.jb == 1)
-    launch_rows_jb<XT, PRESCALE, 1>(x, ldx, M, K, s, sdt, s_j, s_k, s_rows, svec, R, prescale, p, part, stream);
+    launch_rows_jb<XT, PRESCALE, 1, 4>(x, ldx, M, K, s, sdt, s_j, s_k, s_rows, svec, R, prescale, p, part, stream);
   else if (p.jb == 2)
-    launch_rows_jb<XT, PRESCALE, 2>(x, ldx, M, K, s, sdt, s_j, s_k, s_rows, svec, R, prescale, p, part, stream);
+    launch_rows_jb<XT, PRESCALE, 2, 4>(x, ldx, M, K, s, sdt, s_j, s_k, s_rows, svec, R, prescale, p, part, stream);
   else
-    launch_rows_jb<XT, PRESCALE, 4>(x, ldx, M, K, s, sdt, s_j, s_k, s_rows, svec, R, prescale, p, part, stream);
+    launch_rows_jb<XT, PRESCALE, 4, 8>(x, ldx, M, K, s, sdt, s_j, s_k, s_rows, svec, R, prescale, p, part, stream);
 }
 
 int run_lora_rows(int xt, const uint16_t* x, int64_t ldx, int64_t M, int64_t K, const void* s, int s_dt,
