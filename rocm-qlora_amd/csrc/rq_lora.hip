@@ -30,9 +30,10 @@ constexpr int kLoraMaxSplits = 16;
 // s_rows: s_k == 1 (each rank's row contiguous); otherwise s_j == 1 and each
 // k holds the ranks contiguously, and the staging transposes them.
 // PRESCALE multiplies each x element by `prescale` and rounds it to XT
-// first.  Output: part[ks][m][j] fp32 for m < M, j < R.
+// first.  Output: part[ks][m][j] fp32 for m < M, j < R.  At most 128 VGPRs
+// (four waves per SIMD), so that two 8-wave workgroups share a compute unit.
 template <int XT, bool PRESCALE, int JB, int W>
-__global__ __launch_bounds__(64 * W) void lora_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(4))) void lora_rows_kernel(const uint16_t* __restrict__ x, int64_t ldx, int64_t M,
                                                         int64_t K, const void* __restrict__ s, int sdt, int64_t s_j,
                                                         int64_t s_k, bool s_rows, bool svec, int R, float prescale,
                                                         int64_t k_per_split, float* __restrict__ part) {
