@@ -63,6 +63,7 @@ def _sync_words_zero(dev):
 @pytest.mark.parametrize("K,N,M,rank", [
     (4096, 4096, 1, 16),     # q / o: two tiles per workgroup leave room for the producers
     (4096, 14336, 1, 16),    # gate / up
+    (14336, 4096, 1, 16),    # down: the tiles fill the CUs, the jobs run as a launch of their own
     (4096, 1024, 2, 16),     # k / v
     (4096, 4096, 5, 8),      # activations as register operands
     (4096, 1024, 16, 64),    # four rank groups x four K splits of producers
