@@ -150,8 +150,8 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
             if lora_b.dtype != lora_a.dtype:
                 lora_b = lora_b.to(lora_a.dtype)
             la = lora_a.contiguous()
-            lb = lora_b.contiguous()
-            ldb = rank
+            # B rows may be strided (a column slice of a wider parameter)
+            lb, ldb = _rows(lora_b, rank)
             lcode = nat.dtype_code(la.dtype)
             if lora_x is not None:
                 xl, ldxl = _rows(lora_x.to(x.dtype), K)
@@ -235,8 +235,8 @@ def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: O
             if lora_b.dtype != lora_a.dtype:
                 lora_b = lora_b.to(lora_a.dtype)
             la = lora_a.contiguous()
-            lb = lora_b.contiguous()
-            ldb = rank
+            # B rows may be strided (a column slice of a wider parameter)
+            lb, ldb = _rows(lora_b, rank)
             lcode = nat.dtype_code(la.dtype)
         import ctypes
         nbytes = ctypes.c_int64(0)

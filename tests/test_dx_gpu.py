@@ -61,7 +61,7 @@ def test_dx_llama3_shapes_bf16(dev, K, N):
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", ["plain", "no_lora", "m1", "m5", "m17", "odd_m", "k_tail", "block128",
                                   "rank8", "rank16", "rank24", "rank96", "rank256", "bf16_lora", "strided_dy",
-                                  "n64"])
+                                  "n64", "strided_b"])
 def test_dx_variants(dev, dtype, case):
     N, K, M = 512, 640, 300
     M = {"m1": 1, "m5": 5, "m17": 17, "odd_m": 777}.get(case, M)
@@ -80,6 +80,11 @@ def test_dx_variants(dev, dtype, case):
         big[:, 32:32 + N] = dyd
         dyd = big[:, 32:32 + N]
     la, lb = (None, None) if case == "no_lora" else (a.to(dev), b.to(dev))
+    if case == "strided_b":
+        # rows of B 4 * (rank + 3) bytes apart: no 16-byte loads of them
+        wide = torch.zeros(N, rank + 3, dtype=b.dtype, device=dev)
+        wide[:, 1:1 + rank] = lb
+        lb = wide[:, 1:1 + rank]
     dx = ops.nf4_linear_dx(dyd, packed, absmax, K, bs, lora_a=la, lora_b=lb, scaling=0.5)
     ref = R.nf4_dx(dy, packed.cpu(), absmax.cpu(), N, K,
                    None if la is None else a, None if lb is None else b, 0.5, bs)

@@ -64,7 +64,7 @@ def test_gemm_llama3_shapes_bf16(dev, K, N):
 @pytest.mark.parametrize("case", ["plain", "bias", "odd_n", "odd_m", "m17", "block128", "strided_x",
                                   "dropout_x", "no_lora", "k64", "k320", "rank8", "rank16", "rank24", "rank96",
                                   "rank256",
-                                  "bf16_lora", "tiles8"])
+                                  "bf16_lora", "tiles8", "strided_b"])
 def test_gemm_variants(dev, dtype, case):
     N, K, M = 640, 512, 300
     N = {"odd_n": 1000, "tiles8": 512}.get(case, N)
@@ -86,6 +86,11 @@ def test_gemm_variants(dev, dtype, case):
     if case == "dropout_x":
         xl = (x * (torch.rand(x.shape, generator=torch.Generator().manual_seed(3)) > 0.3)).to(dtype)
     la, lb = (None, None) if case == "no_lora" else (a.to(dev), b.to(dev))
+    if case == "strided_b":
+        # rows of B 4 * (rank + 3) bytes apart: no 16-byte loads of them
+        wide = torch.zeros(N, rank + 3, dtype=b.dtype, device=dev)
+        wide[:, 1:1 + rank] = lb
+        lb = wide[:, 1:1 + rank]
     y = ops.nf4_linear(xd, packed, absmax, N, bs, bias=None if bvec is None else bvec.to(dev),
                        lora_a=la, lora_b=lb, scaling=0.5, lora_x=None if xl is None else xl.to(dev))
     wf = R.dequantize_int4(packed.cpu(), absmax.cpu(), bs)

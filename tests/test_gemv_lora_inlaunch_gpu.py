@@ -165,7 +165,7 @@ def test_two_graphs_replayed_in_turn(dev):
         assert torch.equal(got, want), f"replay {i} of graph {j} differs from the eager call"
 
 
-@pytest.mark.parametrize("case", ["lora_x_offset", "a_offset", "bf16_a_offset"])
+@pytest.mark.parametrize("case", ["lora_x_offset", "a_offset", "bf16_a_offset", "strided_b"])
 def test_unaligned_operands_run_separate_kernel(dev, case):
     K, N, M, rank = 1024, 1024, 2, 16
     lora_dtype = torch.bfloat16 if case == "bf16_a_offset" else torch.float32
@@ -183,7 +183,14 @@ def test_unaligned_operands_run_separate_kernel(dev, case):
         buf = torch.zeros(rank * K + 2, dtype=lora_dtype, device=dev)
         ad = buf[2:].view(rank, K)
         ad.copy_(a.to(dev))
-    y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=ad, lora_b=b.to(dev), scaling=2.0, lora_x=xld)
+    bd = b.to(dev)
+    if case == "strided_b":
+        # rows of B 4 * (rank + 3) bytes apart: the LoRA term is added by the
+        # split-K finisher, which reads B by element
+        wide = torch.zeros(N, rank + 3, dtype=lora_dtype, device=dev)
+        wide[:, 1:1 + rank] = bd
+        bd = wide[:, 1:1 + rank]
+    y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0, lora_x=xld)
     base = R.quant_linear_forward(x, R.dequantize_int4(packed.cpu(), absmax.cpu(), 64), None, N, K)
     ref = R.lora_forward(xl, base, a, b, 2.0)
     _check(y, ref)
