@@ -166,6 +166,14 @@ int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
  * previous value. */
 uint32_t rq_set_gemv_spin_limit(uint32_t polls);
 
+/* Tile configuration of the MFMA GEMM behind rq_nf4_linear (M > 16),
+ * rq_nf4_linear_dx, rq_int8_linear and rq_fp8_linear: out[0..4] = rows and
+ * columns of a workgroup tile, k per step, wavefronts per workgroup, LDS
+ * pipeline stages.  Replaces the tile table of get_kernel_config
+ * (kernels/kernel_config.py:18-48), which describes the reference's Triton
+ * tiles. */
+int rq_gemm_tile_config(int32_t* out);
+
 /* Bytes of device workspace rq_nf4_linear_dx needs (0 when none). */
 int rq_nf4_linear_dx_workspace_size(int dy_dtype, int64_t M, int64_t N, int64_t K, int64_t rank,
                                     int64_t* bytes);
@@ -173,18 +181,24 @@ int rq_nf4_linear_dx_workspace_size(int dy_dtype, int64_t M, int64_t N, int64_t 
 /* Replaces the backward of _FusedNF4MatmulFunc (kernels/dequant_matmul.py:
  * 338-351: dX = dY . W_deq in dY's dtype) together with the adapter's input
  * gradient of LoRALinear.forward (lora_layer.py:67 differentiated):
- *   dX[M, K] = RND(RND(dY W) + RND(RND(RND(dY * scaling) RND(B)) RND(A)))
- * with RND the rounding to dy_dtype (bf16 or fp16) and W = T[code] * scale.
+ *   dX[M, K] = RND(RND(dY W) + RND(RND(RND(RND(dY * scaling) RND(B)) RND(A)) * d))
+ * with RND the rounding to dy_dtype (bf16 or fp16), W = T[code] * scale, and
+ * d = 1, or -- with the adapter's input dropout (lora_layer.py:67's
+ * self.lora_dropout(x)) -- dropout's backward d = lora_mask[m, k] ? mask_scale
+ * : 0 (mask_scale = 1 / (1 - p)).
  *   dy: [M, N] rows of stride lddy (N % 64 == 0); w_packed, block_size,
  *   absmax, c2, c2_format, block2 as for rq_nf4_linear (K % 64 == 0);
  *   LoRA (rank > 0, lora_a and lora_b non-NULL): A [rank, K], B [N, rank]
- *   stride ld_lora_b, both of lora_dtype.  dx: [M, K] stride lddx, dy_dtype. */
+ *   stride ld_lora_b, both of lora_dtype; lora_mask: NULL or [M, K] bytes
+ *   (non-zero = kept) of row stride ld_lora_mask.  dx: [M, K] stride lddx,
+ *   dy_dtype. */
 int rq_nf4_linear_dx(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t lddy,
                      const uint8_t* w_packed, int64_t K, int64_t block_size,
                      const void* absmax, int absmax_dtype,
                      const uint8_t* c2, int c2_format, int64_t block2,
                      const void* lora_a, const void* lora_b, int64_t ld_lora_b, int lora_dtype,
-                     int64_t rank, float scaling, void* dx, int64_t lddx,
+                     int64_t rank, float scaling, const uint8_t* lora_mask, int64_t ld_lora_mask,
+                     float mask_scale, void* dx, int64_t lddx,
                      void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------------

@@ -252,6 +252,7 @@ int validate_dx(const DxArgs& D) {
     if (!D.lora_a || !D.lora_b) return RQ_ERR_NULL_POINTER;
     if (D.rank > 256 || D.ld_lora_b < D.rank) return RQ_ERR_BAD_SHAPE;
     if (D.lora_dtype != RQ_DTYPE_F32 && D.lora_dtype != D.dy_dtype) return RQ_ERR_BAD_DTYPE;
+    if (D.lora_mask && D.ld_lora_mask < D.K) return RQ_ERR_BAD_SHAPE;
   }
   return RQ_OK;
 }
@@ -273,6 +274,9 @@ int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t st
   e.rank = int(rank);
   e.rank16 = p.rank16;
   e.scaling = 1.0f;
+  e.mask = rank > 0 ? D.lora_mask : nullptr;
+  e.ldm = D.ld_lora_mask;
+  e.mask_scale = D.mask_scale;
   e.y = static_cast<uint16_t*>(D.dx);
   e.ldy = D.lddx;
   if (rank > 0) {
@@ -319,13 +323,15 @@ static rq::DxArgs pack_dx_args(const void* dy, int dy_dtype, int64_t M, int64_t 
                                const uint8_t* w_packed, int64_t K, int64_t block_size, const void* absmax,
                                int absmax_dtype, const uint8_t* c2, int c2_format, int64_t block2,
                                const void* lora_a, const void* lora_b, int64_t ld_lora_b, int lora_dtype,
-                               int64_t rank, float scaling, void* dx, int64_t lddx) {
+                               int64_t rank, float scaling, const uint8_t* lora_mask, int64_t ld_lora_mask,
+                               float mask_scale, void* dx, int64_t lddx) {
   rq::DxArgs D;
   D.dy = dy; D.dy_dtype = dy_dtype; D.M = M; D.N = N; D.lddy = lddy;
   D.w_packed = w_packed; D.K = K; D.block_size = block_size;
   D.absmax = absmax; D.absmax_dtype = absmax_dtype; D.c2 = c2; D.c2_format = c2_format; D.block2 = block2;
   D.lora_a = lora_a; D.lora_b = lora_b; D.ld_lora_b = ld_lora_b; D.lora_dtype = lora_dtype;
   D.rank = (lora_a && lora_b) ? rank : 0; D.scaling = scaling;
+  D.lora_mask = lora_mask; D.ld_lora_mask = ld_lora_mask; D.mask_scale = mask_scale;
   D.dx = dx; D.lddx = lddx;
   return D;
 }
@@ -347,10 +353,21 @@ extern "C" int rq_nf4_linear_dx(const void* dy, int dy_dtype, int64_t M, int64_t
                                 const uint8_t* w_packed, int64_t K, int64_t block_size, const void* absmax,
                                 int absmax_dtype, const uint8_t* c2, int c2_format, int64_t block2,
                                 const void* lora_a, const void* lora_b, int64_t ld_lora_b, int lora_dtype,
-                                int64_t rank, float scaling, void* dx, int64_t lddx, void* workspace,
+                                int64_t rank, float scaling, const uint8_t* lora_mask, int64_t ld_lora_mask,
+                                float mask_scale, void* dx, int64_t lddx, void* workspace,
                                 int64_t workspace_bytes, hipStream_t stream) {
   const rq::DxArgs D = pack_dx_args(dy, dy_dtype, M, N, lddy, w_packed, K, block_size, absmax, absmax_dtype, c2,
-                                    c2_format, block2, lora_a, lora_b, ld_lora_b, lora_dtype, rank, scaling, dx,
-                                    lddx);
+                                    c2_format, block2, lora_a, lora_b, ld_lora_b, lora_dtype, rank, scaling,
+                                    lora_mask, ld_lora_mask, mask_scale, dx, lddx);
   return rq::run_nf4_dx(D, workspace, workspace_bytes < 0 ? 0 : size_t(workspace_bytes), stream);
+}
+
+extern "C" int rq_gemm_tile_config(int32_t* out) {
+  if (!out) return RQ_ERR_NULL_POINTER;
+  out[0] = rq::kGemmBM;
+  out[1] = rq::kGemmBN;
+  out[2] = rq::kGemmBK;
+  out[3] = rq::kGemm8Threads / 64;  // wavefronts per workgroup
+  out[4] = 2;                       // weight / activation tiles in flight in LDS (double buffered)
+  return RQ_OK;
 }

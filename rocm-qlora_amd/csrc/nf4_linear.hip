@@ -14,6 +14,7 @@
 // dequantize_int4 + .to(x.dtype) produces (fp32 product, one RNE rounding);
 // only the order of the fp32 sums differs from the CPU GEMM.
 #include <algorithm>
+#include <atomic>
 
 #include "rq_mfma.h"
 #include "rq_launch.h"
@@ -905,13 +906,11 @@ __global__ __launch_bounds__(kGemvThreads) void lora_u_jobs_kernel(GemvArgs a, L
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-static uint32_t gemv_spin_limit = kGemvSpinLimit;
+// The poll bound of rq_set_gemv_spin_limit (a test hook): an atomic, so
+// that setting it from one host thread while another launches is defined.
+static std::atomic<uint32_t> gemv_spin_limit{kGemvSpinLimit};
 
-uint32_t set_gemv_spin_limit(uint32_t polls) {
-  const uint32_t old = gemv_spin_limit;
-  gemv_spin_limit = polls;
-  return old;
-}
+uint32_t set_gemv_spin_limit(uint32_t polls) { return gemv_spin_limit.exchange(polls, std::memory_order_relaxed); }
 
 // Work plan of the GEMV: K splits, tiles per workgroup, units per wave, the
 // unit table, the activation stage, and the workspace layout.
@@ -1055,16 +1054,20 @@ static int launch_lora_u_jobs(const LinearArgs& L, const LinearEpi& e, float* up
   return rq_check_launch();
 }
 
+// Devices on which an instantiation's dynamic-LDS limit has been raised
+// (one bit per device index), one set per instantiation.
+template <int XT, class Scale, int U, int XM>
+static std::atomic<uint64_t>& attr_devices() {
+  static std::atomic<uint64_t> bits{0};
+  return bits;
+}
+
 template <int XT, class Scale, int U, int XM>
 static int launch_gemv_u(const GemvArgs& a, const GemvPlan& p, Scale scale, const LinearEpi& e, hipStream_t stream) {
   auto kern = nf4_gemv_kernel<XT, Scale, U, XM>;
-  static bool attr_set = false;  // one flag per instantiation
-  if (!attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            kGemvLdsBudget) != hipSuccess)
-      return RQ_ERR_HIP;
-    attr_set = true;
-  }
+  if (int st = allow_dynamic_lds(reinterpret_cast<const void*>(kern), kGemvLdsBudget, attr_devices<XT, Scale, U, XM>());
+      st != RQ_OK)
+    return st;
   dim3 grid(unsigned(p.grid + p.jt), unsigned(p.S));
   kern<<<grid, kGemvThreads, p.lds_bytes, stream>>>(a, scale, e);
   return rq_check_launch();
@@ -1088,7 +1091,7 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.xvec = gemv_xvec(L);
   a.bvec_log2 = gemv_bvec_log2(L);
   a.jt = p.jt;
-  a.spin_limit = gemv_spin_limit;
+  a.spin_limit = gemv_spin_limit.load(std::memory_order_relaxed);
   a.done = static_cast<uint32_t*>(sync);
   a.ubits = reinterpret_cast<uint32_t*>(static_cast<char*>(sync) + kLinearCountBytes);
   a.lora_x = static_cast<const uint16_t*>(L.lora_x);

@@ -324,6 +324,7 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   }
 
   // ---- epilogue.  y = RND(RND(acc + RND(bias)) + RND(RND(lora) * scaling))
+  // (dX with LoRA dropout: scaling replaced by mask ? mask_scale : 0)
   // with lora = RND(u) RND(B)^T accumulated by MFMA in chunks of 64 ranks,
   // both operands staged into LDS (u rows and B rows of the tile, 144-byte
   // pitch); FP8: y = RND(RND(acc * post_a * post_b) + RND(bias)).
@@ -394,8 +395,10 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
           if (e.bias) v = __fadd_rn(v, bias);
           v = round_x<XT>(v);
         }
-        if (rank > 0)
-          v = round_x<XT>(__fadd_rn(v, round_x<XT>(__fmul_rn(round_x<XT>(lo[mb][nb][r]), e.scaling))));
+        if (rank > 0) {
+          const float ls = e.mask ? (e.mask[m * e.ldm + n] ? e.mask_scale : 0.0f) : e.scaling;
+          v = round_x<XT>(__fadd_rn(v, round_x<XT>(__fmul_rn(round_x<XT>(lo[mb][nb][r]), ls))));
+        }
         e.y[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
       }
     }

@@ -58,6 +58,12 @@ struct GemmEpi {
   int64_t b_sn, b_sj;
   bool b_vec;            // b_sj == 1 and braw rows 16-byte aligned (fp32 vector loads)
   float scaling;         // 1 for dX
+  // dX with LoRA dropout: the adapter term is RND(RND(lora) * (mask ? mask_scale
+  // : 0)) (dropout's backward, mask [M][N] bytes with row stride ldm);
+  // nullptr otherwise
+  const uint8_t* mask;
+  int64_t ldm;
+  float mask_scale;
   // FP8: y = RND(RND(acc * (*post_a) * (*post_b)) + RND(bias)) (the scaled
   // product is rounded before the bias is added); nullptr otherwise
   const float* post_a;

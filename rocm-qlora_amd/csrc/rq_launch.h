@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 #include "rocm_qlora_amd.h"
 
 namespace rq {
@@ -22,6 +24,19 @@ constexpr int64_t kMaxThreads1D = (int64_t(1) << 32) - 1024;
 inline int rq_check_launch() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RQ_OK : RQ_ERR_HIP;
+}
+
+// Raises `kernel`'s dynamic LDS limit to `bytes` on the current device once
+// (bit d of `done` marks device d; setting it twice from racing threads is
+// harmless, the attribute value being the same).
+inline int allow_dynamic_lds(const void* kernel, int bytes, std::atomic<uint64_t>& done) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return RQ_ERR_HIP;
+  const uint64_t bit = dev < 64 ? (uint64_t(1) << dev) : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return RQ_OK;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) return RQ_ERR_HIP;
+  done.fetch_or(bit, std::memory_order_release);
+  return RQ_OK;
 }
 
 }  // namespace rq

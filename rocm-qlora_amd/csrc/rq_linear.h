@@ -104,6 +104,9 @@ struct DxArgs {
   int lora_dtype;
   int64_t rank;
   float scaling;
+  const uint8_t* lora_mask;  // dropout mask [M][K] (row stride ld_lora_mask), or nullptr
+  int64_t ld_lora_mask;
+  float mask_scale;
   void* dx;
   int64_t lddx;
 };

@@ -41,12 +41,14 @@ SIGNATURES = {
                       _P, _I64, _P, _P, _I64, _I32, _I64, _F32,  # lora x, ld, A, B, ldB, dtype, rank, scaling
                       _P, _I64, _P, _I64, _P],               # y, ldy, workspace, bytes, stream
     "rq_set_gemv_spin_limit": [ctypes.c_uint32],
+    "rq_gemm_tile_config": [_P],
     "rq_stream_capture_id": [_P, _P],
     "rq_nf4_linear_dx_workspace_size": [_I32, _I64, _I64, _I64, _I64, _P],
     "rq_nf4_linear_dx": [_P, _I32, _I64, _I64, _I64,         # dy, dtype, M, N, lddy
                          _P, _I64, _I64, _P, _I32,           # packed, K, block, absmax, dtype
                          _P, _I32, _I64,                     # c2, c2 format, block2
                          _P, _P, _I64, _I32, _I64, _F32,     # A, B, ldB, dtype, rank, scaling
+                         _P, _I64, _F32,                     # dropout mask, ld, mask scale
                          _P, _I64, _P, _I64, _P],            # dx, lddx, workspace, bytes, stream
     "rq_int8_linear": [_P, _I32, _I64, _I64, _I64,           # x, dtype, M, K, ldx
                        _P, _I64, _I64, _P, _I32,             # q, N, block, scales, dtype
@@ -117,8 +119,13 @@ def set_gemv_spin_limit(polls: int) -> int:
 
 def capture_id(device: torch.device) -> int:
     """Identifier of the graph capture active on the current stream (0: none)."""
+    return stream_capture_id(stream_handle(device))
+
+
+def stream_capture_id(handle: int) -> int:
+    """Identifier of the graph capture active on a raw HIP stream (0: none)."""
     cid = ctypes.c_uint64(0)
-    call("rq_stream_capture_id", stream_handle(device), ctypes.byref(cid))
+    call("rq_stream_capture_id", handle, ctypes.byref(cid))
     return int(cid.value)
 
 

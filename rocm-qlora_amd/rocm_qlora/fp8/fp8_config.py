@@ -25,11 +25,8 @@ def detect_fp8_support() -> Dict[str, Any]:
         except ValueError:
             pass
     info["arch"] = get_device_info().get("arch", "unknown")
-    try:
-        import transformer_engine.pytorch  # noqa: F401
-        info["transformer_engine_available"] = True
-    except ImportError:
-        pass
+    # the FP8 linears run on this package's own kernels: TransformerEngine is
+    # never imported or dispatched to, so it is reported as unavailable
     if not info["fp8_dtypes_available"]:
         info["reason"] = "FP8 dtypes unavailable in this PyTorch build"
     elif rocm_ver < (6, 2):
@@ -48,7 +45,7 @@ class FP8Config:
     enabled: bool = True
     forward_dtype: str = "e4m3"
     backward_dtype: str = "e5m2"
-    use_transformer_engine: bool = True
+    use_transformer_engine: bool = True  # kept for interface; TransformerEngine is never used
     fallback_dtype: torch.dtype = torch.bfloat16
     amax_history_len: int = 16
     amax_compute_algo: str = "max"
@@ -71,10 +68,9 @@ def get_fp8_dtype(format_str: str) -> torch.dtype:
 
 
 def get_fp8_recipe(config: FP8Config):
-    """TransformerEngine DelayedScaling recipe when TE is importable, else None."""
-    try:
-        import transformer_engine.pytorch as te
-    except ImportError:
-        return None
-    return te.recipe.DelayedScaling(amax_history_len=config.amax_history_len,
-                                    amax_compute_algo=config.amax_compute_algo)
+    """The reference returns a TransformerEngine DelayedScaling recipe when TE
+    is importable (fp8_config.py:91-101).  This package's FP8 linears use the
+    per-tensor current-scaling recipe of fp8_linear.py:33-42 on its own
+    kernels and never dispatch to TransformerEngine, so there is no recipe
+    object: always None."""
+    return None

@@ -17,7 +17,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from rocm_qlora import ops
-from rocm_qlora.fp8.fp8_config import detect_fp8_support, FP8Config, get_fp8_recipe
+from rocm_qlora.fp8.fp8_config import detect_fp8_support, FP8Config
 from rocm_qlora.lora.lora_layer import LoRALinear
 
 _FNUZ_MAX = 240.0
@@ -57,21 +57,16 @@ class _FP8LinearFunc(torch.autograd.Function):
 class FP8LinearWrapper(nn.Module):
     """Runs a LoRALinear's base matmul in FP8 (fp8_linear.py:69-118).  Backend
     'native' (this package's FP8 kernels) when FP8 is supported and enabled,
-    'transformer_engine' when TE is importable and preferred, else 'bf16'
-    (the wrapped layer unchanged).  The FP8 weight codes are cached until the
-    stored weight changes."""
+    else 'bf16' (the wrapped layer unchanged).  The reference's third
+    backend, TransformerEngine, is not dispatched to: there is one FP8 code
+    path.  The FP8 weight codes are cached until the stored weight changes."""
 
     def __init__(self, base_lora_linear: nn.Module, config: Optional[FP8Config] = None):
         super().__init__()
         self.config = config if config is not None else FP8Config()
         self.base = base_lora_linear
         self.fp8_info = detect_fp8_support()
-        if not self.config.enabled or not self.fp8_info["fp8_supported"]:
-            self.backend = "bf16"
-        elif self.fp8_info["transformer_engine_available"] and self.config.use_transformer_engine:
-            self.backend = "transformer_engine"
-            self.te_recipe = get_fp8_recipe(self.config)
-        elif self.fp8_info["fp8_dtypes_available"]:
+        if self.config.enabled and self.fp8_info["fp8_supported"] and self.fp8_info["fp8_dtypes_available"]:
             self.backend = "native"
         else:
             self.backend = "bf16"
@@ -89,10 +84,6 @@ class FP8LinearWrapper(nn.Module):
         return self._cache
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.backend == "transformer_engine":
-            import transformer_engine.pytorch as te
-            with te.fp8_autocast(enabled=True, fp8_recipe=self.te_recipe):
-                return self.base(x)
         if self.backend == "native":
             ql = self.base.base_layer
             w, w_q = self._weight(x.dtype)
@@ -129,13 +120,7 @@ def wrap_model_for_fp8(model: nn.Module, config: Optional[FP8Config] = None) -> 
 
 
 def enable_fp8_autocast(model: nn.Module, config: Optional[FP8Config] = None):
-    """TransformerEngine fp8_autocast when TE is importable and preferred,
-    else a null context (fp8_linear.py:162-174)."""
-    config = config if config is not None else FP8Config()
-    try:
-        import transformer_engine.pytorch as te
-        if config.use_transformer_engine:
-            return te.fp8_autocast(enabled=True, fp8_recipe=get_fp8_recipe(config))
-    except ImportError:
-        pass
+    """A null context (fp8_linear.py:164-174 enters TransformerEngine's
+    fp8_autocast when TE is importable; here FP8 runs only through
+    FP8LinearWrapper's own kernels, which need no autocast region)."""
     return contextlib.nullcontext()

@@ -116,22 +116,34 @@ def _lora_term(x, lora_a, lora_b, scaling):
 
 class _FusedNF4LinearFunc(torch.autograd.Function):
     """y = x . W_deq^T + bias (+ LoRA) by the HIP kernels; backward gives dX
-    (NF4 dX kernel, LoRA term fused) and the adapters' gradients."""
+    (NF4 dX kernel, LoRA term fused) and the adapters' gradients.
+
+    With LoRA dropout p > 0 the adapter reads drop(x) (lora_layer.py:67):
+    the mask comes from torch's own dropout kernel (aten::native_dropout,
+    the kernel nn.Dropout runs, so the random stream is the same), the
+    forward passes drop(x) as the LoRA input of the fused kernels, and the
+    dX kernel applies dropout's backward (mask / (1 - p)) to the adapter's
+    input gradient in its epilogue."""
 
     @staticmethod
-    def forward(ctx, x, lora_a, lora_b, bias, w: NF4Weight, scaling: float):
+    def forward(ctx, x, lora_a, lora_b, bias, w: NF4Weight, scaling: float, dropout_p: float = 0.0):
         lora = _lora_present(lora_a, lora_b)
+        xl = mask = None
+        if lora and dropout_p > 0.0:
+            xl, mask = torch.ops.aten.native_dropout(x, float(dropout_p), True)
         ctx.w = w
         ctx.scaling = float(scaling)
         ctx.lora = lora
-        ctx.save_for_backward(x if lora else None, lora_a if lora else None, lora_b if lora else None)
+        ctx.mask_scale = 1.0 / (1.0 - dropout_p) if mask is not None else 1.0
+        ctx.save_for_backward(x if lora else None, lora_a if lora else None, lora_b if lora else None,
+                              xl, mask)
         return ops.nf4_linear(x, w.packed, w.scales, w.N, w.block_size, bias,
                               lora_a=lora_a if lora else None, lora_b=lora_b if lora else None,
-                              scaling=scaling, **w.dq_kwargs())
+                              scaling=scaling, lora_x=xl, **w.dq_kwargs())
 
     @staticmethod
     def backward(ctx, dy):
-        x, A, B = ctx.saved_tensors
+        x, A, B, xl, mask = ctx.saved_tensors
         w: NF4Weight = ctx.w
         s = ctx.scaling
         need_x, need_a, need_b = ctx.needs_input_grad[:3]
@@ -139,23 +151,28 @@ class _FusedNF4LinearFunc(torch.autograd.Function):
         if need_x:
             if w.dx_ok(dy.dtype):
                 dx = ops.nf4_linear_dx(dy, w.packed, w.scales, w.K, w.block_size,
-                                       lora_a=A, lora_b=B, scaling=s, **w.dq_kwargs())
+                                       lora_a=A, lora_b=B, scaling=s, lora_mask=mask,
+                                       mask_scale=ctx.mask_scale, **w.dq_kwargs())
             else:
                 dx = dy @ w.dense(dy.dtype)
                 if ctx.lora:
-                    dx = dx + ((dy * s) @ B.to(dy.dtype)) @ A.to(dy.dtype)
+                    dl = ((dy * s) @ B.to(dy.dtype)) @ A.to(dy.dtype)
+                    if mask is not None:
+                        dl = torch.ops.aten.native_dropout_backward(dl, mask, ctx.mask_scale)
+                    dx = dx + dl
         if ctx.lora and (need_a or need_b):
-            # lora_out = ((x A^T) B^T) * s in x's dtype: dv = dY * s,
-            # dB = dv^T (x A^T), dA = (dv B)^T x, cast to the parameters' dtype
+            # lora_out = ((xl A^T) B^T) * s in x's dtype, xl = drop(x) or x:
+            # dv = dY * s, dB = dv^T (xl A^T), dA = (dv B)^T xl, cast to the
+            # parameters' dtype
             dt = x.dtype
-            x2 = x.reshape(-1, x.shape[-1])
+            x2 = (xl if xl is not None else x).reshape(-1, x.shape[-1])
             dv = dy.reshape(-1, dy.shape[-1]).to(dt) * s
             if need_b:
                 u = x2 @ A.to(dt).T
                 db = (dv.T @ u).to(B.dtype)
             if need_a:
                 da = ((dv @ B.to(dt)).T @ x2).to(A.dtype)
-        return dx, da, db, None, None, None
+        return dx, da, db, None, None, None, None
 
 
 class _FusedInt8LinearFunc(torch.autograd.Function):
@@ -176,17 +193,19 @@ class _FusedInt8LinearFunc(torch.autograd.Function):
 
 def nf4_linear(x: torch.Tensor, w: NF4Weight, bias: Optional[torch.Tensor] = None,
                lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
-               scaling: float = 0.0) -> torch.Tensor:
-    """Autograd-aware NF4 linear (+ LoRA): fused HIP kernels where they apply,
+               scaling: float = 0.0, dropout_p: float = 0.0) -> torch.Tensor:
+    """Autograd-aware NF4 linear (+ LoRA, its input through dropout of
+    probability dropout_p when > 0): fused HIP kernels where they apply,
     otherwise the HIP dequantizer followed by the library GEMM."""
     nat.require_gpu(x, w.packed)
     # the reference adds bias.to(x.dtype) (quant_linear.py:196)
     bias = bias.to(x.dtype) if bias is not None else None
     if w.kernel_ok(x.dtype):
-        return _FusedNF4LinearFunc.apply(x, lora_a, lora_b, bias, w, scaling)
+        return _FusedNF4LinearFunc.apply(x, lora_a, lora_b, bias, w, scaling, float(dropout_p))
     y = F.linear(x, w.dense(x.dtype), bias)
     if _lora_present(lora_a, lora_b):
-        y = y + _lora_term(x, lora_a, lora_b, scaling).to(y.dtype)
+        xl = F.dropout(x, dropout_p, True) if dropout_p > 0.0 else x
+        y = y + _lora_term(xl, lora_a, lora_b, scaling).to(y.dtype)
     return y
 
 

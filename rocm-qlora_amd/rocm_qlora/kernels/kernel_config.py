@@ -29,9 +29,10 @@ class KernelConfig:
 # The name callers of the reference import.
 TritonKernelConfig = KernelConfig
 
-# gfx950 = MI355X / MI350X (CDNA4): the NF4 GEMM's 256x128x64 tiles, four
-# wavefronts, four weight tiles in flight (csrc/rq_gemm_core.h)
-CDNA4_CONFIG = KernelConfig(BLOCK_M=256, BLOCK_N=128, BLOCK_K=64, num_warps=4, num_stages=4, wavefront_size=64)
+# gfx950 = MI355X / MI350X (CDNA4): the MFMA GEMM's 256x128 workgroup tiles,
+# 64 k per step, eight wavefronts (two per SIMD), activation ring and weight
+# tile double buffered in LDS -- the values rq_gemm_tile_config reports
+CDNA4_CONFIG = KernelConfig(BLOCK_M=256, BLOCK_N=128, BLOCK_K=64, num_warps=8, num_stages=2, wavefront_size=64)
 CDNA3_CONFIG = KernelConfig(BLOCK_M=64, BLOCK_N=64, BLOCK_K=32, num_warps=4, num_stages=2, wavefront_size=64)
 CDNA2_CONFIG = KernelConfig(BLOCK_M=128, BLOCK_N=64, BLOCK_K=32, num_warps=8, num_stages=2, wavefront_size=64)
 RDNA3_CONFIG = KernelConfig(BLOCK_M=64, BLOCK_N=64, BLOCK_K=64, num_warps=4, num_stages=2, wavefront_size=32)

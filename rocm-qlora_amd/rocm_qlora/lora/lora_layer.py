@@ -3,10 +3,11 @@
 
 y = base(x) + ((drop(x) @ A^T) @ B^T * s).to(base dtype), s = alpha / r,
 A [r, in] Kaiming-uniform(a=sqrt 5), B [out, r] zeros.  With an NF4 base on
-the GPU and no active dropout, the adapter term runs inside the quantized
-linear's kernel sequence (the LoRA epilogue of the GEMV / GEMM), and the
-backward pass runs the fused NF4 dX kernel plus two small library GEMMs for
-dA and dB.  Otherwise the base layer and the adapter are composed as in the
+the GPU, the adapter term runs inside the quantized linear's kernel sequence
+(the LoRA epilogue of the GEMV / GEMM) -- with active dropout, on drop(x),
+whose mask the dX kernel applies in the backward pass -- and the backward
+pass runs the fused NF4 dX kernel plus two small library GEMMs for dA and
+dB.  Otherwise the base layer and the adapter are composed as in the
 reference.
 """
 from __future__ import annotations
@@ -49,8 +50,9 @@ class LoRALinear(nn.Module):
         if self.merged:
             return self.base_layer(x)
         base = self.base_layer
-        if isinstance(base, QuantLinear) and not base.merged_mode and not self._dropout_active():
-            return base.fused_forward(x, self.lora_A, self.lora_B, self.scaling)
+        if isinstance(base, QuantLinear) and not base.merged_mode:
+            p = self.lora_dropout.p if self._dropout_active() else 0.0
+            return base.fused_forward(x, self.lora_A, self.lora_B, self.scaling, p)
         if hasattr(base, "weight"):
             base_out = base(x.to(base.weight.dtype))
         else:
@@ -60,9 +62,11 @@ class LoRALinear(nn.Module):
 
     @torch.no_grad()
     def merge_lora(self) -> None:
-        """Store fp16(W_deq + B @ A * s) as the base layer's merged weight and
-        zero the adapters (lora_layer.py:72-113).  No re-quantization.  The
-        dequantization honours double quantization."""
+        """Store fp16(W_deq + B @ A * s) as the base layer's merged weight
+        (lora_layer.py:72-113).  No re-quantization.  Unlike the reference,
+        the dequantization honours double quantization and the adapters are
+        kept (the reference zeroes A and B, lora_layer.py:111-113, so its
+        unmerge_lora cannot restore the adapted layer; here it does)."""
         if self.merged:
             raise RuntimeError("LoRA already merged")
         delta = (self.lora_B @ self.lora_A) * self.scaling
@@ -71,11 +75,10 @@ class LoRALinear(nn.Module):
         self.base_layer.merged_fp16_weight = merged
         self.base_layer.merged_mode = True
         self.merged = True
-        self.lora_A.data.zero_()
-        self.lora_B.data.zero_()
 
     def unmerge_lora(self) -> None:
-        """Drop the merged fp16 weight (lora_layer.py:115-128)."""
+        """Drop the merged fp16 weight (lora_layer.py:115-128); the adapters,
+        kept by merge_lora, apply again."""
         if not self.merged:
             raise RuntimeError("LoRA is not merged — nothing to unmerge")
         self.base_layer.merged_fp16_weight = None

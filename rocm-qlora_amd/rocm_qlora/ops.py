@@ -18,6 +18,8 @@ from rocm_qlora._device import on
 # activation rows up to which the NF4 linear runs as a weight-streaming GEMV
 # (kGemvMaxM in csrc/rq_linear.h); above it, the MFMA GEMM
 GEMV_MAX_M = 16
+# largest N * (row stride of LoRA B) the decode GEMV addresses (2^29 elements)
+GEMV_MAX_B_ELEMS = 1 << 29
 
 
 def _rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
@@ -28,30 +30,30 @@ def _rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
     return t2, (t2.stride(0) if t2.shape[0] > 1 else K)
 
 
-# rq_nf4_linear's workspace per (device, stream): its first
-# RQ_LINEAR_SYNC_BYTES (include/rocm_qlora_amd.h) are a synchronization area
-# that must be zero before a call and is zero again after it, so one buffer,
-# its area zeroed once, serves every call ordered on the stream.  It grows
-# by reallocation; a dropped buffer returns to torch's caching allocator,
-# which reuses it only after the work already queued on the stream.
-#
-# A graph capture gets a buffer of its own, shared by the calls it captures
-# and reused by every replay: a spare that eager calls zeroed beforehand (so
-# the graph records no fill), or, when no spare is large enough, one from
-# the graph's memory pool zeroed by a fill kernel recorded in the graph.  A
-# spare given to a capture is held for the life of the process (the graph's
-# replays may come at any time).
+# rq_nf4_linear's workspace.  Its first RQ_LINEAR_SYNC_BYTES
+# (include/rocm_qlora_amd.h) are a synchronization area that must be zero
+# before a call and is zero again once the call's kernels are done, so one
+# buffer, zeroed once on the stream that uses it, serves every call ordered
+# on that stream.  Calls that may run at the same time need buffers of their
+# own, hence the keys:
+#   * eager calls: one buffer per (device, stream), zeroed by a fill kernel
+#     on that stream when it is created; it grows by reallocation (a dropped
+#     buffer returns to torch's caching allocator, which hands it out again
+#     only in stream order);
+#   * graph capture: one buffer per (device, capture, stream) -- the branches
+#     of a capture that forks side streams each get their own -- allocated
+#     from the graph's private memory pool (so it lives exactly as long as
+#     the graph) and zeroed by a fill kernel recorded in the graph, which
+#     every replay runs before the captured calls.
+# No host synchronization is involved either way.
 LINEAR_SYNC_BYTES = 65792
 _LINEAR_WS: dict = {}
 _CAPTURE_WS: dict = {}
-_SPARES: dict = {}
-_HELD_BY_GRAPHS: list = []
-_N_SPARES = 2
 _WS_MIN_BYTES = 1 << 20
 
 
-def _zeroed_area(nbytes: int, dev) -> torch.Tensor:
-    ws = torch.empty(max(nbytes, _WS_MIN_BYTES), dtype=torch.uint8, device=dev)
+def _zeroed_area(nbytes: int, dev, min_bytes: int = _WS_MIN_BYTES) -> torch.Tensor:
+    ws = torch.empty(max(nbytes, min_bytes), dtype=torch.uint8, device=dev)
     ws[:LINEAR_SYNC_BYTES].zero_()
     return ws
 
@@ -64,32 +66,30 @@ def _workspace(x_dtype: torch.dtype, M: int, K: int, N: int, rank: int, dev) -> 
     if need == 0:
         return None
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    stream = torch.cuda.current_stream(dev).cuda_stream
     if torch.cuda.is_current_stream_capturing():
         cid = nat.capture_id(dev)
-        ws = _CAPTURE_WS.get(idx)
-        if ws is None or ws[0] != cid or ws[1].numel() < need:
-            spares = _SPARES.get(idx, [])
-            fit = next((i for i, b in enumerate(spares) if b.numel() >= need), None)
-            if fit is not None:
-                buf = spares.pop(fit)
-                _HELD_BY_GRAPHS.append(buf)
-            else:
-                buf = _zeroed_area(need, dev)  # stays in the graph's pool
-            ws = (cid, buf)
-            _CAPTURE_WS[idx] = ws
-        return ws[1]
-    key = (idx, torch.cuda.current_stream(dev).cuda_stream)
+        # the buffers of captures that have ended belong to their graphs'
+        # pools and are dropped here; a capture still running (on another
+        # stream or thread) keeps its buffer, since its pool could otherwise
+        # hand the memory to a later allocation of the same capture
+        for k in [k for k in _CAPTURE_WS if k[0] == idx and k[1] != cid]:
+            if nat.stream_capture_id(k[2]) != k[1]:
+                del _CAPTURE_WS[k]
+        key = (idx, cid, stream)
+        ws = _CAPTURE_WS.get(key)
+        if ws is None or ws.numel() < need:
+            # a larger buffer replaces a smaller one for the calls captured
+            # from here on; calls captured before keep theirs (both are
+            # zeroed by their own recorded fills)
+            ws = _zeroed_area(need, dev, min_bytes=LINEAR_SYNC_BYTES)
+            _CAPTURE_WS[key] = ws
+        return ws
+    key = (idx, stream)
     ws = _LINEAR_WS.get(key)
     if ws is None or ws.numel() < need:
         ws = _zeroed_area(max(need, 2 * ws.numel() if ws is not None else 0), dev)
         _LINEAR_WS[key] = ws
-    spares = _SPARES.setdefault(idx, [])
-    if len(spares) < _N_SPARES or any(b.numel() < need for b in spares):
-        spares[:] = [b for b in spares if b.numel() >= need]
-        while len(spares) < _N_SPARES:
-            spares.append(_zeroed_area(need, dev))
-        # a capture on another stream may take a spare: its fill must be done
-        torch.cuda.synchronize(dev)
     return ws
 
 
@@ -150,11 +150,16 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
             if lora_b.dtype != lora_a.dtype:
                 lora_b = lora_b.to(lora_a.dtype)
             la = lora_a.contiguous()
-            # B rows may be strided (a column slice of a wider parameter)
+            # B rows may be strided (a column slice of a wider parameter);
+            # the decode GEMV addresses B with 32-bit offsets, so a stride
+            # that would overflow them is packed first
             lb, ldb = _rows(lora_b, rank)
+            if M <= GEMV_MAX_M and N * ldb > GEMV_MAX_B_ELEMS:
+                lb, ldb = lb.contiguous(), rank
             lcode = nat.dtype_code(la.dtype)
             if lora_x is not None:
-                xl, ldxl = _rows(lora_x.to(x.dtype), K)
+                # the GEMM's LoRA operand kernel loads 16 bytes at a time
+                xl, ldxl = (_aligned_rows if M > GEMV_MAX_M else _rows)(lora_x.to(x.dtype), K)
         b = bias.contiguous() if bias is not None else None
         ws = _workspace(x.dtype, M, K, N, rank, dev)
         codes = c2.reshape(-1).view(torch.uint8).contiguous() if dq else None
@@ -195,10 +200,13 @@ def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: O
                   c2: Optional[torch.Tensor] = None, c2_scales: Optional[torch.Tensor] = None,
                   blocksize_2: int = 256, use_fp8_c2: bool = True,
                   lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
-                  scaling: float = 0.0) -> torch.Tensor:
+                  scaling: float = 0.0, lora_mask: Optional[torch.Tensor] = None,
+                  mask_scale: float = 1.0) -> torch.Tensor:
     """dX = dY . dequant(W) (+ the LoRA term ((dY * s) . B) . A) for an NF4
     weight stored flat (dequant_matmul.py:338-351, lora_layer.py:67
-    differentiated).  dy: [..., N] bf16/fp16 on the GPU, N % 64 == 0;
+    differentiated).  With lora_mask (the dropout mask of the adapter's input,
+    [..., K] bool), the LoRA term goes through dropout's backward: times
+    mask * mask_scale.  dy: [..., N] bf16/fp16 on the GPU, N % 64 == 0;
     output [..., K] in dy's dtype."""
     N = dy.shape[-1]
     K = int(in_features)
@@ -214,10 +222,9 @@ def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: O
     scales = scales.reshape(-1).contiguous()
     lead = dy.shape[:-1]
     with on(dev):
-        dy2, lddy = _rows(dy, N)
+        # the dX kernel loads dY rows 16 bytes at a time
+        dy2, lddy = _aligned_rows(dy, N)
         M = dy2.shape[0]
-        if dy2.data_ptr() % 16:
-            dy2, lddy = dy2.contiguous().clone(), N
         dx = torch.empty((M, K), dtype=dy.dtype, device=dev)
         if M == 0:
             return dx.reshape(*lead, K)
@@ -238,6 +245,11 @@ def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: O
             # B rows may be strided (a column slice of a wider parameter)
             lb, ldb = _rows(lora_b, rank)
             lcode = nat.dtype_code(la.dtype)
+        mk, ldm = None, 0
+        if rank > 0 and lora_mask is not None:
+            mk, ldm = _rows(lora_mask.reshape(-1, K).view(torch.uint8), K)
+            if mk.shape[0] != M:
+                raise RuntimeError(f"lora_mask has {mk.shape[0]} rows, dY {M}")
         import ctypes
         nbytes = ctypes.c_int64(0)
         nat.call("rq_nf4_linear_dx_workspace_size", nat.dtype_code(dy.dtype), M, N, K, rank, ctypes.byref(nbytes))
@@ -248,6 +260,7 @@ def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: O
                  packed.data_ptr(), K, block_size, scales.data_ptr(), nat.dtype_code(scales.dtype),
                  nat.ptr(codes), nat.C2_FP8_E4M3FNUZ if use_fp8_c2 else nat.C2_INT8, blocksize_2,
                  nat.ptr(la), nat.ptr(lb), ldb, lcode, rank, float(scaling),
+                 nat.ptr(mk), ldm, float(mask_scale),
                  dx.data_ptr(), K, nat.ptr(ws), ws.numel() if ws is not None else 0,
                  nat.stream_handle(dev))
     return dx.reshape(*lead, K)

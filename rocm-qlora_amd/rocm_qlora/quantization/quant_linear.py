@@ -119,15 +119,18 @@ class QuantLinear(nn.Module):
         return w.dense(dtype)
 
     def fused_forward(self, x: torch.Tensor, lora_a: Optional[torch.Tensor] = None,
-                      lora_b: Optional[torch.Tensor] = None, scaling: float = 0.0) -> torch.Tensor:
-        """Quantized linear with the LoRA term in the same kernel sequence
-        (NF4); INT8 adds the LoRA term after the int8 kernel."""
+                      lora_b: Optional[torch.Tensor] = None, scaling: float = 0.0,
+                      dropout_p: float = 0.0) -> torch.Tensor:
+        """Quantized linear with the LoRA term (its input through dropout of
+        probability dropout_p when > 0) in the same kernel sequence (NF4);
+        INT8 adds the LoRA term after the int8 kernel."""
         from rocm_qlora.kernels import dequant_matmul as dm
         if self.bits == 4:
-            return dm.nf4_linear(x, self.nf4_weight(), self.bias, lora_a, lora_b, scaling)
+            return dm.nf4_linear(x, self.nf4_weight(), self.bias, lora_a, lora_b, scaling, dropout_p)
         y = dm.int8_linear(x, self.int8_weight(), self.bias)
         if lora_a is not None and lora_b is not None and lora_a.shape[0] > 0:
-            y = y + dm._lora_term(x, lora_a, lora_b, scaling).to(y.dtype)
+            xl = torch.nn.functional.dropout(x, dropout_p, True) if dropout_p > 0.0 else x
+            y = y + dm._lora_term(xl, lora_a, lora_b, scaling).to(y.dtype)
         return y
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -208,6 +208,18 @@ def test_kernel_config_and_device_info(monkeypatch):
     assert (cfg.BLOCK_M, cfg.BLOCK_N, cfg.BLOCK_K, cfg.wavefront_size) == (256, 128, 64, 64)
 
 
+def test_cdna4_config_matches_library():
+    """get_kernel_config's gfx950 entry describes the GEMM the library runs
+    (rq_gemm_tile_config: tile rows, columns, k step, waves, LDS stages)."""
+    import ctypes
+    from rocm_qlora import _native as nat
+    from rocm_qlora.kernels import kernel_config as kc
+    out = (ctypes.c_int32 * 5)()
+    nat.call("rq_gemm_tile_config", out)
+    c = kc.CDNA4_CONFIG
+    assert list(out) == [c.BLOCK_M, c.BLOCK_N, c.BLOCK_K, c.num_warps, c.num_stages]
+
+
 def test_build_utils_and_enable_hip_kernels_without_gpu():
     from rocm_qlora.hip_kernels.build_utils import find_hipcc, is_hipcc_available, compile_hip_kernel
     from rocm_qlora.hip_kernels import enable_hip_kernels, is_hip_kernel_available
