@@ -220,17 +220,41 @@ def fp8_linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = 
     return y
 
 
+class _DropoutWithMask(torch.autograd.Function):
+    """nn.Dropout in training mode with a given keep-mask: forward x * mask *
+    scale and backward grad * mask * scale, each rounded once to x's dtype --
+    the two kernels torch's dropout runs (aten native_dropout /
+    native_dropout_backward), here both through native_dropout_backward,
+    which computes exactly that product."""
+
+    @staticmethod
+    def forward(ctx, x, mask, scale):
+        ctx.save_for_backward(mask)
+        ctx.scale = scale
+        return torch.ops.aten.native_dropout_backward(x, mask, scale)
+
+    @staticmethod
+    def backward(ctx, g):
+        (mask,) = ctx.saved_tensors
+        return torch.ops.aten.native_dropout_backward(g, mask, ctx.scale), None, None
+
+
 def lora_linear_grads(x: torch.Tensor, weight_fp: torch.Tensor, bias: Optional[torch.Tensor],
-                      lora_a: torch.Tensor, lora_b: torch.Tensor, scaling: float, dy: torch.Tensor):
+                      lora_a: torch.Tensor, lora_b: torch.Tensor, scaling: float, dy: torch.Tensor,
+                      dropout_mask: Optional[torch.Tensor] = None, dropout_p: float = 0.0):
     """Gradients of LoRALinear(QuantLinear).forward on the CPU path
     (quant_linear.py:189-197 then lora_layer.py:67-70), by torch autograd on
     the same expression: returns (y, dX, dA, dB) with dA / dB in the
-    parameters' dtype."""
+    parameters' dtype.  With dropout_mask (bool keep-mask of x's shape) the
+    adapter reads self.lora_dropout(x) = x * mask / (1 - dropout_p)
+    (lora_layer.py:67)."""
     N, K = lora_b.shape[0], x.shape[-1]
     x = x.detach().clone().requires_grad_(True)
     a = lora_a.detach().clone().requires_grad_(True)
     b = lora_b.detach().clone().requires_grad_(True)
     base = quant_linear_forward(x, weight_fp, bias, N, K)
-    y = lora_forward(x, base, a, b, scaling)
+    xl = x if dropout_mask is None else _DropoutWithMask.apply(x, dropout_mask, 1.0 / (1.0 - dropout_p))
+    lora_out = xl @ a.to(x.dtype).T @ b.to(x.dtype).T * scaling
+    y = base + lora_out.to(base.dtype)
     y.backward(dy)
     return y.detach(), x.grad, a.grad, b.grad

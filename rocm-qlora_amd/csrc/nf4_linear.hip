@@ -109,6 +109,11 @@ struct GemvArgs {
   // itself in *done; the last one clears ubits and *done, so both are zero
   // again once the launch is over.
   int jt;
+  // The same jobs run by the tile workgroups themselves (jm > 0, when every
+  // compute unit holds a tile workgroup and no workgroup of the launch can
+  // wait for a free one): tile workgroup g < jm runs job g after its first
+  // unit's loads are issued, then its units.  jt and jm are not both > 0.
+  int jm;
   uint32_t spin_limit;     // polls before a tile workgroup computes u itself
   uint32_t* done;          // workgroups past their use of ubits
   uint32_t* ubits;         // [u_splits, M, rank] partials as fp32 bits
@@ -441,7 +446,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
     return;
   }
-  const bool fused = a.jt > 0;
+  const bool fused = a.jt > 0 || a.jm > 0;
   const uint32_t g = blockIdx.x - uint32_t(a.jt), G = gridDim.x - uint32_t(a.jt);  // this tile workgroup, their number
   const int rank = (a.direct && e.rank > 0) ? e.rank : 0;  // LoRA staging only when fused here
   constexpr int RP = kGemvMaxFusedRank;                    // staging pitch
@@ -557,10 +562,22 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
   }
 
-  // 2. the table
+  // 2. the table; a workgroup with a merged job runs it now (its unit loads
+  //    are in flight): partials to ubits as the producer workgroups store them
   fill_f32pair_lut<kGemvThreads>(lut, tid);
-  if (fused && tid == 0) *flag = 0u;
   lds_barrier();
+  if (int(g) < a.jm) {
+    const int ns = e.u_splits;
+    const float v = lora_u_job<XT>(a, e, int(g) / ns, int(g) % ns, ns, tid, wave, reinterpret_cast<float*>(smem));
+    const int jj = 16 * (int(g) / ns) + (tid & 15);
+    if (tid < M * 16 && jj < e.rank) {
+      const uint32_t bits = f2u(v);
+      __hip_atomic_store(&a.ubits[((int(g) % ns) * M + (tid >> 4)) * e.rank + jj], bits != 0u ? bits : 0x80000000u,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    lds_barrier();  // the job's LDS reduction area is read before the units use it
+  }
+  if (fused && tid == 0) *flag = 0u;
 
   // 3. epilogue operands, raw: LoRA B values (value t of thread tid is row
   //    tid / 64 of tile slot t, rank tid % 64), the bias, the RND(u) partials
@@ -658,7 +675,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
       const uint32_t ns = uint32_t(e.u_splits), stride = uint32_t(M) * uint32_t(rank);
       const uint32_t u_idx = uint32_t(wave) * uint32_t(rank) + uint32_t(lj);
       bool ok = false;
-      for (uint32_t i = 0;; ++i) {
+      for (uint32_t i = 0; !ok && a.spin_limit > 0; ++i) {
         // all the loads of a poll in flight together: no branch between
         // them (a split past ns reads split 0 again and is not checked)
 #pragma unroll
@@ -922,8 +939,9 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
   const int64_t ncu = cus > 0 ? cus : 1;
   p.u_splits = 0;
   // K splits of the down-projection jobs (inside the GEMV launch or as
-  // lora_u_jobs_kernel): about 1024 k per job
-  const int fused_splits = int(std::min<int64_t>((K + 1023) / 1024, kGemvMaxUSplits));
+  // lora_u_jobs_kernel): about 256 k per job, so that a job's loads are one
+  // round of 16-byte loads per wave and the jobs end early
+  const int fused_splits = int(std::min<int64_t>((K + 255) / 256, kGemvMaxUSplits));
   if (rank > 0) {
     const int64_t steps_per_wg = 4 * kLoraUStepsPerWave;
     const int64_t ks = (K / 32 + steps_per_wg - 1) / steps_per_wg;
@@ -947,30 +965,49 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     // the down-projection as its own kernel
     const bool prod_fits = size_t(M) * rank * fused_splits * 4 <= kLinearSyncBytes - kLinearCountBytes;
     const int jt = (direct && rank > 0 && lora_prod && prod_fits) ? int((rank + 15) / 16) * fused_splits : 0;
-    int best = 0, best_jt = 0;
-    int64_t best_cost = 0;
-    for (int pass = jt > 0 ? 0 : 1; pass < 2 && best == 0; ++pass) {
-      const int pj = pass == 0 ? jt : 0;
+    // LDS of the in-launch down-projection: the wait flag
+    const size_t job_lds = jt > 0 ? 16 : 0;
+    // best tile count per workgroup, with pj producer workgroups that need
+    // compute units of their own (pj > 0) or none
+    auto search = [&](int pj, int64_t& best_cost) {
+      int bts = 0;
       for (int TS = 1; TS <= kGemvMaxTS && TS <= ts_cap; ++TS) {
         const int U = xslice ? (TS * nseg + kGemvWaves - 1) / kGemvWaves : (TS + R - 1) / R;
         if (U != 1 && U != 2 && U != 4) continue;
-        if (gemv_lds_bytes(TS, nseg, int(M), gather, xslice, direct && rank > 0) + (pj > 0 ? 16 : 0) >
-            size_t(kGemvLdsBudget))
+        if (gemv_lds_bytes(TS, nseg, int(M), gather, xslice, direct && rank > 0) + job_lds > size_t(kGemvLdsBudget))
           continue;
         // tiles a compute unit works through one after another
         const int64_t grid = (tiles + TS - 1) / TS;
         if (pj > 0 && grid * S + pj > ncu) continue;
         const int64_t cost = ((grid * S + ncu - 1) / ncu) * TS;
-        if (best == 0 || cost <= best_cost) {
-          best = TS;
+        if (bts == 0 || cost <= best_cost) {
+          bts = TS;
           best_cost = cost;
-          best_jt = pj;
         }
       }
+      return bts;
+    };
+    // The down-projection jobs run in producer workgroups of their own when
+    // the tile workgroups leave compute units free for them at most at twice
+    // the cost in tiles per compute unit (measured on the Llama-3-8B q/o
+    // shape: two tiles per workgroup with producers beat one tile per
+    // workgroup with the jobs merged); otherwise the first jt tile workgroups
+    // run them before their units (merged), and without the in-launch
+    // handshake as a launch of their own.
+    int64_t cost_prod = 0, cost_free = 0;
+    const int ts_prod = jt > 0 ? search(jt, cost_prod) : 0;
+    const int ts_free = search(0, cost_free);
+    int best = 0;
+    p.jt = p.jm = 0;
+    if (ts_prod > 0 && (ts_free == 0 || cost_prod <= 2 * cost_free)) {
+      best = ts_prod;
+      p.jt = jt;
+    } else if (ts_free > 0) {
+      best = ts_free;
+      if (jt > 0 && (tiles + best - 1) / best >= jt) p.jm = jt;
     }
     if (best == 0) continue;
-    p.jt = best_jt;
-    if (p.jt > 0) p.u_splits = fused_splits;
+    if (p.jt > 0 || p.jm > 0) p.u_splits = fused_splits;
     p.S = S;
     p.nseg = nseg;
     p.TS = best;
@@ -1000,8 +1037,8 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     break;
   }
   p.lds_bytes = gemv_lds_bytes(p.TS, p.nseg, int(M), gather, p.xslice, p.direct && rank > 0);
-  if (p.jt > 0) {
-    // the wait flag after RND(u); the producers' 16 KiB wave partials
+  if (p.jt > 0 || p.jm > 0) {
+    // the wait flag after RND(u); the jobs' 16 KiB wave partials
     p.lds_bytes += 16;
     if (p.lds_bytes < size_t(kGemvWaves) * 256 * 4) p.lds_bytes = size_t(kGemvWaves) * 256 * 4;
   }
@@ -1009,9 +1046,10 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
   // count and partials, left zero by every launch), the split-K partials,
   // the partials of lora_u_kernel
   const size_t parts = p.direct ? 0 : size_t(p.S) * M * N * 4;
-  const size_t uparts = (rank > 0 && p.jt == 0) ? size_t(p.u_splits) * M * rank * 4 : 0;
+  const bool in_launch = p.jt > 0 || p.jm > 0;
+  const size_t uparts = (rank > 0 && !in_launch) ? size_t(p.u_splits) * M * rank * 4 : 0;
   p.u_offset = kLinearSyncBytes + ((parts + 255) & ~size_t(255));
-  p.ws_bytes = p.jt > 0 ? kLinearSyncBytes : (parts + uparts > 0 ? p.u_offset + uparts : 0);
+  p.ws_bytes = in_launch ? kLinearSyncBytes : (parts + uparts > 0 ? p.u_offset + uparts : 0);
   return p;
 }
 
@@ -1091,6 +1129,7 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.xvec = gemv_xvec(L);
   a.bvec_log2 = gemv_bvec_log2(L);
   a.jt = p.jt;
+  a.jm = p.jm;
   a.spin_limit = gemv_spin_limit.load(std::memory_order_relaxed);
   a.done = static_cast<uint32_t*>(sync);
   a.ubits = reinterpret_cast<uint32_t*>(static_cast<char*>(sync) + kLinearCountBytes);
@@ -1220,7 +1259,7 @@ int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   float* up = L.rank > 0 ? reinterpret_cast<float*>(wsb + p.u_offset) : nullptr;
   int st;
   const LinearEpi e = make_epi(L, up, p.u_splits);
-  if (L.rank > 0 && p.jt == 0) {
+  if (L.rank > 0 && p.jt == 0 && p.jm == 0) {
     if (lora_prod) {
       st = L.x_dtype == RQ_DTYPE_BF16 ? launch_lora_u_jobs<RQ_DTYPE_BF16>(L, e, up, stream)
                                       : launch_lora_u_jobs<RQ_DTYPE_F16>(L, e, up, stream);

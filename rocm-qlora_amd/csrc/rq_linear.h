@@ -63,7 +63,8 @@ struct LinearEpi {
 
 struct GemvPlan {
   int S, TS, U, nseg, grid, u_splits;
-  int jt;  // LoRA down-projection workgroups inside the launch (0: lora_u_kernel)
+  int jt;  // LoRA down-projection workgroups inside the launch (0: none)
+  int jm;  // ... or down-projection jobs merged into the first jm tile workgroups
   bool direct, xslice;
   size_t lds_bytes, ws_bytes, u_offset;
   uint8_t unit_t[16][4], unit_s[16][4];  // (tile slot, segment) of unit u of wave w; 0xFF: none

@@ -109,3 +109,45 @@ def test_fp8_linear_is_decode_then_matmul_with_both_scales():
     assert torch.allclose(y.double(), (core.to(torch.bfloat16) + bias).double(), rtol=0, atol=0)
     # and close to the unquantized product (e4m3 keeps ~3 bits)
     assert torch.allclose(y.float(), (x.float() @ w.float().T + bias.float()), rtol=0.15, atol=0.15)
+
+
+def test_lora_grads_with_dropout_mask():
+    """The oracle's LoRA dropout (lora_layer.py:67, drop(x) = x * mask / (1 - p)):
+    in float64 the gradients match central differences of the loss with the
+    dropped input; an all-kept mask at p = 0 gives the no-dropout results bit
+    for bit; in bf16 the dropped input is x * scale rounded once."""
+    N, K, r, M, s, p = 6, 8, 3, 2, 0.5, 0.25
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(M, K, generator=g, dtype=torch.float64)
+    w = torch.randn(N, K, generator=g, dtype=torch.float64) * 0.3
+    bias = torch.randn(N, generator=g, dtype=torch.float64)
+    a = torch.randn(r, K, generator=g, dtype=torch.float64)
+    b = torch.randn(N, r, generator=g, dtype=torch.float64)
+    dy = torch.randn(M, N, generator=g, dtype=torch.float64)
+    mask = torch.rand(M, K, generator=g) > p
+    y, dx, da, db = R.lora_linear_grads(x, w.reshape(-1), bias, a, b, s, dy, dropout_mask=mask, dropout_p=p)
+    keep = mask.to(torch.float64) / (1 - p)
+
+    def fwd(xx, aa, bb):
+        return xx @ w.T + bias + s * ((xx * keep) @ aa.T) @ bb.T
+
+    assert torch.allclose(y, fwd(x, a, b), rtol=1e-12, atol=1e-12)
+    h = 1e-6
+    for t, grad, which in ((x, dx, 0), (a, da, 1), (b, db, 2)):
+        num = torch.zeros_like(t)
+        for i in range(t.numel()):
+            tp, tm = t.clone(), t.clone()
+            tp.view(-1)[i] += h
+            tm.view(-1)[i] -= h
+            ap, am = [x, a, b], [x, a, b]
+            ap[which], am[which] = tp, tm
+            num.view(-1)[i] = (float((dy * fwd(*ap)).sum()) - float((dy * fwd(*am)).sum())) / (2 * h)
+        assert torch.allclose(grad, num, rtol=1e-6, atol=1e-6), which
+    ones = torch.ones(M, K, dtype=torch.bool)
+    got = R.lora_linear_grads(x, w.reshape(-1), bias, a, b, s, dy, dropout_mask=ones, dropout_p=0.0)
+    want = R.lora_linear_grads(x, w.reshape(-1), bias, a, b, s, dy)
+    assert all(torch.equal(u, v) for u, v in zip(got, want))
+    xb = torch.randn(64, generator=g).to(torch.bfloat16)
+    mk = torch.rand(64, generator=g) > 0.1
+    dropped = R._DropoutWithMask.apply(xb, mk, 1.0 / 0.9)
+    assert torch.equal(dropped, (xb.float() * mk.float() * (1.0 / 0.9)).to(torch.bfloat16))
