@@ -141,6 +141,10 @@ int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, int64_t N, i
  * launch_int4_dequant_matmul (hip_kernels/int4_matmul.hip:413-437):
  *   y[M, N] = RND(RND(x W^T + RND(bias)) + RND(RND(RND(xl A^T) RND(B)^T) * scaling))
  * with RND the rounding to x_dtype (bf16 or fp16) and W = T[code] * scale.
+ * x_dtype fp32 computes everything in fp32 as the reference's fp32 path does
+ * (W = T[code] * scale rounded to fp32, no other roundings; x rows, A and the
+ * packed weights 16-byte aligned, rank <= 64); its workspace holds the LoRA
+ * operand u and needs no zeroing.
  *   x: [M, K] rows of stride ldx; w_packed: flat N*K/2 bytes; block_size a
  *   power of two >= 64 dividing K; absmax: N*K/block_size scales of
  *   absmax_dtype, or -- when c2 != NULL -- the c2_scales of the double

@@ -1187,11 +1187,14 @@ static int launch_splitk_epilogue(const LinearArgs& L, const GemvPlan& p, const 
 }
 
 int validate_linear(const LinearArgs& L) {
-  if (L.x_dtype != RQ_DTYPE_BF16 && L.x_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
+  if (!valid_float_dtype(L.x_dtype)) return RQ_ERR_BAD_DTYPE;
   if (!valid_float_dtype(L.absmax_dtype)) return RQ_ERR_BAD_DTYPE;
   if (L.bias && !valid_float_dtype(L.bias_dtype)) return RQ_ERR_BAD_DTYPE;
-  // LoRA A/B: fp32 (the trainable parameters) or the activation dtype
-  if (L.rank > 0 && L.lora_dtype != RQ_DTYPE_F32 && L.lora_dtype != L.x_dtype) return RQ_ERR_BAD_DTYPE;
+  // LoRA A/B: fp32 (the trainable parameters) or the activation dtype; with
+  // fp32 activations any float dtype (widened exactly, as A.to(x.dtype) does)
+  if (L.rank > 0 && L.lora_dtype != RQ_DTYPE_F32 && L.lora_dtype != L.x_dtype &&
+      !(L.x_dtype == RQ_DTYPE_F32 && valid_float_dtype(L.lora_dtype)))
+    return RQ_ERR_BAD_DTYPE;
   if (L.c2 && L.c2_format != RQ_C2_FP8_E4M3FNUZ && L.c2_format != RQ_C2_INT8) return RQ_ERR_BAD_DTYPE;
   if (L.M < 0 || L.N < 1 || L.K < 64 || L.K % 64 != 0) return RQ_ERR_BAD_SHAPE;
   if (L.block_size < 64 || L.block_size % 64 != 0 || L.K % L.block_size != 0) return RQ_ERR_BAD_SHAPE;
@@ -1204,7 +1207,7 @@ int validate_linear(const LinearArgs& L) {
   if (!L.x || !L.w_packed || !L.absmax || !L.y) return RQ_ERR_NULL_POINTER;
   if (L.rank > 0 && (!L.lora_x || !L.lora_a || !L.lora_b)) return RQ_ERR_NULL_POINTER;
   if (!aligned(L.w_packed, 8)) return RQ_ERR_BAD_ALIGNMENT;
-  if (!aligned(L.x, 2) || !aligned(L.y, 2)) return RQ_ERR_BAD_ALIGNMENT;
+  if (!aligned(L.x, dtype_size(L.x_dtype)) || !aligned(L.y, dtype_size(L.x_dtype))) return RQ_ERR_BAD_ALIGNMENT;
   return RQ_OK;
 }
 
@@ -1307,11 +1310,16 @@ extern "C" uint32_t rq_set_gemv_spin_limit(uint32_t polls) { return set_gemv_spi
 extern "C" int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, int64_t N, int64_t rank,
                                             int64_t* bytes) {
   if (!bytes) return RQ_ERR_NULL_POINTER;
-  if (x_dtype != RQ_DTYPE_BF16 && x_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
+  if (!valid_float_dtype(x_dtype)) return RQ_ERR_BAD_DTYPE;
   if (M < 0 || N < 1 || K < 64 || K % 64 || rank < 0 || rank > 256) return RQ_ERR_BAD_SHAPE;
   size_t b = 0;
   LinearArgs L{};
   L.x_dtype = x_dtype; L.M = M; L.K = K; L.N = N; L.rank = rank;
+  if (x_dtype == RQ_DTYPE_F32) {
+    f32_linear_workspace(L, &b);
+    *bytes = int64_t(b);
+    return RQ_OK;
+  }
   int st = M <= kGemvMaxM ? gemv_workspace(L, &b) : gemm_workspace(L, &b);
   if (M > kGemvMaxM && b > 0) b += kLinearSyncBytes;
   *bytes = int64_t(b);
@@ -1331,6 +1339,7 @@ extern "C" int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, i
   int st = validate_linear(L);
   if (st != RQ_OK || M == 0) return st;
   if (workspace_bytes < 0) return RQ_ERR_BAD_SHAPE;
+  if (x_dtype == RQ_DTYPE_F32) return run_nf4_linear_f32(L, workspace, size_t(workspace_bytes), stream);
   if (M <= kGemvMaxM) return run_nf4_gemv(L, workspace, size_t(workspace_bytes), stream);
   // the GEMM's workspace follows the synchronization area, whose zeroed
   // words past the count block serve as its K splits' tile counters

@@ -1,0 +1,245 @@
+// NF4 quantized linear with fp32 activations (+ bias, + LoRA) for gfx950, on
+// the fp32 matrix cores (v_mfma_f32_16x16x4_f32).
+//
+// For fp32 inputs the reference computes everything in fp32
+// (quant_linear.py:189-197: W = dequantize_int4(...) is fp32 and .to(x.dtype)
+// keeps it; F.linear(x, W, bias); lora_layer.py:67: (x @ A^T) @ B^T * s with
+// A, B in fp32):
+//   base[m,n] = sum_k x[m,k] * W[n,k] + bias[n],  W = T[code] * scale (fp32)
+//   u[m,j]    = sum_k x[m,k] * A[j,k]
+//   y[m,n]    = base[m,n] + (sum_j u[m,j] * B[n,j]) * scaling
+// The weight operand is T[code] * scale rounded once to fp32 -- the value
+// dequantize_int4 produces -- and every product and sum is an fp32 MFMA
+// operation, so the result differs from the reference's only in the order of
+// the fp32 sums.
+//
+// Layout of one 16 x 16 x 4 step (checked by the parity tests): lane l holds
+// A[l % 16][l / 16] (activation row m, k group q = l / 16), B[l / 16][l % 16]
+// (k group q, weight row n), and D[4 (l / 16) + r][l % 16] in register r.
+// Within a chunk of 128 k, lane group q owns k = 128 i + 32 q + 8 d + e
+// (d = 0..3 code dword, e = 0..7 code in the dword): each lane reads one 16-byte
+// piece of packed codes (32 codes of its row) and 32 activations of its row,
+// and step (d, e) of the 32 steps multiplies the k set {32 q + 8 d + e}.
+#include "rq_launch.h"
+#include "rq_linear.h"
+#include "rq_linear_dev.h"
+
+namespace rq {
+
+constexpr int kF32Threads = 256;  // four waves; wave w takes chunks w, w + 4, ...
+constexpr int kF32Waves = kF32Threads / 64;
+constexpr int kF32ChunkK = 128;
+
+__device__ __forceinline__ f32x4 mfma16x16x4_f32(float a, float b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// 32 consecutive values of a row (fp32 or 16-bit, widened exactly to fp32),
+// zeros where the row or the k range is past the end.
+template <int DT>
+__device__ __forceinline__ void load32_f32(const void* p, int64_t off, bool live, float (&v)[32]) {
+  if (!live) {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = 0.0f;
+    return;
+  }
+  if constexpr (DT == RQ_DTYPE_F32) {
+    const f32x4* s = reinterpret_cast<const f32x4*>(static_cast<const float*>(p) + off);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const f32x4 t = s[i];
+      v[4 * i] = t.x; v[4 * i + 1] = t.y; v[4 * i + 2] = t.z; v[4 * i + 3] = t.w;
+    }
+  } else {
+    const u32x4* s = reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(p) + off);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 t = s[i];
+      const uint32_t w[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        v[8 * i + 2 * h] = DT == RQ_DTYPE_BF16 ? bf16_to_f32(uint16_t(w[h])) : f16_to_f32(uint16_t(w[h]));
+        v[8 * i + 2 * h + 1] = DT == RQ_DTYPE_BF16 ? bf16_to_f32(uint16_t(w[h] >> 16))
+                                                   : f16_to_f32(uint16_t(w[h] >> 16));
+      }
+    }
+  }
+}
+
+// y rows [m0, m0 + 16) (fewer when M is shorter) of one 16-row weight tile.
+// u: RND-free fp32 LoRA operand [M][rank] (rank 0: none).
+template <class Scale>
+__global__ __launch_bounds__(kF32Threads) void nf4_gemv_f32_kernel(const float* __restrict__ x, int64_t ldx,
+                                                                   int64_t M, int64_t K,
+                                                                   const uint8_t* __restrict__ packed, int64_t N,
+                                                                   int bs_log2, Scale scale, LinearEpi e) {
+  __shared__ float tab[16];
+  __shared__ float red[kF32Waves][16][16];
+  __shared__ float us[16][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i16 = lane & 15, q = lane >> 4;
+  const int64_t n0 = int64_t(blockIdx.x) * 16;
+  if (tid < 16) tab[tid] = u2f(kNF4Bits[tid]);
+  __syncthreads();
+  const int64_t n = n0 + i16;               // weight row of this lane's B operands
+  const bool nlive = n < N;
+  const int64_t row_bytes = K / 2;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int64_t nchunks = (K + kF32ChunkK - 1) / kF32ChunkK;
+  for (int64_t c = wave; c < nchunks; c += kF32Waves) {
+    const int64_t k0 = c * kF32ChunkK + 32 * q;  // this lane group's 32 k
+    const bool klive = k0 < K;
+    u32x4 codes = u32x4{0u, 0u, 0u, 0u};
+    float s = 0.0f;
+    if (nlive && klive) {
+      codes = *reinterpret_cast<const u32x4*>(packed + n * row_bytes + k0 / 2);
+      s = scale((n * K + k0) >> bs_log2);
+    }
+    float xv[32];
+    load32_f32<RQ_DTYPE_F32>(x, i16 * ldx + k0, i16 < M && klive, xv);
+    const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+#pragma unroll
+      for (int ee = 0; ee < 8; ++ee) {
+        const float wv = __fmul_rn(tab[(w[d] >> (4 * ee)) & 15u], s);
+        acc = mfma16x16x4_f32(xv[8 * d + ee], wv, acc);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) red[wave][4 * q + r][i16] = acc[r];
+  // the LoRA operand rows of this launch's activation rows
+  const int rank = e.rank;
+  for (int idx = tid; idx < 16 * rank; idx += kF32Threads) {
+    const int m = idx / rank, j = idx - m * rank;
+    us[m][j] = m < M ? e.u[m * rank + j] : 0.0f;
+  }
+  __syncthreads();
+  // one thread per output (row m = tid / 16, column n0 + tid % 16)
+  const int m = tid >> 4, nn = tid & 15;
+  const int64_t on = n0 + nn;
+  if (m >= M || on >= N) return;
+  float v = 0.0f;
+#pragma unroll
+  for (int w2 = 0; w2 < kF32Waves; ++w2) v = __fadd_rn(v, red[w2][m][nn]);
+  if (e.bias) v = __fadd_rn(v, load_as_f32(e.bias, on, e.bias_dt));
+  if (rank > 0) {
+    float l = 0.0f;
+    for (int j = 0; j < rank; ++j) l = __fmaf_rn(us[m][j], load_as_f32(e.lora_b, on * e.ld_lora_b + j, e.lora_dt), l);
+    v = __fadd_rn(v, __fmul_rn(l, e.scaling));
+  }
+  static_cast<float*>(e.y)[m * e.ldy + on] = v;
+}
+
+// u[m, j] = sum_k xl[m, k] * A[j, k] in fp32 for m < M <= 16: workgroup j0 / 16
+// takes ranks [j0, j0 + 16); its four waves take chunks of 128 k in turn and
+// their partial products are summed in wave order.
+template <int ADT>
+__global__ __launch_bounds__(kF32Threads) void lora_u_f32_kernel(const float* __restrict__ xl, int64_t ldxl,
+                                                                 int64_t M, int64_t K, const void* __restrict__ A,
+                                                                 int rank, float* __restrict__ u) {
+  __shared__ float red[kF32Waves][16][16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int i16 = lane & 15, q = lane >> 4;
+  const int j = int(blockIdx.x) * 16 + i16;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  const int64_t nchunks = (K + kF32ChunkK - 1) / kF32ChunkK;
+  for (int64_t c = wave; c < nchunks; c += kF32Waves) {
+    const int64_t k0 = c * kF32ChunkK + 32 * q;
+    float xv[32], av[32];
+    load32_f32<RQ_DTYPE_F32>(xl, i16 * ldxl + k0, i16 < M && k0 < K, xv);
+    load32_f32<ADT>(A, int64_t(j) * K + k0, j < rank && k0 < K, av);
+#pragma unroll
+    for (int t = 0; t < 32; ++t) acc = mfma16x16x4_f32(xv[t], av[t], acc);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) red[wave][4 * q + r][i16] = acc[r];
+  __syncthreads();
+  const int m = tid >> 4, jj = int(blockIdx.x) * 16 + (tid & 15);
+  if (m >= M || jj >= rank) return;
+  float v = 0.0f;
+#pragma unroll
+  for (int w2 = 0; w2 < kF32Waves; ++w2) v = __fadd_rn(v, red[w2][m][tid & 15]);
+  u[m * rank + jj] = v;
+}
+
+template <class Scale>
+static int launch_f32_gemv(const LinearArgs& L, int64_t m0, int64_t rows, Scale scale, const LinearEpi& e,
+                           hipStream_t stream) {
+  const float* x = static_cast<const float*>(L.x) + m0 * L.ldx;
+  LinearEpi ec = e;
+  ec.y = static_cast<float*>(L.y) + m0 * L.ldy;
+  const unsigned grid = unsigned((L.N + 15) / 16);
+  nf4_gemv_f32_kernel<Scale><<<grid, kF32Threads, 0, stream>>>(x, L.ldx, rows, L.K, L.w_packed, L.N,
+                                                               pow2_shift(L.block_size), scale, ec);
+  return rq_check_launch();
+}
+
+template <class Scale>
+static int run_f32_rows(const LinearArgs& L, int64_t m0, int64_t rows, Scale scale, float* u, hipStream_t stream) {
+  LinearEpi e = make_epi(L, u, 1);
+  if (L.rank > 0) {
+    const float* xl = static_cast<const float*>(L.lora_x) + m0 * L.ld_lora_x;
+    const unsigned grid = unsigned((L.rank + 15) / 16);
+    switch (L.lora_dtype) {
+      case RQ_DTYPE_F32:
+        lora_u_f32_kernel<RQ_DTYPE_F32><<<grid, kF32Threads, 0, stream>>>(xl, L.ld_lora_x, rows, L.K, L.lora_a,
+                                                                          int(L.rank), u);
+        break;
+      case RQ_DTYPE_BF16:
+        lora_u_f32_kernel<RQ_DTYPE_BF16><<<grid, kF32Threads, 0, stream>>>(xl, L.ld_lora_x, rows, L.K, L.lora_a,
+                                                                           int(L.rank), u);
+        break;
+      default:
+        lora_u_f32_kernel<RQ_DTYPE_F16><<<grid, kF32Threads, 0, stream>>>(xl, L.ld_lora_x, rows, L.K, L.lora_a,
+                                                                          int(L.rank), u);
+        break;
+    }
+    if (int st = rq_check_launch(); st != RQ_OK) return st;
+  }
+  return launch_f32_gemv(L, m0, rows, scale, e, stream);
+}
+
+template <class Scale>
+static int run_f32_all(const LinearArgs& L, Scale scale, float* u, hipStream_t stream) {
+  // 16 activation rows per launch pair (the MFMA's row count); larger M runs
+  // as consecutive row blocks
+  for (int64_t m0 = 0; m0 < L.M; m0 += 16) {
+    const int64_t rows = L.M - m0 < 16 ? L.M - m0 : 16;
+    if (int st = run_f32_rows(L, m0, rows, scale, u, stream); st != RQ_OK) return st;
+  }
+  return RQ_OK;
+}
+
+int f32_linear_workspace(const LinearArgs& L, size_t* bytes) {
+  *bytes = L.rank > 0 ? size_t(16) * size_t(L.rank) * 4 : 0;
+  return RQ_OK;
+}
+
+int run_nf4_linear_f32(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  size_t need = 0;
+  f32_linear_workspace(L, &need);
+  if (need > 0 && (!workspace || ws_bytes < need)) return RQ_ERR_WORKSPACE;
+  if (L.rank > 64) return RQ_ERR_UNSUPPORTED;  // the epilogue stages 64 ranks per activation row
+  // 16-byte loads of activations, codes and (fp32) LoRA A rows
+  if (!aligned(L.x, 16) || L.ldx % 4 != 0 || !aligned(L.w_packed, 16) || L.K % 64 != 0) return RQ_ERR_BAD_ALIGNMENT;
+  if (L.rank > 0 && (!aligned(L.lora_x, 16) || L.ld_lora_x % 4 != 0 || !aligned(L.lora_a, 16)))
+    return RQ_ERR_BAD_ALIGNMENT;
+  float* u = static_cast<float*>(workspace);
+  if (L.c2) {
+    const int sh = pow2_shift(L.block2);
+    switch (L.absmax_dtype) {
+      case RQ_DTYPE_F32: return run_f32_all(L, ScaleDQ<RQ_DTYPE_F32>{L.c2, L.absmax, L.c2_format, sh, L.block2}, u, stream);
+      case RQ_DTYPE_BF16: return run_f32_all(L, ScaleDQ<RQ_DTYPE_BF16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, u, stream);
+      default: return run_f32_all(L, ScaleDQ<RQ_DTYPE_F16>{L.c2, L.absmax, L.c2_format, sh, L.block2}, u, stream);
+    }
+  }
+  switch (L.absmax_dtype) {
+    case RQ_DTYPE_F32: return run_f32_all(L, ScaleAbsmax<RQ_DTYPE_F32>{L.absmax}, u, stream);
+    case RQ_DTYPE_BF16: return run_f32_all(L, ScaleAbsmax<RQ_DTYPE_BF16>{L.absmax}, u, stream);
+    default: return run_f32_all(L, ScaleAbsmax<RQ_DTYPE_F16>{L.absmax}, u, stream);
+  }
+}
+
+}  // namespace rq

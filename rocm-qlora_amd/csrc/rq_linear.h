@@ -82,6 +82,9 @@ int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream);
 int gemv_workspace(const LinearArgs& L, size_t* bytes);
 int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream);
 int gemm_workspace(const LinearArgs& L, size_t* bytes);
+// fp32 activations (any M): the fp32-MFMA GEMV over 16-row blocks
+int f32_linear_workspace(const LinearArgs& L, size_t* bytes);
+int run_nf4_linear_f32(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream);
 // tile_cnt: n_cnt zeroed counters the GEMM's K splits use (and leave zero);
 // without them the GEMM runs unsplit.
 int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t* tile_cnt, size_t n_cnt,

@@ -24,7 +24,10 @@ import torch.nn.functional as F
 from rocm_qlora import ops
 from rocm_qlora import _native as nat
 
-_KERNEL_DTYPES = (torch.bfloat16, torch.float16)
+# activation dtypes of the fused forward kernels (fp32: the fp32-MFMA path)
+_KERNEL_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
+# ... and of the NF4 dX kernel
+_DX_DTYPES = (torch.bfloat16, torch.float16)
 
 
 def _pow2(v: int) -> bool:
@@ -55,8 +58,8 @@ class NF4Weight:
         return dtype in _KERNEL_DTYPES and self._shape_ok()
 
     def dx_ok(self, dtype: torch.dtype) -> bool:
-        """The NF4 dX kernel takes it (also needs N % 64 == 0)."""
-        return self.kernel_ok(dtype) and self.N % 64 == 0
+        """The NF4 dX kernel takes it (bf16/fp16, N % 64 == 0)."""
+        return dtype in _DX_DTYPES and self.kernel_ok(dtype) and self.N % 64 == 0
 
     def dq_kwargs(self) -> dict:
         if self.c2 is None:
@@ -91,7 +94,7 @@ class Int8Weight:
 
     def kernel_ok(self, dtype: torch.dtype) -> bool:
         b = self.block_size
-        return (dtype in _KERNEL_DTYPES and self.K % 64 == 0
+        return (dtype in _DX_DTYPES and self.K % 64 == 0
                 and (b == 0 or (b >= 64 and _pow2(b) and self.K % b == 0)))
 
     def dense(self, dtype: torch.dtype) -> torch.Tensor:

@@ -101,12 +101,11 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
                scaling: float = 0.0, lora_x: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y = x . dequant(W)^T + bias (+ LoRA) for an NF4 weight stored flat
     (quant_linear.py:182-197 and lora_layer.py:60-70 in one kernel launch
-    sequence).  x: [..., K] bf16/fp16 on the GPU; output has x's dtype."""
+    sequence).  x: [..., K] bf16/fp16 (bf16/fp16 MFMA kernels) or fp32 (the
+    fp32-MFMA kernel, everything in fp32 as the reference computes it) on the
+    GPU; output has x's dtype."""
     K = x.shape[-1]
     N = int(out_features)
-    if x.dtype == torch.float32:
-        return _nf4_linear_fp32(x, weight_quant, weight_scales, N, block_size, bias, c2, c2_scales,
-                                blocksize_2, use_fp8_c2, lora_a, lora_b, scaling, lora_x)
     xcode = nat.dtype_code(x.dtype)
     dq = c2 is not None
     scales = c2_scales if dq else weight_scales
@@ -131,7 +130,7 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
     with on(dev):
         x2, ldx = _rows(x, K)
         M = x2.shape[0]
-        if M > GEMV_MAX_M:  # the MFMA GEMM streams x in 16-byte pieces
+        if M > GEMV_MAX_M or x.dtype == torch.float32:  # 16-byte activation loads
             x2, ldx = _aligned_rows(x2, K)
         y = torch.empty((M, N), dtype=x.dtype, device=dev)
         if M == 0:
@@ -158,8 +157,10 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
                 lb, ldb = lb.contiguous(), rank
             lcode = nat.dtype_code(la.dtype)
             if lora_x is not None:
-                # the GEMM's LoRA operand kernel loads 16 bytes at a time
-                xl, ldxl = (_aligned_rows if M > GEMV_MAX_M else _rows)(lora_x.to(x.dtype), K)
+                # the GEMM's and the fp32 path's LoRA operand kernels load 16
+                # bytes at a time
+                wide = M > GEMV_MAX_M or x.dtype == torch.float32
+                xl, ldxl = (_aligned_rows if wide else _rows)(lora_x.to(x.dtype), K)
         b = bias.contiguous() if bias is not None else None
         ws = _workspace(x.dtype, M, K, N, rank, dev)
         codes = c2.reshape(-1).view(torch.uint8).contiguous() if dq else None
@@ -172,27 +173,6 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
                  y.data_ptr(), N, nat.ptr(ws), ws.numel() if ws is not None else 0,
                  nat.stream_handle(dev))
     return y.reshape(*lead, N)
-
-
-def _nf4_linear_fp32(x, weight_quant, weight_scales, N, block_size, bias, c2, c2_scales, blocksize_2,
-                     use_fp8_c2, lora_a, lora_b, scaling, lora_x):
-    """fp32 activations: the weight is dequantized to fp32 by the HIP codec
-    kernel and multiplied by the library fp32 GEMM (quant_linear.py:189-197
-    computes in fp32 for fp32 inputs; the MFMA kernels take bf16/fp16)."""
-    from rocm_qlora.quantization.quant_ops import nf4_dequantize_to
-    from rocm_qlora.quantization.double_quant import dq_dequantize_to
-    K = x.shape[-1]
-    nat.require_gpu(x, weight_quant)
-    if c2 is not None:
-        w = dq_dequantize_to(weight_quant, c2, c2_scales, block_size, blocksize_2, use_fp8_c2,
-                             torch.float32, N * K)
-    else:
-        w = nf4_dequantize_to(weight_quant, weight_scales, block_size, torch.float32, N * K)
-    y = F.linear(x, w.view(N, K), bias.to(x.dtype) if bias is not None else None)
-    if lora_a is not None and lora_b is not None and lora_a.shape[0] > 0:
-        xl = x if lora_x is None else lora_x
-        y = y + (xl @ lora_a.to(x.dtype).T @ lora_b.to(x.dtype).T * scaling)
-    return y
 
 
 def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optional[torch.Tensor],
@@ -270,7 +250,7 @@ def _aligned_rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
     """2-D [rows, K] view with a 16-byte aligned base and a row stride that
     keeps every row 16-byte aligned (the MFMA kernels load 16 bytes at a time)."""
     t2, ld = _rows(t, K)
-    if t2.data_ptr() % 16 or ld % 8:
+    if t2.data_ptr() % 16 or (ld * t2.element_size()) % 16:
         t2 = t2.contiguous().clone()
         ld = K
     return t2, ld
