@@ -124,7 +124,8 @@ int rq_int8_dequantize(const int8_t* q, const void* scales, int scales_dtype,
  * ------------------------------------------------------------------------ */
 
 /* Bytes of device workspace rq_nf4_linear needs for these sizes (0 when
- * none).  The caller allocates it (256-byte aligned) and passes it in.  Its
+ * none).  The caller allocates it (256-byte aligned) and passes it in (the
+ * MFMA GEMM, M > 16, also runs with less: then without K splits).  Its
  * first RQ_LINEAR_SYNC_BYTES are a synchronization area of the decode GEMV
  * (a count and the LoRA down-projection's partials, exchanged between the
  * workgroups of one launch): it must be zero before the workspace's first
@@ -144,7 +145,7 @@ int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, int64_t N, i
  * x_dtype fp32 computes everything in fp32 as the reference's fp32 path does
  * (W = T[code] * scale rounded to fp32, no other roundings; x rows, A and the
  * packed weights 16-byte aligned, rank <= 64); its workspace holds the LoRA
- * operand u and needs no zeroing.
+ * operand u after the synchronization area.
  *   x: [M, K] rows of stride ldx; w_packed: flat N*K/2 bytes; block_size a
  *   power of two >= 64 dividing K; absmax: N*K/block_size scales of
  *   absmax_dtype, or -- when c2 != NULL -- the c2_scales of the double

@@ -174,14 +174,19 @@ int gemm_workspace(const LinearArgs& L, size_t* bytes) {
   return RQ_OK;
 }
 
+size_t gemm_min_workspace(const LinearArgs& L) {
+  return plan_gemm(L.M, L.N, L.K, L.rank, device_cus(), false).ws_bytes;
+}
+
 int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t* tile_cnt, size_t n_cnt,
                  hipStream_t stream) {
   // the activation operands are loaded 16 bytes at a time
   if (!aligned(L.x, 16) || L.ldx % 8 != 0) return RQ_ERR_BAD_ALIGNMENT;
   if (!offsets_fit(L.M, L.ldx, L.N, L.K)) return RQ_ERR_UNSUPPORTED;
-  // K splits need the zeroed tile counts
+  // K splits need the zeroed tile counts and room for their partial tiles;
+  // without them the GEMM runs unsplit
   GemmPlan p = plan_gemm(L.M, L.N, L.K, L.rank, device_cus(), true);
-  if (p.splits > 1 && (!tile_cnt || size_t(8) * p.lt > n_cnt))
+  if (p.splits > 1 && (!tile_cnt || size_t(8) * p.lt > n_cnt || !workspace || ws_bytes < p.ws_bytes))
     p = plan_gemm(L.M, L.N, L.K, L.rank, device_cus(), false);
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
   if (workspace && !aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;

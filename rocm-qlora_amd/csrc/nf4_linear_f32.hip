@@ -212,8 +212,10 @@ static int run_f32_all(const LinearArgs& L, Scale scale, float* u, hipStream_t s
   return RQ_OK;
 }
 
+// The LoRA operand u [16][rank] lies after the workspace's synchronization
+// area (which every rq_nf4_linear call leaves zero for the decode GEMV).
 int f32_linear_workspace(const LinearArgs& L, size_t* bytes) {
-  *bytes = L.rank > 0 ? size_t(16) * size_t(L.rank) * 4 : 0;
+  *bytes = L.rank > 0 ? kLinearSyncBytes + size_t(16) * size_t(L.rank) * 4 : 0;
   return RQ_OK;
 }
 
@@ -226,7 +228,7 @@ int run_nf4_linear_f32(const LinearArgs& L, void* workspace, size_t ws_bytes, hi
   if (!aligned(L.x, 16) || L.ldx % 4 != 0 || !aligned(L.w_packed, 16) || L.K % 64 != 0) return RQ_ERR_BAD_ALIGNMENT;
   if (L.rank > 0 && (!aligned(L.lora_x, 16) || L.ld_lora_x % 4 != 0 || !aligned(L.lora_a, 16)))
     return RQ_ERR_BAD_ALIGNMENT;
-  float* u = static_cast<float*>(workspace);
+  float* u = L.rank > 0 ? reinterpret_cast<float*>(static_cast<char*>(workspace) + kLinearSyncBytes) : nullptr;
   if (L.c2) {
     const int sh = pow2_shift(L.block2);
     switch (L.absmax_dtype) {

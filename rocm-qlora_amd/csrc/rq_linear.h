@@ -82,6 +82,8 @@ int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream);
 int gemv_workspace(const LinearArgs& L, size_t* bytes);
 int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream);
 int gemm_workspace(const LinearArgs& L, size_t* bytes);
+// the GEMM's workspace without K splits (the smallest it runs with)
+size_t gemm_min_workspace(const LinearArgs& L);
 // fp32 activations (any M): the fp32-MFMA GEMV over 16-row blocks
 int f32_linear_workspace(const LinearArgs& L, size_t* bytes);
 int run_nf4_linear_f32(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStream_t stream);

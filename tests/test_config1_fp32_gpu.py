@@ -102,3 +102,26 @@ def test_fp32_strided_activations_and_lora_input(dev):
                                   None, N, K)
     ref = base + (xl @ a16.cpu().float().T @ b16.cpu().float().T * 2.0)
     _check(y, ref)
+
+
+def test_fp32_call_leaves_sync_area_zero(dev):
+    """An fp32 LoRA call shares the stream's rq_nf4_linear workspace with the
+    bf16 decode GEMV, whose in-launch LoRA handshake needs the workspace's
+    synchronization area zero: the fp32 path keeps its LoRA operand after the
+    area, so a bf16 call right after it gives the same bits as on a fresh
+    stream."""
+    ql, lora = _layer(dev, seed=12, bias=False)
+    a, b = lora.lora_A.detach(), lora.lora_B.detach()
+    x16 = torch.randn(2, K, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(dev)
+    fresh = torch.cuda.Stream(dev)
+    with torch.cuda.stream(fresh):
+        want = ops.nf4_linear(x16, ql.weight_quant, ql.weight_scales, N, 64, lora_a=a, lora_b=b, scaling=2.0)
+    torch.cuda.synchronize(dev)
+    x32 = torch.randn(16, K, generator=torch.Generator().manual_seed(5)).to(dev)
+    ops.nf4_linear(x32, ql.weight_quant, ql.weight_scales, N, 64, lora_a=a, lora_b=b, scaling=2.0)
+    got = ops.nf4_linear(x16, ql.weight_quant, ql.weight_scales, N, 64, lora_a=a, lora_b=b, scaling=2.0)
+    torch.cuda.synchronize(dev)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(),
+           torch.cuda.current_stream(dev).cuda_stream)
+    assert int(ops._LINEAR_WS[key][:ops.LINEAR_SYNC_BYTES].cpu().count_nonzero()) == 0
+    assert torch.equal(got, want)
