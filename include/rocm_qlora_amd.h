@@ -42,6 +42,7 @@ extern "C" {
 #define RQ_ERR_UNSUPPORTED    5
 #define RQ_ERR_WORKSPACE      6
 #define RQ_ERR_HIP            7
+#define RQ_ERR_SCRATCH_LIMIT  8   /* needs more than rq_nf4_linear_noalloc's scratch */
 
 /* Human-readable text for a status code (static storage). */
 const char* rq_status_string(int status);
@@ -163,6 +164,31 @@ int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   int64_t ld_lora_b, int lora_dtype, int64_t rank, float scaling,
                   void* y, int64_t ldy, void* workspace, int64_t workspace_bytes,
                   hipStream_t stream);
+
+/* Bytes of the device scratch array behind rq_nf4_linear_noalloc (per GPU,
+ * held until the process ends). */
+#define RQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* rq_nf4_linear without a workspace argument: no counterpart in the
+ * reference.  For callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc): the
+ * workspace is a static device array of RQ_NOALLOC_SCRATCH_BYTES per GPU,
+ * shared by every call on that GPU.  Allocates nothing and calls no
+ * allocating routine.  The MFMA GEMM (M > 16) runs without K splits when
+ * their partial tiles do not fit; a call that still needs more than the array
+ * returns RQ_ERR_SCRATCH_LIMIT before launching anything.
+ * The first call on a device also launches a fill kernel that clears the
+ * array's synchronization area; every call leaves it clear.  Calls that may
+ * overlap on one GPU (other streams, other threads) race on the array: order
+ * them on one stream, or use rq_nf4_linear with workspaces of their own. */
+int rq_nf4_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                          const uint8_t* w_packed, int64_t N, int64_t block_size,
+                          const void* absmax, int absmax_dtype,
+                          const uint8_t* c2, int c2_format, int64_t block2,
+                          const void* bias, int bias_dtype,
+                          const void* lora_x, int64_t ld_lora_x, const void* lora_a, const void* lora_b,
+                          int64_t ld_lora_b, int lora_dtype, int64_t rank, float scaling,
+                          void* y, int64_t ldy, hipStream_t stream);
 
 /* Test hook, no counterpart in the reference: how many times a decode-GEMV
  * workgroup polls for the workgroups that compute the LoRA down-projection

@@ -11,6 +11,7 @@ extern "C" const char* rq_status_string(int status) {
     case RQ_ERR_UNSUPPORTED: return "unsupported configuration";
     case RQ_ERR_WORKSPACE: return "workspace missing or too small";
     case RQ_ERR_HIP: return "HIP launch error";
+    case RQ_ERR_SCRATCH_LIMIT: return "call needs more workspace than the allocation-free entry point's scratch";
     default: return "unknown status";
   }
 }

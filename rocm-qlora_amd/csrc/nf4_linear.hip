@@ -1349,3 +1349,80 @@ extern "C" int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, i
                       area ? reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kLinearCountBytes) : nullptr,
                       (kLinearSyncBytes - kLinearCountBytes) / 4, stream);
 }
+
+// ===========================================================================
+// Allocation-free variant of rq_nf4_linear (no counterpart in the reference):
+// its workspace is a file-scope device array, so the call allocates nothing.
+// ===========================================================================
+namespace rq {
+
+// The workspace of rq_nf4_linear_noalloc on every device the library runs on
+// (each device holds its own copy until the process ends).  Host code never
+// uses this name as an address: the per-device address comes from
+// hipGetSymbolAddress.  Zero at load; its synchronization area is cleared
+// once more on a device's first call and left zero by every call.
+static __device__ __align__(256) uint8_t scratch[RQ_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxScratchDevices = 64;
+// per device: the array's device address (nullptr until the first call)
+static std::atomic<void*> scratch_ptr[kMaxScratchDevices];
+
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// The current device's scratch address; on the device's first call, looks it
+// up and clears the synchronization area with a fill kernel on `stream` (a
+// kernel, not a memset, so that a graph capture records a kernel node).
+static int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return RQ_ERR_HIP;
+  if (dev < 0 || dev >= kMaxScratchDevices) return RQ_ERR_UNSUPPORTED;
+  void* p = scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    void* q = nullptr;
+    if (hipGetSymbolAddress(&q, HIP_SYMBOL(scratch)) != hipSuccess || !q) return RQ_ERR_HIP;
+    constexpr int64_t words = int64_t(kLinearSyncBytes) / 4;
+    zero_words_kernel<<<unsigned((words + 255) / 256), 256, 0, stream>>>(static_cast<uint32_t*>(q), words);
+    if (int st = rq_check_launch(); st != RQ_OK) return st;
+    void* expected = nullptr;
+    // racing first calls on one device look up the same address
+    scratch_ptr[dev].compare_exchange_strong(expected, q, std::memory_order_acq_rel);
+    p = q;
+  }
+  *out = p;
+  return RQ_OK;
+}
+
+}  // namespace rq
+
+extern "C" int rq_nf4_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                                     const uint8_t* w_packed, int64_t N, int64_t block_size, const void* absmax,
+                                     int absmax_dtype, const uint8_t* c2, int c2_format, int64_t block2,
+                                     const void* bias, int bias_dtype, const void* lora_x, int64_t ld_lora_x,
+                                     const void* lora_a, const void* lora_b, int64_t ld_lora_b, int lora_dtype,
+                                     int64_t rank, float scaling, void* y, int64_t ldy, hipStream_t stream) {
+  const LinearArgs L = pack_linear_args(x, x_dtype, M, K, ldx, w_packed, N, block_size, absmax, absmax_dtype,
+                                        c2, c2_format, block2, bias, bias_dtype, lora_x, ld_lora_x, lora_a,
+                                        lora_b, ld_lora_b, lora_dtype, rank, scaling, y, ldy);
+  int st = validate_linear(L);
+  if (st != RQ_OK || M == 0) return st;
+  // the smallest workspace the call runs with (the GEMM drops its K splits
+  // when their partial tiles do not fit)
+  int64_t need = 0;
+  if (x_dtype != RQ_DTYPE_F32 && M > kGemvMaxM) {
+    const size_t b = gemm_min_workspace(L);
+    need = b > 0 ? int64_t(b + kLinearSyncBytes) : 0;
+  } else {
+    st = rq_nf4_linear_workspace_size(x_dtype, M, K, N, L.rank, &need);
+    if (st != RQ_OK) return st;
+  }
+  if (need > int64_t(RQ_NOALLOC_SCRATCH_BYTES)) return RQ_ERR_SCRATCH_LIMIT;
+  void* ws = nullptr;
+  st = noalloc_scratch(stream, &ws);
+  if (st != RQ_OK) return st;
+  return rq_nf4_linear(x, x_dtype, M, K, ldx, w_packed, N, block_size, absmax, absmax_dtype, c2, c2_format, block2,
+                       bias, bias_dtype, lora_x, ld_lora_x, lora_a, lora_b, ld_lora_b, lora_dtype, rank, scaling,
+                       y, ldy, ws, int64_t(RQ_NOALLOC_SCRATCH_BYTES), stream);
+}

@@ -40,6 +40,12 @@ SIGNATURES = {
                       _P, _I32,                              # bias, dtype
                       _P, _I64, _P, _P, _I64, _I32, _I64, _F32,  # lora x, ld, A, B, ldB, dtype, rank, scaling
                       _P, _I64, _P, _I64, _P],               # y, ldy, workspace, bytes, stream
+    "rq_nf4_linear_noalloc": [_P, _I32, _I64, _I64, _I64,    # x, dtype, M, K, ldx
+                              _P, _I64, _I64, _P, _I32,      # packed, N, block, absmax, dtype
+                              _P, _I32, _I64,                # c2, c2 format, block2
+                              _P, _I32,                      # bias, dtype
+                              _P, _I64, _P, _P, _I64, _I32, _I64, _F32,  # lora x, ld, A, B, ldB, dtype, rank, scaling
+                              _P, _I64, _P],                 # y, ldy, stream
     "rq_set_gemv_spin_limit": [ctypes.c_uint32],
     "rq_gemm_tile_config": [_P],
     "rq_stream_capture_id": [_P, _P],
