@@ -52,6 +52,7 @@ for _p in (ROOT, os.path.join(ROOT, "rocm-qlora_amd")):
 METRIC = "NF4 dequant-GEMV GB/s + GEMM TFLOP/s (% roofline), Llama-3-8B proj shapes"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+FP8_PEAK_TFLOPS = 5000.0       # MI355X dense fp8 MFMA
 
 # (name, in_features K, out_features N)
 LLAMA3_8B_PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
@@ -254,7 +255,7 @@ def bench_codec(dev, stream):
 
 
 def bench_byte_linears(dev, stream):
-    """INT8 per-row-absmax and FP8 (e4m3fnuz) linears at 8192 -> 28672 with
+    """INT8 per-row-absmax (bf16 MFMA) and FP8 (e4m3, fp8 MFMA) linears at 8192 -> 28672 with
     bf16 activations N(0,1), weights N(0,0.02); M = 1 rotates two weight
     copies (470 MB each kind, past the MALL), M = 512 and 4096 one copy."""
     import torch
@@ -266,7 +267,9 @@ def bench_byte_linears(dev, stream):
     for c in range(2):
         w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
         int8_w.append(quantize_int8(w, per_channel=True))
-        fp8_w.append(ops.fp8_quantize(w))
+        codes, scale = ops.fp8_quantize(w)
+        fp8_w.append((ops.fp8_to_e4m3fn(codes), scale))  # as FP8LinearWrapper caches it
+        del codes
         del w
     out = {}
     for M in (1, 512, 4096):
@@ -288,8 +291,9 @@ def bench_byte_linears(dev, stream):
                                         "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm"}
             else:
                 tf = 2 * M * N * K / us / 1e6
+                peak, bound = (BF16_PEAK_TFLOPS, "bf16 mfma") if kind == "int8" else (FP8_PEAK_TFLOPS, "fp8 mfma")
                 out[f"{kind}_m{M}"] = {"us": round(us, 2), "tflops": round(tf, 1),
-                                        "frac": round(tf / BF16_PEAK_TFLOPS, 4), "bound": "bf16 mfma"}
+                                        "frac": round(tf / peak, 4), "bound": bound}
         del x
     return {"workload": f"INT8 per-row and FP8 per-tensor linears, K={K} N={N}, bf16 activations", **out}
 

@@ -198,7 +198,7 @@ int rq_nf4_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int6
 uint32_t rq_set_gemv_spin_limit(uint32_t polls);
 
 /* Tile configuration of the MFMA GEMM behind rq_nf4_linear (M > 16),
- * rq_nf4_linear_dx, rq_int8_linear and rq_fp8_linear: out[0..4] = rows and
+ * rq_nf4_linear_dx and rq_int8_linear: out[0..4] = rows and
  * columns of a workgroup tile, k per step, wavefronts per workgroup, LDS
  * pipeline stages.  Replaces the tile table of get_kernel_config
  * (kernels/kernel_config.py:18-48), which describes the reference's Triton
@@ -261,15 +261,29 @@ int rq_fp8_quantize(const void* t, int t_dtype, int64_t rows, int64_t cols, int6
                     uint8_t* codes, float* scale, void* workspace, int64_t workspace_bytes,
                     hipStream_t stream);
 
+/* e4m3fnuz codes (the reference's torch.float8_e4m3fnuz, as rq_fp8_quantize
+ * writes them) -> e4m3fn codes of the same values, the OCP format gfx950's
+ * fp8 matrix cores read (torch.float8_e4m3fn; in place when out == codes).
+ * Exact except the 8 odd-mantissa magnitudes below 2^-6, which round to
+ * the nearest even e4m3fn code (a change of at most 2^-10), as torch's own
+ * .to(torch.float8_e4m3fn) does; 0x80 (NaN) becomes 0x7F (NaN).  No
+ * counterpart in the reference, which multiplies decoded fnuz values
+ * (fp8/fp8_linear.py:44-52); a weight is converted once, when it is
+ * quantized.  codes, out: 16-byte aligned. */
+int rq_fp8_fnuz_to_e4m3fn(const uint8_t* codes, int64_t n, uint8_t* out, hipStream_t stream);
+
 /* Bytes of workspace rq_fp8_linear needs for M rows of K activations. */
 int rq_fp8_linear_workspace_size(int64_t M, int64_t K, int64_t* bytes);
 
 /* Replaces _FP8LinearFunc.forward (fp8/fp8_linear.py:27-60) for a weight
- * already quantized by rq_fp8_quantize: x is quantized per tensor the same
- * way, then y = RND(RND(sum_k x8 w8 * x_scale * w_scale) + bias) with the
- * e4m3fnuz products summed exactly in fp32.
- *   x: [M, K] bf16/fp16 stride ldx (K % 64 == 0); w_codes: [N, K] e4m3fnuz;
- *   w_scale: device fp32; bias [N] or NULL; y: [M, N] stride ldy. */
+ * already quantized (rq_fp8_quantize, then rq_fp8_fnuz_to_e4m3fn): x is
+ * quantized per tensor the same way (scale = fp32(double(max|x|) / 240),
+ * codes = e4m3fnuz(RND(x / scale)) re-encoded to e4m3fn), then
+ *   y = RND(RND(sum_k x8 w8 * x_scale * w_scale) + RND(bias))
+ * with the fp8 products summed by the fp8 matrix cores in fp32.
+ *   x: [M, K] bf16/fp16 stride ldx (K % 64 == 0); w_codes: [N, K] e4m3fn;
+ *   w_scale: device fp32; bias [N] or NULL; y: [M, N] stride ldy.
+ * M <= 16 runs a weight-streaming GEMV, larger M the fp8 MFMA GEMM. */
 int rq_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   const uint8_t* w_codes, int64_t N, const float* w_scale,
                   const void* bias, int bias_dtype, void* y, int64_t ldy,

@@ -1,74 +1,41 @@
-// INT8 and FP8 (e4m3fnuz) weight linears for gfx950.
+// INT8 weight linears for gfx950, and the reference's FP8 quantizer.
 //
 // INT8 (QuantLinear bits=8 and the row-absmax recipe): W = RND(float(q) *
 // scale) with one scale per output row (quant_ops.py:28-35, :63-65) or per
 // 64-element block of the flat weight (quant_ops.py:36-53, :69-78), then
 // y = RND(x W^T + RND(bias)) as F.linear does (quant_linear.py:193-197).
-//
-// FP8 (_FP8LinearFunc, fp8_linear.py:27-60): per-tensor scales
-// s = fp32(double(max|t|) / 240) for W and x, codes = fnuz(RND(t / s)),
-// y = RND(RND(sum x8 w8 * s_x * s_w) + bias).  fnuz values are exact in
-// bf16/fp16, so both operands are decoded to the activation dtype and the
-// products summed by bf16/fp16 MFMA in fp32 -- exact products, fp32 sums.
-// gfx950's v_cvt_pk_f32_fp8 decodes the OCP e4m3fn format; a fnuz code c
-// has half the OCP value of the same bits, except 0x7F/0xFF (fnuz +-240, OCP
-// NaN) and 0x80 (fnuz NaN, OCP -0), which are fixed up.
+// The weights are decoded exactly (one fp32 multiply, one rounding to the
+// activation dtype) and multiplied by bf16/fp16 MFMA in fp32.
 //
 // M > 16 runs the shared MFMA core (rq_gemm_core.h) with a byte-weight
 // producer; M <= 16 runs byte_gemv_kernel, a weight-streaming MFMA GEMV.
+//
+// FP8 per-tensor quantization (fp8_linear.py:33-42) to the reference's
+// e4m3fnuz codes is here too; the FP8 linear itself runs on the fp8 matrix
+// cores (fp8_mfma.hip).
 #include "rq_gemm_core.h"
 #include "rq_gemm8.h"
 
 namespace rq {
 
-// 4 weight bytes -> 4 fp32 operand values.  INT8: float(int8) * s (one
-// fp32 rounding, as q.float() * scale).  FP8: the fnuz value.
-template <bool FP8>
+// 4 weight bytes -> 4 fp32 operand values: float(int8) * s (one fp32
+// rounding, as q.float() * scale).
 __device__ __forceinline__ void decode4(uint32_t w, float s, float (&v)[4]) {
-  if constexpr (FP8) {
-    const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(int(w), false);
-    const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(int(w), true);
-    v[0] = lo.x * 0.5f;
-    v[1] = lo.y * 0.5f;
-    v[2] = hi.x * 0.5f;
-    v[3] = hi.y * 0.5f;
-    // bytes whose low 7 bits are all ones (+-240), and 0x80 (NaN): bit 7 of
-    // each byte of `ones` is set iff its low 7 bits are 0x7F, of `nonzero`
-    // iff they are not all zero (no carries cross bytes in either sum)
-    const uint32_t low7 = w & 0x7F7F7F7Fu;
-    const uint32_t ones = (low7 + 0x01010101u) & 0x80808080u;
-    const uint32_t nonzero = (low7 + 0x7F7F7F7Fu) & 0x80808080u;
-    const uint32_t special = ones | (w & 0x80808080u & ~nonzero);
-    if (__builtin_expect(special != 0u, 0)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = fnuz_to_f32(uint8_t(w >> (8 * i)));
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(float(int8_t(uint8_t(w >> (8 * i)))), s);
-  }
+  for (int i = 0; i < 4; ++i) v[i] = __fmul_rn(float(int8_t(uint8_t(w >> (8 * i)))), s);
 }
 
-template <int XT, bool FP8>
+template <int XT>
 __device__ __forceinline__ uint2 decode4_pk(uint32_t w, float s) {
   float v[4];
-  decode4<FP8>(w, s, v);
+  decode4(w, s, v);
   return uint2{cvt_pk<XT>(v[0], v[1]), cvt_pk<XT>(v[2], v[3])};
 }
-
-// Scale provider for FP8 (no per-block scale: the per-tensor scales are
-// applied in the epilogue).
-struct ScaleNone {
-  static constexpr int kLoads = 0;
-  typedef uint32_t Raw;
-  __device__ __forceinline__ Raw load(int64_t) const { return 0u; }
-  __device__ __forceinline__ float value(Raw) const { return 1.0f; }
-};
 
 // Forward producer for byte weights (512 threads): tile row = output feature
 // n, 64 reduction k per step = 64 weight bytes per row.  Thread t decodes
 // row t / 4, bytes 16 (t % 4) .. +16 of the step (piece p = bytes 8p .. 8p + 7).
-template <int XT, class Scale, bool FP8>
+template <int XT, class Scale>
 struct Byte8Producer {
   static constexpr int kLoads = 1 + Scale::kLoads;
   struct Regs {
@@ -107,7 +74,7 @@ struct Byte8Producer {
   __device__ __forceinline__ void finish(Step& S, int p, int hh, uint8_t* tile) const {
     const int d = 2 * p + hh;  // dword of this thread's 16 bytes
     const uint32_t word = d == 0 ? S.w.x : d == 1 ? S.w.y : d == 2 ? S.w.z : S.w.w;
-    const uint2 pk = decode4_pk<XT, FP8>(word, S.sc);
+    const uint2 pk = decode4_pk<XT>(word, S.sc);
     S.r[2 * hh] = pk.x;
     S.r[2 * hh + 1] = pk.y;
     if (hh == 1)
@@ -129,7 +96,7 @@ struct Byte8Producer {
 constexpr int kByteGemvDepth = 8;  // 64-k steps of weights in flight per lane
 
 struct ByteGemvArgs {
-  const uint16_t* x;   // [M][K] activation rows (FP8: decoded codes)
+  const uint16_t* x;   // [M][K] activation rows
   int64_t ldx;
   const uint8_t* w;    // [N][K] weight bytes
   int64_t M, N, K;
@@ -137,13 +104,11 @@ struct ByteGemvArgs {
   int bs_log2;
   const void* bias;
   int bias_dt;
-  const float* post_a;  // FP8 per-tensor scales (device), else nullptr
-  const float* post_b;
   uint16_t* y;
   int64_t ldy;
 };
 
-template <int XT, class Scale, bool FP8>
+template <int XT, class Scale>
 __global__ __launch_bounds__(256) void byte_gemv_kernel(ByteGemvArgs a, Scale scale) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int i16 = lane & 15, q4 = lane >> 4;
@@ -181,28 +146,21 @@ __global__ __launch_bounds__(256) void byte_gemv_kernel(ByteGemvArgs a, Scale sc
       const int64_t kn = k + kByteGemvDepth < nk ? k + kByteGemvDepth : nk - 1;
       wq[d] = *reinterpret_cast<const u32x4*>(wr + kn * 64);
       sq[d] = scale.load(sb + ((kn * 64) >> a.bs_log2));
-      const uint2 a0 = decode4_pk<XT, FP8>(w.x, s), a1 = decode4_pk<XT, FP8>(w.y, s);
-      const uint2 a2 = decode4_pk<XT, FP8>(w.z, s), a3 = decode4_pk<XT, FP8>(w.w, s);
+      const uint2 a0 = decode4_pk<XT>(w.x, s), a1 = decode4_pk<XT>(w.y, s);
+      const uint2 a2 = decode4_pk<XT>(w.z, s), a3 = decode4_pk<XT>(w.w, s);
       acc = mfma16x16x32<XT>(u32x4{a0.x, a0.y, a1.x, a1.y}, xb0, acc);
       acc = mfma16x16x32<XT>(u32x4{a2.x, a2.y, a3.x, a3.y}, xb1, acc);
     }
   }
   // epilogue: lane (i, q), register r -> y[m = i][n0 + 4 q + r]
   if (!mlive) return;
-  const float post = a.post_a ? __fmul_rn(*a.post_a, *a.post_b) : 1.0f;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t no = n0 + 4 * q4 + r;
     if (no >= a.N) continue;
     float v = acc[r];
-    const float bias = a.bias ? round_x<XT>(load_as_f32(a.bias, no, a.bias_dt)) : 0.0f;
-    if (a.post_a) {
-      v = round_x<XT>(__fmul_rn(v, post));
-      if (a.bias) v = round_x<XT>(__fadd_rn(v, bias));
-    } else {
-      if (a.bias) v = __fadd_rn(v, bias);
-      v = round_x<XT>(v);
-    }
+    if (a.bias) v = __fadd_rn(v, round_x<XT>(load_as_f32(a.bias, no, a.bias_dt)));
+    v = round_x<XT>(v);
     a.y[int64_t(i16) * a.ldy + no] = uint16_t(to_x16<XT>(v));
   }
 }
@@ -258,24 +216,16 @@ __global__ __launch_bounds__(256) void absmax_final_kernel(const float* __restri
   if (threadIdx.x == 0) scale[0] = float(double(red[0]) / 240.0);
 }
 
-// codes[r][c] = fnuz(RND_dt(t / s)); dec (if non-null) = the code's value in
-// DT (exact).
+// codes[r][c] = fnuz(RND_dt(t / s)).
 template <int DT>
 __global__ __launch_bounds__(256) void fp8_encode_kernel(const void* __restrict__ t, int64_t rows, int64_t cols,
                                                          int64_t ld, const float* __restrict__ scale,
-                                                         uint8_t* __restrict__ codes, uint16_t* __restrict__ dec) {
+                                                         uint8_t* __restrict__ codes) {
   const float s = *scale;
   const int64_t total = rows * cols;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
     const int64_t r = i / cols, c = i - r * cols;
-    const float v = ld_f32<DT>(t, r * ld + c);
-    const float q = round_to(__fdiv_rn(v, s), DT);
-    const uint8_t code = f32_to_fnuz_rne(q);
-    if (codes) codes[i] = code;
-    if (dec) {
-      const float f = fnuz_to_f32(code);
-      dec[i] = DT == RQ_DTYPE_BF16 ? f32_to_bf16_rne(f) : f32_to_f16_rne(f);
-    }
+    codes[i] = f32_to_fnuz_rne(round_to(__fdiv_rn(ld_f32<DT>(t, r * ld + c), s), DT));
   }
 }
 
@@ -288,126 +238,96 @@ struct ByteLinearArgs {
   int64_t M, K, ldx;
   const uint8_t* w;
   int64_t N;
-  bool fp8;
-  int64_t block_size;   // INT8: 0 = per output row, else blockwise over the flat weight
-  const void* scales;   // INT8 scales of scales_dtype
+  int64_t block_size;   // 0 = per output row, else blockwise over the flat weight
+  const void* scales;   // scales of scales_dtype
   int scales_dtype;
-  const float* w_scale;  // FP8: device fp32 per-tensor weight scale
   const void* bias;
   int bias_dtype;
   void* y;
   int64_t ldy;
 };
 
-static size_t byte_linear_ws(const ByteLinearArgs& A) {
-  if (!A.fp8) return 0;
-  // [absmax partials][x scale][decoded x M x K]
-  return size_t(kAbsmaxBlocks) * 4 + 256 + ((size_t(A.M) * A.K * 2 + 255) & ~size_t(255));
-}
-
 static int validate_byte(const ByteLinearArgs& A) {
-  if (!A.x || !A.w || !A.y) return RQ_ERR_NULL_POINTER;
+  if (!A.x || !A.w || !A.y || !A.scales) return RQ_ERR_NULL_POINTER;
   if (A.x_dtype != RQ_DTYPE_BF16 && A.x_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
   if (A.M < 0 || A.N <= 0 || A.K <= 0 || A.K % 64 != 0) return RQ_ERR_BAD_SHAPE;
   if (A.ldx < A.K || A.ldy < A.N) return RQ_ERR_BAD_SHAPE;
-  if (A.fp8) {
-    if (!A.w_scale) return RQ_ERR_NULL_POINTER;
-  } else {
-    if (!A.scales) return RQ_ERR_NULL_POINTER;
-    if (A.scales_dtype != RQ_DTYPE_F32 && A.scales_dtype != RQ_DTYPE_BF16 && A.scales_dtype != RQ_DTYPE_F16)
-      return RQ_ERR_BAD_DTYPE;
-    if (A.block_size != 0 && (A.block_size < 64 || (A.block_size & (A.block_size - 1)) || A.K % A.block_size))
-      return RQ_ERR_BAD_SHAPE;
-  }
+  if (A.scales_dtype != RQ_DTYPE_F32 && A.scales_dtype != RQ_DTYPE_BF16 && A.scales_dtype != RQ_DTYPE_F16)
+    return RQ_ERR_BAD_DTYPE;
+  if (A.block_size != 0 && (A.block_size < 64 || (A.block_size & (A.block_size - 1)) || A.K % A.block_size))
+    return RQ_ERR_BAD_SHAPE;
   if (!aligned(A.x, 16) || A.ldx % 8 != 0 || !aligned(A.w, 16)) return RQ_ERR_BAD_ALIGNMENT;
   if (!offsets_fit(A.M, A.ldx, A.N, 2 * A.K)) return RQ_ERR_UNSUPPORTED;
   return RQ_OK;
 }
 
-template <int XT, class Scale, bool FP8>
-static int launch_byte(const ByteLinearArgs& A, const uint16_t* xact, int64_t ldx, Scale scale,
-                       const float* post_a, const float* post_b, hipStream_t stream) {
+template <int XT, class Scale>
+static int launch_byte(const ByteLinearArgs& A, Scale scale, hipStream_t stream) {
+  const uint16_t* x = static_cast<const uint16_t*>(A.x);
   const int64_t bpr = A.block_size ? A.K / A.block_size : 1;
   const int bsl = A.block_size ? pow2_shift(A.block_size) : 62;  // per row: k >> 62 == 0
   if (A.M <= kGemvMaxM) {
     ByteGemvArgs g;
-    g.x = xact; g.ldx = ldx; g.w = A.w; g.M = A.M; g.N = A.N; g.K = A.K;
+    g.x = x; g.ldx = A.ldx; g.w = A.w; g.M = A.M; g.N = A.N; g.K = A.K;
     g.blocks_per_row = bpr; g.bs_log2 = bsl;
-    g.bias = A.bias; g.bias_dt = A.bias_dtype; g.post_a = post_a; g.post_b = post_b;
+    g.bias = A.bias; g.bias_dt = A.bias_dtype;
     g.y = static_cast<uint16_t*>(A.y); g.ldy = A.ldy;
-    byte_gemv_kernel<XT, Scale, FP8><<<unsigned((A.N + 63) / 64), 256, 0, stream>>>(g, scale);
+    byte_gemv_kernel<XT, Scale><<<unsigned((A.N + 63) / 64), 256, 0, stream>>>(g, scale);
     return rq_check_launch();
   }
   const GemmPlan p = plan_gemm(A.M, A.N, A.K, 0, device_cus());
   GemmArgs a{};
-  a.x = xact; a.ldx = ldx; a.M = A.M; a.N = A.N; a.K = A.K;
+  a.x = x; a.ldx = A.ldx; a.M = A.M; a.N = A.N; a.K = A.K;
   a.tiles_m = p.tiles_m; a.tiles_n = p.tiles_n; a.xcd_map = p.xcd_map;
   a.splits = 1; a.lf = p.tiles_m * p.tiles_n / 8;
   GemmEpi e{};
   e.bias = A.bias; e.bias_dt = A.bias_dtype; e.scaling = 1.0f;
-  e.post_a = post_a; e.post_b = post_b;
   e.y = static_cast<uint16_t*>(A.y); e.ldy = A.ldy;
   ProducerParams pp{A.w, A.K, A.N, bpr, bsl};
   const unsigned grid = unsigned(int64_t(p.tiles_m) * p.tiles_n);
-  nf4_gemm8_kernel<XT, Byte8Producer<XT, Scale, FP8>, Scale><<<grid, kGemm8Threads, 0, stream>>>(a, pp, scale, e);
+  nf4_gemm8_kernel<XT, Byte8Producer<XT, Scale>, Scale><<<grid, kGemm8Threads, 0, stream>>>(a, pp, scale, e);
   return rq_check_launch();
+}
+
+template <int XT>
+static int run_byte(const ByteLinearArgs& A, hipStream_t stream) {
+  switch (A.scales_dtype) {
+    case RQ_DTYPE_F32:
+      return launch_byte<XT>(A, ScaleAbsmax<RQ_DTYPE_F32>{A.scales}, stream);
+    case RQ_DTYPE_BF16:
+      return launch_byte<XT>(A, ScaleAbsmax<RQ_DTYPE_BF16>{A.scales}, stream);
+    default:
+      return launch_byte<XT>(A, ScaleAbsmax<RQ_DTYPE_F16>{A.scales}, stream);
+  }
+}
+
+static int byte_linear(const ByteLinearArgs& A, hipStream_t stream) {
+  int st = validate_byte(A);
+  if (st != RQ_OK) return st;
+  if (A.M == 0) return RQ_OK;
+  if (A.x_dtype == RQ_DTYPE_BF16) return run_byte<RQ_DTYPE_BF16>(A, stream);
+  return run_byte<RQ_DTYPE_F16>(A, stream);
 }
 
 template <int DT>
 static int fp8_quantize_t(const void* t, int64_t rows, int64_t cols, int64_t ld, float* part, float* scale,
-                          uint8_t* codes, uint16_t* dec, hipStream_t stream) {
+                          uint8_t* codes, hipStream_t stream) {
   absmax_partial_kernel<DT><<<kAbsmaxBlocks, 256, 0, stream>>>(t, rows, cols, ld, part);
   absmax_final_kernel<<<1, 256, 0, stream>>>(part, kAbsmaxBlocks, scale);
   const int64_t blocks = (rows * cols + 255) / 256;
   fp8_encode_kernel<DT><<<unsigned(blocks < 65536 ? blocks : 65536), 256, 0, stream>>>(t, rows, cols, ld, scale,
-                                                                                      codes, dec);
+                                                                                      codes);
   return rq_check_launch();
 }
 
 static int fp8_quantize(int dt, const void* t, int64_t rows, int64_t cols, int64_t ld, float* part, float* scale,
-                        uint8_t* codes, uint16_t* dec, hipStream_t stream) {
+                        uint8_t* codes, hipStream_t stream) {
   switch (dt) {
-    case RQ_DTYPE_F32: return fp8_quantize_t<RQ_DTYPE_F32>(t, rows, cols, ld, part, scale, codes, dec, stream);
-    case RQ_DTYPE_BF16: return fp8_quantize_t<RQ_DTYPE_BF16>(t, rows, cols, ld, part, scale, codes, dec, stream);
-    case RQ_DTYPE_F16: return fp8_quantize_t<RQ_DTYPE_F16>(t, rows, cols, ld, part, scale, codes, dec, stream);
+    case RQ_DTYPE_F32: return fp8_quantize_t<RQ_DTYPE_F32>(t, rows, cols, ld, part, scale, codes, stream);
+    case RQ_DTYPE_BF16: return fp8_quantize_t<RQ_DTYPE_BF16>(t, rows, cols, ld, part, scale, codes, stream);
+    case RQ_DTYPE_F16: return fp8_quantize_t<RQ_DTYPE_F16>(t, rows, cols, ld, part, scale, codes, stream);
     default: return RQ_ERR_BAD_DTYPE;
   }
-}
-
-template <int XT>
-static int run_byte(const ByteLinearArgs& A, void* workspace, hipStream_t stream) {
-  if (A.fp8) {
-    char* ws = static_cast<char*>(workspace);
-    float* part = reinterpret_cast<float*>(ws);
-    float* xs = reinterpret_cast<float*>(ws + size_t(kAbsmaxBlocks) * 4);
-    uint16_t* xdec = reinterpret_cast<uint16_t*>(ws + size_t(kAbsmaxBlocks) * 4 + 256);
-    const int st = fp8_quantize(A.x_dtype, A.x, A.M, A.K, A.ldx, part, xs, nullptr, xdec, stream);
-    if (st != RQ_OK) return st;
-    return launch_byte<XT, ScaleNone, true>(A, xdec, A.K, ScaleNone{}, xs, A.w_scale, stream);
-  }
-  const uint16_t* x = static_cast<const uint16_t*>(A.x);
-  switch (A.scales_dtype) {
-    case RQ_DTYPE_F32:
-      return launch_byte<XT, ScaleAbsmax<RQ_DTYPE_F32>, false>(A, x, A.ldx, ScaleAbsmax<RQ_DTYPE_F32>{A.scales},
-                                                              nullptr, nullptr, stream);
-    case RQ_DTYPE_BF16:
-      return launch_byte<XT, ScaleAbsmax<RQ_DTYPE_BF16>, false>(A, x, A.ldx, ScaleAbsmax<RQ_DTYPE_BF16>{A.scales},
-                                                               nullptr, nullptr, stream);
-    default:
-      return launch_byte<XT, ScaleAbsmax<RQ_DTYPE_F16>, false>(A, x, A.ldx, ScaleAbsmax<RQ_DTYPE_F16>{A.scales},
-                                                              nullptr, nullptr, stream);
-  }
-}
-
-static int byte_linear(const ByteLinearArgs& A, void* workspace, int64_t ws_bytes, hipStream_t stream) {
-  int st = validate_byte(A);
-  if (st != RQ_OK) return st;
-  if (A.M == 0) return RQ_OK;
-  const size_t need = byte_linear_ws(A);
-  if (need > 0 && (!workspace || ws_bytes < int64_t(need))) return RQ_ERR_WORKSPACE;
-  if (workspace && !aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;
-  if (A.x_dtype == RQ_DTYPE_BF16) return run_byte<RQ_DTYPE_BF16>(A, workspace, stream);
-  return run_byte<RQ_DTYPE_F16>(A, workspace, stream);
 }
 
 }  // namespace rq
@@ -420,10 +340,10 @@ extern "C" int rq_int8_linear(const void* x, int x_dtype, int64_t M, int64_t K, 
                               int bias_dtype, void* y, int64_t ldy, hipStream_t stream) {
   rq::ByteLinearArgs A{};
   A.x = x; A.x_dtype = x_dtype; A.M = M; A.K = K; A.ldx = ldx;
-  A.w = reinterpret_cast<const uint8_t*>(q); A.N = N; A.fp8 = false;
+  A.w = reinterpret_cast<const uint8_t*>(q); A.N = N;
   A.block_size = block_size; A.scales = scales; A.scales_dtype = scales_dtype;
   A.bias = bias; A.bias_dtype = bias_dtype; A.y = y; A.ldy = ldy;
-  return rq::byte_linear(A, nullptr, 0, stream);
+  return rq::byte_linear(A, stream);
 }
 
 extern "C" int rq_fp8_quantize_workspace_size(int64_t* bytes) {
@@ -438,24 +358,5 @@ extern "C" int rq_fp8_quantize(const void* t, int t_dtype, int64_t rows, int64_t
   if (rows < 0 || cols < 0 || ld < cols) return RQ_ERR_BAD_SHAPE;
   if (workspace_bytes < int64_t(rq::kAbsmaxBlocks) * 4) return RQ_ERR_WORKSPACE;
   if (rows * cols == 0) return RQ_ERR_BAD_SHAPE;
-  return rq::fp8_quantize(t_dtype, t, rows, cols, ld, static_cast<float*>(workspace), scale, codes, nullptr, stream);
-}
-
-extern "C" int rq_fp8_linear_workspace_size(int64_t M, int64_t K, int64_t* bytes) {
-  if (!bytes) return RQ_ERR_NULL_POINTER;
-  if (M < 0 || K <= 0) return RQ_ERR_BAD_SHAPE;
-  rq::ByteLinearArgs A{};
-  A.M = M; A.K = K; A.fp8 = true;
-  *bytes = int64_t(rq::byte_linear_ws(A));
-  return RQ_OK;
-}
-
-extern "C" int rq_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const uint8_t* w_codes,
-                             int64_t N, const float* w_scale, const void* bias, int bias_dtype, void* y, int64_t ldy,
-                             void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-  rq::ByteLinearArgs A{};
-  A.x = x; A.x_dtype = x_dtype; A.M = M; A.K = K; A.ldx = ldx;
-  A.w = w_codes; A.N = N; A.fp8 = true; A.w_scale = w_scale;
-  A.bias = bias; A.bias_dtype = bias_dtype; A.y = y; A.ldy = ldy;
-  return rq::byte_linear(A, workspace, workspace_bytes, stream);
+  return rq::fp8_quantize(t_dtype, t, rows, cols, ld, static_cast<float*>(workspace), scale, codes, stream);
 }

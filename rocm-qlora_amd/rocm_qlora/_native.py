@@ -61,6 +61,7 @@ SIGNATURES = {
                        _P, _I32, _P, _I64, _P],              # bias, dtype, y, ldy, stream
     "rq_fp8_quantize_workspace_size": [_P],
     "rq_fp8_quantize": [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _I64, _P],
+    "rq_fp8_fnuz_to_e4m3fn": [_P, _I64, _P, _P],
     "rq_fp8_linear_workspace_size": [_I64, _I64, _P],
     "rq_fp8_linear": [_P, _I32, _I64, _I64, _I64,            # x, dtype, M, K, ldx
                       _P, _I64, _P, _P, _I32,                # codes, N, w scale, bias, dtype

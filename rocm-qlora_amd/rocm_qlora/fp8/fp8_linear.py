@@ -59,7 +59,8 @@ class FP8LinearWrapper(nn.Module):
     'native' (this package's FP8 kernels) when FP8 is supported and enabled,
     else 'bf16' (the wrapped layer unchanged).  The reference's third
     backend, TransformerEngine, is not dispatched to: there is one FP8 code
-    path.  The FP8 weight codes are cached until the stored weight changes."""
+    path.  The FP8 weight codes are cached, in the matrix cores' e4m3fn
+    encoding, until the stored weight changes."""
 
     def __init__(self, base_lora_linear: nn.Module, config: Optional[FP8Config] = None):
         super().__init__()
@@ -79,7 +80,11 @@ class FP8LinearWrapper(nn.Module):
                getattr(ql, "c2", ql.weight_scales).data_ptr())
         if self._cache_key != key:
             w = ql.dequantized_weight(dtype)
-            self._cache = (w, ops.fp8_quantize(w) if dtype != torch.float32 else None)
+            wq = None
+            if dtype != torch.float32:
+                codes, scale = ops.fp8_quantize(w)
+                wq = (ops.fp8_to_e4m3fn(codes), scale)
+            self._cache = (w, wq)
             self._cache_key = key
         return self._cache
 

@@ -315,17 +315,35 @@ def fp8_quantize(t: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     return codes.view(torch.float8_e4m3fnuz), scale
 
 
+def fp8_to_e4m3fn(codes: torch.Tensor) -> torch.Tensor:
+    """e4m3fnuz codes (fp8_quantize's) -> e4m3fn codes of the same values,
+    the format gfx950's fp8 matrix cores read: exact except the 8 odd-mantissa
+    magnitudes below 2^-6, which round to the nearest even e4m3fn code (as
+    torch's .to(torch.float8_e4m3fn) does); NaN stays NaN."""
+    dev = nat.require_gpu(codes)
+    src = codes.view(torch.uint8).contiguous()
+    with on(dev):
+        out = torch.empty(src.shape, dtype=torch.uint8, device=dev)
+        nat.call("rq_fp8_fnuz_to_e4m3fn", src.data_ptr(), src.numel(), out.data_ptr(), nat.stream_handle(dev))
+    return out.view(torch.float8_e4m3fn)
+
+
 def fp8_linear(x: torch.Tensor, w_codes: torch.Tensor, w_scale: torch.Tensor,
                bias: Optional[torch.Tensor] = None) -> torch.Tensor:
     """_FP8LinearFunc.forward (fp8_linear.py:27-60) for a weight quantized by
-    fp8_quantize: x is quantized per tensor, the e4m3fnuz products are summed
-    exactly in fp32, scaled by x_scale * w_scale, rounded to x's dtype, and
-    the bias is added.  x: [..., K] bf16/fp16 on the GPU."""
+    fp8_quantize: x is quantized per tensor, the fp8 products are summed by
+    the fp8 matrix cores in fp32, scaled by x_scale * w_scale, rounded to x's
+    dtype, and the bias is added.  w_codes: torch.float8_e4m3fn (fp8_to_e4m3fn
+    of the quantized weight, used as is) or torch.float8_e4m3fnuz / uint8
+    (re-encoded on every call).  x: [..., K] bf16/fp16 on the GPU."""
     K = x.shape[-1]
-    wc = w_codes.reshape(-1, K)
-    N = wc.shape[0]
     dev = nat.require_gpu(x, w_codes, w_scale, bias)
-    wc = wc.view(torch.uint8).contiguous()
+    if w_codes.dtype != torch.float8_e4m3fn:
+        if w_codes.dtype not in (torch.float8_e4m3fnuz, torch.uint8):
+            raise TypeError(f"fp8 weight codes expected, got {w_codes.dtype}")
+        w_codes = fp8_to_e4m3fn(w_codes)
+    wc = w_codes.reshape(-1, K).view(torch.uint8).contiguous()
+    N = wc.shape[0]
     ws_scale = w_scale.reshape(()).to(torch.float32).contiguous()
     lead = x.shape[:-1]
     with on(dev):

@@ -171,3 +171,49 @@ def test_byte_k_step_tails(dev, K):
     for y in fs:
         _check(y, fref)
         assert torch.equal(y.view(torch.int16), fs[0].view(torch.int16))
+
+
+def test_fp8_to_e4m3fn_matches_torch(dev):
+    """rq_fp8_fnuz_to_e4m3fn (the fp8 matrix cores' operand encoding) equals
+    torch's value conversion .to(torch.float8_e4m3fn) bit for bit: every code
+    once, then a ragged random buffer (length not a multiple of 16)."""
+    allc = torch.arange(256, dtype=torch.uint8)
+    rnd = torch.randint(0, 256, (4099,), generator=torch.Generator().manual_seed(3), dtype=torch.uint8)
+    for c in (allc, rnd):
+        got = ops.fp8_to_e4m3fn(c.to(dev).view(torch.float8_e4m3fnuz)).view(torch.uint8).cpu()
+        want = c.view(torch.float8_e4m3fnuz).to(torch.float8_e4m3fn).view(torch.uint8)
+        assert torch.equal(got, want)
+    # exact except the 8 odd subnormal-range magnitudes (and their negatives)
+    fz = allc.view(torch.float8_e4m3fnuz).float()
+    fn = ops.fp8_to_e4m3fn(allc.to(dev).view(torch.float8_e4m3fnuz)).cpu().float()
+    same = (fz == fn) | (fz.isnan() & fn.isnan())
+    assert int((~same).sum()) == 16
+    assert float((fz - fn)[~same].abs().max()) <= 2.0 ** -10
+
+
+@pytest.mark.parametrize("M", [1, 7, 16, 40, 300])
+def test_fp8_e4m3fn_weights_same_as_fnuz(dev, M):
+    """A weight passed as e4m3fn codes (converted once) gives the same bits as
+    the same weight passed as fnuz codes (converted per call), GEMV and GEMM."""
+    N, K = 2048, 1024
+    w = _weights(N, K, seed=51, dtype=torch.bfloat16)
+    x = _x(M, K, torch.bfloat16, seed=52)
+    wc, ws = ops.fp8_quantize(w.to(dev))
+    y1 = ops.fp8_linear(x.to(dev), wc, ws)
+    y2 = ops.fp8_linear(x.to(dev), ops.fp8_to_e4m3fn(wc), ws)
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    _check(y1, R.fp8_linear(x, w))
+
+
+@pytest.mark.parametrize("K", [64, 128, 192, 1088])
+@pytest.mark.parametrize("M", [3, 16, 70])
+def test_fp8_short_and_ragged_k(dev, M, K):
+    """K shorter than the GEMM's load pipeline (1 to 3 stages of 64 k) and K
+    not a multiple of the GEMV's 128-k step, with a bias."""
+    N = 320
+    w = _weights(N, K, seed=K + 60, dtype=torch.bfloat16)
+    x = _x(M, K, torch.bfloat16, seed=K + 61)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(62)) * 0.1).to(torch.bfloat16)
+    wc, ws = ops.fp8_quantize(w.to(dev))
+    y = ops.fp8_linear(x.to(dev), wc, ws, bias.to(dev))
+    _check(y, R.fp8_linear(x, w, bias))
