@@ -12,9 +12,19 @@ over enough layer copies (> 512 MB) that the 256 MB MALL cannot serve them.
 The step is captured once per layer copy as a HIP graph and replayed.
 
 Also reported:
+  config        p10 / p50 / p90 of the headline's per-step times (an event
+                after every step).
   roofline      the dominant kernel (the GEMV at the gate/up shape, no LoRA),
                 timed with HIP events over back-to-back launches on the stream
                 they run on; algorithmic bytes / average launch time vs 8 TB/s.
+  decode_m      the same decode step at the configuration's other batch sizes
+                (M in {1, 4, 8, 16}), 50 steps each.
+  decode_per_shape
+                per projection at the headline M: median launch time with the
+                LoRA term fused and without it, and a minimal launch (a 4-byte
+                fill) of the same graph structure.
+  config1       one NF4 4096x4096 QuantLinear with LoRA r = 16 on fp32
+                activations (M = 1 and 16), the fp32-MFMA path.
   gemm          the prefill/training shapes: the same seven projections at
                 M = 2048 tokens with LoRA r = 64, alpha = 16, forward and dX
                 backward, TFLOP/s and fraction of the 2.5 PFLOP/s bf16 MFMA peak.
@@ -22,13 +32,17 @@ Also reported:
                 with 0.1 % outliers at +-8 sigma, blocks 64 / 256): quantize ->
                 pack -> double-quantize the absmax, and double-dequantize ->
                 bf16; algorithmic bytes / time vs 8 TB/s.
-  byte_linears  INT8 (per-row absmax) and FP8 (e4m3fnuz, per-tensor scales)
-                linears at the Llama-3-70B MLP shape 8192 -> 28672, M = 1
-                (HBM: bytes / time, two weight copies rotating) and M = 512,
-                4096 (TFLOP/s against the bf16 MFMA peak).
-  cpu_baseline  the oracle's restatement of the reference's CPU path
-                (dequantize_int4 -> .to(bf16) -> F.linear + LoRA) over a bounded
-                sample of the same decode step on the host cores.
+  byte_linears  INT8 (per-row absmax, bf16 MFMA) and FP8 (e4m3 per-tensor
+                scales, fp8 MFMA) linears at the Llama-3-70B MLP shape
+                8192 -> 28672, M = 1 (HBM: bytes / time, two weight copies
+                rotating) and M = 512, 4096 (TFLOP/s against the bf16 and fp8
+                MFMA peaks, 2.5 and 5.0 PFLOP/s).
+  cpu_baseline  the oracle's restatement of the reference's CPU path on the
+                host cores: the headline decode step whole (`value`), and per
+                configuration (fp32 config 1, codec, GEMM forward / dX, INT8 /
+                FP8) on stated samples, each beside the GPU time of the same
+                work; 2 warm-ups, median of 10 runs, thread count, core count
+                and CPU model reported.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m M] [--no-gemm] [--no-extra] [--no-cpu]
     python bench.py --summarize-profile DIR   # per-kernel, per-grid rocprofv3 kernel-trace table
@@ -139,6 +153,29 @@ def _time_graph(graph, reps):
     return t0.elapsed_time(t1) / reps
 
 
+def _time_graph_stats(graph, reps):
+    """Per-replay HIP-event times (ms) of `reps` back-to-back replays on the
+    current stream: mean, p10, median and p90."""
+    import torch
+    cur = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    graph.replay()
+    torch.cuda.synchronize()
+    ev[0].record(cur)
+    for i in range(reps):
+        graph.replay()
+        ev[i + 1].record(cur)
+    torch.cuda.synchronize()
+    d = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(reps))
+    return {"mean": ev[0].elapsed_time(ev[-1]) / reps, "p10": _pct(d, 10), "p50": _pct(d, 50), "p90": _pct(d, 90)}
+
+
+def _pct(sorted_vals, q):
+    """Nearest-rank percentile of an ascending list."""
+    i = min(len(sorted_vals) - 1, max(0, math.ceil(q / 100 * len(sorted_vals)) - 1))
+    return sorted_vals[i]
+
+
 def _capture(fn, stream):
     import torch
     fn()
@@ -151,25 +188,172 @@ def _capture(fn, stream):
     return g
 
 
-def cpu_baseline(layer_cpu, xs_cpu, budget_s=20.0):
-    """The oracle's CPU restatement of the reference path over whole decode
-    steps, as many as fit in about budget_s (at least one), on torch's
-    default intra-op thread count."""
-    from oracle import qlora_ref as R
+def _cpu_threads():
+    """Host threads for the CPU leg: the process's OpenMP share (the GPU box
+    gives one GPU's job a share of its cores through OMP_NUM_THREADS), else
+    every core os.cpu_count() reports."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return int(env) if env.isdigit() and int(env) > 0 else (os.cpu_count() or 1)
 
+
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _cpu_time(fn, runs=10, warmup=2):
+    """time.perf_counter() median (and p10 / p90) of `runs` calls after
+    `warmup` calls, in seconds."""
+    for _ in range(warmup):
+        fn()
+    d = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        d.append(time.perf_counter() - t0)
+    d.sort()
+    return {"median": d[len(d) // 2], "p10": _pct(d, 10), "p90": _pct(d, 90), "runs": runs}
+
+
+def cpu_baselines(layer_cpu, xs_cpu, M, gpu):
+    """The oracle's CPU restatement of the reference's CPU path (dequantize ->
+    .to(x.dtype) -> F.linear + LoRA; the NF4 / double-quant codec; INT8 and
+    FP8 dequantize-then-matmul), timed on this host's cores: 2 warm-up calls,
+    median of 10.  Config 3 (the headline decode step) runs whole; the other
+    configurations run a sample of whole rows or blocks (every operation is
+    per row or per block, so time scales with the sample), stated in each
+    entry.  `gpu` holds the GPU time of the same work where bench.py measured
+    it."""
+    import torch
+    from oracle import qlora_ref as R
+    threads = _cpu_threads()
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(2024)
+    out = {"threads": torch.get_num_threads(), "os_cpu_count": os.cpu_count(), "cpu_model": _cpu_model(),
+           "timing": "time.perf_counter, 2 warm-ups, median (p10 / p90) of 10 runs", "seed": 2024}
+
+    def entry(t, work, unit, gpu_s=None, note=""):
+        e = {"cpu_ms": round(t["median"] * 1e3, 3), "cpu_ms_p10": round(t["p10"] * 1e3, 3),
+             "cpu_ms_p90": round(t["p90"] * 1e3, 3), unit: round(work / t["median"] / (1e9 if unit == "gbs" else 1e12), 4)}
+        if gpu_s:
+            e["gpu_us"] = round(gpu_s * 1e6, 3)
+            e["speedup"] = round(t["median"] / gpu_s, 1)
+        if note:
+            e["sample"] = note
+        return e
+
+    # config 3: one decode step of the seven projections (headline)
     def step():
         for name, K, N in LLAMA3_8B_PROJ:
             packed, absmax, a, b, _, _ = layer_cpu[name]
             R.nf4_lora_linear(xs_cpu[K], packed, absmax, None, a, b, SCALING, N, BLOCK)
+    step_bytes = sum(gemv_bytes(M, N, K) for _, K, N in LLAMA3_8B_PROJ)
+    t3 = _cpu_time(step)
+    out["config3_decode_step"] = entry(t3, step_bytes, "gbs", gpu.get("decode_step_s"),
+                                       f"whole step, M={M}")
+    # config 1: fp32 4096x4096 NF4 + LoRA r=16, M in {1, 16}
+    K1 = N1 = 4096
+    w1 = torch.randn(N1, K1, generator=g) * 0.02
+    p1, s1 = R.quantize_int4(w1, 64)
+    a1 = (torch.rand(RANK, K1, generator=g) * 2 - 1) / math.sqrt(K1)
+    b1 = torch.randn(N1, RANK, generator=g) * 0.01
+    for m in (1, 16):
+        x1 = torch.randn(m, K1, generator=g)
+        t = _cpu_time(lambda: R.nf4_lora_linear(x1, p1, s1, None, a1, b1, SCALING, N1, 64))
+        out[f"config1_m{m}"] = entry(t, gemv_bytes(m, N1, K1), "gbs", gpu.get(f"config1_m{m}_s"), "whole call, fp32")
+    del w1, p1, s1
+    # config 2: codec on 1376 of the 11008 rows (1/8 of the blocks)
+    rows, K2 = 1376, 4096
+    w2 = torch.randn(rows, K2, generator=g) * 0.02
+    n_out = rows * K2 // 1000
+    idx = torch.randperm(rows * K2, generator=g)[:n_out]
+    w2.view(-1)[idx] = (torch.randint(0, 2, (n_out,), generator=g).float() * 2 - 1) * 0.16
+    w2 = w2.to(torch.bfloat16)
+    numel2 = rows * K2
+    codec_bytes = 2 * numel2 + numel2 // 2 + numel2 // 64 + 4 * numel2 // 16384
+    state = {}
 
-    t0 = time.perf_counter()
-    step()  # warm-up, also sizes the sample
-    first = time.perf_counter() - t0
-    n = max(1, min(10, int(budget_s / max(first, 1e-3))))
-    t0 = time.perf_counter()
-    for _ in range(n):
-        step()
-    return (time.perf_counter() - t0) / n, n
+    def enc():
+        state["dq"] = R.double_quantize(w2, 64, 256, True)
+
+    t = _cpu_time(enc)
+    frac = numel2 / (11008 * 4096)
+    out["config2_encode"] = entry(t, codec_bytes, "gbs", gpu["codec_encode_s"] * frac if gpu.get("codec_encode_s") else None,
+                                  f"{rows} of 11008 rows; gpu_us scaled to the same rows")
+    pk, c2, c2s, fp8 = state["dq"]
+    t = _cpu_time(lambda: R.double_dequantize(pk, c2, c2s, (numel2,), 64, 256, fp8).to(torch.bfloat16))
+    out["config2_decode"] = entry(t, codec_bytes, "gbs", gpu["codec_decode_s"] * frac if gpu.get("codec_decode_s") else None,
+                                  f"{rows} of 11008 rows; gpu_us scaled to the same rows")
+    del w2, state
+    # config 4: q projection (4096 -> 4096) forward and dX at M = 2048, r = 64
+    K4 = N4 = 4096
+    w4 = torch.randn(N4, K4, generator=g) * 0.02
+    p4, s4 = R.quantize_int4(w4, 64)
+    a4 = (torch.rand(GEMM_RANK, K4, generator=g) * 2 - 1) / math.sqrt(K4)
+    b4 = torch.randn(N4, GEMM_RANK, generator=g) * 0.01
+    x4 = torch.randn(GEMM_M, K4, generator=g).to(torch.bfloat16)
+    dy4 = (torch.randn(GEMM_M, N4, generator=g) * 1e-2).to(torch.bfloat16)
+    sc4 = GEMM_ALPHA / GEMM_RANK
+    fl = gemm_flops(GEMM_M, N4, K4, GEMM_RANK)
+    t = _cpu_time(lambda: R.nf4_lora_linear(x4, p4, s4, None, a4, b4, sc4, N4, 64), runs=10)
+    out["config4_q_fwd"] = entry(t, fl, "tflops", gpu.get("gemm_q_fwd_s"), "q projection only")
+    t = _cpu_time(lambda: R.nf4_dx(dy4, p4, s4, N4, K4, a4, b4, sc4), runs=10)
+    out["config4_q_dx"] = entry(t, fl, "tflops", gpu.get("gemm_q_dx_s"), "q projection only")
+    del w4, p4, s4, x4, dy4
+    # config 5: 1792 of the 28672 output rows, M = 1
+    K5, N5, n5 = 8192, 28672, 1792
+    w5 = (torch.randn(n5, K5, generator=g) * 0.02).to(torch.bfloat16)
+    x5 = torch.randn(1, K5, generator=g).to(torch.bfloat16)
+    q5, sc5 = R.quantize_int8(w5, per_channel=True)
+    b5 = n5 * K5 + 4 * n5 + 2 * K5 + 2 * n5
+    f = n5 / N5
+    t = _cpu_time(lambda: R.int8_linear(x5, q5, sc5))
+    out["config5_int8_m1"] = entry(t, b5, "gbs", gpu["int8_m1_s"] * f if gpu.get("int8_m1_s") else None,
+                                   f"{n5} of {N5} rows; gpu_us scaled to the same rows")
+    t = _cpu_time(lambda: R.fp8_linear(x5, w5))
+    out["config5_fp8_m1"] = entry(t, b5, "gbs", gpu["fp8_m1_s"] * f if gpu.get("fp8_m1_s") else None,
+                                  f"{n5} of {N5} rows, W quantized per call as the reference does; "
+                                  f"gpu_us scaled to the same rows")
+    return out, t3
+
+
+def bench_config1(dev, stream):
+    """Config 1 on the GPU: one NF4 QuantLinear 4096 -> 4096 with LoRA r = 16,
+    alpha = 32 on fp32 activations (the fp32-MFMA path), M in {1, 16}; fp32
+    weights N(0,0.02) quantized with block 64 and fp32 absmax, 20 replays of
+    a graph of 8 calls over 8 weight copies."""
+    import torch
+    from rocm_qlora import ops
+    from rocm_qlora.quantization import quantize_int4
+    K = N = 4096
+    g = torch.Generator(device=dev).manual_seed(13)
+    ws = []
+    for _ in range(8):
+        w = torch.randn(N, K, generator=g, device=dev) * 0.02
+        p, s_ = quantize_int4(w, BLOCK)
+        a = (torch.rand(RANK, K, generator=g, device=dev) * 2 - 1) / math.sqrt(K)
+        b = torch.randn(N, RANK, generator=g, device=dev) * 0.01
+        ws.append((p, s_, a, b))
+        del w
+    out = {"workload": f"NF4 {K}x{N} fp32 activations, LoRA r={RANK} alpha={ALPHA}, block {BLOCK} fp32 absmax"}
+    for m in (1, 16):
+        x = torch.randn(m, K, generator=g, device=dev)
+        gr = _capture(lambda: [ops.nf4_linear(x, p, s_, N, BLOCK, lora_a=a, lora_b=b, scaling=SCALING)
+                               for p, s_, a, b in ws], stream)
+        with _Range(f"rq-config1 fp32 M={m}"):
+            t = _time_graph_stats(gr, 20)
+        del gr
+        us = t["p50"] * 1e3 / len(ws)
+        out[f"m{m}"] = {"us": round(us, 2), "gbs": round(gemv_bytes(m, N, K) / (us * 1e-6) / 1e9, 1),
+                        "frac": round(gemv_bytes(m, N, K) / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+    return out
 
 
 def bench_gemm(dev, stream):
@@ -282,18 +466,20 @@ def bench_byte_linears(dev, stream):
                 fn = lambda: [ops.fp8_linear(x, cw, sc) for cw, sc in fp8_w[:copies]]
             gr = _capture(fn, stream)
             with _Range(f"rq-{kind}-linear M={M} K={K} N={N}"):
-                us = _time_graph(gr, 10) * 1e3 / copies
+                t = _time_graph_stats(gr, 20)
             del gr
+            us = t["p50"] * 1e3 / copies
+            pct = {"p10_us": round(t["p10"] * 1e3 / copies, 2), "p90_us": round(t["p90"] * 1e3 / copies, 2)}
             if M == 1:
                 nb = N * K + 4 * N + 2 * M * K + 2 * M * N
                 gbs = nb / us / 1e3
                 out[f"{kind}_m{M}"] = {"us": round(us, 2), "gbs": round(gbs, 1),
-                                        "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm"}
+                                        "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm", **pct}
             else:
                 tf = 2 * M * N * K / us / 1e6
                 peak, bound = (BF16_PEAK_TFLOPS, "bf16 mfma") if kind == "int8" else (FP8_PEAK_TFLOPS, "fp8 mfma")
                 out[f"{kind}_m{M}"] = {"us": round(us, 2), "tflops": round(tf, 1),
-                                        "frac": round(tf / peak, 4), "bound": bound}
+                                        "frac": round(tf / peak, 4), "bound": bound, **pct}
         del x
     return {"workload": f"INT8 per-row and FP8 per-tensor linears, K={K} N={N}, bf16 activations", **out}
 
@@ -456,31 +642,83 @@ def main():
     n_copies = max(2, math.ceil(520e6 / layer_bytes / 2) * 2)
     layers = [make_layer(dev, 1000 + c) for c in range(n_copies)]
     gx = torch.Generator(device=dev).manual_seed(7)
-    xs = {K: torch.randn(M, K, generator=gx, device=dev).to(torch.bfloat16) for K in (4096, 14336)}
     stream = torch.cuda.Stream()
 
-    def step(layer):
-        for name, K, N in LLAMA3_8B_PROJ:
-            packed, absmax, a, b, _, _ = layer[name]
-            ops.nf4_linear(xs[K], packed, absmax, N, BLOCK, lora_a=a, lora_b=b, scaling=SCALING)
+    def decode_graphs(m):
+        xs = {K: torch.randn(m, K, generator=gx, device=dev).to(torch.bfloat16) for K in (4096, 14336)}
 
-    graphs = [_capture(lambda L=layer: step(L), stream) for layer in layers]
-    for i in range(args.warmup):
-        graphs[i % n_copies].replay()
-    torch.cuda.synchronize()
-    cur = torch.cuda.current_stream()
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    with _Range("rq-decode-step"):
-        t0.record(cur)
-        for i in range(args.steps):
+        def step(layer):
+            for name, K, N in LLAMA3_8B_PROJ:
+                packed, absmax, a, b, _, _ = layer[name]
+                ops.nf4_linear(xs[K], packed, absmax, N, BLOCK, lora_a=a, lora_b=b, scaling=SCALING)
+
+        return xs, [_capture(lambda L=layer: step(L), stream) for layer in layers]
+
+    def time_steps(graphs, steps, warmup):
+        """`steps` back-to-back step replays (rotating layer copies) between
+        two synchronizations, an event after each: (total ms, per-step ms)."""
+        for i in range(warmup):
             graphs[i % n_copies].replay()
-        t1.record(cur)
         torch.cuda.synchronize()
-    ms_step = t0.elapsed_time(t1) / args.steps
+        cur = torch.cuda.current_stream()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        ev[0].record(cur)
+        for i in range(steps):
+            graphs[i % n_copies].replay()
+            ev[i + 1].record(cur)
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[-1]), sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+
+    xs, graphs = decode_graphs(M)
+    with _Range("rq-decode-step"):
+        total_ms, per = time_steps(graphs, args.steps, args.warmup)
+    ms_step = total_ms / args.steps
     step_bytes = sum(gemv_bytes(M, N, K) for _, K, N in LLAMA3_8B_PROJ)
     value = step_bytes / (ms_step * 1e-3) / 1e9
+    step_pct = {"p10_us": round(_pct(per, 10) * 1e3, 2), "p50_us": round(_pct(per, 50) * 1e3, 2),
+                "p90_us": round(_pct(per, 90) * 1e3, 2)}
     del graphs
+
+    # the other decode batch sizes of the configuration (M in {1, 4, 8, 16})
+    decode_m = {}
+    for m in (1, 4, 8, 16):
+        if m == M:
+            continue
+        _, gm = decode_graphs(m)
+        with _Range(f"rq-decode-step M={m}"):
+            tm, pm = time_steps(gm, 50, 10)
+        b = sum(gemv_bytes(m, N, K) for _, K, N in LLAMA3_8B_PROJ)
+        decode_m[f"m{m}"] = {"us_per_step": round(tm / 50 * 1e3, 2), "gbs": round(b / (tm / 50 * 1e-3) / 1e9, 1),
+                             "frac": round(b / (tm / 50 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                             "p10_us": round(_pct(pm, 10) * 1e3, 2), "p90_us": round(_pct(pm, 90) * 1e3, 2)}
+        del gm
+    print("bench: decode " + ", ".join(f"{k} {v['us_per_step']} us" for k, v in decode_m.items()),
+          file=sys.stderr, flush=True)
+
+    # per projection at M: launches of one shape over every layer copy, with
+    # and without the fused LoRA term, beside a minimal launch (a 4-byte fill)
+    per_shape = {}
+    tiny = torch.zeros(1, device=dev)
+    gt = _capture(lambda: [tiny.zero_() for _ in range(n_copies)], stream)
+    with _Range("rq-minimal-launch"):
+        t_min = _time_graph_stats(gt, 20)
+    del gt
+    for name, K, N in LLAMA3_8B_PROJ:
+        ws = [layer[name] for layer in layers]
+        x = xs[K]
+        gl = _capture(lambda: [ops.nf4_linear(x, p, s_, N, BLOCK, lora_a=a, lora_b=b, scaling=SCALING)
+                               for p, s_, a, b, _, _ in ws], stream)
+        gp = _capture(lambda: [ops.nf4_linear(x, p, s_, N, BLOCK) for p, s_, _, _, _, _ in ws], stream)
+        with _Range(f"rq-shape {name} lora M={M} K={K} N={N}"):
+            tl = _time_graph_stats(gl, 20)
+        with _Range(f"rq-shape {name} plain M={M} K={K} N={N}"):
+            tp = _time_graph_stats(gp, 20)
+        del gl, gp
+        nl = len(ws)
+        per_shape[name] = {"lora_us": round(tl["p50"] * 1e3 / nl, 2), "plain_us": round(tp["p50"] * 1e3 / nl, 2),
+                           "lora_gbs": round(gemv_bytes(M, N, K) / (tl["p50"] * 1e-3 / nl) / 1e9, 1),
+                           "plain_gbs": round(kernel_bytes(M, N, K) / (tp["p50"] * 1e-3 / nl) / 1e9, 1)}
+    per_shape["minimal_launch_us"] = round(t_min["p50"] * 1e3 / n_copies, 2)
 
     # roofline of the dominant kernel: plain GEMV launches at the gate/up shape
     K, N = 4096, 14336
@@ -501,6 +739,12 @@ def main():
     print(f"bench: decode {ms_step * 1e3:.1f} us/step, {value:.0f} GB/s; gate/up GEMV {us_launch:.2f} us",
           file=sys.stderr, flush=True)
 
+    gpu_s = {"decode_step_s": ms_step * 1e-3}
+    cfg1 = bench_config1(dev, stream)
+    for k, v in cfg1.items():
+        if isinstance(v, dict):
+            gpu_s[f"config1_{k}_s"] = v["us"] * 1e-6
+
     gemm = None
     if not args.no_gemm:
         del layers
@@ -508,6 +752,8 @@ def main():
         gemm = bench_gemm(dev, stream)
         print(f"bench: GEMM fwd {gemm['fwd_tflops']} TF/s, dX {gemm['dx_tflops']} TF/s", file=sys.stderr,
               flush=True)
+        gpu_s["gemm_q_fwd_s"] = gemm["per_shape"]["q"]["fwd_us"] * 1e-6
+        gpu_s["gemm_q_dx_s"] = gemm["per_shape"]["q"]["dx_us"] * 1e-6
         layer0 = make_layer(dev, 1000)
     else:
         layer0 = layers[0]
@@ -517,22 +763,30 @@ def main():
         codec = bench_codec(dev, stream)
         print(f"bench: codec encode {codec['encode_gbs']} GB/s, decode {codec['decode_gbs']} GB/s",
               file=sys.stderr, flush=True)
+        gpu_s["codec_encode_s"] = codec["encode_us"] * 1e-6
+        gpu_s["codec_decode_s"] = codec["decode_us"] * 1e-6
         torch.cuda.empty_cache()
         byte = bench_byte_linears(dev, stream)
         print("bench: byte linears " + ", ".join(f"{k} {v['us']} us" for k, v in byte.items()
                                                   if isinstance(v, dict)), file=sys.stderr, flush=True)
+        gpu_s["int8_m1_s"] = byte["int8_m1"]["us"] * 1e-6
+        gpu_s["fp8_m1_s"] = byte["fp8_m1"]["us"] * 1e-6
         torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
         layer_cpu = {nm: tuple(t.cpu() if torch.is_tensor(t) else t for t in v) for nm, v in layer0.items()}
         xs_cpu = {k: v.cpu() for k, v in xs.items()}
-        dt, n = cpu_baseline(layer_cpu, xs_cpu)
-        cpu = {"value": round(step_bytes / dt / 1e9, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
-               "kind": "port",
-               "sample": f"{n} decode step(s) of one 7-projection Llama-3-8B layer (M={M}, LoRA r={RANK}) "
+        configs, t3 = cpu_baselines(layer_cpu, xs_cpu, M, gpu_s)
+        cpu = {"value": round(step_bytes / t3["median"] / 1e9, 3), "unit": "GB/s",
+               "cores": configs["threads"], "kind": "port",
+               "sample": f"whole decode steps of one 7-projection Llama-3-8B layer (M={M}, LoRA r={RANK}) "
                          f"through the oracle's torch CPU restatement of dequantize_int4 -> .to(bf16) -> "
-                         f"F.linear + LoRA; {dt * 1e3:.1f} ms/step"}
+                         f"F.linear + LoRA; median of 10 after 2 warm-ups, "
+                         f"{t3['median'] * 1e3:.1f} ms/step; {configs['threads']} threads of "
+                         f"{configs['os_cpu_count']} cores ({configs['cpu_model']})",
+               "configs": configs}
+        print(f"bench: cpu decode step {t3['median'] * 1e3:.1f} ms", file=sys.stderr, flush=True)
 
     traffic = MEASURED_TRAFFIC.get(("nf4_gemv_kernel", M, K, N))
     rec = {
@@ -550,11 +804,14 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"Llama-3-8B decoder layer, 7 NF4 projections, decode dequant-GEMV "
                                f"M={M}, LoRA r={RANK} fused, block {BLOCK} fp32 absmax",
-                   "tokens": M, "layer_copies": n_copies, "step_bytes": step_bytes},
+                   "tokens": M, "layer_copies": n_copies, "step_bytes": step_bytes, **step_pct},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "nf4_gemv_kernel", "shape": f"M={M} K={K} N={N}",
                      "bytes_per_launch": kb, "us_per_launch": round(us_launch, 3)},
+        "decode_m": decode_m,
+        "decode_per_shape": per_shape,
+        "config1": cfg1,
         "gemm": gemm,
         "codec": codec,
         "byte_linears": byte,

@@ -153,12 +153,12 @@ __global__ __launch_bounds__(256) void fp8_absmax16_kernel(const uint16_t* __res
   if (threadIdx.x == 0) part[blockIdx.x] = red[0];
 }
 
-// Reduces the partial maxima and writes the scale; every workgroup of the
-// encode kernel does this for itself (1024 partials, read from L2), so the
-// scale needs no launch of its own.
-__device__ __forceinline__ float scale_from_parts(const float* __restrict__ part, float* red) {
+// Reduces the partial maxima (at most 1024, read from L2); every workgroup
+// of the encode kernel does this for itself, so the scale needs no launch of
+// its own.
+__device__ __forceinline__ float scale_from_parts(const float* __restrict__ part, int nparts, float* red) {
   float m = 0.0f;
-  for (int i = threadIdx.x; i < kFp8AbsmaxBlocks; i += 256) {
+  for (int i = threadIdx.x; i < nparts; i += 256) {
     const float v = part[i];
     m = (v > m || v != v) ? v : m;
   }
@@ -177,9 +177,10 @@ __device__ __forceinline__ float scale_from_parts(const float* __restrict__ part
 template <int DT>
 __global__ __launch_bounds__(256) void fp8_encode16_kernel(const uint16_t* __restrict__ x, int64_t rows,
                                                            int64_t cols, int64_t ld, const float* __restrict__ part,
-                                                           float* __restrict__ scale, uint8_t* __restrict__ codes) {
+                                                           int nparts, float* __restrict__ scale,
+                                                           uint8_t* __restrict__ codes) {
   __shared__ float red[256];
-  const float s = scale_from_parts(part, red);
+  const float s = scale_from_parts(part, nparts, red);
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
   const int64_t gpr = cols / 8, total = rows * gpr;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
@@ -278,22 +279,30 @@ void fp8_gemv_kernel(Fp8Args a) {
 
 // ---------------------------------------------------------------------------
 // GEMM (M > 16): out[M, N] = x[M, K] W[N, K]^T on 256 x 256 workgroup tiles,
-// 64 k per stage, a ring of 4 LDS stages (x tile then W tile, 16 KiB each,
+// 64 k per stage, a ring of 5 LDS stages (x tile then W tile, 16 KiB each,
 // rows of 64 bytes with 16-byte chunk c of row r at chunk c ^ ((r / 4) % 4),
 // so that any 16 consecutive lanes reading one chunk of 16 consecutive rows
 // hit 16 distinct 16-byte bank groups).  Both operands move by direct-to-LDS
-// loads, three stages ahead of the MFMAs.  Eight waves, two per SIMD: wave w
-// owns rows 128 (w % 2) .. +127 and columns 64 (w / 2) .. +63 of the tile as
-// 4 x 2 blocks of the 32x32x64 MFMA; lane (i, h) (i = lane % 32, h =
+// loads, issued four stages ahead of their MFMAs.  Eight waves, two per SIMD:
+// wave w owns rows 128 (w % 2) .. +127 and columns 64 (w / 2) .. +63 of the
+// tile as 4 x 2 blocks of the 32x32x64 MFMA; lane (i, h) (i = lane % 32, h =
 // lane / 32) feeds bytes k = 32 h .. 32 h + 31 of the stage.  D[m][n]: lane
 // (i, h), register r = row 8 (r / 4) + 4 h + r % 4, column i.
+//
+// Iteration j: wait until stages j and j + 1 have landed (this wave's loads;
+// j + 2 and j + 3 may be in flight), barrier (every wave's loads of them too,
+// and every wave is done reading stage j - 1), loads of stage j + 4 into
+// stage j - 1's buffer, then the MFMAs of stage j on operands read in
+// iteration j - 1 while the operands of stage j + 1 are read from LDS.  The
+// matrix cores so never wait for an LDS read after the barrier.  Stages past
+// the end re-load the last stage (in bounds, never used).
 //
 // With xcd_map, XCD x (= workgroup id % 8) takes tiles x T / 8 .. +T / 8 of
 // the m-fastest tile order: the 32 workgroups an XCD runs at a time share
 // their weight columns in its L2.
 // ---------------------------------------------------------------------------
 constexpr int kF8BM = 256, kF8BN = 256, kF8BK = 64;
-constexpr int kF8Stages = 4;
+constexpr int kF8Stages = 5;
 constexpr int kF8Threads = 512;
 constexpr int kF8TileBytes = kF8BM * kF8BK;       // 16 KiB
 constexpr int kF8StageBytes = 2 * kF8TileBytes;   // x tile, W tile
@@ -301,6 +310,10 @@ static_assert(kF8BM == kF8BN, "one DMA lane map serves both operands");
 static_assert(kF8Stages * kF8StageBytes <= 160 * 1024, "LDS plan");
 
 __device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return r * 64u + ((c ^ ((r >> 2) & 3u)) << 4); }
+
+struct Fp8Frags {
+  u32x4 a[4][2], b[2][2];
+};
 
 template <int XT>
 __global__ __launch_bounds__(kF8Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -332,13 +345,32 @@ void fp8_gemm_kernel(Fp8Args a) {
   }
   const uint32_t dst = __builtin_amdgcn_readfirstlane(uint32_t(32 * wave * kF8BK));
   const int nk = int(a.K / kF8BK);
-  auto issue = [&](int ks, int buf) {
-    const uint32_t sb = uint32_t(buf * kF8StageBytes) + dst;
+  auto issue = [&](int ks) {
+    ks = ks < nk ? ks : nk - 1;
+    const uint32_t sb = uint32_t((ks % kF8Stages) * kF8StageBytes) + dst;
     const uint32_t ko = uint32_t(ks) * uint32_t(kF8BK);
     dma16(a.x, xo[0] + ko, sb);
     dma16(a.x, xo[1] + ko, sb + 1024);
     dma16(a.w, wo[0] + ko, sb + kF8TileBytes);
     dma16(a.w, wo[1] + ko, sb + kF8TileBytes + 1024);
+  };
+  // the buffer of stage j is j % kF8Stages; stages past the end sit in the
+  // last stage's buffer
+  const uint32_t arow = uint32_t(128 * wm + i32), brow = uint32_t(64 * wn + i32);
+  auto read = [&](Fp8Frags& f, int j) {
+    j = j < nk ? j : nk - 1;
+    const uint8_t* xt = lds + (j % kF8Stages) * kF8StageBytes;
+    const uint8_t* wt = xt + kF8TileBytes;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        f.b[nb][e] = *reinterpret_cast<const u32x4*>(wt + swz64(brow + 32 * nb, uint32_t(2 * h + e)));
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+        f.a[mb][e] = *reinterpret_cast<const u32x4*>(xt + swz64(arow + 32 * mb, uint32_t(2 * h + e)));
   };
 
   f32x16 acc[4][2];
@@ -349,36 +381,23 @@ void fp8_gemm_kernel(Fp8Args a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
 
-  // stage j lives in buffer j % 4.  Iteration j: wait for this wave's loads
-  // of stage j (stages j + 1, j + 2 may still be in flight), barrier (every
-  // wave's part of stage j has landed and every wave is done with buffer
-  // (j - 1) % 4), loads of stage j + 3 into that buffer (past the end: the
-  // last stage again, in bounds and never read), MFMAs on stage j.
+  // prologue: stages 0 .. 3 in flight, stage 0 read once it has landed
 #pragma unroll
-  for (int s = 0; s < kF8Stages - 1; ++s) issue(s < nk ? s : nk - 1, s);
-  const uint32_t arow = uint32_t(128 * wm + i32), brow = uint32_t(64 * wn + i32);
+  for (int s = 0; s < kF8Stages - 1; ++s) issue(s);
+  step_barrier<4 * (kF8Stages - 2)>();
+  Fp8Frags cur;
+  read(cur, 0);
   for (int j = 0; j < nk; ++j) {
-    step_barrier<4 * (kF8Stages - 2)>();
-    const int jn = j + kF8Stages - 1;
-    issue(jn < nk ? jn : nk - 1, jn % kF8Stages);
-    const uint8_t* xt = lds + (j % kF8Stages) * kF8StageBytes;
-    const uint8_t* wt = xt + kF8TileBytes;
-    u32x4 A[4][2], B[2][2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-#pragma unroll
-      for (int e = 0; e < 2; ++e)
-        B[nb][e] = *reinterpret_cast<const u32x4*>(wt + swz64(brow + 32 * nb, uint32_t(2 * h + e)));
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-      for (int e = 0; e < 2; ++e)
-        A[mb][e] = *reinterpret_cast<const u32x4*>(xt + swz64(arow + 32 * mb, uint32_t(2 * h + e)));
+    step_barrier<4 * (kF8Stages - 3)>();
+    issue(j + kF8Stages - 1);
+    Fp8Frags nxt;
+    read(nxt, j + 1);
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
-        acc[mb][nb] = mfma_fn_32x32x64(A[mb][0], A[mb][1], B[nb][0], B[nb][1], acc[mb][nb]);
+        acc[mb][nb] = mfma_fn_32x32x64(cur.a[mb][0], cur.a[mb][1], cur.b[nb][0], cur.b[nb][1], acc[mb][nb]);
+    cur = nxt;
   }
   wait_vmcnt<0>();  // no load may still be landing in LDS when the workgroup ends
 
@@ -421,15 +440,17 @@ size_t fp8_act_ws_bytes(int64_t M, int64_t K) {
 template <int XT>
 static int fp8_quantize_act(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, float* part, float* scale,
                             uint8_t* codes, hipStream_t stream) {
-  if (M * K <= (int64_t(1) << 18)) {
+  // one workgroup when each of its threads has at most 2 vectors to encode
+  if (M * K <= 16384) {
     fp8_quant_small_kernel<XT><<<1, 1024, 0, stream>>>(x, M, K, ldx, scale, codes);
     return rq_check_launch();
   }
-  fp8_absmax16_kernel<XT><<<kFp8AbsmaxBlocks, 256, 0, stream>>>(x, M, K, ldx, part);
   const int64_t groups = M * (K / 8);
   const int64_t blocks = (groups + 255) / 256;
-  fp8_encode16_kernel<XT><<<unsigned(blocks < 4096 ? blocks : 4096), 256, 0, stream>>>(x, M, K, ldx, part, scale,
-                                                                                      codes);
+  const int nparts = int(blocks < kFp8AbsmaxBlocks ? blocks : kFp8AbsmaxBlocks);
+  fp8_absmax16_kernel<XT><<<unsigned(nparts), 256, 0, stream>>>(x, M, K, ldx, part);
+  fp8_encode16_kernel<XT><<<unsigned(blocks < 4096 ? blocks : 4096), 256, 0, stream>>>(x, M, K, ldx, part, nparts,
+                                                                                      scale, codes);
   return rq_check_launch();
 }
 
