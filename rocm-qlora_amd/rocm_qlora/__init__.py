@@ -8,6 +8,7 @@ time (rocm-qlora_amd/build.py) and loaded on first use.
 """
 __version__ = "5.0.0+mi355x"
 
+from rocm_qlora import torch_ops  # noqa: E402,F401  (registers the rocm_qlora:: operators)
 from rocm_qlora.quantization import (  # noqa: E402
     quantize_int8, dequantize_int8, quantize_int4, dequantize_int4,
     double_quantize, double_dequantize, DoubleQuantState,

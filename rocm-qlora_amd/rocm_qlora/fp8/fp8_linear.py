@@ -17,6 +17,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from rocm_qlora import ops
+from rocm_qlora import torch_ops
 from rocm_qlora.fp8.fp8_config import detect_fp8_support, FP8Config
 from rocm_qlora.lora.lora_layer import LoRALinear
 
@@ -26,13 +27,13 @@ _FNUZ_MAX = 240.0
 def _fp8_forward(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor],
                  w_q: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
     if x.dtype in (torch.bfloat16, torch.float16):
-        wc, ws = w_q if w_q is not None else ops.fp8_quantize(w)
-        return ops.fp8_linear(x, wc, ws, bias)
+        wc, ws = w_q if w_q is not None else torch_ops.call_fp8_quantize(w)
+        return torch_ops.call_fp8_linear(x, wc, ws, bias)
     # fp32 activations: the same codes and scales from the HIP quantizer,
     # decoded and multiplied by the library GEMM in fp32
     x2 = x.reshape(-1, x.shape[-1])
-    xc, xs = ops.fp8_quantize(x2)
-    wc, ws = w_q if w_q is not None else ops.fp8_quantize(w)
+    xc, xs = torch_ops.call_fp8_quantize(x2)
+    wc, ws = w_q if w_q is not None else torch_ops.call_fp8_quantize(w)
     out = (xc.to(torch.float32) * xs) @ (wc.to(torch.float32) * ws).T
     out = out.to(x.dtype).reshape(*x.shape[:-1], -1)
     return out + bias if bias is not None else out

@@ -21,8 +21,8 @@ from typing import Optional
 import torch
 import torch.nn.functional as F
 
-from rocm_qlora import ops
 from rocm_qlora import _native as nat
+from rocm_qlora import torch_ops
 
 # activation dtypes of the fused forward kernels (fp32: the fp32-MFMA path)
 _KERNEL_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
@@ -140,9 +140,9 @@ class _FusedNF4LinearFunc(torch.autograd.Function):
         ctx.mask_scale = 1.0 / (1.0 - dropout_p) if mask is not None else 1.0
         ctx.save_for_backward(x if lora else None, lora_a if lora else None, lora_b if lora else None,
                               xl, mask)
-        return ops.nf4_linear(x, w.packed, w.scales, w.N, w.block_size, bias,
-                              lora_a=lora_a if lora else None, lora_b=lora_b if lora else None,
-                              scaling=scaling, lora_x=xl, **w.dq_kwargs())
+        return torch_ops.call_nf4_linear(x, w.packed, w.scales, w.N, w.block_size, bias,
+                                         lora_a=lora_a if lora else None, lora_b=lora_b if lora else None,
+                                         scaling=scaling, lora_x=xl, **w.dq_kwargs())
 
     @staticmethod
     def backward(ctx, dy):
@@ -153,9 +153,9 @@ class _FusedNF4LinearFunc(torch.autograd.Function):
         dx = da = db = None
         if need_x:
             if w.dx_ok(dy.dtype):
-                dx = ops.nf4_linear_dx(dy, w.packed, w.scales, w.K, w.block_size,
-                                       lora_a=A, lora_b=B, scaling=s, lora_mask=mask,
-                                       mask_scale=ctx.mask_scale, **w.dq_kwargs())
+                dx = torch_ops.call_nf4_linear_dx(dy, w.packed, w.scales, w.K, w.block_size,
+                                                  lora_a=A, lora_b=B, scaling=s, lora_mask=mask,
+                                                  mask_scale=ctx.mask_scale, **w.dq_kwargs())
             else:
                 dx = dy @ w.dense(dy.dtype)
                 if ctx.lora:
@@ -185,7 +185,7 @@ class _FusedInt8LinearFunc(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, bias, w: Int8Weight):
         ctx.w = w
-        return ops.int8_linear(x, w.q, w.scales, w.N, w.block_size, bias)
+        return torch_ops.call_int8_linear(x, w.q, w.scales, w.N, w.block_size, bias)
 
     @staticmethod
     def backward(ctx, dy):

@@ -252,3 +252,28 @@ def test_estimate_double_quant_savings_closed_form():
     from rocm_qlora.quantization import estimate_double_quant_savings
     r = estimate_double_quant_savings(torch.empty(4096 * 4096))
     assert abs(r["bits_saved_per_param"] - 0.373046875) < 1e-9
+
+
+def test_custom_operators_registered_with_fake_shapes():
+    """The HIP entry points are torch.library custom operators whose fake
+    implementations give the output shapes and dtypes (what torch.compile
+    traces with)."""
+    import rocm_qlora  # noqa: F401  (registers the operators)
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    for name in ("nf4_linear", "nf4_linear_dx", "int8_linear", "fp8_quantize", "fp8_linear"):
+        assert hasattr(torch.ops.rocm_qlora, name)
+    with FakeTensorMode():
+        x = torch.empty(3, 5, 256, dtype=torch.bfloat16)
+        p = torch.empty(64 * 128, dtype=torch.uint8)
+        s = torch.empty(256)
+        y = torch.ops.rocm_qlora.nf4_linear(x, p, s, 64, 64, None, None, None, 256, True, None, None, 0.0, None)
+        assert y.shape == (3, 5, 64) and y.dtype == torch.bfloat16
+        d = torch.ops.rocm_qlora.nf4_linear_dx(y, p, s, 256, 64, None, None, 256, True, None, None, 0.0, None, 1.0)
+        assert d.shape == (3, 5, 256) and d.dtype == torch.bfloat16
+        q = torch.empty(64, 256, dtype=torch.int8)
+        y8 = torch.ops.rocm_qlora.int8_linear(x, q, torch.empty(64), 64, 0, None)
+        assert y8.shape == (3, 5, 64)
+        c, sc = torch.ops.rocm_qlora.fp8_quantize(x)
+        assert c.shape == (15, 256) and c.dtype == torch.float8_e4m3fnuz and sc.shape == () and sc.dtype == torch.float32
+        yf = torch.ops.rocm_qlora.fp8_linear(x, torch.empty(64, 256, dtype=torch.float8_e4m3fn), sc, None)
+        assert yf.shape == (3, 5, 64) and yf.dtype == torch.bfloat16
