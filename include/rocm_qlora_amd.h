@@ -33,6 +33,14 @@ extern "C" {
 #define RQ_C2_FP8_E4M3FNUZ 0   /* torch.float8_e4m3fnuz codes */
 #define RQ_C2_INT8         1   /* round(c1 / c2s * 127) int8 fallback */
 
+/* weight formats of rq_merge_lora */
+#define RQ_WEIGHT_NF4      0   /* flat packed NF4 codes, two per byte */
+#define RQ_WEIGHT_INT8     1   /* flat int8 codes */
+
+/* rounding of rq_merge_lora */
+#define RQ_MERGE_SUM_THEN_ROUND  0   /* RND(W + d): LoRALinear.merge_lora */
+#define RQ_MERGE_ROUND_THEN_SUM  1   /* RND(RND(W) + RND(d)): the export path */
+
 /* status codes */
 #define RQ_OK                 0
 #define RQ_ERR_NULL_POINTER   1
@@ -288,6 +296,32 @@ int rq_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   const uint8_t* w_codes, int64_t N, const float* w_scale,
                   const void* bias, int bias_dtype, void* y, int64_t ldy,
                   void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Merged LoRA weights
+ * ------------------------------------------------------------------------ */
+
+/* Replaces the dequantize-then-add of LoRALinear.merge_lora
+ * (lora/lora_layer.py:72-106) and of the export path's _export_dequant_layer
+ * (export/gguf_export.py:30-79): a 16-bit [N, K] weight
+ *   mode RQ_MERGE_SUM_THEN_ROUND: out = RND_o(W + d)
+ *   mode RQ_MERGE_ROUND_THEN_SUM: out = RND_o(RND_o(W) + RND_o(d))
+ * with W the fp32 dequantized base weight (NF4: T[code] * scale, the scale
+ * c2 * c2_scale when c2 is non-NULL; INT8: float(q) * scale) and d =
+ * RND_L(RND_L(B A) * scaling) the LoRA delta in the adapters' dtype L (the
+ * sum over the rank an fp32 fma chain in ascending rank order), RND_o the
+ * rounding to out_dtype (bf16 or fp16).
+ *   w: flat codes (RQ_WEIGHT_NF4: packed, byte e / 2 holds element e's code
+ *   in its low (even e) or high nibble; RQ_WEIGHT_INT8: int8), element
+ *   n * K + k; block_size: a power of two (INT8: 0 = one scale per row);
+ *   scales: [N*K / block_size] (per row: [N]) of scales_dtype, or with c2
+ *   the c2_scales [ceil(blocks / block2)]; c2: [blocks] codes or NULL;
+ *   lora_a [rank, K], lora_b [N, rank] of row stride ld_lora_b, both of
+ *   lora_dtype (rank 0: no delta); out [N, K] of row stride ld_out. */
+int rq_merge_lora(const void* w, int w_format, int64_t N, int64_t K, int64_t block_size,
+                  const void* scales, int scales_dtype, const uint8_t* c2, int c2_format, int64_t block2,
+                  const void* lora_a, const void* lora_b, int64_t ld_lora_b, int lora_dtype, int64_t rank,
+                  float scaling, int mode, void* out, int out_dtype, int64_t ld_out, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,10 @@ tests/test_oracle_linear.py:
     weight columns, bias and the s * B A[:, k] adapter term exactly.
   * nf4_dx: float64 dY W + s dY B A.
   * lora_linear_grads: float64 central differences of sum(dY * y).
+  * merge_lora_weight / export_dequant_layer: zero adapters give the
+    dequantized weight cast to fp16; dyadic adapters (exact in fp32) against
+    float64 sums rounded once (merge) or twice then added in float64 and
+    rounded once (export).
   * int8_linear: float64 x (q s)^T and linearity in the row scale.
   * fp8_linear: decode-then-matmul with each scale applied once (exact), and
     closeness to the unquantized product.
@@ -218,6 +222,27 @@ def fp8_linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = 
     if bias is not None:
         y = y + bias
     return y
+
+
+# ----------------------------------------------------------- merge / export
+def merge_lora_weight(w_flat: torch.Tensor, lora_a: torch.Tensor, lora_b: torch.Tensor, scaling: float,
+                      out_features: int, in_features: int) -> torch.Tensor:
+    """LoRALinear.merge_lora (lora_layer.py:80-103): delta = (B @ A) * s, the
+    fp32 dequantized weight sliced and reshaped, fp32 + delta cast to its
+    dtype, then .to(float16)."""
+    delta = (lora_b @ lora_a) * scaling                                    # :82
+    base = w_flat[:out_features * in_features].reshape(out_features, in_features)  # :99-100
+    return (base + delta.to(base.dtype)).to(torch.float16)                 # :103
+
+
+def export_dequant_layer(w_flat: torch.Tensor, lora_a: torch.Tensor, lora_b: torch.Tensor, scaling: float,
+                         out_features: int, in_features: int) -> torch.Tensor:
+    """_export_dequant_layer (export/gguf_export.py:53-77): the dequantized
+    weight reshaped and cast to fp16, the delta (B @ A) * s cast to fp16, and
+    the two fp16 tensors added."""
+    w = w_flat.reshape(out_features, in_features).to(torch.float16)       # :69
+    delta = ((lora_b @ lora_a) * scaling).to(torch.float16)               # :73-74
+    return w + delta                                                        # :77
 
 
 class _DropoutWithMask(torch.autograd.Function):

@@ -19,6 +19,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 # dtype codes (include/rocm_qlora_amd.h)
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 C2_FP8_E4M3FNUZ, C2_INT8 = 0, 1
+WEIGHT_NF4, WEIGHT_INT8 = 0, 1
+MERGE_SUM_THEN_ROUND, MERGE_ROUND_THEN_SUM = 0, 1
 
 _P, _I64, _I32, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 
@@ -59,6 +61,10 @@ SIGNATURES = {
     "rq_int8_linear": [_P, _I32, _I64, _I64, _I64,           # x, dtype, M, K, ldx
                        _P, _I64, _I64, _P, _I32,             # q, N, block, scales, dtype
                        _P, _I32, _P, _I64, _P],              # bias, dtype, y, ldy, stream
+    "rq_merge_lora": [_P, _I32, _I64, _I64, _I64,           # w, format, N, K, block
+                      _P, _I32, _P, _I32, _I64,             # scales, dtype, c2, c2 format, block2
+                      _P, _P, _I64, _I32, _I64, _F32,       # A, B, ldB, dtype, rank, scaling
+                      _I32, _P, _I32, _I64, _P],            # mode, out, dtype, ld, stream
     "rq_fp8_quantize_workspace_size": [_P],
     "rq_fp8_quantize": [_P, _I32, _I64, _I64, _I64, _P, _P, _P, _I64, _P],
     "rq_fp8_fnuz_to_e4m3fn": [_P, _I64, _P, _P],

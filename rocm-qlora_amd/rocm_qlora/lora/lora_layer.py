@@ -69,9 +69,10 @@ class LoRALinear(nn.Module):
         unmerge_lora cannot restore the adapted layer; here it does)."""
         if self.merged:
             raise RuntimeError("LoRA already merged")
-        delta = (self.lora_B @ self.lora_A) * self.scaling
-        base_w = self.base_layer.dequantized_weight(torch.float32)
-        merged = (base_w + delta.to(base_w.dtype)).to(torch.float16)
+        # one kernel: RND_fp16(W_deq + RND(RND(B @ A) * s)) from the quantized
+        # buffers (double quantization included)
+        merged = self.base_layer.merged_weight(self.lora_A, self.lora_B, self.scaling, "sum_then_round",
+                                               torch.float16)
         self.base_layer.merged_fp16_weight = merged
         self.base_layer.merged_mode = True
         self.merged = True

@@ -362,3 +362,58 @@ def fp8_linear(x: torch.Tensor, w_codes: torch.Tensor, w_scale: torch.Tensor,
                  nat.dtype_code(b.dtype) if b is not None else 0,
                  y.data_ptr(), N, ws.data_ptr(), ws.numel(), nat.stream_handle(dev))
     return y.reshape(*lead, N)
+
+
+MERGE_MODES = {"sum_then_round": nat.MERGE_SUM_THEN_ROUND, "round_then_sum": nat.MERGE_ROUND_THEN_SUM}
+
+
+def merge_lora(weight_quant: torch.Tensor, weight_scales: torch.Tensor, out_features: int, in_features: int,
+               block_size: int = 64, lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
+               scaling: float = 0.0, *, bits: int = 4, c2: Optional[torch.Tensor] = None,
+               use_fp8_c2: bool = True, blocksize_2: int = 256, mode: str = "sum_then_round",
+               out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """[out, in] 16-bit weight of dequant(W) + (B @ A) * scaling, straight
+    from the quantized buffers in one kernel.  mode "sum_then_round":
+    RND(W + d) as LoRALinear.merge_lora rounds it (lora_layer.py:84-103);
+    "round_then_sum": RND(RND(W) + RND(d)) as the export path does
+    (export/gguf_export.py:53-77).  bits 4: NF4 codes with per-block absmax,
+    or c2 codes with weight_scales = c2_scales under double quantization;
+    bits 8: int8 codes, block_size 0 meaning one scale per row."""
+    N, K = int(out_features), int(in_features)
+    dev = nat.require_gpu(weight_quant, weight_scales, lora_a, lora_b, c2)
+    if mode not in MERGE_MODES:
+        raise ValueError(f"mode must be one of {sorted(MERGE_MODES)}, got {mode!r}")
+    if out_dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError(f"out_dtype must be float16 or bfloat16, got {out_dtype}")
+    w = weight_quant.reshape(-1).contiguous()
+    if bits == 4:
+        fmt = nat.WEIGHT_NF4
+        if w.dtype != torch.uint8 or w.numel() * 2 < N * K:
+            raise RuntimeError(f"NF4 weight_quant must hold {N}x{K} codes as uint8")
+    elif bits == 8:
+        fmt = nat.WEIGHT_INT8
+        if w.dtype != torch.int8 or w.numel() < N * K:
+            raise RuntimeError(f"INT8 weight_quant must hold {N}x{K} int8 values")
+    else:
+        raise ValueError(f"bits must be 4 or 8, got {bits}")
+    sc = weight_scales.reshape(-1).contiguous()
+    rank = 0
+    la = lb = None
+    ldb = lcode = 0
+    if lora_a is not None and lora_b is not None and lora_a.shape[0] > 0:
+        rank = lora_a.shape[0]
+        if lora_a.shape[1] != K or lora_b.shape != (N, rank):
+            raise RuntimeError(f"LoRA shapes {tuple(lora_a.shape)} / {tuple(lora_b.shape)} do not fit {N}x{K}")
+        if lora_b.dtype != lora_a.dtype:
+            lora_b = lora_b.to(lora_a.dtype)
+        la = lora_a.detach().contiguous()
+        lb, ldb = _rows(lora_b.detach(), rank)
+        lcode = nat.dtype_code(la.dtype)
+    codes = c2.reshape(-1).view(torch.uint8).contiguous() if c2 is not None else None
+    with on(dev):
+        out = torch.empty((N, K), dtype=out_dtype, device=dev)
+        nat.call("rq_merge_lora", w.data_ptr(), fmt, N, K, block_size, sc.data_ptr(), nat.dtype_code(sc.dtype),
+                 nat.ptr(codes), nat.C2_FP8_E4M3FNUZ if use_fp8_c2 else nat.C2_INT8, blocksize_2,
+                 nat.ptr(la), nat.ptr(lb), ldb, lcode, rank, float(scaling), MERGE_MODES[mode],
+                 out.data_ptr(), nat.dtype_code(out_dtype), K, nat.stream_handle(dev))
+    return out

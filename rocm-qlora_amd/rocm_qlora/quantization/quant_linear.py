@@ -118,6 +118,20 @@ class QuantLinear(nn.Module):
         w = self.nf4_weight() if self.bits == 4 else self.int8_weight()
         return w.dense(dtype)
 
+    def merged_weight(self, lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
+                      scaling: float = 0.0, mode: str = "sum_then_round",
+                      dtype: torch.dtype = torch.float16) -> torch.Tensor:
+        """[out, in] 16-bit weight of the dequantized weight plus (B @ A) *
+        scaling, from the quantized buffers in one kernel (ops.merge_lora:
+        "sum_then_round" as merge_lora rounds, "round_then_sum" as the export
+        path does)."""
+        from rocm_qlora import ops
+        dq = self.bits == 4 and self.use_double_quant
+        return ops.merge_lora(self.weight_quant, self.c2_scales if dq else self.weight_scales, self.out_features,
+                              self.in_features, self.block_size, lora_a, lora_b, scaling, bits=self.bits,
+                              c2=self.c2 if dq else None, use_fp8_c2=getattr(self, "use_fp8_c2", True),
+                              blocksize_2=getattr(self, "blocksize_2", 256), mode=mode, out_dtype=dtype)
+
     def fused_forward(self, x: torch.Tensor, lora_a: Optional[torch.Tensor] = None,
                       lora_b: Optional[torch.Tensor] = None, scaling: float = 0.0,
                       dropout_p: float = 0.0) -> torch.Tensor:

@@ -151,3 +151,28 @@ def test_lora_grads_with_dropout_mask():
     mk = torch.rand(64, generator=g) > 0.1
     dropped = R._DropoutWithMask.apply(xb, mk, 1.0 / 0.9)
     assert torch.equal(dropped, (xb.float() * mk.float() * (1.0 / 0.9)).to(torch.bfloat16))
+
+
+def _dyadic(shape, g, scale_pow):
+    """Integers in [-8, 8] times 2^-scale_pow: products and rank sums stay
+    exact in fp32, so the delta does not depend on the summation order."""
+    return torch.randint(-8, 9, shape, generator=g).to(torch.float32) * 2.0 ** -scale_pow
+
+
+def test_merge_and_export_restatements_pinned():
+    """merge_lora_weight rounds W + d once to fp16; export_dequant_layer
+    rounds W and d to fp16 and adds them (float64 sum of two fp16 values,
+    rounded once).  Zero adapters give the dequantized weight cast to fp16."""
+    g = torch.Generator().manual_seed(81)
+    N, K, r, s = 24, 128, 5, 2.0
+    w = torch.randn(N * K, generator=g) * 0.02
+    a, b = _dyadic((r, K), g, 6), _dyadic((N, r), g, 7)
+    d64 = (b.double() @ a.double()) * s                       # exact, as is the fp32 product
+    want_merge = (w.double().reshape(N, K) + d64).float().to(torch.float16)
+    assert torch.equal(R.merge_lora_weight(w, a, b, s, N, K).view(torch.int16), want_merge.view(torch.int16))
+    w16 = w.reshape(N, K).to(torch.float16)
+    want_export = (w16.double() + d64.to(torch.float16).double()).to(torch.float16)
+    assert torch.equal(R.export_dequant_layer(w, a, b, s, N, K).view(torch.int16), want_export.view(torch.int16))
+    z = torch.zeros(N, r)
+    for fn in (R.merge_lora_weight, R.export_dequant_layer):
+        assert torch.equal(fn(w, a, z, s, N, K), w16)
