@@ -84,16 +84,21 @@ struct Byte8Producer {
 };
 
 // ---------------------------------------------------------------------------
-// Decode GEMV for M <= 16 rows of activations.  Wave w of a workgroup owns
-// 16 weight rows; lane (i, q) (i = lane % 16, q = lane / 16) streams 16
-// bytes of row i per 64-k step (k = 16 q .. 16 q + 15 of the step, so a
-// wave instruction reads 16 rows x 64 contiguous bytes) and feeds them as
-// two v_mfma_f32_16x16x32 A operands (k order 16 q + e and 16 q + 8 + e,
-// the activation operand uses the same order).  D[n][m] = sum_k W[n][k]
-// x[m][k]: lane (i, q), register r holds row n = 4 q + r, activation row
-// m = i.
+// Decode GEMV for M <= 16 rows of activations.  Workgroup: 16 weight rows n0
+// .. n0 + 15 and all of K, sixteen waves, wave w the k chunks w, w + 16, ...
+// of 256 k.  A chunk is 4 pieces of 64 k; lane (i, g) (i = lane % 16, g =
+// lane / 16) loads 16 bytes of row n0 + i per piece, k = 64 t + 16 g .. +15,
+// and feeds them as two 16x16x32 MFMA steps (h = 0, 1: bytes 8 h .. 8 h + 7);
+// the activation operand (row i, zero for i >= M) takes the same k, so step
+// (t, h) sums k = 64 t + 16 g + 8 h + e over g and e -- inside one 64-k block
+// of the weight's scales.  Weights are decoded exactly, RND(float(q) * s), as
+// the MFMA's B operand; D[m][n]: lane (i, g), register r = (row 4 g + r,
+// column n0 + i).  The waves' sums meet in LDS and wave 0 adds them in wave
+// order.  A wave holds its chunk's activations (32 VGPRs) and weights (16).
 // ---------------------------------------------------------------------------
-constexpr int kByteGemvDepth = 8;  // 64-k steps of weights in flight per lane
+constexpr int kByteGvWaves = 16;
+constexpr int kByteGvChunk = 256;   // k per wave chunk
+constexpr int kByteGvPieces = kByteGvChunk / 64;
 
 struct ByteGemvArgs {
   const uint16_t* x;   // [M][K] activation rows
@@ -109,59 +114,68 @@ struct ByteGemvArgs {
 };
 
 template <int XT, class Scale>
-__global__ __launch_bounds__(256) void byte_gemv_kernel(ByteGemvArgs a, Scale scale) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int i16 = lane & 15, q4 = lane >> 4;
-  const int64_t n0 = (int64_t(blockIdx.x) * 4 + wave) * 16;
+__global__ __launch_bounds__(64 * kByteGvWaves) void byte_gemv_kernel(ByteGemvArgs a, Scale scale) {
+  __shared__ f32x4 red[kByteGvWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
+  const int i16 = lane & 15, g4 = lane >> 4;
+  const int64_t n0 = int64_t(blockIdx.x) * 16;
   int64_t n = n0 + i16;
   n = n < a.N ? n : a.N - 1;  // rows past N re-read a live row; never stored
-  const uint8_t* wr = a.w + n * a.K + 16 * q4;
   const bool mlive = i16 < a.M;
-  const uint16_t* xr = a.x + (mlive ? int64_t(i16) : 0) * a.ldx + 16 * q4;
-  const int64_t nk = a.K / 64;
+  const uint8_t* wr = a.w + n * a.K + 16 * g4;
+  const uint16_t* xr = a.x + (mlive ? int64_t(i16) : 0) * a.ldx + 16 * g4;
   const int64_t sb = n * a.blocks_per_row;
-
-  u32x4 wq[kByteGemvDepth];
-  typename Scale::Raw sq[kByteGemvDepth];
-#pragma unroll
-  for (int d = 0; d < kByteGemvDepth; ++d) {
-    const int64_t kt = d < nk ? d : nk - 1;
-    wq[d] = *reinterpret_cast<const u32x4*>(wr + kt * 64);
-    sq[d] = scale.load(sb + ((kt * 64) >> a.bs_log2));
-  }
+  const int64_t nchunks = (a.K + kByteGvChunk - 1) / kByteGvChunk;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int64_t kt = 0; kt < nk; kt += kByteGemvDepth) {
+  for (int64_t c = wave; c < nchunks; c += kByteGvWaves) {
+    const int64_t kb = c * kByteGvChunk;
+    // piece t covers k = kb + 64 t .. + 63; a piece at or past K is zero in
+    // both operands (its loads stay inside the row)
+    u32x4 wq[kByteGvPieces], xa[kByteGvPieces][2];
+    typename Scale::Raw sq[kByteGvPieces];
 #pragma unroll
-    for (int d = 0; d < kByteGemvDepth; ++d) {
-      const int64_t k = kt + d;
-      if (k >= nk) break;
-      const u32x4 w = wq[d];
-      const float s = scale.value(sq[d]);
-      // activation operands of this step (rows >= M are zero)
-      u32x4 xb0 = *reinterpret_cast<const u32x4*>(xr + k * 64);
-      u32x4 xb1 = *reinterpret_cast<const u32x4*>(xr + k * 64 + 8);
-      if (!mlive) xb0 = xb1 = u32x4{0u, 0u, 0u, 0u};
-      // refill this slot with the step kByteGemvDepth ahead (past the end:
-      // re-read the last step, in bounds and unused)
-      const int64_t kn = k + kByteGemvDepth < nk ? k + kByteGemvDepth : nk - 1;
-      wq[d] = *reinterpret_cast<const u32x4*>(wr + kn * 64);
-      sq[d] = scale.load(sb + ((kn * 64) >> a.bs_log2));
-      const uint2 a0 = decode4_pk<XT>(w.x, s), a1 = decode4_pk<XT>(w.y, s);
-      const uint2 a2 = decode4_pk<XT>(w.z, s), a3 = decode4_pk<XT>(w.w, s);
-      acc = mfma16x16x32<XT>(u32x4{a0.x, a0.y, a1.x, a1.y}, xb0, acc);
-      acc = mfma16x16x32<XT>(u32x4{a2.x, a2.y, a3.x, a3.y}, xb1, acc);
+    for (int t = 0; t < kByteGvPieces; ++t) {
+      const int64_t k = kb + 64 * t;
+      const bool live = k < a.K;
+      const int64_t ko = live ? k : 0;
+      wq[t] = *reinterpret_cast<const u32x4*>(wr + ko);
+      sq[t] = scale.load(sb + (ko >> a.bs_log2));
+      xa[t][0] = xa[t][1] = u32x4{0u, 0u, 0u, 0u};
+      if (mlive && live) {
+        xa[t][0] = *reinterpret_cast<const u32x4*>(xr + ko);
+        xa[t][1] = *reinterpret_cast<const u32x4*>(xr + ko + 8);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kByteGvPieces; ++t) {
+      if (kb + 64 * t >= a.K) break;
+      const float s = scale.value(sq[t]);
+      const uint2 p0 = decode4_pk<XT>(wq[t].x, s), p1 = decode4_pk<XT>(wq[t].y, s);
+      const uint2 p2 = decode4_pk<XT>(wq[t].z, s), p3 = decode4_pk<XT>(wq[t].w, s);
+      acc = mfma16x16x32<XT>(xa[t][0], u32x4{p0.x, p0.y, p1.x, p1.y}, acc);
+      acc = mfma16x16x32<XT>(xa[t][1], u32x4{p2.x, p2.y, p3.x, p3.y}, acc);
     }
   }
-  // epilogue: lane (i, q), register r -> y[m = i][n0 + 4 q + r]
-  if (!mlive) return;
+  red[wave][lane] = acc;
+  __syncthreads();
+  if (wave != 0) return;
+  f32x4 sum = red[0][lane];
+#pragma unroll
+  for (int w = 1; w < kByteGvWaves; ++w) {
+    const f32x4 v = red[w][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sum[r] = __fadd_rn(sum[r], v[r]);
+  }
+  // lane (i, g): outputs y[4 g + r][n0 + i], r = 0..3
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int64_t no = n0 + 4 * q4 + r;
-    if (no >= a.N) continue;
-    float v = acc[r];
+    const int64_t m = 4 * g4 + r;
+    const int64_t no = n0 + i16;
+    if (m >= a.M || no >= a.N) continue;
+    float v = sum[r];
     if (a.bias) v = __fadd_rn(v, round_x<XT>(load_as_f32(a.bias, no, a.bias_dt)));
-    v = round_x<XT>(v);
-    a.y[int64_t(i16) * a.ldy + no] = uint16_t(to_x16<XT>(v));
+    a.y[m * a.ldy + no] = uint16_t(to_x16<XT>(round_x<XT>(v)));
   }
 }
 
@@ -272,7 +286,7 @@ static int launch_byte(const ByteLinearArgs& A, Scale scale, hipStream_t stream)
     g.blocks_per_row = bpr; g.bs_log2 = bsl;
     g.bias = A.bias; g.bias_dt = A.bias_dtype;
     g.y = static_cast<uint16_t*>(A.y); g.ldy = A.ldy;
-    byte_gemv_kernel<XT, Scale><<<unsigned((A.N + 63) / 64), 256, 0, stream>>>(g, scale);
+    byte_gemv_kernel<XT, Scale><<<unsigned((A.N + 15) / 16), 64 * kByteGvWaves, 0, stream>>>(g, scale);
     return rq_check_launch();
   }
   const GemmPlan p = plan_gemm(A.M, A.N, A.K, 0, device_cus());

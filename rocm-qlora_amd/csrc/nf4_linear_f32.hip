@@ -26,7 +26,7 @@
 
 namespace rq {
 
-constexpr int kF32Threads = 256;  // four waves; wave w takes chunks w, w + 4, ...
+constexpr int kF32Threads = 1024;  // sixteen waves; wave w takes chunks w, w + 16, ...
 constexpr int kF32Waves = kF32Threads / 64;
 constexpr int kF32ChunkK = 128;
 
@@ -67,12 +67,16 @@ __device__ __forceinline__ void load32_f32(const void* p, int64_t off, bool live
 }
 
 // y rows [m0, m0 + 16) (fewer when M is shorter) of one 16-row weight tile.
-// u: RND-free fp32 LoRA operand [M][rank] (rank 0: none).
+// The sixteen waves take the tile's 128-k chunks in turn, two chunks' loads
+// in flight per wave; their partials are summed in wave order.
+// u: fp32 LoRA operand partials [usplits][M][rank] (rank 0: none), summed in
+// split order.
 template <class Scale>
 __global__ __launch_bounds__(kF32Threads) void nf4_gemv_f32_kernel(const float* __restrict__ x, int64_t ldx,
                                                                    int64_t M, int64_t K,
                                                                    const uint8_t* __restrict__ packed, int64_t N,
-                                                                   int bs_log2, Scale scale, LinearEpi e) {
+                                                                   int bs_log2, Scale scale, LinearEpi e,
+                                                                   int usplits) {
   __shared__ float tab[16];
   __shared__ float red[kF32Waves][16][16];
   __shared__ float us[16][64];
@@ -86,37 +90,55 @@ __global__ __launch_bounds__(kF32Threads) void nf4_gemv_f32_kernel(const float* 
   const int64_t row_bytes = K / 2;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   const int64_t nchunks = (K + kF32ChunkK - 1) / kF32ChunkK;
-  for (int64_t c = wave; c < nchunks; c += kF32Waves) {
-    const int64_t k0 = c * kF32ChunkK + 32 * q;  // this lane group's 32 k
-    const bool klive = k0 < K;
-    u32x4 codes = u32x4{0u, 0u, 0u, 0u};
-    float s = 0.0f;
-    if (nlive && klive) {
-      codes = *reinterpret_cast<const u32x4*>(packed + n * row_bytes + k0 / 2);
-      s = scale((n * K + k0) >> bs_log2);
-    }
+  struct Chunk {
+    u32x4 codes;
+    float s;
     float xv[32];
-    load32_f32<RQ_DTYPE_F32>(x, i16 * ldx + k0, i16 < M && klive, xv);
-    const uint32_t w[4] = {codes.x, codes.y, codes.z, codes.w};
+  };
+  auto load = [&](Chunk& ch, int64_t c) {
+    const int64_t k0 = c * kF32ChunkK + 32 * q;  // this lane group's 32 k
+    const bool live = c < nchunks && k0 < K;
+    ch.codes = u32x4{0u, 0u, 0u, 0u};
+    ch.s = 0.0f;
+    if (nlive && live) {
+      ch.codes = *reinterpret_cast<const u32x4*>(packed + n * row_bytes + k0 / 2);
+      ch.s = scale((n * K + k0) >> bs_log2);
+    }
+    load32_f32<RQ_DTYPE_F32>(x, i16 * ldx + k0, i16 < M && live, ch.xv);
+  };
+  auto compute = [&](const Chunk& ch) {
+    const uint32_t w[4] = {ch.codes.x, ch.codes.y, ch.codes.z, ch.codes.w};
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
 #pragma unroll
       for (int ee = 0; ee < 8; ++ee) {
-        const float wv = __fmul_rn(tab[(w[d] >> (4 * ee)) & 15u], s);
-        acc = mfma16x16x4_f32(xv[8 * d + ee], wv, acc);
+        const float wv = __fmul_rn(tab[(w[d] >> (4 * ee)) & 15u], ch.s);
+        acc = mfma16x16x4_f32(ch.xv[8 * d + ee], wv, acc);
       }
     }
+  };
+  for (int64_t c = wave; c < nchunks; c += 2 * kF32Waves) {
+    Chunk c0, c1;
+    load(c0, c);
+    load(c1, c + kF32Waves);
+    compute(c0);
+    compute(c1);  // a chunk past the end has zero codes, scale and activations
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[wave][4 * q + r][i16] = acc[r];
-  // the LoRA operand rows of this launch's activation rows
+  // the LoRA operand rows of this launch's activation rows: the splits'
+  // partials summed in split order
   const int rank = e.rank;
   for (int idx = tid; idx < 16 * rank; idx += kF32Threads) {
     const int m = idx / rank, j = idx - m * rank;
-    us[m][j] = m < M ? e.u[m * rank + j] : 0.0f;
+    float v = 0.0f;
+    if (m < M)
+      for (int sp = 0; sp < usplits; ++sp) v = __fadd_rn(v, e.u[(int64_t(sp) * M + m) * rank + j]);
+    us[m][j] = v;
   }
   __syncthreads();
   // one thread per output (row m = tid / 16, column n0 + tid % 16)
+  if (tid >= 256) return;
   const int m = tid >> 4, nn = tid & 15;
   const int64_t on = n0 + nn;
   if (m >= M || on >= N) return;
@@ -132,9 +154,10 @@ __global__ __launch_bounds__(kF32Threads) void nf4_gemv_f32_kernel(const float* 
   static_cast<float*>(e.y)[m * e.ldy + on] = v;
 }
 
-// u[m, j] = sum_k xl[m, k] * A[j, k] in fp32 for m < M <= 16: workgroup j0 / 16
-// takes ranks [j0, j0 + 16); its four waves take chunks of 128 k in turn and
-// their partial products are summed in wave order.
+// Partials of u[m, j] = sum_k xl[m, k] * A[j, k] in fp32 for m < M <= 16:
+// workgroup (j0 / 16, sp) takes ranks [j0, j0 + 16) over K split sp (chunks
+// sp * 16 .. sp * 16 + 15 of 128 k, one per wave); the waves' products are
+// summed in wave order into u[sp][m][j].
 template <int ADT>
 __global__ __launch_bounds__(kF32Threads) void lora_u_f32_kernel(const float* __restrict__ xl, int64_t ldxl,
                                                                  int64_t M, int64_t K, const void* __restrict__ A,
@@ -143,36 +166,42 @@ __global__ __launch_bounds__(kF32Threads) void lora_u_f32_kernel(const float* __
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int i16 = lane & 15, q = lane >> 4;
   const int j = int(blockIdx.x) * 16 + i16;
+  const int64_t c = int64_t(blockIdx.y) * kF32Waves + wave;
+  const int64_t k0 = c * kF32ChunkK;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  const int64_t nchunks = (K + kF32ChunkK - 1) / kF32ChunkK;
-  for (int64_t c = wave; c < nchunks; c += kF32Waves) {
-    const int64_t k0 = c * kF32ChunkK + 32 * q;
+  if (k0 < K) {
     float xv[32], av[32];
-    load32_f32<RQ_DTYPE_F32>(xl, i16 * ldxl + k0, i16 < M && k0 < K, xv);
-    load32_f32<ADT>(A, int64_t(j) * K + k0, j < rank && k0 < K, av);
+    const int64_t kq = k0 + 32 * q;
+    load32_f32<RQ_DTYPE_F32>(xl, i16 * ldxl + kq, i16 < M && kq < K, xv);
+    load32_f32<ADT>(A, int64_t(j) * K + kq, j < rank && kq < K, av);
 #pragma unroll
     for (int t = 0; t < 32; ++t) acc = mfma16x16x4_f32(xv[t], av[t], acc);
   }
 #pragma unroll
   for (int r = 0; r < 4; ++r) red[wave][4 * q + r][i16] = acc[r];
   __syncthreads();
+  if (tid >= 256) return;
   const int m = tid >> 4, jj = int(blockIdx.x) * 16 + (tid & 15);
   if (m >= M || jj >= rank) return;
   float v = 0.0f;
 #pragma unroll
   for (int w2 = 0; w2 < kF32Waves; ++w2) v = __fadd_rn(v, red[w2][m][tid & 15]);
-  u[m * rank + jj] = v;
+  u[(int64_t(blockIdx.y) * M + m) * rank + jj] = v;
 }
+
+// K splits of the LoRA operand: 16 chunks of 128 k each.
+inline int f32_usplits(int64_t K) { return int((K + kF32Waves * kF32ChunkK - 1) / (kF32Waves * kF32ChunkK)); }
 
 template <class Scale>
 static int launch_f32_gemv(const LinearArgs& L, int64_t m0, int64_t rows, Scale scale, const LinearEpi& e,
                            hipStream_t stream) {
+  const int usplits = L.rank > 0 ? f32_usplits(L.K) : 0;
   const float* x = static_cast<const float*>(L.x) + m0 * L.ldx;
   LinearEpi ec = e;
   ec.y = static_cast<float*>(L.y) + m0 * L.ldy;
   const unsigned grid = unsigned((L.N + 15) / 16);
   nf4_gemv_f32_kernel<Scale><<<grid, kF32Threads, 0, stream>>>(x, L.ldx, rows, L.K, L.w_packed, L.N,
-                                                               pow2_shift(L.block_size), scale, ec);
+                                                               pow2_shift(L.block_size), scale, ec, usplits);
   return rq_check_launch();
 }
 
@@ -181,7 +210,7 @@ static int run_f32_rows(const LinearArgs& L, int64_t m0, int64_t rows, Scale sca
   LinearEpi e = make_epi(L, u, 1);
   if (L.rank > 0) {
     const float* xl = static_cast<const float*>(L.lora_x) + m0 * L.ld_lora_x;
-    const unsigned grid = unsigned((L.rank + 15) / 16);
+    const dim3 grid(unsigned((L.rank + 15) / 16), unsigned(f32_usplits(L.K)));
     switch (L.lora_dtype) {
       case RQ_DTYPE_F32:
         lora_u_f32_kernel<RQ_DTYPE_F32><<<grid, kF32Threads, 0, stream>>>(xl, L.ld_lora_x, rows, L.K, L.lora_a,
@@ -212,10 +241,11 @@ static int run_f32_all(const LinearArgs& L, Scale scale, float* u, hipStream_t s
   return RQ_OK;
 }
 
-// The LoRA operand u [16][rank] lies after the workspace's synchronization
-// area (which every rq_nf4_linear call leaves zero for the decode GEMV).
+// The LoRA operand partials [usplits][16][rank] lie after the workspace's
+// synchronization area (which every rq_nf4_linear call leaves zero for the
+// decode GEMV).
 int f32_linear_workspace(const LinearArgs& L, size_t* bytes) {
-  *bytes = L.rank > 0 ? kLinearSyncBytes + size_t(16) * size_t(L.rank) * 4 : 0;
+  *bytes = L.rank > 0 ? kLinearSyncBytes + size_t(f32_usplits(L.K)) * 16 * size_t(L.rank) * 4 : 0;
   return RQ_OK;
 }
 
