@@ -47,7 +47,7 @@ Also reported:
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m M] [--no-gemm] [--no-extra] [--no-cpu]
     python bench.py --summarize-profile DIR   # per-kernel, per-grid rocprofv3 kernel-trace table
-    python bench.py --counters                # short eager run for rocprofv3 --pmc passes
+    python bench.py --counters [gemv|fp8_gemm|nf4_gemm]   # short eager run for rocprofv3 --pmc passes
     python bench.py --summarize-counters DIR [DIR ...]   # HBM bytes per launch from those passes
 """
 import argparse
@@ -541,6 +541,39 @@ def summarize_profile(path):
                       f"{sum(ds):>10.1f}")
 
 
+def run_counters_kernel(which, reps=4):
+    """Eager launches of one MFMA kernel for counter passes (rocprofv3 --pmc):
+    "fp8_gemm" -- the FP8 linear at M = 4096, K = 8192, N = 28672 (weights
+    N(0,0.02) quantized per tensor, e4m3fn codes cached); "nf4_gemm" -- the
+    NF4 forward and dX at the gate shape, M = 2048, K = 4096, N = 14336, LoRA
+    r = 64, alpha = 16."""
+    import torch
+    from rocm_qlora import ops
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev).manual_seed(9)
+    if which == "fp8_gemm":
+        K, N, M = 8192, 28672, 4096
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        codes, scale = ops.fp8_quantize(w)
+        wf = ops.fp8_to_e4m3fn(codes)
+        del w, codes
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        for _ in range(reps):
+            ops.fp8_linear(x, wf, scale)
+    else:
+        layer = make_layer(dev, 4242, rank=GEMM_RANK)
+        packed, absmax, a, b, N, K = layer["gate"]
+        x = torch.randn(GEMM_M, K, generator=g, device=dev).to(torch.bfloat16)
+        dy = (torch.randn(GEMM_M, N, generator=g, device=dev) * 1e-2).to(torch.bfloat16)
+        s = GEMM_ALPHA / GEMM_RANK
+        for _ in range(reps):
+            ops.nf4_linear(x, packed, absmax, N, BLOCK, lora_a=a, lora_b=b, scaling=s)
+            ops.nf4_linear_dx(dy, packed, absmax, K, BLOCK, lora_a=a, lora_b=b, scaling=s)
+    torch.cuda.synchronize()
+    print(f"counters: {reps} rounds of {which}", flush=True)
+
+
 def run_counters(reps=4):
     """Eager launches for counter collection: one plain device copy of
     COPY_BYTES (calibration: its FETCH_SIZE / WRITE_SIZE readings against the
@@ -623,7 +656,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the codec and INT8/FP8 sections")
     ap.add_argument("--summarize-profile", metavar="DIR", help="summarize a rocprofv3 CSV kernel trace and exit")
-    ap.add_argument("--counters", action="store_true", help="short eager run for rocprofv3 --pmc passes")
+    ap.add_argument("--counters", nargs="?", const="gemv", choices=["gemv", "fp8_gemm", "nf4_gemm"],
+                    help="short eager run for rocprofv3 --pmc passes (default: the roofline GEMV and a copy)")
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
                     help="HBM bytes per launch from rocprofv3 --pmc CSV output and exit")
     args = ap.parse_args()
@@ -634,7 +668,10 @@ def main():
         summarize_counters(args.summarize_counters)
         return
     if args.counters:
-        run_counters()
+        if args.counters == "gemv":
+            run_counters()
+        else:
+            run_counters_kernel(args.counters)
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this path is built and measured on a single MI355X; "

@@ -192,17 +192,21 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   Prod prod;
   prod.init(pp, scale, lut, tid, n0);
 
-  // Staggered start: step j covers k-step ks(j) = kbeg + (j + k_off) mod nk.
-  // Workgroups sharing an activation row slice (one XCD) and those sharing a
-  // weight tile start at different steps, so that one of them misses on each
-  // line and the rest find it in L2 or the MALL.
+  // Step j covers k-step ks(j) = kbeg + j mod nk (the prefetches past the
+  // end wrap around the split's K range: in bounds, never used).  The
+  // workgroups of an XCD walk K together, so the activation (dY) rows they
+  // share are fetched once into its L2.  (Starting them at staggered steps,
+  // to spread the misses, measured 3 % slower forward and 7 % slower dX: with
+  // activation tiles larger than the L2 every workgroup then missed on its
+  // own lines.)
   const int nk32 = __builtin_amdgcn_readfirstlane(int(nk));
-  const int k_off = __builtin_amdgcn_readfirstlane(int((((nt + 4 * mt) & 31) * nk) >> 5));
   const int kb32 = __builtin_amdgcn_readfirstlane(int(kbeg));
   auto ks = [&](int64_t j) -> int64_t {
-    int v = int(j) + k_off;
-    v = v >= nk32 ? v - nk32 : v;
-    v = v >= nk32 ? v - nk32 : v;
+    int v = int(j);  // j < nk + kWDepth
+    if (v >= nk32) {
+      v -= nk32;
+      if (v >= nk32) v %= nk32;  // only when nk < kWDepth
+    }
     return kb32 + v;
   };
 
