@@ -56,8 +56,18 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
 __device__ __forceinline__ float f16_to_f32(uint16_t h) {
   return float(__builtin_bit_cast(_Float16, h));
 }
+// Keeps an fp32 value opaque to the instruction selector, so that the fp16
+// narrowing after it stays a separate rounding: without it the compiler folds
+// fptrunc(fmul / fadd) into one v_fma_mix{lo,hi}_f16, which rounds the exact
+// product once to fp16 instead of first to fp32 -- a one-ulp difference
+// whenever the fp32 result lands on an fp16 rounding tie.  Emits nothing.
+__device__ __forceinline__ float f16_narrowing_barrier(float f) {
+  asm("" : "+v"(f));
+  return f;
+}
+
 __device__ __forceinline__ uint16_t f32_to_f16_rne(float f) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f16_narrowing_barrier(f)));
 }
 
 // Load/store one element of a runtime-selected float dtype ------------------

@@ -49,8 +49,12 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 template <int XT>
 __device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
   const f32x2 v = {lo, hi};
-  if constexpr (XT == RQ_DTYPE_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
-  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+  if constexpr (XT == RQ_DTYPE_BF16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  } else {
+    const f32x2 o = {f16_narrowing_barrier(lo), f16_narrowing_barrier(hi)};  // two roundings, as written
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(o, f16x2));
+  }
 }
 
 // Round-to-nearest-even of an fp32 value to the 16-bit operand type, as bits
@@ -72,7 +76,7 @@ __device__ __forceinline__ float from_x16(uint32_t b) {
 template <int XT>
 __device__ __forceinline__ float round_x(float v) {
   if constexpr (XT == RQ_DTYPE_BF16) return u2f(cvt_pk<XT>(v, 0.0f) << 16);
-  else return float(static_cast<_Float16>(v));
+  else return f16_to_f32(f32_to_f16_rne(v));
 }
 
 // ---------------------------------------------------------------------------
