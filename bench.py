@@ -33,11 +33,13 @@ Also reported:
                 with 0.1 % outliers at +-8 sigma, blocks 64 / 256): quantize ->
                 pack -> double-quantize the absmax, and double-dequantize ->
                 bf16; algorithmic bytes / time vs 8 TB/s.
-  byte_linears  INT8 (per-row absmax, bf16 MFMA) and FP8 (e4m3 per-tensor
-                scales, fp8 MFMA) linears at the Llama-3-70B MLP shape
-                8192 -> 28672, M = 1 (HBM: bytes / time, two weight copies
-                rotating) and M = 512, 4096 (TFLOP/s against the bf16 and fp8
-                MFMA peaks, 2.5 and 5.0 PFLOP/s).
+  byte_linears  INT8 (per-row absmax: W8A16 on the bf16 MFMA, and the
+                separate W8A8 mode on the int8 MFMA) and FP8 (e4m3
+                per-tensor scales, fp8 MFMA) linears at the Llama-3-70B MLP
+                shape 8192 -> 28672, M = 1 (HBM: bytes / time, two weight
+                copies rotating) and M = 512, 4096 (TFLOP/s against the bf16,
+                int8 and fp8 MFMA peaks, 2.5, 5.0 and 5.0 P/s), plus W8A8's
+                relative deviation from W8A16 at M = 512.
   cpu_baseline  the oracle's restatement of the reference's CPU path on the
                 host cores: the headline decode step whole (`value`), and per
                 configuration (fp32 config 1, codec, GEMM forward / dX, INT8 /
@@ -47,7 +49,7 @@ Also reported:
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m M] [--no-gemm] [--no-extra] [--no-cpu]
     python bench.py --summarize-profile DIR   # per-kernel, per-grid rocprofv3 kernel-trace table
-    python bench.py --counters [gemv|fp8_gemm|nf4_gemm]   # short eager run for rocprofv3 --pmc passes
+    python bench.py --counters [gemv|fp8_gemm|int8_gemm|nf4_gemm]   # short eager run for rocprofv3 --pmc passes
     python bench.py --summarize-counters DIR [DIR ...]   # HBM bytes per launch from those passes
 """
 import argparse
@@ -68,6 +70,7 @@ METRIC = "NF4 dequant-GEMV GB/s + GEMM TFLOP/s (% roofline), Llama-3-8B proj sha
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 FP8_PEAK_TFLOPS = 5000.0       # MI355X dense fp8 MFMA
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA (TOP/s)
 
 # (name, in_features K, out_features N)
 LLAMA3_8B_PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
@@ -449,7 +452,8 @@ def bench_codec(dev, stream):
 
 
 def bench_byte_linears(dev, stream):
-    """INT8 per-row-absmax (bf16 MFMA) and FP8 (e4m3, fp8 MFMA) linears at 8192 -> 28672 with
+    """INT8 per-row-absmax (W8A16 on bf16 MFMA; W8A8 on int8 MFMA) and FP8 (e4m3, fp8 MFMA)
+    linears at 8192 -> 28672 with
     bf16 activations N(0,1), weights N(0,0.02); M = 1 rotates two weight
     copies (470 MB each kind, past the MALL), M = 512 and 4096 one copy."""
     import torch
@@ -469,9 +473,11 @@ def bench_byte_linears(dev, stream):
     for M in (1, 512, 4096):
         x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
         copies = 2 if M == 1 else 1
-        for kind in ("int8", "fp8"):
+        for kind in ("int8", "int8_w8a8", "fp8"):
             if kind == "int8":
                 fn = lambda: [ops.int8_linear(x, q, s, N) for q, s in int8_w[:copies]]
+            elif kind == "int8_w8a8":
+                fn = lambda: [ops.int8_linear_w8a8(x, q, s) for q, s in int8_w[:copies]]
             else:
                 fn = lambda: [ops.fp8_linear(x, cw, sc) for cw, sc in fp8_w[:copies]]
             gr = _capture(fn, stream)
@@ -487,11 +493,20 @@ def bench_byte_linears(dev, stream):
                                         "frac": round(gbs / HBM_PEAK_GBS, 4), "bound": "hbm", **pct}
             else:
                 tf = 2 * M * N * K / us / 1e6
-                peak, bound = (BF16_PEAK_TFLOPS, "bf16 mfma") if kind == "int8" else (FP8_PEAK_TFLOPS, "fp8 mfma")
+                peak, bound = {"int8": (BF16_PEAK_TFLOPS, "bf16 mfma"),
+                               "int8_w8a8": (INT8_PEAK_TOPS, "int8 mfma"),
+                               "fp8": (FP8_PEAK_TFLOPS, "fp8 mfma")}[kind]
                 out[f"{kind}_m{M}"] = {"us": round(us, 2), "tflops": round(tf, 1),
                                         "frac": round(tf / peak, 4), "bound": bound, **pct}
+        if M == 512:
+            # what the activation rounding of W8A8 costs against the W8A16 path
+            q, s = int8_w[0]
+            ref = ops.int8_linear(x, q, s, N).float()
+            d = (ops.int8_linear_w8a8(x, q, s).float() - ref).norm() / ref.norm()
+            out["int8_w8a8_rel_dev_vs_w8a16"] = round(float(d), 5)
         del x
-    return {"workload": f"INT8 per-row and FP8 per-tensor linears, K={K} N={N}, bf16 activations", **out}
+    return {"workload": f"INT8 per-row (W8A16 and W8A8) and FP8 per-tensor linears, K={K} N={N}, "
+                        "bf16 activations", **out}
 
 
 def _short(name, n=70):
@@ -544,7 +559,9 @@ def summarize_profile(path):
 def run_counters_kernel(which, reps=4):
     """Eager launches of one MFMA kernel for counter passes (rocprofv3 --pmc):
     "fp8_gemm" -- the FP8 linear at M = 4096, K = 8192, N = 28672 (weights
-    N(0,0.02) quantized per tensor, e4m3fn codes cached); "nf4_gemm" -- the
+    N(0,0.02) quantized per tensor, e4m3fn codes cached); "int8_gemm" -- the
+    W8A8 INT8 linear at the same shape (weights quantized per row);
+    "nf4_gemm" -- the
     NF4 forward and dX at the gate shape, M = 2048, K = 4096, N = 14336, LoRA
     r = 64, alpha = 16."""
     import torch
@@ -561,6 +578,15 @@ def run_counters_kernel(which, reps=4):
         x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
         for _ in range(reps):
             ops.fp8_linear(x, wf, scale)
+    elif which == "int8_gemm":
+        from rocm_qlora.quantization import quantize_int8
+        K, N, M = 8192, 28672, 4096
+        w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        q, s = quantize_int8(w, per_channel=True)
+        del w
+        x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+        for _ in range(reps):
+            ops.int8_linear_w8a8(x, q, s)
     else:
         layer = make_layer(dev, 4242, rank=GEMM_RANK)
         packed, absmax, a, b, N, K = layer["gate"]
@@ -656,7 +682,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="skip the codec and INT8/FP8 sections")
     ap.add_argument("--summarize-profile", metavar="DIR", help="summarize a rocprofv3 CSV kernel trace and exit")
-    ap.add_argument("--counters", nargs="?", const="gemv", choices=["gemv", "fp8_gemm", "nf4_gemm"],
+    ap.add_argument("--counters", nargs="?", const="gemv", choices=["gemv", "fp8_gemm", "int8_gemm", "nf4_gemm"],
                     help="short eager run for rocprofv3 --pmc passes (default: the roofline GEMV and a copy)")
     ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
                     help="HBM bytes per launch from rocprofv3 --pmc CSV output and exit")

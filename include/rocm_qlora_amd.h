@@ -298,6 +298,42 @@ int rq_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------------
+ * W8A8 INT8 mode (int8 activations x int8 weights on the int8 matrix cores)
+ *
+ * No counterpart in the reference, whose INT8 linear multiplies dequantized
+ * weights with 16-bit activations (rq_int8_linear above).  This mode
+ * quantizes the activations too, per row, with quantize_int8's per-row recipe
+ * (quantization/quant_ops.py:29-35) computed in fp32, and sums the int8
+ * products exactly in int32; its outputs differ from rq_int8_linear's by the
+ * activation rounding, so it is a separate mode, not a replacement.
+ * ------------------------------------------------------------------------ */
+
+/* Per-row int8 quantization of 16-bit activations:
+ *   scales[m] = max(fp32(max_k |x[m, k]|) / 127, 1e-12)  (device fp32)
+ *   codes[m, k] = RNE(fp32(x[m, k]) / scales[m])  in [-127, 127]
+ * x: [M, K] bf16/fp16 stride ldx (K % 8 == 0, 16-byte aligned rows);
+ * codes: [M, K] dense, 8-byte aligned.  A row holding NaN gets a NaN scale
+ * and zero codes. */
+int rq_int8_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                          int8_t* codes, float* scales, hipStream_t stream);
+
+/* Bytes of workspace rq_int8_linear_w8a8 needs for M rows of K activations. */
+int rq_int8_linear_w8a8_workspace_size(int64_t M, int64_t K, int64_t* bytes);
+
+/* y = RND(RND(float(sum_k xq[m, k] wq[n, k]) * xs[m] * ws[n]) + RND(bias[n]))
+ * with (xq, xs) = rq_int8_quantize_rows(x) and wq, ws the weight's per-row
+ * codes and scales (quantize_int8(w, per_channel=True),
+ * quant_ops.py:29-35); the int32 sum is exact, its conversion to fp32
+ * rounds to nearest even, and the two scale products round in that order.
+ *   x: [M, K] bf16/fp16 stride ldx (K % 64 == 0); w: [N, K] int8 dense;
+ *   w_scales: [N] fp32/bf16/fp16; bias [N] or NULL; y: [M, N] stride ldy.
+ * M <= 16 runs the weight-streaming GEMV, larger M the int8 MFMA GEMM. */
+int rq_int8_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
+                        const int8_t* w, int64_t N, const void* w_scales, int w_scales_dtype,
+                        const void* bias, int bias_dtype, void* y, int64_t ldy,
+                        void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
  * Merged LoRA weights
  * ------------------------------------------------------------------------ */
 

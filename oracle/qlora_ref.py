@@ -31,6 +31,10 @@ tests/test_oracle_linear.py:
   * int8_linear: float64 x (q s)^T and linearity in the row scale.
   * fp8_linear: decode-then-matmul with each scale applied once (exact), and
     closeness to the unquantized product.
+  * quantize_rows_int8 / w8a8_linear (the W8A8 INT8 mode, no counterpart in
+    the reference): equal to quantize_int8(per_channel=True) on fp32 rows;
+    an int64 brute-force sum; rows whose absmax is 127 * 2^-j (power-of-two
+    scales, exact codes) give int8_linear's float64 product exactly.
 No function of this module is left without such a check.
 """
 from __future__ import annotations
@@ -222,6 +226,32 @@ def fp8_linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = 
     if bias is not None:
         y = y + bias
     return y
+
+
+# ------------------------------------------------------------- W8A8 INT8 mode
+def quantize_rows_int8(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row int8 activations: quant_ops.py:29-35 (per_channel) applied to
+    the rows of x in fp32.  Returns (codes [M, K] int8, scales [M] fp32)."""
+    xf = x.reshape(-1, x.shape[-1]).to(torch.float32)
+    s = xf.abs().amax(dim=1, keepdim=True) / 127.0                          # :31
+    s = torch.clamp(s, min=1e-12)                                           # :33
+    q = torch.round(xf / s).to(torch.int8)                                  # :34
+    return q, s.reshape(-1)
+
+
+def w8a8_linear(x: torch.Tensor, q: torch.Tensor, w_scales: torch.Tensor,
+                bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """W8A8: y = dtype(fp32(sum_k xq wq) * xs[m] * ws[n]) (+ bias in dtype).
+    The integer sum is exact (float64 holds every partial sum of |q| <= 127
+    products for K < 2^39), its fp32 conversion rounds to nearest even."""
+    K = x.shape[-1]
+    qx, sx = quantize_rows_int8(x)
+    acc = qx.to(torch.float64) @ q.reshape(-1, K).to(torch.float64).T
+    y = (acc.to(torch.float32) * sx[:, None]) * w_scales.reshape(-1).to(torch.float32)[None, :]
+    y = y.to(x.dtype)
+    if bias is not None:
+        y = y + bias.to(x.dtype)
+    return y.reshape(*x.shape[:-1], -1)
 
 
 # ----------------------------------------------------------- merge / export

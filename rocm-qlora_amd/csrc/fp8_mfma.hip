@@ -20,8 +20,10 @@
 //                          (absmax, scale and fn codes in one workgroup)
 //   fp8_absmax16 / fp8_encode16
 //                          the same for large activations, 16-byte vectors
-//   fp8_gemv_kernel        M <= 16: 16 weight rows x 1024 k per wave
-//   fp8_gemm_kernel        M > 16: 256 x 256 tiles, 4-stage LDS ring
+//   byte_mfma_gemv_kernel  M <= 16: 16 weight rows x 1024 k per wave
+//   byte_mfma_gemm_kernel  M > 16: 256 x 256 tiles, 5-stage LDS ring
+// The GEMV and GEMM are templates on the operand policy: Fp8Mma here, I8Mma
+// for the W8A8 int8 mode (int8 activations quantized per row, int32 sums).
 #include "rq_fp8.h"
 #include "rq_gemm_core.h"
 
@@ -42,6 +44,73 @@ __device__ __forceinline__ f32x4 mfma_fn_16x16x128(const u32x4& a0, const u32x4&
   const i32x8 a = {int(a0.x), int(a0.y), int(a0.z), int(a0.w), int(a1.x), int(a1.y), int(a1.z), int(a1.w)};
   const i32x8 b = {int(b0.x), int(b0.y), int(b0.z), int(b0.w), int(b1.x), int(b1.y), int(b1.z), int(b1.w)};
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+// Operand policies of the byte-operand GEMM / GEMV below.
+//   Fp8Mma: e4m3fn x e4m3fn, fp32 sums, per-tensor scales (the FP8 linear);
+//   I8Mma:  int8 x int8, exact int32 sums (v_mfma_i32_{32x32x32,16x16x64}_i8,
+//           two per step: the lane's first and second 16 bytes), per-row
+//           scales of both operands (the W8A8 mode).
+// Both take a lane's 32 bytes per step as two 16-byte halves, the same k
+// order for both operands.  A step is kParts instructions (FP8: one over
+// both halves; int8: one per half): the GEMV keeps one accumulator per part
+// (part p of mma16 issues instruction p), the GEMM issues the int8 halves as
+// two passes over its tiles (mma32h) and FP8 steps whole (mma32).
+struct Fp8Mma {
+  static constexpr bool kPerRow = false;
+  static constexpr int kParts = 1;
+  typedef f32x16 Acc32;
+  typedef f32x4 Acc16;
+  __device__ static Acc32 mma32(const u32x4& a0, const u32x4& a1, const u32x4& b0, const u32x4& b1, const Acc32& c) {
+    return mfma_fn_32x32x64(a0, a1, b0, b1, c);
+  }
+  template <int P>
+  __device__ static Acc16 mma16(const u32x4& a0, const u32x4& a1, const u32x4& b0, const u32x4& b1, const Acc16& c) {
+    return mfma_fn_16x16x128(a0, a1, b0, b1, c);
+  }
+  __device__ static float to_f32(float v) { return v; }
+};
+
+struct I8Mma {
+  static constexpr bool kPerRow = true;
+  static constexpr int kParts = 2;
+  typedef i32x16 Acc32;
+  typedef i32x4 Acc16;
+  __device__ static i32x4 bits(const u32x4& v) { return __builtin_bit_cast(i32x4, v); }
+  __device__ static Acc32 mma32h(const u32x4& a, const u32x4& b, const Acc32& c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(bits(a), bits(b), c, 0, 0, 0);
+  }
+  template <int P>
+  __device__ static Acc16 mma16(const u32x4& a0, const u32x4& a1, const u32x4& b0, const u32x4& b1, const Acc16& c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(bits(P ? a1 : a0), bits(P ? b1 : b0), c, 0, 0, 0);
+  }
+  __device__ static float to_f32(int v) { return float(v); }  // round to nearest
+};
+
+// Output scale of (m, n): FP8 the product of the two per-tensor scales, W8A8
+// the activation row's scale times the weight row's.
+template <class Op>
+__device__ __forceinline__ float out_scale(const Fp8Args& a, int64_t m, int64_t n) {
+  if constexpr (Op::kPerRow) return __fmul_rn(a.sx[m], load_as_f32(a.w_row_scale, n, a.w_row_scale_dt));
+  else return __fmul_rn(*a.sx, *a.sw);
+}
+
+// y = RND(RND(float(acc) * scale) + RND(bias)).  FP8 applies the product of
+// its two scalars at once (the reference multiplies by x_scale * w_scale
+// folded into its GEMM); W8A8 multiplies by the row scales one at a time.
+template <int XT, class Op, class V>
+__device__ __forceinline__ float byte_epilogue(const Fp8Args& a, V acc, int64_t m, int64_t n) {
+  float v;
+  if constexpr (Op::kPerRow)
+    v = __fmul_rn(__fmul_rn(Op::to_f32(acc), a.sx[m]), load_as_f32(a.w_row_scale, n, a.w_row_scale_dt));
+  else
+    v = __fmul_rn(Op::to_f32(acc), out_scale<Op>(a, m, n));
+  v = round_x<XT>(v);
+  if (a.bias) v = round_x<XT>(__fadd_rn(v, round_x<XT>(load_as_f32(a.bias, n, a.bias_dt))));
+  return v;
 }
 
 // ---------------------------------------------------------------------------
@@ -153,6 +222,52 @@ __global__ __launch_bounds__(256) void fp8_absmax16_kernel(const uint16_t* __res
   if (threadIdx.x == 0) part[blockIdx.x] = red[0];
 }
 
+// ---------------------------------------------------------------------------
+// W8A8 activation quantization, one workgroup of T threads per row: the
+// per-row recipe of quantize_int8 (quant_ops.py:29-35) on the row in fp32,
+//   s_m = max(fp32(max_k |x[m][k]|) / 127, 1e-12),
+//   q[m][k] = RNE(fp32(x[m][k]) / s_m)  (|q| <= 127 for finite rows).
+// A NaN in the row makes its scale NaN (max and clamp propagate NaN, as
+// torch's amax and clamp do) and its codes 0; codes are clamped to
+// [-127, 127], so every output stays defined.  The second pass re-reads the
+// row from the cache.
+// ---------------------------------------------------------------------------
+template <int DT, int T>
+__global__ __launch_bounds__(T) void i8_row_quant_kernel(const uint16_t* __restrict__ x, int64_t K, int64_t ld,
+                                                         float* __restrict__ scales, int8_t* __restrict__ codes) {
+  __shared__ float red[T];
+  const int64_t m = blockIdx.x;
+  const uint16_t* xr = x + m * ld;
+  const int64_t groups = K / 8;
+  float mx = 0.0f;
+  for (int64_t i = threadIdx.x; i < groups; i += T) mx = absmax8<DT>(*reinterpret_cast<const u32x4*>(xr + 8 * i), mx);
+  red[threadIdx.x] = mx;
+  __syncthreads();
+  for (int o = T / 2; o > 0; o >>= 1) {
+    if (int(threadIdx.x) < o) {
+      const float b = red[threadIdx.x + o], c = red[threadIdx.x];
+      red[threadIdx.x] = (b > c || b != b) ? b : c;
+    }
+    __syncthreads();
+  }
+  const float q127 = __fdiv_rn(red[0], 127.0f);
+  const float s = q127 > 1e-12f ? q127 : (q127 != q127 ? q127 : 1e-12f);  // torch.clamp keeps NaN
+  if (threadIdx.x == 0) scales[m] = s;
+  int8_t* cr = codes + m * K;
+  for (int64_t i = threadIdx.x; i < groups; i += T) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(xr + 8 * i);
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    uint32_t c[2] = {0u, 0u};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float q = __builtin_rintf(__fdiv_rn(h2f<DT>((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu), s));
+      q = q != q ? 0.0f : (q > 127.0f ? 127.0f : (q < -127.0f ? -127.0f : q));
+      c[e >> 2] |= (uint32_t(int32_t(q)) & 0xFFu) << (8 * (e & 3));
+    }
+    *reinterpret_cast<u32x2*>(cr + 8 * i) = u32x2{c[0], c[1]};
+  }
+}
+
 // Reduces the partial maxima (at most 1024, read from L2); every workgroup
 // of the encode kernel does this for itself, so the scale needs no launch of
 // its own.
@@ -205,10 +320,11 @@ constexpr int kF8GvWaves = 8;
 constexpr int kF8GvSteps = 8;   // 128-k steps per chunk, at most
 constexpr int kF8GvDepth = 4;   // weight steps in flight
 
-template <int XT>
+template <int XT, class Op>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4)))
-void fp8_gemv_kernel(Fp8Args a) {
-  __shared__ f32x4 red[kF8GvWaves][64];
+void byte_mfma_gemv_kernel(Fp8Args a) {
+  typedef typename Op::Acc16 Acc;
+  __shared__ Acc red[kF8GvWaves][64];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(int(threadIdx.x >> 6));
   const int i16 = lane & 15, g = lane >> 4;
@@ -222,7 +338,7 @@ void fp8_gemv_kernel(Fp8Args a) {
   const int64_t chunk = int64_t(steps) * 128;
   const int64_t nchunks = (a.K + chunk - 1) / chunk;
 
-  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  Acc acc = {}, acc1 = {};  // acc1: the int8 policy's second part
   for (int64_t c = wave; c < nchunks; c += kF8GvWaves) {
     const int64_t kb = c * chunk;
     // half h of step s covers k = kb + 128 s + 64 h .. + 63; halves at or
@@ -253,26 +369,29 @@ void fp8_gemv_kernel(Fp8Args a) {
         for (int h = 0; h < 2; ++h)
           wq[s % kF8GvDepth][h] = *reinterpret_cast<const u32x4*>(wr + koff(s + kF8GvDepth, h));
       }
-      acc = mfma_fn_16x16x128(w0, w1, xa[s][0], xa[s][1], acc);
+      acc = Op::template mma16<0>(w0, w1, xa[s][0], xa[s][1], acc);
+      if constexpr (Op::kParts == 2) acc1 = Op::template mma16<1>(w0, w1, xa[s][0], xa[s][1], acc1);
     }
   }
+  if constexpr (Op::kParts == 2) acc += acc1;  // exact int32 sums
   red[wave][lane] = acc;
   __syncthreads();
   if (wave != 0 || !xlive) return;
-  f32x4 sum = red[0][lane];
+  Acc sum = red[0][lane];
 #pragma unroll
   for (int w = 1; w < kF8GvWaves; ++w) {
-    const f32x4 v = red[w][lane];
+    const Acc v = red[w][lane];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sum[r] = __fadd_rn(sum[r], v[r]);
+    for (int r = 0; r < 4; ++r) {
+      if constexpr (Op::kPerRow) sum[r] += v[r];  // exact int32 sums
+      else sum[r] = __fadd_rn(sum[r], v[r]);
+    }
   }
-  const float post = __fmul_rn(*a.sx, *a.sw);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t no = n0 + 4 * g + r;
     if (no >= a.N) continue;
-    float v = round_x<XT>(__fmul_rn(sum[r], post));
-    if (a.bias) v = round_x<XT>(__fadd_rn(v, round_x<XT>(load_as_f32(a.bias, no, a.bias_dt))));
+    const float v = byte_epilogue<XT, Op>(a, sum[r], int64_t(i16), no);
     a.y[int64_t(i16) * a.ldy + no] = uint16_t(to_x16<XT>(v));
   }
 }
@@ -314,10 +433,13 @@ __device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return r * 6
 struct Fp8Frags {
   u32x4 a[4][2], b[2][2];
 };
+struct HalfFrags {  // one 16-byte k-half of a stage's fragments
+  u32x4 a[4], b[2];
+};
 
-template <int XT>
+template <int XT, class Op>
 __global__ __launch_bounds__(kF8Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void fp8_gemm_kernel(Fp8Args a) {
+void byte_mfma_gemm_kernel(Fp8Args a) {
   __shared__ __attribute__((aligned(16))) uint8_t lds[kF8Stages * kF8StageBytes];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -372,50 +494,97 @@ void fp8_gemm_kernel(Fp8Args a) {
       for (int e = 0; e < 2; ++e)
         f.a[mb][e] = *reinterpret_cast<const u32x4*>(xt + swz64(arow + 32 * mb, uint32_t(2 * h + e)));
   };
+  auto read_half = [&](HalfFrags& f, int j, int e) {
+    j = j < nk ? j : nk - 1;
+    const uint8_t* xt = lds + (j % kF8Stages) * kF8StageBytes;
+    const uint8_t* wt = xt + kF8TileBytes;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+      f.b[nb] = *reinterpret_cast<const u32x4*>(wt + swz64(brow + 32 * nb, uint32_t(2 * h + e)));
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+      f.a[mb] = *reinterpret_cast<const u32x4*>(xt + swz64(arow + 32 * mb, uint32_t(2 * h + e)));
+  };
 
-  f32x16 acc[4][2];
+  typename Op::Acc32 acc[4][2];
 #pragma unroll
   for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) acc[mb][nb][r] = 0;
 
   // prologue: stages 0 .. 3 in flight, stage 0 read once it has landed
 #pragma unroll
   for (int s = 0; s < kF8Stages - 1; ++s) issue(s);
   step_barrier<4 * (kF8Stages - 2)>();
-  Fp8Frags cur;
-  read(cur, 0);
-  for (int j = 0; j < nk; ++j) {
-    step_barrier<4 * (kF8Stages - 3)>();
-    issue(j + kF8Stages - 1);
-    Fp8Frags nxt;
-    read(nxt, j + 1);
+  if constexpr (Op::kParts == 2) {
+    // int8: one instruction per k-half, so the fragments are double-buffered
+    // by half: half 1 of stage j is read while half 0 computes, half 0 of
+    // stage j + 1 while half 1 computes (48 fragment VGPRs beside the 128
+    // accumulators; a whole second stage of fragments would not fit)
+    // (each pass: one MFMA, one LDS read, six times, then the last two MFMAs)
+    auto interleave = [] {
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+      for (int i = 0; i < 6; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    };
+    HalfFrags lo;
+    read_half(lo, 0, 0);
+    for (int j = 0; j < nk; ++j) {
+      step_barrier<4 * (kF8Stages - 3)>();
+      issue(j + kF8Stages - 1);
+      __builtin_amdgcn_sched_barrier(0);
+      HalfFrags hi;
+      read_half(hi, j, 1);
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-        acc[mb][nb] = mfma_fn_32x32x64(cur.a[mb][0], cur.a[mb][1], cur.b[nb][0], cur.b[nb][1], acc[mb][nb]);
-    cur = nxt;
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Op::mma32h(lo.a[mb], lo.b[nb], acc[mb][nb]);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+      HalfFrags nlo;
+      read_half(nlo, j + 1, 0);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Op::mma32h(hi.a[mb], hi.b[nb], acc[mb][nb]);
+      interleave();
+      __builtin_amdgcn_sched_barrier(0);
+      lo = nlo;
+    }
+  } else {
+    Fp8Frags cur;
+    read(cur, 0);
+    for (int j = 0; j < nk; ++j) {
+      step_barrier<4 * (kF8Stages - 3)>();
+      issue(j + kF8Stages - 1);
+      Fp8Frags nxt;
+      read(nxt, j + 1);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          acc[mb][nb] = Op::mma32(cur.a[mb][0], cur.a[mb][1], cur.b[nb][0], cur.b[nb][1], acc[mb][nb]);
+      cur = nxt;
+    }
   }
   wait_vmcnt<0>();  // no load may still be landing in LDS when the workgroup ends
 
-  const float post = __fmul_rn(*a.sx, *a.sw);
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
     const int64_t n = n0 + 64 * wn + 32 * nb + i32;
     if (n >= a.N) continue;
-    const float bias = a.bias ? round_x<XT>(load_as_f32(a.bias, n, a.bias_dt)) : 0.0f;
 #pragma unroll
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t m = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * h + (r & 3);
         if (m >= a.M) continue;
-        float v = round_x<XT>(__fmul_rn(acc[mb][nb][r], post));
-        if (a.bias) v = round_x<XT>(__fadd_rn(v, bias));
-        a.y[m * a.ldy + n] = uint16_t(to_x16<XT>(v));
+        a.y[m * a.ldy + n] = uint16_t(to_x16<XT>(byte_epilogue<XT, Op>(a, acc[mb][nb][r], m, n)));
       }
   }
 }
@@ -470,20 +639,79 @@ static int fp8_linear_t(const Fp8LinearCall& c, void* workspace, hipStream_t str
     const int64_t steps128 = (c.K + 127) / 128;
     const int64_t per = (steps128 + kF8GvWaves - 1) / kF8GvWaves;
     a.gv_steps = int(per < 1 ? 1 : (per > kF8GvSteps ? kF8GvSteps : per));
-    fp8_gemv_kernel<XT><<<unsigned((c.N + 15) / 16), 512, 0, stream>>>(a);
+    byte_mfma_gemv_kernel<XT, Fp8Mma><<<unsigned((c.N + 15) / 16), 512, 0, stream>>>(a);
     return rq_check_launch();
   }
   a.tiles_m = int((c.M + kF8BM - 1) / kF8BM);
   a.tiles_n = int((c.N + kF8BN - 1) / kF8BN);
   const int64_t T = int64_t(a.tiles_m) * a.tiles_n;
   a.xcd_map = T % 8 == 0;
-  fp8_gemm_kernel<XT><<<unsigned(T), kF8Threads, 0, stream>>>(a);
+  byte_mfma_gemm_kernel<XT, Fp8Mma><<<unsigned(T), kF8Threads, 0, stream>>>(a);
   return rq_check_launch();
 }
 
 int fp8_linear_run(const Fp8LinearCall& c, void* workspace, hipStream_t stream) {
   if (c.x_dtype == RQ_DTYPE_BF16) return fp8_linear_t<RQ_DTYPE_BF16>(c, workspace, stream);
   return fp8_linear_t<RQ_DTYPE_F16>(c, workspace, stream);
+}
+
+// ---------------------------------------------------------------------------
+// W8A8: int8 activations (per row) x int8 weights (per row) on the int8
+// matrix cores.  Workspace: [M row scales, fp32][M x K int8 codes].
+// ---------------------------------------------------------------------------
+static size_t w8a8_scales_bytes(int64_t M) { return (size_t(M) * 4 + 255) & ~size_t(255); }
+
+size_t w8a8_ws_bytes(int64_t M, int64_t K) {
+  return w8a8_scales_bytes(M) + ((size_t(M) * size_t(K) + 255) & ~size_t(255));
+}
+
+template <int XT>
+static int i8_quantize_rows_t(const uint16_t* x, int64_t M, int64_t K, int64_t ldx, float* scales, int8_t* codes,
+                              hipStream_t stream) {
+  // few rows: 1024 threads per row shorten the row's two passes
+  if (M <= 64) i8_row_quant_kernel<XT, 1024><<<unsigned(M), 1024, 0, stream>>>(x, K, ldx, scales, codes);
+  else i8_row_quant_kernel<XT, 256><<<unsigned(M), 256, 0, stream>>>(x, K, ldx, scales, codes);
+  return rq_check_launch();
+}
+
+int i8_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, float* scales, int8_t* codes,
+                     hipStream_t stream) {
+  const uint16_t* xp = static_cast<const uint16_t*>(x);
+  if (x_dtype == RQ_DTYPE_BF16) return i8_quantize_rows_t<RQ_DTYPE_BF16>(xp, M, K, ldx, scales, codes, stream);
+  return i8_quantize_rows_t<RQ_DTYPE_F16>(xp, M, K, ldx, scales, codes, stream);
+}
+
+template <int XT>
+static int w8a8_linear_t(const W8A8LinearCall& c, void* workspace, hipStream_t stream) {
+  char* ws = static_cast<char*>(workspace);
+  float* xs = reinterpret_cast<float*>(ws);
+  int8_t* xq = reinterpret_cast<int8_t*>(ws + w8a8_scales_bytes(c.M));
+  int st = i8_quantize_rows_t<XT>(static_cast<const uint16_t*>(c.x), c.M, c.K, c.ldx, xs, xq, stream);
+  if (st != RQ_OK) return st;
+  Fp8Args a{};
+  a.x = reinterpret_cast<const uint8_t*>(xq); a.w = reinterpret_cast<const uint8_t*>(c.w);
+  a.M = c.M; a.N = c.N; a.K = c.K;
+  a.sx = xs; a.w_row_scale = c.w_scales; a.w_row_scale_dt = c.w_scales_dtype;
+  a.bias = c.bias; a.bias_dt = c.bias_dtype;
+  a.y = static_cast<uint16_t*>(c.y); a.ldy = c.ldy;
+  if (c.M <= 16) {
+    const int64_t steps128 = (c.K + 127) / 128;
+    const int64_t per = (steps128 + kF8GvWaves - 1) / kF8GvWaves;
+    a.gv_steps = int(per < 1 ? 1 : (per > kF8GvSteps ? kF8GvSteps : per));
+    byte_mfma_gemv_kernel<XT, I8Mma><<<unsigned((c.N + 15) / 16), 512, 0, stream>>>(a);
+    return rq_check_launch();
+  }
+  a.tiles_m = int((c.M + kF8BM - 1) / kF8BM);
+  a.tiles_n = int((c.N + kF8BN - 1) / kF8BN);
+  const int64_t T = int64_t(a.tiles_m) * a.tiles_n;
+  a.xcd_map = T % 8 == 0;
+  byte_mfma_gemm_kernel<XT, I8Mma><<<unsigned(T), kF8Threads, 0, stream>>>(a);
+  return rq_check_launch();
+}
+
+int w8a8_linear_run(const W8A8LinearCall& c, void* workspace, hipStream_t stream) {
+  if (c.x_dtype == RQ_DTYPE_BF16) return w8a8_linear_t<RQ_DTYPE_BF16>(c, workspace, stream);
+  return w8a8_linear_t<RQ_DTYPE_F16>(c, workspace, stream);
 }
 
 }  // namespace rq
@@ -523,4 +751,46 @@ extern "C" int rq_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, i
   c.w = w_codes; c.N = N; c.w_scale = w_scale; c.bias = bias; c.bias_dtype = bias_dtype;
   c.y = y; c.ldy = ldy;
   return rq::fp8_linear_run(c, workspace, stream);
+}
+
+extern "C" int rq_int8_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, int8_t* codes,
+                                     float* scales, hipStream_t stream) {
+  if (!x || !codes || !scales) return RQ_ERR_NULL_POINTER;
+  if (x_dtype != RQ_DTYPE_BF16 && x_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
+  if (M < 0 || K <= 0 || K % 8 != 0 || ldx < K) return RQ_ERR_BAD_SHAPE;
+  if (!rq::aligned(x, 16) || ldx % 8 != 0 || !rq::aligned(codes, 8)) return RQ_ERR_BAD_ALIGNMENT;
+  if (M > 0x7FFFFFFF) return RQ_ERR_UNSUPPORTED;
+  if (M == 0) return RQ_OK;
+  return rq::i8_quantize_rows(x, x_dtype, M, K, ldx, scales, codes, stream);
+}
+
+extern "C" int rq_int8_linear_w8a8_workspace_size(int64_t M, int64_t K, int64_t* bytes) {
+  if (!bytes) return RQ_ERR_NULL_POINTER;
+  if (M < 0 || K <= 0) return RQ_ERR_BAD_SHAPE;
+  *bytes = int64_t(rq::w8a8_ws_bytes(M, K));
+  return RQ_OK;
+}
+
+extern "C" int rq_int8_linear_w8a8(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, const int8_t* w,
+                                   int64_t N, const void* w_scales, int w_scales_dtype, const void* bias,
+                                   int bias_dtype, void* y, int64_t ldy, void* workspace, int64_t workspace_bytes,
+                                   hipStream_t stream) {
+  if (!x || !w || !w_scales || !y) return RQ_ERR_NULL_POINTER;
+  if (x_dtype != RQ_DTYPE_BF16 && x_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
+  if (!rq::valid_float_dtype(w_scales_dtype)) return RQ_ERR_BAD_DTYPE;
+  if (bias && !rq::valid_float_dtype(bias_dtype)) return RQ_ERR_BAD_DTYPE;
+  if (M < 0 || N <= 0 || K <= 0 || K % 64 != 0 || ldx < K || ldy < N) return RQ_ERR_BAD_SHAPE;
+  if (!rq::aligned(x, 16) || ldx % 8 != 0 || !rq::aligned(w, 16)) return RQ_ERR_BAD_ALIGNMENT;
+  // the GEMM addresses both code matrices with 32-bit byte offsets
+  if (double(M) * double(K) >= 4294967296.0 || double(N) * double(K) >= 4294967296.0) return RQ_ERR_UNSUPPORTED;
+  if (M > 0x7FFFFFFF) return RQ_ERR_UNSUPPORTED;
+  if (M == 0) return RQ_OK;
+  if (!workspace) return RQ_ERR_NULL_POINTER;
+  if (workspace_bytes < int64_t(rq::w8a8_ws_bytes(M, K))) return RQ_ERR_WORKSPACE;
+  if (!rq::aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;
+  rq::W8A8LinearCall c{};
+  c.x = x; c.x_dtype = x_dtype; c.M = M; c.K = K; c.ldx = ldx;
+  c.w = w; c.N = N; c.w_scales = w_scales; c.w_scales_dtype = w_scales_dtype;
+  c.bias = bias; c.bias_dtype = bias_dtype; c.y = y; c.ldy = ldy;
+  return rq::w8a8_linear_run(c, workspace, stream);
 }

@@ -34,8 +34,10 @@ struct Fp8Args {
   int tiles_m, tiles_n;
   bool xcd_map;
   int gv_steps;          // GEMV: 128-k steps per wave chunk
-  const float* sx;       // device per-tensor scales
-  const float* sw;
+  const float* sx;       // device scale(s) of the activations: per tensor (FP8) or per row (W8A8)
+  const float* sw;       // FP8: device per-tensor weight scale
+  const void* w_row_scale;  // W8A8: per-row weight scales of w_row_scale_dt
+  int w_row_scale_dt;
   const void* bias;
   int bias_dt;
   uint16_t* y;
@@ -56,7 +58,25 @@ struct Fp8LinearCall {
   int64_t ldy;
 };
 
+struct W8A8LinearCall {
+  const void* x;
+  int x_dtype;
+  int64_t M, K, ldx;
+  const int8_t* w;  // [N, K] int8, one scale per row
+  int64_t N;
+  const void* w_scales;
+  int w_scales_dtype;
+  const void* bias;
+  int bias_dtype;
+  void* y;
+  int64_t ldy;
+};
+
 size_t fp8_act_ws_bytes(int64_t M, int64_t K);
+size_t w8a8_ws_bytes(int64_t M, int64_t K);
+int w8a8_linear_run(const W8A8LinearCall& c, void* workspace, hipStream_t stream);
+int i8_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx, float* scales, int8_t* codes,
+                     hipStream_t stream);
 int fp8_linear_run(const Fp8LinearCall& c, void* workspace, hipStream_t stream);
 int fp8_fnuz_to_fn(const uint8_t* in, int64_t n, uint8_t* out, hipStream_t stream);
 

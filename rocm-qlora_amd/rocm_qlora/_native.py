@@ -72,6 +72,11 @@ SIGNATURES = {
     "rq_fp8_linear": [_P, _I32, _I64, _I64, _I64,            # x, dtype, M, K, ldx
                       _P, _I64, _P, _P, _I32,                # codes, N, w scale, bias, dtype
                       _P, _I64, _P, _I64, _P],               # y, ldy, workspace, bytes, stream
+    "rq_int8_quantize_rows": [_P, _I32, _I64, _I64, _I64, _P, _P, _P],
+    "rq_int8_linear_w8a8_workspace_size": [_I64, _I64, _P],
+    "rq_int8_linear_w8a8": [_P, _I32, _I64, _I64, _I64,      # x, dtype, M, K, ldx
+                            _P, _I64, _P, _I32, _P, _I32,    # w, N, w scales, dtype, bias, dtype
+                            _P, _I64, _P, _I64, _P],         # y, ldy, workspace, bytes, stream
 }
 _RESTYPE = {"rq_status_string": ctypes.c_char_p, "rq_build_arch": ctypes.c_char_p,
             "rq_set_gemv_spin_limit": ctypes.c_uint32}

@@ -364,6 +364,65 @@ def fp8_linear(x: torch.Tensor, w_codes: torch.Tensor, w_scale: torch.Tensor,
     return y.reshape(*lead, N)
 
 
+def int8_quantize_rows(x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row int8 quantization of 16-bit activations on the GPU: the
+    per-row recipe of quantize_int8 (quant_ops.py:29-35) in fp32.  Returns
+    (codes int8 [rows, K], scales fp32 [rows]) with scales[m] =
+    max(max|x[m]| / 127, 1e-12) and codes = RNE(x / scales[m])."""
+    K = x.shape[-1]
+    dev = nat.require_gpu(x)
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"bf16/fp16 activations expected, got {x.dtype}")
+    with on(dev):
+        x2, ldx = _aligned_rows(x, K)
+        M = x2.shape[0]
+        codes = torch.empty((M, K), dtype=torch.int8, device=dev)
+        scales = torch.empty((M,), dtype=torch.float32, device=dev)
+        if M:
+            nat.call("rq_int8_quantize_rows", x2.data_ptr(), nat.dtype_code(x.dtype), M, K, ldx,
+                     codes.data_ptr(), scales.data_ptr(), nat.stream_handle(dev))
+    return codes, scales
+
+
+def int8_linear_w8a8(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor,
+                     bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """W8A8 INT8 mode: x quantized per row to int8 (int8_quantize_rows), the
+    int8 products summed exactly in int32 by the int8 matrix cores, then
+    y = RND(RND(float(acc) * x_scale[m] * w_scale[n]) + RND(bias)).
+    q: [N, K] int8 with one scale per row (quantize_int8(w,
+    per_channel=True)); x: [..., K] bf16/fp16 on the GPU, K % 64 == 0.
+    Not the reference's INT8 linear (int8_linear: 16-bit activations times
+    dequantized weights): a separate, faster mode with activation rounding."""
+    K = x.shape[-1]
+    dev = nat.require_gpu(x, q, scales, bias)
+    if q.dtype != torch.int8:
+        raise TypeError(f"int8 weights expected, got {q.dtype}")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError(f"bf16/fp16 activations expected, got {x.dtype}")
+    wq = q.reshape(-1, K).contiguous()
+    N = wq.shape[0]
+    sc = scales.reshape(-1).contiguous()
+    if sc.numel() != N:
+        raise RuntimeError(f"W8A8 needs one weight scale per row: {sc.numel()} scales for {N} rows")
+    lead = x.shape[:-1]
+    with on(dev):
+        x2, ldx = _aligned_rows(x, K)
+        M = x2.shape[0]
+        y = torch.empty((M, N), dtype=x.dtype, device=dev)
+        if M == 0:
+            return y.reshape(*lead, N)
+        import ctypes
+        nb = ctypes.c_int64(0)
+        nat.call("rq_int8_linear_w8a8_workspace_size", M, K, ctypes.byref(nb))
+        ws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
+        b = bias.to(x.dtype).contiguous() if bias is not None else None
+        nat.call("rq_int8_linear_w8a8", x2.data_ptr(), nat.dtype_code(x.dtype), M, K, ldx,
+                 wq.data_ptr(), N, sc.data_ptr(), nat.dtype_code(sc.dtype), nat.ptr(b),
+                 nat.dtype_code(b.dtype) if b is not None else 0,
+                 y.data_ptr(), N, ws.data_ptr(), ws.numel(), nat.stream_handle(dev))
+    return y.reshape(*lead, N)
+
+
 MERGE_MODES = {"sum_then_round": nat.MERGE_SUM_THEN_ROUND, "round_then_sum": nat.MERGE_ROUND_THEN_SUM}
 
 

@@ -10,6 +10,7 @@ nodes instead of breaking the graph at every ctypes call:
     torch.ops.rocm_qlora.int8_linear     ops.int8_linear
     torch.ops.rocm_qlora.fp8_quantize    ops.fp8_quantize
     torch.ops.rocm_qlora.fp8_linear      ops.fp8_linear
+    torch.ops.rocm_qlora.int8_linear_w8a8  ops.int8_linear_w8a8
 
 Every operator returns new tensors and mutates none of its inputs.  Eager
 calls in this package go to the `ops` functions directly (the dispatcher
@@ -95,6 +96,17 @@ def _fp8_linear_fake(x, w_codes, w_scale, bias):
     return x.new_empty((*x.shape[:-1], n))
 
 
+@torch.library.custom_op("rocm_qlora::int8_linear_w8a8", mutates_args=())
+def int8_linear_w8a8(x: Tensor, q: Tensor, scales: Tensor, bias: Optional[Tensor]) -> Tensor:
+    return ops.int8_linear_w8a8(x, q, scales, bias)
+
+
+@int8_linear_w8a8.register_fake
+def _int8_linear_w8a8_fake(x, q, scales, bias):
+    n = q.numel() // x.shape[-1]
+    return x.new_empty((*x.shape[:-1], n))
+
+
 def _compiling() -> bool:
     try:
         return torch.compiler.is_compiling()
@@ -148,3 +160,10 @@ def call_fp8_linear(x, w_codes, w_scale, bias=None):
     if _compiling():
         return torch.ops.rocm_qlora.fp8_linear(x, w_codes, w_scale, bias)
     return ops.fp8_linear(x, w_codes, w_scale, bias)
+
+
+def call_int8_linear_w8a8(x, q, scales, bias=None):
+    """ops.int8_linear_w8a8, through the registered operator while being traced."""
+    if _compiling():
+        return torch.ops.rocm_qlora.int8_linear_w8a8(x, q, scales, bias)
+    return ops.int8_linear_w8a8(x, q, scales, bias)

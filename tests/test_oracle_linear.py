@@ -176,3 +176,67 @@ def test_merge_and_export_restatements_pinned():
     z = torch.zeros(N, r)
     for fn in (R.merge_lora_weight, R.export_dequant_layer):
         assert torch.equal(fn(w, a, z, s, N, K), w16)
+
+
+def test_w8a8_activation_codes_are_the_per_row_recipe():
+    """quantize_rows_int8 is quantize_int8(per_channel=True) on fp32 rows
+    (that function is pinned against the C restatement)."""
+    g = torch.Generator().manual_seed(51)
+    x = (torch.randn(7, 96, generator=g) * 3).to(torch.bfloat16)
+    x[2] = 0
+    q, s = R.quantize_rows_int8(x)
+    q2, s2 = R.quantize_int8(x.float(), per_channel=True)
+    assert torch.equal(q, q2) and torch.equal(s, s2.reshape(-1))
+    assert float(s[2]) == pytest.approx(1e-12) and int(q[2].abs().max()) == 0
+    assert int(q.abs().max()) == 127
+
+
+def test_w8a8_integer_sum_brute_force():
+    """The integer core of w8a8_linear against a Python-int brute force, and
+    the scales applied to it in fp32, each rounding once."""
+    g = torch.Generator().manual_seed(52)
+    x = torch.randn(3, 64, generator=g).to(torch.bfloat16)
+    q = torch.randint(-127, 128, (5, 64), generator=g).to(torch.int8)
+    ws = torch.rand(5, generator=g) * 0.01 + 1e-3
+    qx, sx = R.quantize_rows_int8(x)
+    y = R.w8a8_linear(x, q, ws)
+    for m in range(3):
+        for n in range(5):
+            acc = sum(int(qx[m, k]) * int(q[n, k]) for k in range(64))
+            want = torch.tensor(float(acc), dtype=torch.float32) * sx[m] * ws[n]
+            assert y[m, n] == want.to(torch.bfloat16)
+
+
+def test_w8a8_power_of_two_scales_equal_the_w8a16_product():
+    """Rows of x with absmax 127 * 2^-j (scales 2^-j, codes exact) and weights
+    with power-of-two row scales: every step is exact, so W8A8 equals the
+    reference's INT8 linear (x times dequantized weights) bit for bit."""
+    g = torch.Generator().manual_seed(53)
+    M, N, K = 4, 6, 128
+    kx = torch.randint(-127, 128, (M, K), generator=g)
+    kx[:, 5] = 127
+    x = (kx.double() * 2.0 ** -torch.arange(3, 3 + M).double()[:, None]).to(torch.bfloat16)
+    q = torch.randint(-127, 128, (N, K), generator=g).to(torch.int8)
+    ws = 2.0 ** -torch.randint(4, 9, (N,), generator=g).float()
+    bias = (torch.randint(-64, 64, (N,), generator=g).float() / 8).to(torch.bfloat16)
+    y = R.w8a8_linear(x, q, ws, bias)
+    want = (R.int8_linear(x.float(), q, ws)).to(torch.bfloat16) + bias
+    assert torch.equal(y, want)
+    exact = (x.double() @ (q.double() * ws.double()[:, None]).T).to(torch.bfloat16) + bias
+    assert torch.equal(y, exact)
+
+
+def test_w8a8_close_to_float64_of_its_codes():
+    """General scales: within one bf16 ulp of the float64 product of the
+    decoded codes (three fp32 roundings, then one to bf16)."""
+    g = torch.Generator().manual_seed(54)
+    x = torch.randn(9, 256, generator=g).to(torch.bfloat16)
+    w = torch.randn(33, 256, generator=g) * 0.02
+    q, ws = R.quantize_int8(w, per_channel=True)
+    y = R.w8a8_linear(x, q, ws)
+    qx, sx = R.quantize_rows_int8(x)
+    exact = (qx.double() * sx.double()[:, None]) @ (q.double() * ws.double()[:, None]).T
+    ulp = (exact.abs().to(torch.bfloat16).double().abs() * 2.0 ** -7).clamp_min(2.0 ** -133)
+    assert bool(((y.double() - exact).abs() <= ulp).all())
+    # and close to the unquantized product
+    assert torch.allclose(y.float(), x.float() @ w.T, rtol=0.05, atol=0.05)
