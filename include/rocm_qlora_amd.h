@@ -359,6 +359,53 @@ int rq_merge_lora(const void* w, int w_format, int64_t N, int64_t K, int64_t blo
                   const void* lora_a, const void* lora_b, int64_t ld_lora_b, int lora_dtype, int64_t rank,
                   float scaling, int mode, void* out, int out_dtype, int64_t ld_out, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Optimizer step for the LoRA parameters
+ * ------------------------------------------------------------------------ */
+
+/* Elements per chunk: tensors' state offsets are multiples of it, and one
+ * workgroup updates one chunk. */
+#define RQ_ADAMW_CHUNK 2048
+
+/* One tensor of a fused AdamW step (72 bytes).  The fp32 scalars are the
+ * reference's Python doubles rounded to fp32 (as torch passes them to its
+ * kernels), for this tensor's step count t:
+ *   decay = 1 - lr * weight_decay (applied when apply_decay, i.e. wd != 0),
+ *   beta1, one_minus_beta1 = 1 - beta1, beta2, one_minus_beta2 = 1 - beta2,
+ *   bias_correction2_sqrt = (1 - beta2 ** t) ** 0.5, eps,
+ *   neg_step_size = -(lr / (1 - beta1 ** t)). */
+typedef struct rq_adamw_tensor {
+  void* param;            /* [numel] of dtype, updated in place */
+  const void* grad;       /* [numel] of dtype */
+  int64_t numel;
+  int64_t state_offset;   /* first element in the state buffers; multiple of RQ_ADAMW_CHUNK */
+  int32_t dtype;          /* RQ_DTYPE_F32 / BF16 / F16, parameter and gradient */
+  int32_t apply_decay;
+  float decay, beta1, one_minus_beta1, beta2, one_minus_beta2, bias_correction2_sqrt, eps, neg_step_size;
+} rq_adamw_tensor;
+
+/* Replaces the per-parameter update of PagedAdamW.step
+ * (optim/paged_adamw.py:84-113): AdamW with decoupled weight decay on every
+ * listed tensor in one launch, in the reference's order of operations --
+ *   p = RND_p(p * decay); m = fma(1 - b1, g, RND(m * b1));
+ *   v = fma(RND((1 - b2) * g), g, RND(v * b2));
+ *   d = RND(RND(sqrt(v)) / bias_correction2_sqrt) + eps;
+ *   p = RND_p(p + RND(RND(neg_step_size * m) / d))
+ * (fp32 arithmetic, the square root correctly rounded, RND_p the rounding to
+ * the parameter's dtype; the fused multiply-adds are where torch's kernels
+ * fuse them).  The exp_avg (m) and exp_avg_sq (v) states are fp32 buffers
+ * indexed by state offset: this call updates the chunks chunk_begin ..
+ * chunk_end - 1, and exp_avg / exp_avg_sq (16-byte aligned) point at the
+ * element chunk_begin * RQ_ADAMW_CHUNK and hold (chunk_end - chunk_begin) *
+ * RQ_ADAMW_CHUNK elements (so a caller can stream the states through a
+ * device page).  tensors: host array of n_tensors descriptors in ascending,
+ * non-overlapping state order (each spans numel rounded up to a chunk),
+ * copied to device_table (>= n_tensors * 72 bytes) on the stream before the
+ * launch; tensors without a gradient are left out of the array. */
+int rq_adamw_step(const rq_adamw_tensor* tensors, int64_t n_tensors, void* device_table,
+                  int64_t device_table_bytes, int64_t chunk_begin, int64_t chunk_end,
+                  float* exp_avg, float* exp_avg_sq, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,10 @@ tests/test_oracle_linear.py:
     the reference): equal to quantize_int8(per_channel=True) on fp32 rows;
     an int64 brute-force sum; rows whose absmax is 127 * 2^-j (power-of-two
     scales, exact codes) give int8_linear's float64 product exactly.
+  * paged_adamw_step: torch.optim.AdamW (the same update rule, the library's
+    own implementation) over several steps; zero gradients give exactly
+    p * (1 - lr wd)^t; a constant gradient moves p by lr * t * g / (|g| + eps)
+    (bias-corrected moments equal g and g^2).
 No function of this module is left without such a check.
 """
 from __future__ import annotations
@@ -252,6 +256,33 @@ def w8a8_linear(x: torch.Tensor, q: torch.Tensor, w_scales: torch.Tensor,
     if bias is not None:
         y = y + bias.to(x.dtype)
     return y.reshape(*x.shape[:-1], -1)
+
+
+# ------------------------------------------------------------ optimizer step
+def paged_adamw_step(params, grads, exp_avgs, exp_avg_sqs, steps, lr: float = 2e-4,
+                     betas: Tuple[float, float] = (0.9, 0.999), eps: float = 1e-8,
+                     weight_decay: float = 0.01, exact_sqrt: bool = False) -> None:
+    """One PagedAdamW step, paged_adamw.py:84-113, in place on CPU tensors:
+    params / grads / exp_avgs / exp_avg_sqs are lists (states fp32); steps is
+    the list of per-parameter step counts after this step.  Parameters with a
+    None gradient are skipped (:86-87).  exact_sqrt: take the square root of
+    exp_avg_sq correctly rounded (through float64) instead of with torch's
+    vectorized CPU sqrt, which is one fp32 ulp off for some inputs, by how
+    much depending on the host's SIMD path; every other op is torch's."""
+    beta1, beta2 = betas
+    for p, grad, exp_avg, exp_avg_sq, t in zip(params, grads, exp_avgs, exp_avg_sqs, steps):
+        if grad is None:
+            continue
+        bias_correction1 = 1 - beta1 ** t                                   # :94
+        bias_correction2 = 1 - beta2 ** t                                   # :95
+        if weight_decay != 0:                                               # :103-104
+            p.mul_(1 - lr * weight_decay)
+        exp_avg.mul_(beta1).add_(grad, alpha=1 - beta1)                     # :107
+        exp_avg_sq.mul_(beta2).addcmul_(grad, grad, value=1 - beta2)        # :108
+        root = exp_avg_sq.double().sqrt().float() if exact_sqrt else exp_avg_sq.sqrt()
+        denom = (root / (bias_correction2 ** 0.5)).add_(eps)                # :110
+        step_size = lr / bias_correction1                                   # :111
+        p.addcdiv_(exp_avg, denom, value=-step_size)                        # :113
 
 
 # ----------------------------------------------------------- merge / export

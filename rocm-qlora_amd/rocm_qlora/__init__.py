@@ -18,6 +18,7 @@ from rocm_qlora.quantization.quant_linear import QuantLinear  # noqa: E402
 from rocm_qlora.quantization.w8a8_linear import W8A8Linear  # noqa: E402
 from rocm_qlora.lora.lora_layer import LoRALinear  # noqa: E402
 from rocm_qlora.model.quantize_model import quantize_model, enable_all_kernels  # noqa: E402
+from rocm_qlora.optim import PagedAdamW  # noqa: E402
 from rocm_qlora.kernels import (  # noqa: E402
     fused_dequant_int8_matmul, fused_dequant_nf4_matmul, get_device_info, is_triton_available,
 )
@@ -30,7 +31,7 @@ from rocm_qlora.hip_kernels.build_utils import (  # noqa: E402
 )
 
 __all__ = [
-    "quantize_model", "QuantLinear", "LoRALinear", "W8A8Linear",
+    "quantize_model", "QuantLinear", "LoRALinear", "W8A8Linear", "PagedAdamW",
     "fused_dequant_int8_matmul", "fused_dequant_nf4_matmul",
     "get_device_info", "is_triton_available", "enable_all_kernels",
     "is_hip_kernel_available", "enable_hip_kernels", "hip_dequant_int4_matmul", "hip_dequant_int8_matmul",

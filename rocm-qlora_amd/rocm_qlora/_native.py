@@ -73,6 +73,8 @@ SIGNATURES = {
                       _P, _I64, _P, _P, _I32,                # codes, N, w scale, bias, dtype
                       _P, _I64, _P, _I64, _P],               # y, ldy, workspace, bytes, stream
     "rq_int8_quantize_rows": [_P, _I32, _I64, _I64, _I64, _P, _P, _P],
+    "rq_adamw_step": [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _P],  # table, n, dev table, bytes,
+                                                                  # chunks [b, e), m, v, stream
     "rq_int8_linear_w8a8_workspace_size": [_I64, _I64, _P],
     "rq_int8_linear_w8a8": [_P, _I32, _I64, _I64, _I64,      # x, dtype, M, K, ldx
                             _P, _I64, _P, _I32, _P, _I32,    # w, N, w scales, dtype, bias, dtype
