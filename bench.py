@@ -40,10 +40,15 @@ Also reported:
                 copies rotating) and M = 512, 4096 (TFLOP/s against the bf16,
                 int8 and fp8 MFMA peaks, 2.5, 5.0 and 5.0 P/s), plus W8A8's
                 relative deviation from W8A16 at M = 512.
+  optimizer     the fused AdamW step over the LoRA adapters of a whole
+                Llama-3-8B (r = 16, 7 projections x 32 layers, 41.9 M fp32
+                parameters): kernel time vs 8 TB/s (28 bytes per parameter),
+                and PagedAdamW.step() wall time with the states resident and
+                offloaded to pinned host memory.
   cpu_baseline  the oracle's restatement of the reference's CPU path on the
                 host cores: the headline decode step whole (`value`), and per
                 configuration (fp32 config 1, codec, GEMM forward / dX, INT8 /
-                FP8) on stated samples, each beside the GPU time of the same
+                FP8, the AdamW update) on stated samples, each beside the GPU time of the same
                 work; 2 warm-ups, median of 10 runs, thread count, core count
                 and CPU model reported.
 
@@ -334,6 +339,26 @@ def cpu_baselines(layer_cpu, xs_cpu, M, gpu):
     out["config5_fp8_m1"] = entry(t, b5, "gbs", gpu["fp8_m1_s"] * f if gpu.get("fp8_m1_s") else None,
                                   f"{n5} of {N5} rows, W quantized per call as the reference does; "
                                   f"gpu_us scaled to the same rows")
+    del w5, x5, q5
+    # optimizer: the PagedAdamW update on the adapters of 4 of the 32 layers
+    shapes = lora_param_shapes(layers=4)
+    ps = [torch.randn(sh, generator=g) * 0.02 for sh in shapes]
+    gs = [torch.randn(sh, generator=g) * 1e-3 for sh in shapes]
+    ms = [torch.zeros(sh) for sh in shapes]
+    vs = [torch.zeros(sh) for sh in shapes]
+    cnt = [0]
+
+    def opt_step():
+        cnt[0] += 1
+        R.paged_adamw_step(ps, gs, ms, vs, [cnt[0]] * len(ps), lr=2e-4, weight_decay=0.01)
+    n_opt = sum(a * b for a, b in shapes)
+    t = _cpu_time(opt_step)
+    f = 4 / ADAMW_LAYERS
+    out["optimizer_adamw_step"] = entry(t, 28 * n_opt, "gbs",
+                                        gpu["adamw_step_s"] * f if gpu.get("adamw_step_s") else None,
+                                        f"LoRA adapters of 4 of the 32 Llama-3-8B layers ({n_opt} fp32 parameters), "
+                                        f"the update alone (no host/device copies); gpu_us scaled to the same "
+                                        f"parameters")
     return out, t3
 
 
@@ -507,6 +532,86 @@ def bench_byte_linears(dev, stream):
         del x
     return {"workload": f"INT8 per-row (W8A16 and W8A8) and FP8 per-tensor linears, K={K} N={N}, "
                         "bf16 activations", **out}
+
+
+ADAMW_LAYERS = 32  # Llama-3-8B
+
+
+def lora_param_shapes(layers=ADAMW_LAYERS, rank=RANK):
+    """LoRA A [r, K] and B [N, r] of the seven projections of `layers` layers."""
+    out = []
+    for _ in range(layers):
+        for _, K, N in LLAMA3_8B_PROJ:
+            out += [(rank, K), (N, rank)]
+    return out
+
+
+def bench_optimizer(dev, stream):
+    """The fused AdamW step (rq_adamw_step behind PagedAdamW) over the LoRA
+    adapters of a whole Llama-3-8B: r = 16 on the seven projections of 32
+    layers, 448 fp32 tensors, 41.9 M parameters, gradients N(0, 1e-3);
+    algorithmic bytes 28 per parameter (p, m, v read and written, g read).
+    `kernel_us`: back-to-back rq_adamw_step calls (a 32 KB descriptor copy and
+    one launch each), HIP events on the launch stream, mean of 50;
+    `step_resident_ms` / `step_offload_ms`: wall time of PagedAdamW.step()
+    with the states resident in HBM / in pinned host memory paged through
+    256 MB device pages (the reference's memory behaviour; PCIe-bound),
+    median of 20 and 5."""
+    import torch
+    from rocm_qlora import _native as nat
+    from rocm_qlora.optim import PagedAdamW
+    shapes = lora_param_shapes()
+    n_params = sum(a * b for a, b in shapes)
+    nbytes = 28 * n_params
+    g = torch.Generator(device=dev).manual_seed(77)
+    params = [torch.nn.Parameter(torch.randn(s, generator=g, device=dev) * 0.02) for s in shapes]
+    for p in params:
+        p.grad = torch.randn(p.shape, generator=g, device=dev) * 1e-3
+    out = {"workload": f"AdamW step over Llama-3-8B LoRA adapters (r={RANK}, 7 projections x "
+                       f"{ADAMW_LAYERS} layers, {len(shapes)} fp32 tensors)",
+           "params": n_params, "bytes_per_step": nbytes}
+    with torch.cuda.stream(stream):
+        opt = PagedAdamW(params, lr=2e-4, weight_decay=0.01, offload_states=False)
+        opt.step()
+        table, keep, _ = opt._table(dev)
+        nch = opt._total // 2048
+        call = lambda: nat.call("rq_adamw_step", table.ctypes.data, len(table), opt._dev_table.data_ptr(),
+                                opt._dev_table.numel(), 0, nch, opt._m.data_ptr(), opt._v.data_ptr(),
+                                stream.cuda_stream)
+        for _ in range(5):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 50
+        e0.record(stream)
+        for _ in range(reps):
+            call()
+        e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        gbs = nbytes / us / 1e3
+        out.update({"kernel_us": round(us, 2), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        t = []
+        for _ in range(20):
+            stream.synchronize()
+            t0 = time.perf_counter()
+            opt.step()
+            stream.synchronize()
+            t.append(time.perf_counter() - t0)
+        t.sort()
+        out["step_resident_ms"] = round(t[len(t) // 2] * 1e3, 3)
+        del opt, keep
+        opt = PagedAdamW(params, lr=2e-4, weight_decay=0.01, offload_states=True, page_size_mb=256)
+        opt.step()
+        t = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            opt.step()  # ends with a synchronization, as the reference's step
+            t.append(time.perf_counter() - t0)
+        t.sort()
+        out["step_offload_ms"] = round(t[len(t) // 2] * 1e3, 3)
+        out["offload_pcie_gbs"] = round(16 * n_params / t[len(t) // 2] / 1e9, 1)
+    del opt, params
+    return out
 
 
 def _short(name, n=70):
@@ -841,7 +946,7 @@ def main():
     else:
         layer0 = layers[0]
 
-    codec = byte = None
+    codec = byte = optim = None
     if not args.no_extra:
         codec = bench_codec(dev, stream)
         print(f"bench: codec encode {codec['encode_gbs']} GB/s, decode {codec['decode_gbs']} GB/s",
@@ -854,6 +959,12 @@ def main():
                                                   if isinstance(v, dict)), file=sys.stderr, flush=True)
         gpu_s["int8_m1_s"] = byte["int8_m1"]["us"] * 1e-6
         gpu_s["fp8_m1_s"] = byte["fp8_m1"]["us"] * 1e-6
+        torch.cuda.empty_cache()
+        optim = bench_optimizer(dev, stream)
+        print(f"bench: AdamW step {optim['kernel_us']} us ({optim['gbs']} GB/s), resident step "
+              f"{optim['step_resident_ms']} ms, offloaded step {optim['step_offload_ms']} ms",
+              file=sys.stderr, flush=True)
+        gpu_s["adamw_step_s"] = optim["kernel_us"] * 1e-6
         torch.cuda.empty_cache()
 
     cpu = None
@@ -898,6 +1009,7 @@ def main():
         "gemm": gemm,
         "codec": codec,
         "byte_linears": byte,
+        "optimizer": optim,
         "cpu_baseline": cpu,
     }
     print(json.dumps(rec), flush=True)

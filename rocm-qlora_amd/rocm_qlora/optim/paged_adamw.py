@@ -106,6 +106,25 @@ class PagedAdamW(Optimizer):
         self._offsets, self._total, self._m, self._v = offsets, total, m, v
         self._pages = None  # device page buffers (offload), made on first use
         self._dev_table = None
+        self._build_static()
+
+    def _build_static(self) -> None:
+        """The per-tensor descriptor fields that do not change between steps."""
+        plist, gidx = [], []
+        for gi, group in enumerate(self.param_groups):
+            for p in group["params"]:
+                plist.append(p)
+                gidx.append(gi)
+        st = np.zeros(len(plist), dtype=_TABLE)
+        st["param"] = [p.data_ptr() for p in plist]
+        st["numel"] = [p.numel() for p in plist]
+        st["state_offset"] = [self._offsets[p] for p in plist]
+        st["dtype"] = [nat.dtype_code(p.dtype) if p.dtype in (torch.float32, torch.bfloat16, torch.float16) else -1
+                       for p in plist]
+        self._static, self._plist, self._gidx = st, plist, gidx
+        self._contig = [p.is_contiguous() for p in plist]
+        self._states = [self.state[p] for p in plist]
+        self._views = [(t["exp_avg"], t["exp_avg_sq"]) for t in self._states]
 
     def add_param_group(self, param_group: Dict[str, Any]) -> None:
         super().add_param_group(param_group)
@@ -113,45 +132,73 @@ class PagedAdamW(Optimizer):
             self._build_layout()
 
     def _layout_intact(self) -> bool:
-        for p, o in self._offsets.items():
-            st = self.state.get(p)
-            if st is None or "exp_avg" not in st:
+        """The parameter list is the one laid out and every state still holds
+        its views of the flat buffers (load_state_dict or a hand-made state
+        replaces them)."""
+        if len(self._plist) != sum(len(g["params"]) for g in self.param_groups):
+            return False
+        state = self.state
+        for p, st, (m, v) in zip(self._plist, self._states, self._views):
+            if state.get(p) is not st or st.get("exp_avg") is not m or st.get("exp_avg_sq") is not v:
                 return False
-            m, v = st["exp_avg"], st["exp_avg_sq"]
-            if (m.data_ptr() != self._m.data_ptr() + 4 * o or v.data_ptr() != self._v.data_ptr() + 4 * o):
-                return False
-        return set(self._offsets) == set(self._params())
+        return True
 
     # ------------------------------------------------------------- step
     def _table(self, dev: torch.device) -> Tuple[np.ndarray, List[torch.Tensor], List[Tuple[int, int]]]:
-        rows, keep, spans = [], [], []
-        for group in self.param_groups:
-            beta1, beta2 = group["betas"]
-            lr, wd, eps = group["lr"], group["weight_decay"], group["eps"]
-            for p in group["params"]:
-                if p.grad is None:
-                    continue
-                g = p.grad
-                if g.is_sparse:
-                    raise RuntimeError("PagedAdamW does not support sparse gradients")
-                if p.device != dev or g.device != dev:
-                    raise RuntimeError(f"PagedAdamW: every parameter and gradient must be on {dev}")
-                if not p.is_contiguous():
-                    raise RuntimeError("PagedAdamW updates parameters in place: they must be contiguous")
-                if g.dtype != p.dtype:
-                    raise RuntimeError(f"gradient dtype {g.dtype} differs from parameter dtype {p.dtype}")
+        """This step's descriptors (tensors with a gradient, in state order),
+        the gradients to keep alive until the launch, and their chunk spans.
+        Advances the step count of each listed tensor."""
+        plist = self._plist
+        if [p.data_ptr() for p in plist] != self._static["param"].tolist():
+            self._build_static()  # a parameter's storage was replaced
+        grads = [p.grad for p in plist]
+        live = [i for i, g in enumerate(grads) if g is not None]
+        keep, gptr = [], []
+        idx = dev.index if dev.index is not None else torch.cuda.current_device()
+        for i in live:
+            g, p = grads[i], plist[i]
+            if g.layout is not torch.strided:
+                raise RuntimeError("PagedAdamW does not support sparse gradients")
+            if g.dtype is not p.dtype:
+                raise RuntimeError(f"gradient dtype {g.dtype} differs from parameter dtype {p.dtype}")
+            if not self._contig[i]:
+                raise RuntimeError("PagedAdamW updates parameters in place: they must be contiguous")
+            if g.get_device() != idx or p.get_device() != idx:
+                raise RuntimeError(f"PagedAdamW: every parameter and gradient must be on {dev}")
+            if not g.is_contiguous():
                 g = g.contiguous()
-                st = self.state[p]
-                st["step"] += 1
-                t = st["step"]
-                bc1 = 1 - beta1 ** t                                      # paged_adamw.py:97-98
+            keep.append(g)
+            gptr.append(g.data_ptr())
+        if (self._static["dtype"][live] < 0).any():
+            raise RuntimeError("PagedAdamW updates fp32, bf16 and fp16 parameters")
+        rows = self._static[live]
+        rows["grad"] = gptr
+        # per (group, step) scalars, in the reference's double arithmetic
+        cache, vals = {}, []
+        groups = self.param_groups
+        for i in live:
+            st = self._states[i]
+            st["step"] += 1
+            key = (self._gidx[i], st["step"])
+            v = cache.get(key)
+            if v is None:
+                grp = groups[key[0]]
+                beta1, beta2 = grp["betas"]
+                lr, wd, eps, t = grp["lr"], grp["weight_decay"], grp["eps"], key[1]
+                bc1 = 1 - beta1 ** t                                      # paged_adamw.py:94-95
                 bc2 = 1 - beta2 ** t
-                o = self._offsets[p]
-                rows.append((p.data_ptr(), g.data_ptr(), p.numel(), o, nat.dtype_code(p.dtype), int(wd != 0),
-                             1 - lr * wd, beta1, 1 - beta1, beta2, 1 - beta2, bc2 ** 0.5, eps, -(lr / bc1)))
-                keep.append(g)
-                spans.append((o // ADAMW_CHUNK, o // ADAMW_CHUNK + _chunks(p.numel())))
-        return np.array(rows, dtype=_TABLE), keep, spans
+                v = cache[key] = (int(wd != 0), 1 - lr * wd, beta1, 1 - beta1, beta2, 1 - beta2, bc2 ** 0.5, eps,
+                                  -(lr / bc1))
+            vals.append(v)
+        if vals:
+            cols = list(zip(*vals))
+            rows["apply_decay"] = cols[0]
+            for name, col in zip(("decay", "beta1", "one_minus_beta1", "beta2", "one_minus_beta2",
+                                  "bias_correction2_sqrt", "eps", "neg_step_size"), cols[1:]):
+                rows[name] = np.asarray(col, dtype=np.float64)  # rounded to fp32 once, to nearest
+        first = rows["state_offset"] // ADAMW_CHUNK
+        spans = list(zip(first.tolist(), (first + (rows["numel"] + ADAMW_CHUNK - 1) // ADAMW_CHUNK).tolist()))
+        return rows, keep, spans
 
     def _launch(self, table: np.ndarray, c0: int, c1: int, m: torch.Tensor, v: torch.Tensor) -> None:
         need = table.nbytes
