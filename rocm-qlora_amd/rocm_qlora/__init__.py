@@ -30,8 +30,20 @@ from rocm_qlora.hip_kernels.build_utils import (  # noqa: E402
     find_hipcc, is_hipcc_available, compile_hip_kernel, get_or_compile_int4_kernel,
 )
 
+
+
+def __getattr__(name):
+    """RocmQLoraConfig / RocmQLoraQuantizer (the reference's top-level names,
+    rocm_qlora/__init__.py:42) load transformers on first use, not at import."""
+    if name in ("RocmQLoraConfig", "RocmQLoraQuantizer"):
+        from rocm_qlora import hf_integration
+        return getattr(hf_integration, name)
+    raise AttributeError(f"module 'rocm_qlora' has no attribute {name!r}")
+
+
 __all__ = [
     "quantize_model", "QuantLinear", "LoRALinear", "W8A8Linear", "PagedAdamW",
+    "RocmQLoraConfig", "RocmQLoraQuantizer",
     "fused_dequant_int8_matmul", "fused_dequant_nf4_matmul",
     "get_device_info", "is_triton_available", "enable_all_kernels",
     "is_hip_kernel_available", "enable_hip_kernels", "hip_dequant_int4_matmul", "hip_dequant_int8_matmul",

@@ -62,9 +62,14 @@ def quantize_model(model: nn.Module, bits: int = 8, lora_r: int = 8, lora_alpha:
                 continue
             parent, attr = _get_parent_and_attr(model, name)
             replacements.append((parent, attr, module))
-    for parent, attr, linear in replacements:
+    # one layer at a time, each source layer released once replaced, so the
+    # peak holds one layer's 16-bit weight beside the quantized model
+    replacements.reverse()
+    while replacements:
+        parent, attr, linear = replacements.pop()
         ql = QuantLinear.from_linear(linear, bits=bits, block_size=block_size)
         setattr(parent, attr, LoRALinear(ql, r=lora_r, lora_alpha=lora_alpha, lora_dropout=lora_dropout))
+        del linear, ql
 
     print("\n--- Model Quantization Summary ---")
     print_model_summary(model)

@@ -166,7 +166,7 @@ def test_adamw_trains_lora_and_matches_torch_adamw(dev):
             loss.backward()
             opt.step()
             if opt is opt_a:
-                losses.append(float(loss))
+                losses.append(float(loss.detach()))
     assert losses[-1] < losses[0]
     for pa, pb in ((layers[0].lora_A, layers[1].lora_A), (layers[0].lora_B, layers[1].lora_B)):
         assert float((pa - pb).abs().max()) < 1e-5
