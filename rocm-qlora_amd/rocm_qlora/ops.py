@@ -41,15 +41,35 @@ def _rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
 #     buffer returns to torch's caching allocator, which hands it out again
 #     only in stream order);
 #   * graph capture: one buffer per (device, capture, stream) -- the branches
-#     of a capture that forks side streams each get their own -- allocated
+#     of a capture that forks side streams each get their own.  It is taken
+#     from a pool of pre-zeroed buffers (_CAPTURE_POOL_ENTRIES of
+#     _CAPTURE_POOL_BYTES per device, zeroed once, with one stream
+#     synchronization, at the device's first eager call), so the graph needs
+#     no fill node: it holds zeros before the first replay and every replay
+#     leaves it zero.  Such a buffer is held for the life of the process (the
+#     graph may replay it at any time).  A capture on a device without the
+#     pool, with the pool used up, or needing a larger buffer allocates one
 #     from the graph's private memory pool (so it lives exactly as long as
-#     the graph) and zeroed by a fill kernel recorded in the graph, which
-#     every replay runs before the captured calls.
-# No host synchronization is involved either way.
+#     the graph), zeroed by a fill kernel recorded in the graph, which every
+#     replay runs before the captured calls.
 LINEAR_SYNC_BYTES = 65792
 _LINEAR_WS: dict = {}
 _CAPTURE_WS: dict = {}
 _WS_MIN_BYTES = 1 << 20
+_CAPTURE_POOL_ENTRIES = 32
+_CAPTURE_POOL_BYTES = 256 * 1024
+_CAPTURE_POOL: dict = {}       # device index -> pre-zeroed buffers not yet handed out
+_CAPTURE_POOL_BASE: dict = {}  # device index -> the allocation they are views of (kept for good)
+
+
+def _ensure_capture_pool(dev, idx: int) -> None:
+    if idx in _CAPTURE_POOL_BASE:
+        return
+    base = torch.zeros(_CAPTURE_POOL_ENTRIES * _CAPTURE_POOL_BYTES, dtype=torch.uint8, device=dev)
+    torch.cuda.current_stream(dev).synchronize()  # zero before any later capture, on any stream, replays it
+    _CAPTURE_POOL_BASE[idx] = base
+    _CAPTURE_POOL[idx] = [base[i * _CAPTURE_POOL_BYTES:(i + 1) * _CAPTURE_POOL_BYTES]
+                          for i in range(_CAPTURE_POOL_ENTRIES)]
 
 
 def _zeroed_area(nbytes: int, dev, min_bytes: int = _WS_MIN_BYTES) -> torch.Tensor:
@@ -80,11 +100,15 @@ def _workspace(x_dtype: torch.dtype, M: int, K: int, N: int, rank: int, dev) -> 
         ws = _CAPTURE_WS.get(key)
         if ws is None or ws.numel() < need:
             # a larger buffer replaces a smaller one for the calls captured
-            # from here on; calls captured before keep theirs (both are
-            # zeroed by their own recorded fills)
-            ws = _zeroed_area(need, dev, min_bytes=LINEAR_SYNC_BYTES)
+            # from here on; calls captured before keep theirs
+            pool = _CAPTURE_POOL.get(idx)
+            if pool and need <= _CAPTURE_POOL_BYTES:
+                ws = pool.pop()
+            else:
+                ws = _zeroed_area(need, dev, min_bytes=LINEAR_SYNC_BYTES)
             _CAPTURE_WS[key] = ws
         return ws
+    _ensure_capture_pool(dev, idx)
     key = (idx, stream)
     ws = _LINEAR_WS.get(key)
     if ws is None or ws.numel() < need:

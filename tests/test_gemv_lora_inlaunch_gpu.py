@@ -194,3 +194,49 @@ def test_unaligned_operands_run_separate_kernel(dev, case):
     base = R.quant_linear_forward(x, R.dequantize_int4(packed.cpu(), absmax.cpu(), 64), None, N, K)
     ref = R.lora_forward(xl, base, a, b, 2.0)
     _check(y, ref)
+
+
+def test_capture_forking_side_streams(dev):
+    """A capture that forks two side streams, each running fused-LoRA M = 1
+    GEMVs (the in-launch handshake) and a GEMM with K splits: each branch
+    gets a workspace of its own, and every replay matches eager calls bit
+    for bit; the eager workspace's synchronization area stays zero."""
+    K, M, rank = 4096, 1, 16
+    specs = [(4096, 31), (1024, 32)]
+    layers = [(N,) + _layer(N, K, rank, seed=s, dev=dev) for N, s in specs]
+    ops_dev = [(N, p, s_, a.to(dev), b.to(dev)) for N, p, s_, a, b in layers]
+    xs = torch.zeros(M, K, dtype=torch.bfloat16, device=dev)
+    xg = torch.zeros(64, K, dtype=torch.bfloat16, device=dev)
+
+    def run(x, x64):
+        out = []
+        for N, p, s_, ad, bd in ops_dev:
+            out.append(ops.nf4_linear(x, p, s_, N, 64, lora_a=ad, lora_b=bd, scaling=2.0))
+        N, p, s_, ad, bd = ops_dev[1]
+        out.append(ops.nf4_linear(x64, p, s_, N, 64, lora_a=ad, lora_b=bd, scaling=2.0))
+        return out
+
+    run(xs, xg)  # eager warm-up
+    torch.cuda.synchronize(dev)
+    s1, s2 = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        main = torch.cuda.current_stream(dev)
+        s1.wait_stream(main)
+        s2.wait_stream(main)
+        with torch.cuda.stream(s1):
+            o1 = run(xs, xg)
+        with torch.cuda.stream(s2):
+            o2 = run(xs, xg)
+        main.wait_stream(s1)
+        main.wait_stream(s2)
+    for i in range(4):
+        xs.copy_(_x(M, K, seed=90 + i).to(dev))
+        xg.copy_(_x(64, K, seed=95 + i).to(dev))
+        graph.replay()
+        got = [t.clone() for t in o1 + o2]
+        want = run(xs, xg)
+        torch.cuda.synchronize(dev)
+        for g, w in zip(got, want + want):
+            assert torch.equal(g, w), f"replay {i} differs from the eager calls"
+    _sync_words_zero(dev)
