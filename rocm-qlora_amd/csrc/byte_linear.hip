@@ -236,10 +236,11 @@ __global__ __launch_bounds__(256) void fp8_encode_kernel(const void* __restrict_
                                                          int64_t ld, const float* __restrict__ scale,
                                                          uint8_t* __restrict__ codes) {
   const float s = *scale;
+  const float rs = recip_rn(s);
   const int64_t total = rows * cols;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
     const int64_t r = i / cols, c = i - r * cols;
-    codes[i] = f32_to_fnuz_rne(round_to(__fdiv_rn(ld_f32<DT>(t, r * ld + c), s), DT));
+    codes[i] = f32_to_fnuz_rne(div_round<DT>(ld_f32<DT>(t, r * ld + c), s, rs));
   }
 }
 

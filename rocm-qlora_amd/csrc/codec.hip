@@ -8,6 +8,7 @@
 // semantics of quantization/quant_ops.py and quantization/double_quant.py
 // (NaN payloads aside).
 #include "rq_common.h"
+#include "rq_mfma.h"
 #include "nf4_tables.h"
 #include "rq_launch.h"
 
@@ -20,22 +21,21 @@ namespace rq {
 // first NaN.
 // ---------------------------------------------------------------------------
 struct NF4CellTable {
-  uint32_t thr[64];
-  uint32_t base[64];
+  u32x2 e[65];  // {threshold bits, base index} of each 1/32-wide cell; e[64] = e[63] (n = 1)
 };
 
 __device__ __forceinline__ void load_cell_table(NF4CellTable* t) {
-  for (int i = threadIdx.x; i < 64; i += blockDim.x) {
-    t->thr[i] = kNF4CellThr[i];
-    t->base[i] = kNF4CellBase[i];
+  for (int i = threadIdx.x; i < 65; i += blockDim.x) {
+    const int c = i < 64 ? i : 63;
+    t->e[i] = u32x2{kNF4CellThr[c], kNF4CellBase[c]};
   }
 }
 
 __device__ __forceinline__ uint32_t nf4_decide(float n, const NF4CellTable* t) {
   float c = __fmul_rn(__fadd_rn(n, 1.0f), 32.0f);
   c = fminf(fmaxf(c, 0.0f), 63.0f);   // NaN -> 0 (v_max returns the non-NaN operand)
-  int g = int(c);
-  return t->base[g] + (n > u2f(t->thr[g]) ? 1u : 0u);
+  const u32x2 cell = t->e[int(c)];
+  return cell.y + (n > u2f(cell.x) ? 1u : 0u);
 }
 
 // normalised value as torch computes `reshaped / scales` in the input dtype
@@ -105,6 +105,149 @@ __global__ __launch_bounds__(256) void nf4_quantize_fast(const void* __restrict_
   if (!live) return;
   reinterpret_cast<uint32_t*>(packed)[t] = word;
   if ((t & ((int64_t(1) << log2_l) - 1)) == 0) store_from_f32(absmax, t >> log2_l, DT, s);
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit input fast path (bf16 / fp16, block_size = 8 * L, L a power of two
+// <= 64, 16-byte aligned weights): the same decisions as nf4_quantize_fast
+// in fewer instructions per weight (the stream is instruction-bound):
+//  * absmax over the raw 16-bit patterns: |x| is h & 0x7FFF, and for
+//    non-negative 16-bit floats the integer order is the value order with
+//    every NaN above infinity, so a packed unsigned 16-bit max gives the
+//    block maximum, NaN if the block holds one (torch's max propagates NaN);
+//    the L lanes of a block reduce with DPP lane swaps (xor 1, xor 2, mirror
+//    in 8, mirror in 16) and LDS permutes beyond 16 lanes;
+//  * n = RND(x / s) by div_round's shortcut, the rare elements it flags
+//    divided exactly (one branch per 8 weights), rounded by the hardware
+//    RNE conversions (NaN stays NaN, whose decision is 0 either way);
+//  * the cell index as int(fma(n, 32, 32)): 32 (n + 1) is exact up to the
+//    rounding of n + 1, which scaling by 32 commutes with; -1 <= n <= 1 gives
+//    0 .. 64 (cell 64, n = 1 exactly, repeats cell 63) and a NaN converts
+//    to 0.
+// The absmax and rs = RN(1/s) are finite or the quotient is NaN / a signed
+// zero on both routes: s >= the clamp floor (bf16 1e-12; fp16 s >= 2^-24 or
+// 0, where x = 0 and both routes give NaN), so non-finite products need no
+// check.  A workgroup covers kQGroups * 256 groups of 8 weights, lane group g
+// of thread i being group (blockIdx * kQGroups + g) * 256 + i; workgroups
+// wholly inside the tensor issue their four 16-byte loads first.
+// ---------------------------------------------------------------------------
+constexpr int kQGroups = 4;
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t dpp_max_u32(uint32_t m, int ctrl_sel) {
+  uint32_t o;
+  switch (ctrl_sel) {
+    case 0: o = uint32_t(__builtin_amdgcn_update_dpp(int(m), int(m), 0xB1, 0xF, 0xF, false)); break;   // xor 1
+    case 1: o = uint32_t(__builtin_amdgcn_update_dpp(int(m), int(m), 0x4E, 0xF, 0xF, false)); break;   // xor 2
+    case 2: o = uint32_t(__builtin_amdgcn_update_dpp(int(m), int(m), 0x141, 0xF, 0xF, false)); break;  // 7 - i
+    default: o = uint32_t(__builtin_amdgcn_update_dpp(int(m), int(m), 0x140, 0xF, 0xF, false)); break; // 15 - i
+  }
+  return m > o ? m : o;
+}
+
+// Maximum of m over the 2^log2_l lanes of this lane's aligned group.
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t m, int log2_l) {
+  if (log2_l >= 1) m = dpp_max_u32(m, 0);
+  if (log2_l >= 2) m = dpp_max_u32(m, 1);
+  if (log2_l >= 3) m = dpp_max_u32(m, 2);
+  if (log2_l >= 4) m = dpp_max_u32(m, 3);
+  for (int o = 16; o < (1 << log2_l); o <<= 1) {
+    const uint32_t p = uint32_t(__shfl_xor(int(m), o));
+    m = m > p ? m : p;
+  }
+  return m;
+}
+
+template <int DT>
+__device__ __forceinline__ bool needs_exact(float r) {
+  const uint32_t b = f2u(r);
+  constexpr uint32_t kLow = DT == RQ_DTYPE_BF16 ? 0xFFFFu : 0x1FFFu;
+  constexpr uint32_t kMid = DT == RQ_DTYPE_BF16 ? 0x8000u : 0x1000u;
+  bool e = ((b & kLow) - (kMid - 4u)) <= 8u;
+  if constexpr (DT == RQ_DTYPE_F16) e = e || (b & 0x7FFFFFFFu) < 0x38800000u;
+  return e;
+}
+
+__device__ __forceinline__ uint32_t nf4_decide_fma(float n, const NF4CellTable* t) {
+  const u32x2 cell = t->e[int(__builtin_fmaf(n, 32.0f, 32.0f))];
+  return cell.y + (n > u2f(cell.x) ? 1u : 0u);
+}
+
+// Element h (0: low half, 1: high half) of a dword of two 16-bit floats.
+template <int DT>
+__device__ __forceinline__ float half16(uint32_t w, int h) {
+  if constexpr (DT == RQ_DTYPE_BF16) return u2f(h ? (w & 0xFFFF0000u) : (w << 16));
+  else return f16_to_f32(uint16_t(h ? (w >> 16) : (w & 0xFFFFu)));
+}
+
+template <int DT>
+__device__ __forceinline__ void quantize_group16(const u32x4& raw, int64_t t, int log2_l, bool live,
+                                                 const NF4CellTable* table, uint8_t* __restrict__ packed,
+                                                 void* __restrict__ absmax) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  u16x2 a[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) a[j] = __builtin_bit_cast(u16x2, w[j] & 0x7FFF7FFFu);
+  const u16x2 m2 = __builtin_elementwise_max(__builtin_elementwise_max(a[0], a[1]),
+                                             __builtin_elementwise_max(a[2], a[3]));
+  uint32_t mb = m2.x > m2.y ? uint32_t(m2.x) : uint32_t(m2.y);
+  mb = group_max_u32(mb, log2_l);
+  const float s = clamp_floor(from_x16<DT>(mb), DT);
+  const float rs = recip_rn(s);
+  float x[8], r[8];
+  bool any = false;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    x[j] = half16<DT>(w[j >> 1], j & 1);
+    r[j] = __fmul_rn(x[j], rs);
+    any |= needs_exact<DT>(r[j]);
+  }
+  if (any) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (needs_exact<DT>(r[j])) r[j] = __fdiv_rn(x[j], s);
+  }
+  uint32_t word = 0;
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    const uint32_t pk = cvt_pk<DT>(r[j], r[j + 1]);
+    word |= nf4_decide_fma(half16<DT>(pk, 0), table) << (4 * j);
+    word |= nf4_decide_fma(half16<DT>(pk, 1), table) << (4 * j + 4);
+  }
+  if (!live) return;
+  reinterpret_cast<uint32_t*>(packed)[t] = word;
+  if ((t & ((int64_t(1) << log2_l) - 1)) == 0) store_from_f32(absmax, t >> log2_l, DT, s);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void nf4_quantize16_kernel(const uint16_t* __restrict__ w, int64_t numel,
+                                                             int64_t n_lanes, int log2_l,
+                                                             uint8_t* __restrict__ packed,
+                                                             void* __restrict__ absmax) {
+  __shared__ NF4CellTable table;
+  load_cell_table(&table);
+  __syncthreads();
+  const int64_t t0 = int64_t(blockIdx.x) * (256 * kQGroups) + threadIdx.x;
+  const int64_t end = int64_t(blockIdx.x + 1) * (256 * kQGroups);  // groups of this workgroup
+  if (end * 8 <= numel) {
+    u32x4 raw[kQGroups];
+#pragma unroll
+    for (int g = 0; g < kQGroups; ++g)
+      raw[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + (t0 + 256 * g) * 8));
+#pragma unroll
+    for (int g = 0; g < kQGroups; ++g) quantize_group16<DT>(raw[g], t0 + 256 * g, log2_l, true, &table, packed, absmax);
+    return;
+  }
+  for (int g = 0; g < kQGroups; ++g) {
+    const int64_t t = t0 + 256 * g;
+    // lanes past the end still take part in the reductions with zeros
+    const bool live = t < n_lanes;
+    uint32_t h[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (live && t * 8 + j < numel) ? uint32_t(w[t * 8 + j]) : 0u;
+    const u32x4 raw = {h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+    quantize_group16<DT>(raw, t, log2_l, live, &table, packed, absmax);
+  }
 }
 
 // Generic path: one wave per block of any even size; lane l handles element
@@ -330,7 +473,16 @@ extern "C" int rq_nf4_quantize(const void* w, int w_dtype, int64_t numel, int64_
     if ((l & (l - 1)) == 0) log2_l = __builtin_ctzll(l);
   }
   const bool vec = aligned(w, 16);
-  if (log2_l >= 0 && aligned(packed, 4)) {
+  if (log2_l >= 0 && aligned(packed, 4) && vec && w_dtype != RQ_DTYPE_F32) {
+    const int64_t n_lanes = padded / 8;
+    dim3 grid(unsigned(ceil_div(n_lanes, 256 * kQGroups)));
+    if (w_dtype == RQ_DTYPE_BF16)
+      nf4_quantize16_kernel<RQ_DTYPE_BF16><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(w), numel,
+                                                                     n_lanes, log2_l, packed, absmax);
+    else
+      nf4_quantize16_kernel<RQ_DTYPE_F16><<<grid, 256, 0, stream>>>(static_cast<const uint16_t*>(w), numel,
+                                                                    n_lanes, log2_l, packed, absmax);
+  } else if (log2_l >= 0 && aligned(packed, 4)) {
     const int64_t n_lanes = padded / 8;
     dim3 grid(unsigned(ceil_div(n_lanes, 256)));
     RQ_DISPATCH_DT(w_dtype, DT, nf4_quantize_fast<DT><<<grid, 256, 0, stream>>>(

@@ -142,13 +142,13 @@ __device__ __forceinline__ float h2f(uint32_t h) {
 
 // 8 elements (one 16-byte vector) -> 8 fn codes (two dwords).
 template <int DT>
-__device__ __forceinline__ u32x2 encode8_fn(const u32x4& v, float s) {
+__device__ __forceinline__ u32x2 encode8_fn(const u32x4& v, float s, float rs) {
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
   uint32_t c[2] = {0u, 0u};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const float f = h2f<DT>((w[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
-    const uint32_t code = f32_to_fnuz_rne(round_to(__fdiv_rn(f, s), DT));
+    const uint32_t code = f32_to_fnuz_rne(div_round<DT>(f, s, rs));
     c[e >> 2] |= code << (8 * (e & 3));
   }
   return u32x2{fnuz_to_fn4(c[0]), fnuz_to_fn4(c[1])};
@@ -191,9 +191,10 @@ __global__ __launch_bounds__(1024) void fp8_quant_small_kernel(const uint16_t* _
   }
   const float s = float(double(block_absmax_1024(m, red)) / 240.0);
   if (threadIdx.x == 0) *scale = s;
+  const float rs = recip_rn(s);
   for (int i = threadIdx.x; i < total; i += 1024) {
     const int r = i / gpr, c = i - r * gpr;
-    const u32x2 q = encode8_fn<DT>(*reinterpret_cast<const u32x4*>(x + int64_t(r) * ld + 8 * c), s);
+    const u32x2 q = encode8_fn<DT>(*reinterpret_cast<const u32x4*>(x + int64_t(r) * ld + 8 * c), s, rs);
     *reinterpret_cast<u32x2*>(codes + int64_t(r) * cols + 8 * c) = q;
   }
 }
@@ -297,11 +298,12 @@ __global__ __launch_bounds__(256) void fp8_encode16_kernel(const uint16_t* __res
   __shared__ float red[256];
   const float s = scale_from_parts(part, nparts, red);
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
+  const float rs = recip_rn(s);
   const int64_t gpr = cols / 8, total = rows * gpr;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
     const int64_t r = i / gpr, c = i - r * gpr;
     *reinterpret_cast<u32x2*>(codes + r * cols + 8 * c) =
-        encode8_fn<DT>(*reinterpret_cast<const u32x4*>(x + r * ld + 8 * c), s);
+        encode8_fn<DT>(*reinterpret_cast<const u32x4*>(x + r * ld + 8 * c), s, rs);
   }
 }
 

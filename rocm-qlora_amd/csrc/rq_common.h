@@ -101,6 +101,39 @@ __device__ __forceinline__ float max_nan(float m, float a) {
   return (a > m || a != a || m != m) ? ((m != m) ? m : a) : m;
 }
 
+// RND_DT(RN32(x / s)) -- a tensor division in a 16-bit dtype as torch's
+// CPU kernels compute it -- given rs = RN32(1 / s).
+//
+// For 16-bit DT the correctly rounded quotient is needed only up to its
+// rounding to DT.  When rs is finite, r = RN32(x * rs) lies within 2 fp32
+// ulps of RN32(x / s) (|rs - 1/s| <= 2^-24 / s, so |x * rs - x/s| <= one ulp
+// of x/s, plus half an ulp for each of the two roundings), and RND_DT changes
+// value only at the fp32 numbers whose bits below DT's precision are exactly
+// the midpoint pattern (bf16: low 16 bits 0x8000; fp16 normals: low 13 bits
+// 0x1000).  So RND_DT(r) = RND_DT(RN32(x / s)) unless those bits of r are
+// within 4 of the midpoint, r is not finite (an infinite x or rs, a NaN) or
+// |r| is below fp16's normal range (whose rounding drops more bits); those
+// rare elements divide exactly.  (x = 0 with s = 0 or s = inf gives the same
+// NaN or signed zero either way.)  fp32 input divides exactly.
+template <int DT>
+__device__ __forceinline__ float div_round(float x, float s, float rs) {
+  if constexpr (DT == RQ_DTYPE_F32) {
+    return __fdiv_rn(x, s);
+  } else {
+    constexpr uint32_t kLow = DT == RQ_DTYPE_BF16 ? 0xFFFFu : 0x1FFFu;
+    constexpr uint32_t kMid = DT == RQ_DTYPE_BF16 ? 0x8000u : 0x1000u;
+    float r = __fmul_rn(x, rs);
+    const uint32_t b = f2u(r);
+    bool exact = ((b & kLow) - (kMid - 4u)) <= 8u || (b & 0x7F800000u) == 0x7F800000u;
+    if constexpr (DT == RQ_DTYPE_F16) exact = exact || (b & 0x7FFFFFFFu) < 0x38800000u;  // |r| < 2^-14
+    if (exact) r = __fdiv_rn(x, s);
+    return round_to(r, DT);
+  }
+}
+
+// RN32(1 / s) for div_round (one correctly rounded division per scale).
+__device__ __forceinline__ float recip_rn(float s) { return __fdiv_rn(1.0f, s); }
+
 // torch.clamp(s, min=1e-12) in storage dtype `dt` (NaN propagates).
 __device__ __forceinline__ float clamp_floor(float s, int dt) {
   float lo = (dt == RQ_DTYPE_F32) ? u2f(kClampF32) : (dt == RQ_DTYPE_BF16 ? u2f(kClampBF16) : 0.0f);

@@ -39,6 +39,21 @@ def test_quantize_int4_bit_exact(dev, dtype, block):
         assert bits_equal(s, s_ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("block", [32, 64, 256])
+def test_quantize_int4_large_with_edge_blocks(dev, dtype, block):
+    """Sizes where whole workgroups take the straight 16-byte path and the
+    last one the per-group tail: zero, constant, NaN, Inf and tiny blocks first,
+    then N(0, 0.02) weights with outliers, 301 x 4096 + the edge blocks."""
+    edge = _edge_weights(dtype, block).reshape(-1)
+    w = torch.cat([edge, _weights((301, 4096), dtype, 21).reshape(-1)])
+    print(f"quantize_int4 large dtype={dtype} block={block} numel={w.numel()}", flush=True)
+    p_ref, s_ref = R.quantize_int4(w, block)
+    p, s = quantize_int4(w.to(dev), block)
+    assert bits_equal(p, p_ref)
+    assert bits_equal(s, s_ref)
+
+
 def test_quantize_int4_unaligned_view(dev):
     w = _weights((4096 + 3,), torch.bfloat16, 9)
     view = w.to(dev)[3:]  # 6-byte offset: generic (non-vector) loads
@@ -68,6 +83,29 @@ def test_dequantize_int4_bit_exact(dev, sdtype, block):
         print(f"dequant block={block} sdtype={sdtype} out={od}", flush=True)
         got = nf4_dequantize_to(p_ref.to(dev), s_ref.to(dev), block, od, n)
         assert bits_equal(got, ref[:n].to(od))
+
+
+@pytest.mark.parametrize("sdtype", [torch.float32, torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("od", [torch.bfloat16, torch.float16, torch.float32])
+def test_dequantize_int4_large_and_offset_codes(dev, sdtype, od):
+    """Whole workgroups of 16-byte code loads and a ragged last one (300 x
+    4096 - 40 weights), and the same codes through an 8-byte (not 16-byte)
+    aligned view, which takes the 8-byte path everywhere."""
+    w = _weights((300, 4096), sdtype, 22)
+    p_ref, s_ref = R.quantize_int4(w, 64)
+    ref = R.dequantize_int4(p_ref, s_ref, 64)
+    n = w.numel() - 40
+    print(f"dequant large sdtype={sdtype} out={od}", flush=True)
+    got = nf4_dequantize_to(p_ref.to(dev), s_ref.to(dev), 64, od, n)
+    assert bits_equal(got, ref[:n].to(od))
+    # codes from byte 8 on (weights 16 ..): an 8-byte aligned view
+    pad = torch.zeros(8, dtype=torch.uint8)
+    buf = torch.cat([pad, p_ref]).to(dev)
+    view = buf[8:]
+    assert view.data_ptr() % 16 == 8
+    s_view = s_ref.to(dev)
+    got = nf4_dequantize_to(view, s_view, 64, od, n)
+    assert bits_equal(got, ref[:n].to(od))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
