@@ -286,10 +286,12 @@ __global__ __launch_bounds__(256) void nf4_quantize_generic(const void* __restri
 // NF4 dequantize.  Fast path: block_size % 16 == 0, each lane expands 8 packed
 // bytes (16 weights, inside one block) with the code book in LDS.
 // ---------------------------------------------------------------------------
+// (b_off: the block index of the first weight of the launch's range)
 struct ScaleSingle {
   const void* absmax;
   int dt;
-  __device__ __forceinline__ float operator()(int64_t b) const { return load_as_f32(absmax, b, dt); }
+  int64_t b_off;
+  __device__ __forceinline__ float operator()(int64_t b) const { return load_as_f32(absmax, b + b_off, dt); }
 };
 
 struct ScaleDouble {
@@ -298,7 +300,9 @@ struct ScaleDouble {
   int c2s_dt;
   int fmt;
   int64_t block2;
+  int64_t b_off;
   __device__ __forceinline__ float operator()(int64_t b) const {
+    b += b_off;
     float hi = load_as_f32(c2s, b / block2, c2s_dt);
     float lo;
     if (fmt == RQ_C2_FP8_E4M3FNUZ) lo = fnuz_to_f32(c2[b]);
@@ -369,6 +373,62 @@ __global__ __launch_bounds__(256) void nf4_dequant_fast(const uint8_t* __restric
     v[2 * j + 1] = __fmul_rn(lut[byte >> 4], s);
   }
   store16<ODT>(out, e0, n_out, vec, v);
+}
+
+// ---------------------------------------------------------------------------
+// 16-bit output fast path (bf16 / fp16 out, power-of-two block sizes >= 16,
+// codes 4-byte and output 16-byte aligned).  A chunk is 8 weights: one
+// dword of codes, one 16-byte output vector.  Wave v of a workgroup owns
+// chunks 256 v' .. 256 v' + 255 (v' = 4 blockIdx + v) and lane l takes
+// chunks 256 v' + 64 j + l, j = 0..3, so that each of the wave's four
+// stores writes 1 KiB of consecutive bytes and each code load reads 256
+// consecutive bytes.  The scales are template policies with compile-time
+// dtypes, so a lane's four code loads and its scale loads are all issued
+// before the first is used.  Workgroups reaching past the end of the codes
+// or of the output take the generic-width path below.
+// ---------------------------------------------------------------------------
+template <int SDT>
+struct DqScaleAbs {
+  const void* absmax;
+  __device__ __forceinline__ float operator()(int64_t b) const { return load_as_f32(absmax, b, SDT); }
+};
+
+template <int SDT, int FMT>
+struct DqScaleDouble {
+  const uint8_t* c2;
+  const void* c2s;
+  int b2_log2;  // block2 = 2^b2_log2
+  __device__ __forceinline__ float operator()(int64_t b) const {
+    const float hi = load_as_f32(c2s, b >> b2_log2, SDT);
+    const float lo = FMT == RQ_C2_FP8_E4M3FNUZ ? fnuz_to_f32(c2[b]) : __fdiv_rn(float(int8_t(c2[b])), 127.0f);
+    return __fmul_rn(lo, hi);
+  }
+};
+
+template <int ODT, class Scale>
+__global__ __launch_bounds__(256) void nf4_dequant16_kernel(const uint32_t* __restrict__ packed, Scale scale,
+                                                            int bs_log2, uint32_t* __restrict__ out) {
+  __shared__ float lut[16];
+  if (threadIdx.x < 16) lut[threadIdx.x] = u2f(kNF4Bits[threadIdx.x]);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int64_t c0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * 256 + lane;
+  uint32_t p[4];
+  float s[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) p[j] = __builtin_nontemporal_load(packed + c0 + 64 * j);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) s[j] = scale(((c0 + 64 * j) * 8) >> bs_log2);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t byte = (p[j] >> (8 * k)) & 0xFFu;
+      o[k] = cvt_pk<ODT>(__fmul_rn(lut[byte & 0xF], s[j]), __fmul_rn(lut[byte >> 4], s[j]));
+    }
+    __builtin_nontemporal_store(u32x4{o[0], o[1], o[2], o[3]}, reinterpret_cast<u32x4*>(out) + c0 + 64 * j);
+  }
 }
 
 template <int ODT, class Scale>
@@ -495,6 +555,29 @@ extern "C" int rq_nf4_quantize(const void* w, int w_dtype, int64_t numel, int64_
   return rq_check_launch();
 }
 
+static int64_t dtype_bytes(int dt) { return dt == RQ_DTYPE_F32 ? 4 : 2; }
+
+// Runs nf4_dequant16_kernel over the whole workgroups that fit (1024 chunks
+// of 8 weights each) and returns the number of weights covered (0 when the
+// call does not qualify); the rest goes through nf4_dequant_launch.
+template <class Scale>
+static int64_t nf4_dequant16_prefix(const uint8_t* packed, Scale scale, int64_t n_packed, int64_t bs,
+                                    void* out, int out_dtype, int64_t n_out, hipStream_t stream) {
+  if (out_dtype == RQ_DTYPE_F32 || bs < 16 || (bs & (bs - 1)) || !aligned(packed, 4) || !aligned(out, 16))
+    return 0;
+  const int64_t chunks = n_packed / 4 < n_out / 8 ? n_packed / 4 : n_out / 8;
+  const int64_t wgs = chunks / 1024;
+  if (wgs <= 0 || wgs > 0x7FFFFFFF) return 0;
+  const int bs_log2 = __builtin_ctzll(uint64_t(bs));
+  const uint32_t* p = reinterpret_cast<const uint32_t*>(packed);
+  uint32_t* o = static_cast<uint32_t*>(out);
+  if (out_dtype == RQ_DTYPE_BF16)
+    nf4_dequant16_kernel<RQ_DTYPE_BF16, Scale><<<unsigned(wgs), 256, 0, stream>>>(p, scale, bs_log2, o);
+  else
+    nf4_dequant16_kernel<RQ_DTYPE_F16, Scale><<<unsigned(wgs), 256, 0, stream>>>(p, scale, bs_log2, o);
+  return wgs * 1024 * 8;
+}
+
 template <class Scale>
 static int nf4_dequant_launch(const uint8_t* packed, Scale scale, int64_t n_packed, int64_t bs,
                               void* out, int out_dtype, int64_t n_out, hipStream_t stream) {
@@ -522,8 +605,22 @@ extern "C" int rq_nf4_dequantize(const uint8_t* packed, const void* absmax, int 
   if (n_out == 0) return RQ_OK;
   if (!packed || !absmax || !out) return RQ_ERR_NULL_POINTER;
   if (n_packed > (int64_t(1) << 36)) return RQ_ERR_BAD_SHAPE;
-  return nf4_dequant_launch(packed, ScaleSingle{absmax, absmax_dtype}, n_packed, block_size, out,
-                            out_dtype, n_out, stream);
+  int64_t done = 0;
+  if (block_size <= 8192) {
+    if (absmax_dtype == RQ_DTYPE_F32)
+      done = nf4_dequant16_prefix(packed, DqScaleAbs<RQ_DTYPE_F32>{absmax}, n_packed, block_size, out, out_dtype,
+                                  n_out, stream);
+    else if (absmax_dtype == RQ_DTYPE_BF16)
+      done = nf4_dequant16_prefix(packed, DqScaleAbs<RQ_DTYPE_BF16>{absmax}, n_packed, block_size, out,
+                                  out_dtype, n_out, stream);
+    else
+      done = nf4_dequant16_prefix(packed, DqScaleAbs<RQ_DTYPE_F16>{absmax}, n_packed, block_size, out,
+                                  out_dtype, n_out, stream);
+  }
+  if (done == n_out) return rq_check_launch();
+  return nf4_dequant_launch(packed + done / 2, ScaleSingle{absmax, absmax_dtype, done / block_size},
+                            n_packed - done / 2, block_size, static_cast<char*>(out) + done * dtype_bytes(out_dtype),
+                            out_dtype, n_out - done, stream);
 }
 
 extern "C" int rq_dq_quantize(const void* c1, int c1_dtype, int64_t n_c1, int64_t block2,
@@ -551,8 +648,26 @@ extern "C" int rq_dq_dequantize(const uint8_t* packed, const uint8_t* c2, int c2
   if ((2 * n_packed) % block1 != 0) return RQ_ERR_BAD_SHAPE;
   if (n_out == 0) return RQ_OK;
   if (!packed || !c2 || !c2_scales || !out) return RQ_ERR_NULL_POINTER;
-  return nf4_dequant_launch(packed, ScaleDouble{c2, c2_scales, c2s_dtype, c2_format, block2},
-                            n_packed, block1, out, out_dtype, n_out, stream);
+  int64_t done = 0;
+  if (block1 <= 8192 && (block2 & (block2 - 1)) == 0) {
+    const int b2 = __builtin_ctzll(uint64_t(block2));
+    auto run = [&](auto sc) { return nf4_dequant16_prefix(packed, sc, n_packed, block1, out, out_dtype, n_out, stream); };
+    const bool fp8 = c2_format == RQ_C2_FP8_E4M3FNUZ;
+    if (c2s_dtype == RQ_DTYPE_F32)
+      done = fp8 ? run(DqScaleDouble<RQ_DTYPE_F32, RQ_C2_FP8_E4M3FNUZ>{c2, c2_scales, b2})
+                 : run(DqScaleDouble<RQ_DTYPE_F32, RQ_C2_INT8>{c2, c2_scales, b2});
+    else if (c2s_dtype == RQ_DTYPE_BF16)
+      done = fp8 ? run(DqScaleDouble<RQ_DTYPE_BF16, RQ_C2_FP8_E4M3FNUZ>{c2, c2_scales, b2})
+                 : run(DqScaleDouble<RQ_DTYPE_BF16, RQ_C2_INT8>{c2, c2_scales, b2});
+    else
+      done = fp8 ? run(DqScaleDouble<RQ_DTYPE_F16, RQ_C2_FP8_E4M3FNUZ>{c2, c2_scales, b2})
+                 : run(DqScaleDouble<RQ_DTYPE_F16, RQ_C2_INT8>{c2, c2_scales, b2});
+  }
+  if (done == n_out) return rq_check_launch();
+  return nf4_dequant_launch(packed + done / 2,
+                            ScaleDouble{c2, c2_scales, c2s_dtype, c2_format, block2, done / block1},
+                            n_packed - done / 2, block1, static_cast<char*>(out) + done * dtype_bytes(out_dtype),
+                            out_dtype, n_out - done, stream);
 }
 
 extern "C" int rq_int8_quantize(const void* w, int w_dtype, int64_t rows, int64_t cols,
