@@ -476,6 +476,30 @@ def bench_codec(dev, stream):
             "decode_gbs": round(dec, 1), "decode_frac": round(dec / HBM_PEAK_GBS, 4)}
 
 
+def bench_int8_codec(w, qs, stream):
+    """INT8 weight codec on one bf16 weight: per-row quantization (bytes: 2
+    numel read, numel codes + 2 N scales written) and its fp32 reconstruction
+    (numel codes + 2 N scales read, 4 numel written), 10 graph replays each."""
+    from rocm_qlora.quantization import dequantize_int8, quantize_int8
+    N, K = w.shape
+    q, s = qs
+    gq = _capture(lambda: quantize_int8(w, per_channel=True), stream)
+    with _Range(f"rq-int8-codec quantize {N}x{K}"):
+        tq = _time_graph(gq, 10)
+    del gq
+    gd = _capture(lambda: dequantize_int8(q, s), stream)
+    with _Range(f"rq-int8-codec dequantize {N}x{K}"):
+        td = _time_graph(gd, 10)
+    del gd
+    bq = 3 * N * K + 2 * N
+    bd = 5 * N * K + 2 * N
+    return {"workload": f"per-row INT8 quantize / fp32 dequantize of a {N}x{K} bf16 weight",
+            "quantize_us": round(tq * 1e3, 2), "quantize_gbs": round(bq / tq / 1e6, 1),
+            "quantize_frac": round(bq / tq / 1e6 / HBM_PEAK_GBS, 4),
+            "dequantize_us": round(td * 1e3, 2), "dequantize_gbs": round(bd / td / 1e6, 1),
+            "dequantize_frac": round(bd / td / 1e6 / HBM_PEAK_GBS, 4)}
+
+
 def bench_byte_linears(dev, stream):
     """INT8 per-row-absmax (W8A16 on bf16 MFMA; W8A8 on int8 MFMA) and FP8 (e4m3, fp8 MFMA)
     linears at 8192 -> 28672 with
@@ -487,14 +511,16 @@ def bench_byte_linears(dev, stream):
     K, N = 8192, 28672
     g = torch.Generator(device=dev).manual_seed(9)
     int8_w, fp8_w = [], []
+    out = {}
     for c in range(2):
         w = (torch.randn(N, K, generator=g, device=dev) * 0.02).to(torch.bfloat16)
         int8_w.append(quantize_int8(w, per_channel=True))
+        if c == 0:
+            out["int8_codec"] = bench_int8_codec(w, int8_w[0], stream)
         codes, scale = ops.fp8_quantize(w)
         fp8_w.append((ops.fp8_to_e4m3fn(codes), scale))  # as FP8LinearWrapper caches it
         del codes
         del w
-    out = {}
     for M in (1, 512, 4096):
         x = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
         copies = 2 if M == 1 else 1
@@ -956,7 +982,10 @@ def main():
         torch.cuda.empty_cache()
         byte = bench_byte_linears(dev, stream)
         print("bench: byte linears " + ", ".join(f"{k} {v['us']} us" for k, v in byte.items()
-                                                  if isinstance(v, dict)), file=sys.stderr, flush=True)
+                                                  if isinstance(v, dict) and "us" in v), file=sys.stderr, flush=True)
+        ic = byte["int8_codec"]
+        print(f"bench: int8 codec quantize {ic['quantize_gbs']} GB/s, dequantize {ic['dequantize_gbs']} GB/s",
+              file=sys.stderr, flush=True)
         gpu_s["int8_m1_s"] = byte["int8_m1"]["us"] * 1e-6
         gpu_s["fp8_m1_s"] = byte["fp8_m1"]["us"] * 1e-6
         torch.cuda.empty_cache()

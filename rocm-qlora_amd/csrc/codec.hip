@@ -12,6 +12,8 @@
 #include "nf4_tables.h"
 #include "rq_launch.h"
 
+#include <type_traits>
+
 namespace rq {
 
 // ---------------------------------------------------------------------------
@@ -503,11 +505,171 @@ __global__ __launch_bounds__(256) void int8_quantize_kernel(const void* __restri
   if (lane == 0) store_from_f32(scales, b, DT, s);
 }
 
+// ---------------------------------------------------------------------------
+// INT8 codec fast paths: 16-bit weights / outputs, 16-byte aligned weights
+// and 8-byte aligned codes, whole segments of a multiple of 8 elements.  A
+// group is 8 consecutive elements (one 16-byte weight load, one 8-byte code
+// store); the absmax runs over raw 16-bit patterns as in the NF4 encoder
+// (|x| = h & 0x7FFF, a NaN above infinity) and q = int8(int32(rint(
+// RND(x / s)))) takes div_round's shortcut (the same bits as the division).
+// ---------------------------------------------------------------------------
+template <int DT>
+__device__ __forceinline__ uint32_t absmax_bits16(const u32x4& raw) {
+  const u16x2 m2 = __builtin_elementwise_max(
+      __builtin_elementwise_max(__builtin_bit_cast(u16x2, raw.x & 0x7FFF7FFFu), __builtin_bit_cast(u16x2, raw.y & 0x7FFF7FFFu)),
+      __builtin_elementwise_max(__builtin_bit_cast(u16x2, raw.z & 0x7FFF7FFFu), __builtin_bit_cast(u16x2, raw.w & 0x7FFF7FFFu)));
+  return f2u(from_x16<DT>(m2.x > m2.y ? uint32_t(m2.x) : uint32_t(m2.y)));  // fp32 bits of the 16-bit max
+}
+
+template <int DT>
+__device__ __forceinline__ float int8_scale(uint32_t mbits) {
+  return clamp_floor(round_to(__fdiv_rn(u2f(mbits), 127.0f), DT), DT);
+}
+
+template <int DT>
+__device__ __forceinline__ u32x2 int8_codes_group(const u32x4& raw, float s, float rs) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  uint32_t c[2] = {0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float r = rintf(div_round<DT>(half16<DT>(w[j >> 1], j & 1), s, rs));
+    c[j >> 2] |= (uint32_t(int32_t(r)) & 0xFFu) << (8 * (j & 3));
+  }
+  return u32x2{c[0], c[1]};
+}
+
+// Segments of L = 2^log2_l <= 64 groups (blockwise scales): the L lanes of a
+// segment reduce with DPP / shuffles; groups (blockIdx * 4 + g) * 256 + i,
+// all four loads first.  n_groups is a multiple of L.
+template <int DT>
+__global__ __launch_bounds__(256) void int8_quantize_groups16(const uint16_t* __restrict__ w, int64_t n_groups,
+                                                              int log2_l, int8_t* __restrict__ q,
+                                                              void* __restrict__ scales) {
+  const int64_t t0 = int64_t(blockIdx.x) * 1024 + threadIdx.x;
+  u32x4 raw[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int64_t t = t0 + 256 * g;
+    raw[g] = t < n_groups ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + 8 * t))
+                          : u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int64_t t = t0 + 256 * g;
+    const float s = int8_scale<DT>(group_max_u32(absmax_bits16<DT>(raw[g]), log2_l));
+    if (t >= n_groups) continue;
+    *reinterpret_cast<u32x2*>(q + 8 * t) = int8_codes_group<DT>(raw[g], s, recip_rn(s));
+    if ((t & ((int64_t(1) << log2_l) - 1)) == 0) store_from_f32(scales, t >> log2_l, DT, s);
+  }
+}
+
+// Segments of more than 64 groups (a row per output channel): one workgroup
+// of 256 threads per segment; thread i takes groups i + 256 j, up to four of
+// them held in registers for the second pass (segments of up to 8192
+// elements), the rest loaded again.
+template <int DT>
+__global__ __launch_bounds__(256) void int8_quantize_rows16(const uint16_t* __restrict__ w, int64_t seg_groups,
+                                                            int8_t* __restrict__ q, void* __restrict__ scales) {
+  __shared__ uint32_t red[4];
+  const int64_t b = blockIdx.x;
+  const uint16_t* ws = w + b * seg_groups * 8;
+  int8_t* qs = q + b * seg_groups * 8;
+  u32x4 raw[4];
+  uint32_t m = 0u;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t i = threadIdx.x + 256 * j;
+    raw[j] = i < seg_groups ? *reinterpret_cast<const u32x4*>(ws + 8 * i) : u32x4{0u, 0u, 0u, 0u};
+    const uint32_t v = absmax_bits16<DT>(raw[j]);
+    m = m > v ? m : v;
+  }
+  for (int64_t i = threadIdx.x + 1024; i < seg_groups; i += 256) {
+    const uint32_t v = absmax_bits16<DT>(*reinterpret_cast<const u32x4*>(ws + 8 * i));
+    m = m > v ? m : v;
+  }
+  m = group_max_u32(m, 6);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 4; ++k) m = m > red[k] ? m : red[k];
+  const float s = int8_scale<DT>(m);
+  const float rs = recip_rn(s);
+  if (threadIdx.x == 0) store_from_f32(scales, b, DT, s);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t i = threadIdx.x + 256 * j;
+    if (i < seg_groups) *reinterpret_cast<u32x2*>(qs + 8 * i) = int8_codes_group<DT>(raw[j], s, rs);
+  }
+  for (int64_t i = threadIdx.x + 1024; i < seg_groups; i += 256)
+    *reinterpret_cast<u32x2*>(qs + 8 * i) =
+        int8_codes_group<DT>(*reinterpret_cast<const u32x4*>(ws + 8 * i), s, rs);
+}
+
+// Dequantize to a 16-bit dtype, segments a multiple of 8 elements: out =
+// RND(float(q) * s) for groups (blockIdx * 4 + g) * 256 + i -- 8-byte code
+// loads, one scale, 16-byte output stores (consecutive lanes, consecutive
+// bytes), all four groups' loads first.
+template <int ODT, int SDT>
+__global__ __launch_bounds__(256) void int8_dequant16_kernel(const uint32_t* __restrict__ q, const void* scales,
+                                                             int64_t seg_groups, int64_t n_groups,
+                                                             u32x4* __restrict__ out) {
+  const int64_t t0 = int64_t(blockIdx.x) * 1024 + threadIdx.x;
+  u32x2 c[4];
+  float sc[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int64_t t = t0 + 256 * g;
+    const int64_t tl = t < n_groups ? t : n_groups - 1;
+    c[g] = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(q) + tl);
+    sc[g] = load_as_f32(scales, tl / seg_groups, SDT);
+  }
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int64_t t = t0 + 256 * g;
+    if (t >= n_groups) continue;
+    uint32_t o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t word = k < 2 ? c[g].x : c[g].y;
+      const int sh = 16 * (k & 1);
+      o[k] = cvt_pk<ODT>(__fmul_rn(float(int8_t(uint8_t(word >> sh))), sc[g]),
+                         __fmul_rn(float(int8_t(uint8_t(word >> (sh + 8)))), sc[g]));
+    }
+    __builtin_nontemporal_store(u32x4{o[0], o[1], o[2], o[3]}, out + t);
+  }
+}
+
+// The same to fp32: groups of 4 codes (one 4-byte load, one 16-byte store).
+template <int SDT>
+__global__ __launch_bounds__(256) void int8_dequant_f32_kernel(const uint32_t* __restrict__ q, const void* scales,
+                                                               int64_t seg_groups, int64_t n_groups,
+                                                               f32x4* __restrict__ out) {
+  const int64_t t0 = int64_t(blockIdx.x) * 1024 + threadIdx.x;
+  uint32_t c[4];
+  float sc[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int64_t t = t0 + 256 * g;
+    const int64_t tl = t < n_groups ? t : n_groups - 1;
+    c[g] = __builtin_nontemporal_load(q + tl);
+    sc[g] = load_as_f32(scales, tl / seg_groups, SDT);
+  }
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int64_t t = t0 + 256 * g;
+    if (t >= n_groups) continue;
+    f32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = __fmul_rn(float(int8_t(uint8_t(c[g] >> (8 * k)))), sc[g]);
+    __builtin_nontemporal_store(o, out + t);
+  }
+}
+
 template <int ODT>
 __global__ __launch_bounds__(256) void int8_dequant_kernel(const int8_t* __restrict__ q, const void* scales,
                                                            int sdt, int64_t seg, void* __restrict__ out,
-                                                           int64_t n_out) {
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+                                                           int64_t i0, int64_t n_out) {
+  const int64_t i = i0 + int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n_out) return;
   store_from_f32(out, i, ODT, __fmul_rn(float(q[i]), load_as_f32(scales, i / seg, sdt)));
 }
@@ -679,6 +841,28 @@ extern "C" int rq_int8_quantize(const void* w, int w_dtype, int64_t rows, int64_
   if (!w || !q || !scales) return RQ_ERR_NULL_POINTER;
   const int64_t seg = block_size > 0 ? block_size : cols;
   const int64_t n_seg = block_size > 0 ? ceil_div(numel, block_size) : rows;
+  // 16-bit weights in whole segments of 8-element groups: the vector kernels
+  if (w_dtype != RQ_DTYPE_F32 && seg % 8 == 0 && numel % seg == 0 && aligned(w, 16) && aligned(q, 8) &&
+      numel / 8 < (int64_t(1) << 40)) {
+    const int64_t sg = seg / 8, n_groups = numel / 8;
+    const uint16_t* w16 = static_cast<const uint16_t*>(w);
+    if (sg <= 64 && (sg & (sg - 1)) == 0) {
+      const int log2_l = __builtin_ctzll(uint64_t(sg));
+      const dim3 grid(unsigned(ceil_div(n_groups, 1024)));
+      if (w_dtype == RQ_DTYPE_BF16)
+        int8_quantize_groups16<RQ_DTYPE_BF16><<<grid, 256, 0, stream>>>(w16, n_groups, log2_l, q, scales);
+      else
+        int8_quantize_groups16<RQ_DTYPE_F16><<<grid, 256, 0, stream>>>(w16, n_groups, log2_l, q, scales);
+      return rq_check_launch();
+    }
+    if (sg > 64 && n_seg <= 0x7FFFFFFF) {
+      if (w_dtype == RQ_DTYPE_BF16)
+        int8_quantize_rows16<RQ_DTYPE_BF16><<<unsigned(n_seg), 256, 0, stream>>>(w16, sg, q, scales);
+      else
+        int8_quantize_rows16<RQ_DTYPE_F16><<<unsigned(n_seg), 256, 0, stream>>>(w16, sg, q, scales);
+      return rq_check_launch();
+    }
+  }
   dim3 grid(unsigned(ceil_div(n_seg, 4)));
   RQ_DISPATCH_DT(w_dtype, DT, int8_quantize_kernel<DT><<<grid, 256, 0, stream>>>(
                                   w, numel, n_seg, seg, q, scales));
@@ -695,8 +879,48 @@ extern "C" int rq_int8_dequantize(const int8_t* q, const void* scales, int scale
   if (n_out > cap || (seg == 0 && n_out > 0)) return RQ_ERR_BAD_SHAPE;
   if (n_out == 0) return RQ_OK;
   if (!q || !scales || !out) return RQ_ERR_NULL_POINTER;
-  dim3 grid(unsigned(ceil_div(n_out, 256)));
+  // segments of whole groups (fp32 output: 4 elements, 16-bit: 8): the
+  // vector kernels over the whole groups, the generic one over the rest
+  int64_t done = 0;
+  if (out_dtype == RQ_DTYPE_F32 && seg % 4 == 0 && aligned(q, 4) && aligned(out, 16) && n_out >= 4) {
+    const int64_t n_groups = n_out / 4, sg = seg / 4;
+    const dim3 grid(unsigned(ceil_div(n_groups, 1024)));
+    const uint32_t* q32 = reinterpret_cast<const uint32_t*>(q);
+    f32x4* o = static_cast<f32x4*>(out);
+    if (scales_dtype == RQ_DTYPE_F32)
+      int8_dequant_f32_kernel<RQ_DTYPE_F32><<<grid, 256, 0, stream>>>(q32, scales, sg, n_groups, o);
+    else if (scales_dtype == RQ_DTYPE_BF16)
+      int8_dequant_f32_kernel<RQ_DTYPE_BF16><<<grid, 256, 0, stream>>>(q32, scales, sg, n_groups, o);
+    else
+      int8_dequant_f32_kernel<RQ_DTYPE_F16><<<grid, 256, 0, stream>>>(q32, scales, sg, n_groups, o);
+    done = n_groups * 4;
+    if (done == n_out) return rq_check_launch();
+  } else if (out_dtype != RQ_DTYPE_F32 && seg % 8 == 0 && aligned(q, 8) && aligned(out, 16) && n_out >= 8) {
+    const int64_t n_groups = n_out / 8, sg = seg / 8;
+    const dim3 grid(unsigned(ceil_div(n_groups, 1024)));
+    const uint32_t* q32 = reinterpret_cast<const uint32_t*>(q);
+    u32x4* o = static_cast<u32x4*>(out);
+    auto run = [&](auto odt, auto sdt) {
+      int8_dequant16_kernel<decltype(odt)::value, decltype(sdt)::value><<<grid, 256, 0, stream>>>(
+          q32, scales, sg, n_groups, o);
+    };
+    using BF = std::integral_constant<int, RQ_DTYPE_BF16>;
+    using F16 = std::integral_constant<int, RQ_DTYPE_F16>;
+    using F32 = std::integral_constant<int, RQ_DTYPE_F32>;
+    if (out_dtype == RQ_DTYPE_BF16) {
+      if (scales_dtype == RQ_DTYPE_F32) run(BF{}, F32{});
+      else if (scales_dtype == RQ_DTYPE_BF16) run(BF{}, BF{});
+      else run(BF{}, F16{});
+    } else {
+      if (scales_dtype == RQ_DTYPE_F32) run(F16{}, F32{});
+      else if (scales_dtype == RQ_DTYPE_BF16) run(F16{}, BF{});
+      else run(F16{}, F16{});
+    }
+    done = n_groups * 8;
+    if (done == n_out) return rq_check_launch();
+  }
+  dim3 grid(unsigned(ceil_div(n_out - done, 256)));
   RQ_DISPATCH_DT(out_dtype, ODT, int8_dequant_kernel<ODT><<<grid, 256, 0, stream>>>(
-                                     q, scales, scales_dtype, seg, out, n_out));
+                                     q, scales, scales_dtype, seg, out, done, n_out));
   return rq_check_launch();
 }

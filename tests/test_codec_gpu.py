@@ -140,6 +140,40 @@ def test_int8_bit_exact(dev, dtype):
     assert bits_equal(dequantize_int8(q, s), R.dequantize_int8(q_ref, s_ref))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("cols", [8192, 11008, 512])
+def test_int8_per_channel_large_bit_exact(dev, dtype, cols):
+    """Rows of 512 .. 11008 elements (one workgroup per row; rows past 8192
+    elements load their tail twice), edge rows first: zeros, a NaN, an Inf,
+    tiny values; then the fp32 reconstruction of the same codes."""
+    w = _weights((70, cols), dtype, 31)
+    w[0] = 0
+    w[1, 7] = float("nan")
+    w[2, 3] = float("inf")
+    w[3] = (w[3].float() * 1e-30).to(dtype)
+    print(f"int8 per-channel dtype={dtype} cols={cols}", flush=True)
+    q, s = quantize_int8(w.to(dev), per_channel=True)
+    q_ref, s_ref = R.quantize_int8(w, per_channel=True)
+    assert bits_equal(q, q_ref) and bits_equal(s, s_ref)
+    assert bits_equal(dequantize_int8(q, s), R.dequantize_int8(q_ref, s_ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("block,cols", [(64, 1024), (32, 1032), (512, 1024), (8, 1032), (64, 1032)])
+def test_int8_blockwise_large_bit_exact(dev, dtype, block, cols):
+    """Blockwise scales over a flat tensor (300 x cols): whole blocks on the
+    vector kernels (several workgroups of 1024 groups, a partly filled last
+    one), a partial last block (64 x 1032 elements) on the generic kernel;
+    dequantized to fp32."""
+    w = _weights((300, cols), dtype, 32).flatten()
+    w[5] = float("nan")
+    print(f"int8 blockwise dtype={dtype} block={block}", flush=True)
+    q, s = quantize_int8(w.to(dev), block)
+    q_ref, s_ref = R.quantize_int8(w, block)
+    assert bits_equal(q, q_ref) and bits_equal(s, s_ref)
+    assert bits_equal(dequantize_int8(q, s, block), R.dequantize_int8(q_ref, s_ref, block))
+
+
 def _config2_weight():
     """11008x4096 (down-proj) bf16 ~ N(0, 0.02), 0.1% outliers at +-8 sigma."""
     g = torch.Generator().manual_seed(0)
