@@ -81,7 +81,6 @@ constexpr int kGemvMaxUSplits = 16;
 constexpr int kGemvXSliceMaxM = 2;  // activation rows through the per-wave LDS slice
 constexpr int kGemvLutQwords = 256 * 32;  // 64 KiB: code byte -> fp32 (T[lo], T[hi]), 32 copies
 constexpr int kGemvLdsBudget = 160 * 1024 - kGemvLutQwords * 8;
-constexpr uint8_t kGemvNoUnit = 0xFF;
 // Word 3 of a raw (stride 0) buffer resource on gfx9-family GPUs, gfx950
 // included: 32-bit data, bounds checked against num_records.
 constexpr int kBufferRsrcWord3 = 0x00020000;
@@ -120,8 +119,6 @@ struct GemvArgs {
   const uint16_t* lora_x;
   int ld_lora_x;
   const void* lora_a;      // [rank, K]
-  uint8_t unit_t[kGemvWaves][kGemvMaxU];  // tile slot of unit u of wave w (kGemvNoUnit: none)
-  uint8_t unit_s[kGemvWaves][kGemvMaxU];  // segment (within the split) of unit u of wave w
 };
 
 __host__ __device__ inline int gemv_part_floats(int TS, int nseg, int M) { return TS * nseg * M * 16; }
@@ -489,18 +486,30 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   auto tile_of = [&](int t) -> uint32_t { return g + uint32_t(t) * G; };
   const __amdgpu_buffer_rsrc_t wres = buffer_rsrc(a.packed, uint32_t(a.N) * (uint32_t(a.K) >> 1));
   const GemvScale<Scale> sc(scale_src, uint32_t(a.N) * uint32_t(a.bpr));
-  // this wave's units (wave-uniform; one dword of the table per wave, the
-  // host writes segment 0 for a missing unit)
-  const uint32_t tword = reinterpret_cast<const uint32_t*>(&a.unit_t[0][0])[wave];
-  const uint32_t sword = reinterpret_cast<const uint32_t*>(&a.unit_s[0][0])[wave];
+  // this wave's units (tile slot, segment), wave-uniform scalars computed
+  // here rather than read from a table in the arguments: a wave-indexed
+  // argument load is a second round trip to the argument memory before the
+  // first weight load can be addressed.  With the activation slices unit u
+  // of wave w is unit i = w + 16 u of the workgroup's TS * nseg (tile i /
+  // nseg, segment i % nseg); without them the R = 16 / nseg wave groups take
+  // the tiles round-robin, wave w segment w % nseg of tiles w / nseg + R u.
+  // A missing unit reads tile slot 0, segment 0 (its loads are dead).
   int ut[U], useg[U];
   bool ulive[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int t = int((tword >> (8 * u)) & 0xFFu);
-    ulive[u] = t != kGemvNoUnit;
-    ut[u] = ulive[u] ? t : 0;
-    useg[u] = int((sword >> (8 * u)) & 0xFFu);
+    if constexpr (XM == 1) {
+      const int i = wave + kGemvWaves * u;
+      ulive[u] = i < TS * nseg;
+      ut[u] = ulive[u] ? i / nseg : 0;
+      useg[u] = ulive[u] ? i - ut[u] * nseg : 0;
+    } else {
+      const int R = kGemvWaves / nseg;
+      const int t = wave / nseg + u * R;
+      ulive[u] = wave < R * nseg && t < TS;
+      ut[u] = ulive[u] ? t : 0;
+      useg[u] = ulive[u] ? wave - (wave / nseg) * nseg : 0;
+    }
   }
   const __amdgpu_buffer_rsrc_t xres =
       buffer_rsrc(a.x, uint32_t(M - 1) * uint32_t(a.ldx) * 2u + uint32_t(a.K) * 2u);
@@ -631,15 +640,17 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     if (ulive[u]) {
       if constexpr (XM == 1) {
         // the unit's activations through this wave's slice: lane c wrote
-        // row c / 32, k 8 (c % 32); token n16 < M reads its MFMA operands
-        if (lane < 32 * M) *reinterpret_cast<u32x4*>(xs + 8 * lane) = L[u].xc;
-        if (ln.n16 < M) {
-          const uint16_t* xrow = xs + ln.n16 * kSegK + 32 * ln.q;
+        // row c / 32, k 8 (c % 32); token n16 < M reads its MFMA operands.
+        // The lanes of rows n16 >= M read row 0 instead of zeros: an MFMA
+        // output row depends only on its own operand row, and rows >= M are
+        // never stored (no branch, no zero fill).  A unit of the previous
+        // unit's segment (every unit of a wave when K is 16 segments) keeps
+        // the operands already in registers.
+        if (u == 0 || !ulive[u - 1] || useg[u] != useg[u - 1]) {
+          if (lane < 32 * M) *reinterpret_cast<u32x4*>(xs + 8 * lane) = L[u].xc;
+          const uint16_t* xrow = xs + (ln.n16 < M ? ln.n16 : 0) * kSegK + 32 * ln.q;
 #pragma unroll
           for (int c = 0; c < 8; ++c) xa[c] = *reinterpret_cast<const u32x4*>(xrow + 128 * (c >> 2) + 8 * (c & 3));
-        } else {
-#pragma unroll
-          for (int c = 0; c < 8; ++c) xa[c] = u32x4{0u, 0u, 0u, 0u};
         }
       }
       float s1, s2;
@@ -1015,25 +1026,6 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     p.U = xslice ? (best * nseg + kGemvWaves - 1) / kGemvWaves : (best + R - 1) / R;
     p.grid = int((tiles + best - 1) / best);
     p.direct = direct;
-    for (int w = 0; w < kGemvWaves; ++w)
-      for (int u = 0; u < kGemvMaxU; ++u) {
-        p.unit_t[w][u] = kGemvNoUnit;
-        p.unit_s[w][u] = 0;
-        if (u >= p.U) continue;
-        if (xslice) {
-          const int i = w + kGemvWaves * u;
-          if (i < best * nseg) {
-            p.unit_t[w][u] = uint8_t(i / nseg);
-            p.unit_s[w][u] = uint8_t(i % nseg);
-          }
-        } else if (w < R * nseg) {
-          const int t = w / nseg + u * R;
-          if (t < best) {
-            p.unit_t[w][u] = uint8_t(t);
-            p.unit_s[w][u] = uint8_t(w % nseg);
-          }
-        }
-      }
     break;
   }
   p.lds_bytes = gemv_lds_bytes(p.TS, p.nseg, int(M), gather, p.xslice, p.direct && rank > 0);
@@ -1137,11 +1129,6 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.ld_lora_x = int(L.ld_lora_x);
   a.lora_a = L.lora_a;
   a.ws = ws;
-  for (int w = 0; w < kGemvWaves; ++w)
-    for (int u = 0; u < kGemvMaxU; ++u) {
-      a.unit_t[w][u] = p.unit_t[w][u];
-      a.unit_s[w][u] = p.unit_s[w][u];
-    }
   if (p.xslice) {
     switch (p.U) {
       case 1: return launch_gemv_u<XT, Scale, 1, 1>(a, p, scale, e, stream);

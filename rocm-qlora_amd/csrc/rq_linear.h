@@ -67,7 +67,6 @@ struct GemvPlan {
   int jm;  // ... or down-projection jobs merged into the first jm tile workgroups
   bool direct, xslice;
   size_t lds_bytes, ws_bytes, u_offset;
-  uint8_t unit_t[16][4], unit_s[16][4];  // (tile slot, segment) of unit u of wave w; 0xFF: none
 };
 
 GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool xvec, bool gather,
