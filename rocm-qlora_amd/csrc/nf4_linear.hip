@@ -807,50 +807,50 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
 }
 
 // Split-K finisher (and the LoRA epilogue for any M): y = finish(sum_s
-// ws[s]).  Workgroup = 256 columns x 16 activation rows; B values are read 8
-// at a time, all in flight together, and reused for the 16 rows.
+// ws[s]).  One thread per output (row blockIdx.y, column n): the bias, the
+// LoRA B row and the first splits' partials are all requested before any is
+// used, so a launch costs about one memory round trip (a thread per column
+// walking 16 rows took one round trip per row).  The sums keep their order:
+// splits ascending, ranks ascending.
 template <int XT>
 __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* __restrict__ ws, int S, int64_t M,
                                                               int64_t N, LinearEpi e) {
-  extern __shared__ float us[];
-  const int64_t m0 = int64_t(blockIdx.y) * 16;
-  stage_u<XT>(e, M, m0, 16, us, threadIdx.x, blockDim.x);
+  extern __shared__ float us[];  // RND(u) of this row, [rank]
+  const int64_t m = blockIdx.y;
+  stage_u<XT>(e, M, m, 1, us, threadIdx.x, blockDim.x);
   __syncthreads();
   const int64_t n = int64_t(blockIdx.x) * 256 + threadIdx.x;
   if (n >= N) return;
-  const int rows = int(M - m0 < 16 ? M - m0 : 16);
-  float lsum[16];
+  const bool has_bias = e.bias != nullptr;
+  const Raw16x2 br = load_raw(has_bias ? e.bias : ws, has_bias ? n : 0, has_bias ? e.bias_dt : RQ_DTYPE_F32);
+  float v = 0.0f;
+  for (int s0 = 0; s0 < S; s0 += 8) {
+    float p[8];
 #pragma unroll
-  for (int mm = 0; mm < 16; ++mm) lsum[mm] = 0.0f;
+    for (int k = 0; k < 8; ++k) p[k] = (s0 + k < S) ? ws[(int64_t(s0 + k) * M + m) * N + n] : 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (s0 + k < S) v = __fadd_rn(v, p[k]);
+  }
+  float lsum = 0.0f;
   for (int j0 = 0; j0 < e.rank; j0 += 8) {
-    float b[8];
+    Raw16x2 b[8];
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj)
-      b[jj] = (j0 + jj < e.rank) ? round_x<XT>(load_as_f32(e.lora_b, n * e.ld_lora_b + j0 + jj, e.lora_dt)) : 0.0f;
+      b[jj] = load_raw(e.lora_b, n * e.ld_lora_b + (j0 + jj < e.rank ? j0 + jj : 0), e.lora_dt);
 #pragma unroll
-    for (int mm = 0; mm < 16; ++mm)
-      if (mm < rows)
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-          if (j0 + jj < e.rank) lsum[mm] = __fmaf_rn(us[mm * e.rank + j0 + jj], b[jj], lsum[mm]);
+    for (int jj = 0; jj < 8; ++jj)
+      if (j0 + jj < e.rank) lsum = __fmaf_rn(us[j0 + jj], round_x<XT>(raw_to_f32(b[jj], e.lora_dt)), lsum);
   }
-#pragma unroll
-  for (int mm = 0; mm < 16; ++mm) {
-    if (mm >= rows) break;
-    const int64_t m = m0 + mm;
-    float p[8];
-    float v = 0.0f;
-    for (int s0 = 0; s0 < S; s0 += 8) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) p[k] = (s0 + k < S) ? ws[(int64_t(s0 + k) * M + m) * N + n] : 0.0f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (s0 + k < S) v = __fadd_rn(v, p[k]);
-    }
-    v = finish_value<XT>(e, n, v, lsum[mm]);
-    static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
+  if (has_bias) v = __fadd_rn(v, round_x<XT>(raw_to_f32(br, e.bias_dt)));
+  v = round_x<XT>(v);
+  if (e.rank > 0) {
+    const float l = round_x<XT>(__fmul_rn(round_x<XT>(lsum), e.scaling));
+    v = round_x<XT>(__fadd_rn(v, l));
   }
+  static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
 }
+
 
 // ---------------------------------------------------------------------------
 // LoRA down-projection partials: up[ks, m, j] = sum_{k in split ks}
@@ -1167,8 +1167,8 @@ static int run_gemv(const LinearArgs& L, const GemvPlan& p, const LinearEpi& e, 
 template <int XT>
 static int launch_splitk_epilogue(const LinearArgs& L, const GemvPlan& p, const LinearEpi& e, const float* ws,
                                   hipStream_t stream) {
-  dim3 grid(unsigned((L.N + 255) / 256), unsigned((L.M + 15) / 16));
-  const size_t lds = size_t(16) * (L.rank > 0 ? L.rank : 1) * 4;
+  dim3 grid(unsigned((L.N + 255) / 256), unsigned(L.M));
+  const size_t lds = size_t(L.rank > 0 ? L.rank : 1) * 4;
   splitk_epilogue_kernel<XT><<<grid, 256, lds, stream>>>(ws, p.S, L.M, L.N, e);
   return rq_check_launch();
 }

@@ -57,7 +57,10 @@ _LINEAR_WS: dict = {}
 _CAPTURE_WS: dict = {}
 _WS_MIN_BYTES = 1 << 20
 _CAPTURE_POOL_ENTRIES = 32
-_CAPTURE_POOL_BYTES = 256 * 1024
+# 2 MiB holds the decode GEMV's largest workspace (M = 16 with its K-split
+# partials) for the common layer shapes, so that a capture's calls share one
+# pre-zeroed buffer rather than recording a fill kernel at each larger need
+_CAPTURE_POOL_BYTES = 2 << 20
 _CAPTURE_POOL: dict = {}       # device index -> pre-zeroed buffers not yet handed out
 _CAPTURE_POOL_BASE: dict = {}  # device index -> the allocation they are views of (kept for good)
 
