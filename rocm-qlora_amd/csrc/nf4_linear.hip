@@ -126,13 +126,13 @@ __host__ __device__ inline int gemv_part_floats(int TS, int nseg, int M) { retur
 // Dynamic LDS of the GEMV (bytes): segment partials [TS][nseg][M][16], the
 // waves' scale slices [16][64][16 bytes] (gathered absmax), the waves'
 // activation slices [16][M][256] (16-bit), RND(B) of the tiles' rows
-// [TS * 16][64], RND(bias) [TS * 16], RND(u) [M][64] (fp32).
+// [TS * 16][64] (16-bit), RND(bias) [TS * 16], RND(u) [M][64] (fp32).
 constexpr int kGemvScaleSliceBytes = 64 * 16;
 __host__ __device__ inline size_t gemv_lds_bytes(int TS, int nseg, int M, bool gather, bool xslice, bool lora) {
   size_t b = size_t(gemv_part_floats(TS, nseg, M)) * 4;
   if (gather) b += size_t(kGemvWaves) * kGemvScaleSliceBytes;
   if (xslice) b += size_t(kGemvWaves) * M * kSegK * 2;
-  b += (lora ? size_t(TS) * 16 * kGemvMaxFusedRank * 4 : 0) + size_t(TS) * 16 * 4;
+  b += (lora ? size_t(TS) * 16 * kGemvMaxFusedRank * 2 : 0) + size_t(TS) * 16 * 4;
   b += lora ? size_t(M) * kGemvMaxFusedRank * 4 : 0;
   return b;
 }
@@ -455,8 +455,10 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
                                               (kGather ? kGemvWaves * (kGemvScaleSliceBytes / 4) : 0));
   // this wave's activation slice [M][256] (slice mode)
   uint16_t* xs = xs0 + wave * M * kSegK;
-  float* lbs = reinterpret_cast<float*>(xs0 + (XM == 1 ? kGemvWaves * M * kSegK : 0));
-  float* bss = lbs + (rank > 0 ? TS * 16 * RP : 0);
+  // RND(B) rows of the tiles, as activation-dtype bits (exact: RND is the
+  // rounding to that dtype)
+  uint16_t* lbs = xs0 + (XM == 1 ? kGemvWaves * M * kSegK : 0);
+  float* bss = reinterpret_cast<float*>(lbs + (rank > 0 ? TS * 16 * RP : 0));
   float* us = bss + TS * 16;
   uint32_t* flag = reinterpret_cast<uint32_t*>(us + M * RP);  // in-launch LoRA: set when u is computed here
 
@@ -733,16 +735,16 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
 #pragma unroll
   for (int k = 0; k < kGemvMaxUSplits; ++k) asm volatile("" : "+v"(up[k]));
   if (bvec_live) {
-    float* dst = lbs + (bt * 16 + br_row) * RP + bc * int(16u / bbytes);
+    uint16_t* dst = lbs + (bt * 16 + br_row) * RP + bc * int(16u / bbytes);
     if (e.lora_dt == RQ_DTYPE_F32) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dst[i] = round_x<XT>(u2f(bvr[i]));
+      for (int i = 0; i < 4; ++i) dst[i] = uint16_t(to_x16<XT>(u2f(bvr[i])));
     } else {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint16_t lo = uint16_t(bvr[i]), hi = uint16_t(bvr[i] >> 16);
-        dst[2 * i] = round_x<XT>(e.lora_dt == RQ_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo));
-        dst[2 * i + 1] = round_x<XT>(e.lora_dt == RQ_DTYPE_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi));
+        dst[2 * i] = uint16_t(to_x16<XT>(e.lora_dt == RQ_DTYPE_BF16 ? bf16_to_f32(lo) : f16_to_f32(lo)));
+        dst[2 * i + 1] = uint16_t(to_x16<XT>(e.lora_dt == RQ_DTYPE_BF16 ? bf16_to_f32(hi) : f16_to_f32(hi)));
       }
     }
   }
@@ -783,7 +785,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     if (e.bias) v = __fadd_rn(v, bss[t * 16 + nn]);
     v = round_x<XT>(v);
     if (rank > 0) {
-      const float* brow = lbs + (t * 16 + nn) * RP;
+      const uint16_t* brow = lbs + (t * 16 + nn) * RP;
       const float* urow = us + m * RP;
       float l = 0.0f;
       for (int j0 = 0; j0 < rank; j0 += 8) {
@@ -791,7 +793,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
           uu[jj] = urow[j0 + jj];
-          bb[jj] = brow[j0 + jj];
+          bb[jj] = from_x16<XT>(brow[j0 + jj]);
         }
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj)
