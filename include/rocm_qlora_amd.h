@@ -135,13 +135,15 @@ int rq_int8_dequantize(const int8_t* q, const void* scales, int scales_dtype,
 /* Bytes of device workspace rq_nf4_linear needs for these sizes (0 when
  * none).  The caller allocates it (256-byte aligned) and passes it in (the
  * MFMA GEMM, M > 16, also runs with less: then without K splits).  Its
- * first RQ_LINEAR_SYNC_BYTES are a synchronization area of the decode GEMV
- * (a count and the LoRA down-projection's partials, exchanged between the
- * workgroups of one launch): it must be zero before the workspace's first
- * use, and every call leaves it zero once its kernels have finished, so a
- * workspace is reused as it is by calls ordered on one stream.  Calls that
- * may overlap need workspaces of their own. */
-#define RQ_LINEAR_SYNC_BYTES 65792
+ * first RQ_LINEAR_SYNC_BYTES are a synchronization area (the decode GEMV's
+ * LoRA down-projection partials, exchanged between the workgroups of one
+ * launch, and the GEMM's K-split tile counters): it must be zero before the
+ * workspace's first use, and every call leaves it ready for the next one
+ * once its kernels have finished (not necessarily zero: the GEMV keeps the
+ * parity of its partial regions there), so a workspace is reused as it is
+ * by calls ordered on one stream.  Calls that may overlap need workspaces of
+ * their own. */
+#define RQ_LINEAR_SYNC_BYTES 131328
 int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, int64_t N, int64_t rank,
                                  int64_t* bytes);
 

@@ -54,22 +54,27 @@ namespace rq {
 // under a branch and no loaded value is carried around a loop, so the
 // compiler's in-order load counting is exact and each unit waits only for
 // its own data.
-//   1. The first unit's loads: its activations (M <= 2 and 16-byte aligned
+//   1. With the LoRA down-projection in the launch, the state of the
+//      partial regions and, in a wave with a job, the job's operands.  The
+//      first unit's loads: its activations (M <= 2 and 16-byte aligned
 //      rows: the M x 256 values of the unit's segment, one 16-byte load per
 //      lane; otherwise the wave's MFMA operands directly, eight
 //      16-byte loads, and all of the wave's units share one segment), then its
 //      weights and scales.
-//   2. The byte table (built from constants, no loads); one barrier.
+//   2. The byte table (built from constants, no loads); one barrier; a job
+//      wave's MFMAs and its partials' stores.
 //   3. The epilogue operands (the tiles' LoRA B rows, bias, RND(u) partials),
 //      kept as raw bits until the end.
 //   4. Per unit: issue the next unit's loads; put the unit's activations
 //      through the wave's own LDS slice into the MFMA layout (no barrier: the
 //      wave writes and reads its slice itself); dequantize and multiply; the
 //      16 x M partial goes to LDS, indexed by (tile, segment).
-//   5. The epilogue operands into LDS, one barrier; one thread per output sums
+//   5. With the down-projection in the launch, the poll of its partials.
+//      The epilogue operands into LDS, one barrier; one thread per output sums
 //      its tile's segment partials in segment order (deterministic), adds the
 //      bias and the LoRA term, rounds and stores -- or writes the fp32 sum of
-//      its K split to the workspace for the split-K finisher.
+//      its K split to the workspace for the split-K finisher.  The launch's
+//      last job readies the other partial region for the next launch.
 // ---------------------------------------------------------------------------
 constexpr int kGemvThreads = 1024;
 constexpr int kGemvWaves = kGemvThreads / 64;
@@ -86,6 +91,9 @@ constexpr int kGemvLdsBudget = 160 * 1024 - kGemvLutQwords * 8;
 constexpr int kBufferRsrcWord3 = 0x00020000;
 // A buffer offset past every range this file builds: the load returns zero.
 constexpr uint32_t kOobOffset = 0xFFFFFFF0u;
+// Cache policy of a buffer load or store that is device coherent (sc1), as
+// the agent-scope atomic loads and stores are.
+constexpr int kCoherent = 16;
 
 struct GemvArgs {
   const uint16_t* x;
@@ -100,22 +108,28 @@ struct GemvArgs {
   bool xvec;               // x rows 16-byte aligned (vector loads)
   int bvec_log2;           // LoRA B rows read as 16-byte chunks, 2^bvec_log2 per row (-1: by element)
   float* ws;               // [S, M, N] partials when !direct
-  // LoRA down-projection inside this launch (jt > 0): workgroup j < jt
-  // computes the fp32 partials of ranks [16 (j / u_splits), +16) over K split
-  // j % u_splits (the layout lora_u_kernel writes) into ubits, +0.0 stored
-  // as -0.0 so that 0 means "not written yet"; the tile workgroups (from jt
-  // on) poll their partials until none is 0.  Every workgroup then counts
-  // itself in *done; the last one clears ubits and *done, so both are zero
-  // again once the launch is over.
-  int jt;
-  // The same jobs run by the tile workgroups themselves (jm > 0, when every
-  // compute unit holds a tile workgroup and no workgroup of the launch can
-  // wait for a free one): tile workgroup g < jm runs job g after its first
-  // unit's loads are issued, then its units.  jt and jm are not both > 0.
-  int jm;
-  uint32_t spin_limit;     // polls before a tile workgroup computes u itself
-  uint32_t* done;          // workgroups past their use of ubits
-  uint32_t* ubits;         // [u_splits, M, rank] partials as fp32 bits
+  // LoRA down-projection inside this launch (jobs > 0): job b computes the
+  // fp32 partials of ranks [16 (b / u_splits), +16) over K split
+  // b % u_splits, one wave per job (wave b / G of workgroup b % G, G the
+  // workgroups), into region P [u_splits][M][rank] of parts, P = bit 0 of
+  // state[0] as read at the launch's start, +0.0 stored as -0.0 so that 0
+  // means "not written yet"; after its units every workgroup polls the
+  // partials until none is 0.  No workgroup waits on a count at its end:
+  // region P is zero at the start of every launch (but for partials the
+  // launch itself writes), and the other region holds the previous launch's
+  // partials, state[1 + p] words of region p.  Every job counts itself in
+  // *jc after its stores; the last job's wave, at its end, clears the other
+  // region, records this launch's extent and flips the parity, so the next
+  // launch finds its region zero.  Every job has read the state before it
+  // counts itself, and the launch fits the device (one workgroup per compute
+  // unit), so the other workgroups have read it before that wave ends; one
+  // that starts later (the device shared with other work) finds no partials
+  // and computes u itself.
+  int jobs;
+  uint32_t spin_limit;     // polls before a workgroup computes u itself
+  uint32_t* jc;            // jobs done (zero between launches)
+  uint32_t* state;         // parity of the next launch's region, extents of regions 0 and 1
+  uint32_t* parts;         // two regions of kGemvPartWords: partials as fp32 bits
   const uint16_t* lora_x;
   int ld_lora_x;
   const void* lora_a;      // [rank, K]
@@ -142,6 +156,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uin
 }
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ u32x4 buf_load16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherent));
 }
 __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
@@ -334,13 +351,93 @@ __device__ __forceinline__ f32x4 gemv_tile(const GemvUnit<Scale>& U, float s1, f
 // global load, which would serialize the prefetched units.)
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Polls of the ready counter before a tile workgroup gives up waiting for the
-// producers and computes u itself.  The producers have the lowest workgroup
-// indices and never wait, so they are dispatched first and finish; the bound
-// keeps the wait finite when the device is shared with other work.
+// Polls of the LoRA partials before a workgroup gives up waiting for the
+// other workgroups' jobs and computes u itself.  A job runs before its
+// wave's units and never waits, so every job ends once its workgroup has
+// been dispatched; the bound keeps the wait finite when the device is
+// shared with other work (a workgroup still waiting for a compute unit).
 constexpr uint32_t kGemvSpinLimit = 1u << 16;
 
-// One LoRA down-projection job of the GEMV launch: the fp32 partial sums
+// In-launch LoRA down-projection jobs: one wave computes the 16 x 16 fp32
+// sums x[m, k] RND(A[16 p + jj, k]) (tokens m < 16, ranks 16 p + jj) over the
+// 32-k steps [s0, s1) of its K split with one MFMA accumulation in step
+// order, loading kJobChunk steps at once.
+constexpr int kJobChunk = 4;
+// Partials one thread of the epilogue sums: the 16 splits [16 c, 16 c + 16)
+// of one (m, j); the C = 2^i threads of one (m, j) are adjacent lanes.
+constexpr int kUPerThread = 16;
+constexpr int kJobMaxC = 8;
+
+struct JobChunk {
+  u32x4 x[kJobChunk], a0[kJobChunk], a1[kJobChunk];
+};
+
+// Rank group and step range of wave job b of `ns` K splits per group.
+__device__ __forceinline__ void job_range(int K, int ns, int b, int& p, uint32_t& s0, uint32_t& s1) {
+  p = b / ns;
+  const uint32_t s = uint32_t(b - p * ns), nsteps = uint32_t(K) / 32u;
+  s0 = nsteps * s / uint32_t(ns);
+  s1 = nsteps * (s + 1u) / uint32_t(ns);
+}
+
+// The operands of steps [b0, b0 + kJobChunk) of rank group p: lane (i16, q)
+// takes x[i16, k .. k + 7] and A[16 p + i16, k .. k + 7], k = 32 step + 8 q
+// (fp32 A as two 16-byte pieces); steps from s1 on, tokens past M and ranks
+// past rank read zeros.
+template <int XT>
+__device__ __forceinline__ void job_issue(JobChunk& c, const GemvArgs& a, const LinearEpi& e, int p, uint32_t b0,
+                                          uint32_t s1, int lane) {
+  const int i16 = lane & 15, q = lane >> 4;
+  const uint32_t K = uint32_t(a.K);
+  const bool f32 = e.lora_dt == RQ_DTYPE_F32;
+  const uint32_t ab = f32 ? 4u : 2u;
+  const __amdgpu_buffer_rsrc_t xr = buffer_rsrc(a.lora_x, uint32_t(a.M - 1) * uint32_t(a.ld_lora_x) * 2u + K * 2u);
+  const __amdgpu_buffer_rsrc_t ar = buffer_rsrc(a.lora_a, uint32_t(e.rank) * K * ab);
+  const bool mlive = i16 < a.M;
+  const uint32_t j = uint32_t(16 * p + i16);
+  const bool jlive = j < uint32_t(e.rank);
+  const uint32_t xrow = uint32_t(i16) * uint32_t(a.ld_lora_x) * 2u, arow = j * K * ab;
+#pragma unroll
+  for (int t = 0; t < kJobChunk; ++t) {
+    const bool live = b0 + uint32_t(t) < s1;
+    const uint32_t k = 32u * (b0 + uint32_t(t)) + 8u * uint32_t(q);
+    c.x[t] = buf_load16(xr, live && mlive ? xrow + 2u * k : kOobOffset);
+    c.a0[t] = buf_load16(ar, live && jlive ? arow + ab * k : kOobOffset);
+    c.a1[t] = buf_load16(ar, live && jlive && f32 ? arow + 4u * k + 16u : kOobOffset);
+  }
+}
+
+// Steps [b0, min(b0 + kJobChunk, s1)) of a job into acc, in step order; A is
+// rounded to the activation dtype first (lora_layer.py:67's
+// A.to(x.dtype)).  acc[r] of lane (i16, q) is (m, jj) = (4 q + r, i16).
+template <int XT>
+__device__ __forceinline__ f32x4 job_mfma(const JobChunk& c, f32x4 acc, uint32_t b0, uint32_t s1, bool f32) {
+#pragma unroll
+  for (int t = 0; t < kJobChunk; ++t) {
+    if (b0 + uint32_t(t) < s1) {
+      const u32x4 bop = f32 ? u32x4{cvt_pk<XT>(u2f(c.a0[t].x), u2f(c.a0[t].y)), cvt_pk<XT>(u2f(c.a0[t].z), u2f(c.a0[t].w)),
+                                    cvt_pk<XT>(u2f(c.a1[t].x), u2f(c.a1[t].y)), cvt_pk<XT>(u2f(c.a1[t].z), u2f(c.a1[t].w))}
+                            : c.a0[t];
+      acc = mfma16x16x32<XT>(c.x[t], bop, acc);
+    }
+  }
+  return acc;
+}
+
+// A whole job whose first chunk (steps from s0) is already in c.
+template <int XT>
+__device__ __forceinline__ f32x4 job_finish(JobChunk& c, const GemvArgs& a, const LinearEpi& e, int p, uint32_t s0,
+                                            uint32_t s1, int lane) {
+  const bool f32 = e.lora_dt == RQ_DTYPE_F32;
+  f32x4 acc = job_mfma<XT>(c, f32x4{0.f, 0.f, 0.f, 0.f}, s0, s1, f32);
+  for (uint32_t b0 = s0 + kJobChunk; b0 < s1; b0 += kJobChunk) {
+    job_issue<XT>(c, a, e, p, b0, s1, lane);
+    acc = job_mfma<XT>(c, acc, b0, s1, f32);
+  }
+  return acc;
+}
+
+// One LoRA down-projection job of lora_u_jobs_kernel: the fp32 partial sums
 // x[m, k] RND(A[16 p + jj, k]) over the k of split s of `splits` (32-k steps
 // [S s / splits, S (s + 1) / splits)), the steps dealt to the 16 waves in
 // contiguous runs, four in flight at once, then the wave partials summed in
@@ -398,18 +495,6 @@ __device__ __forceinline__ float lora_u_job(const GemvArgs& a, const LinearEpi& 
   return v;
 }
 
-// Wave 0 of a workgroup that has counted itself in *done (old: the count
-// before it): the launch's last workgroup clears the partials and the count
-// for the next launch (every other workgroup is past its use of them).
-__device__ __forceinline__ void gemv_last_clears(const GemvArgs& a, const LinearEpi& e, int lane, uint32_t old) {
-  // every other workgroup counted itself after its last access to ubits
-  // had completed; the clears below depend on the count's result
-  if (old != gridDim.x - 1u) return;
-  const uint32_t n = uint32_t(e.u_splits) * uint32_t(a.M) * uint32_t(e.rank);
-  for (uint32_t i = uint32_t(lane); i < n; i += 64u) a.ubits[i] = 0u;
-  if (lane == 0) __hip_atomic_store(a.done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 template <int XT, class Scale, int U, int XM>
 __global__ __launch_bounds__(kGemvThreads) __attribute__((amdgpu_waves_per_eu(4, 4)))
 void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
@@ -420,31 +505,8 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int M = a.M, TS = a.TS, nseg = a.nseg;
-  if (int(blockIdx.x) < a.jt) {
-    // a LoRA down-projection job: partials to ubits (device-coherent
-    // stores), then count this workgroup once they have all completed
-    const int j = blockIdx.x, ns = e.u_splits;
-    const float v = lora_u_job<XT>(a, e, j / ns, j % ns, ns, tid, wave, reinterpret_cast<float*>(smem));
-    const int jj = 16 * (j / ns) + (tid & 15);
-    if (tid < M * 16 && jj < e.rank) {
-      const uint32_t bits = f2u(v);
-      __hip_atomic_store(&a.ubits[((j % ns) * M + (tid >> 4)) * e.rank + jj], bits != 0u ? bits : 0x80000000u,
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // the device-coherent stores have completed before the count (their
-    // values are their own flags; an agent-scope release fence would write
-    // back the whole L2 instead)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (wave == 0) {
-      uint32_t old = 0u;
-      if (lane == 0) old = __hip_atomic_fetch_add(a.done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      gemv_last_clears(a, e, lane, __builtin_amdgcn_readfirstlane(old));
-    }
-    return;
-  }
-  const bool fused = a.jt > 0 || a.jm > 0;
-  const uint32_t g = blockIdx.x - uint32_t(a.jt), G = gridDim.x - uint32_t(a.jt);  // this tile workgroup, their number
+  const bool fused = a.jobs > 0;
+  const uint32_t g = blockIdx.x, G = gridDim.x;  // this workgroup, their number
   const int rank = (a.direct && e.rank > 0) ? e.rank : 0;  // LoRA staging only when fused here
   constexpr int RP = kGemvMaxFusedRank;                    // staging pitch
   constexpr bool kGather = GemvScale<Scale>::kGather;
@@ -523,6 +585,26 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   // units in flight ahead of the one being computed (two measured slower:
   // the extra bytes in flight only lengthened the loaded latency)
   constexpr int D = 1;
+  // this wave's LoRA down-projection job, if any: its first chunk's loads go
+  // out before the unit loads, so that waiting for them never waits for the
+  // weights
+  const int ns = e.u_splits;
+  const int job = wave * int(G) + int(g);
+  const bool has_job = fused && job < a.jobs;
+  // this launch's partial region and the other region's extent, loaded by
+  // wave 0 (which passes the parity on through LDS) and the job waves (the
+  // state and job loads are a wave's first loads, so waiting for them never
+  // waits for another; one state load per workgroup keeps the line cool)
+  u32x4 st = u32x4{0u, 0u, 0u, 0u};
+  if (fused && (wave == 0 || has_job)) st = buf_load16_coherent(buffer_rsrc(a.state, 16u), 0u);
+  const uint32_t par = st.x & 1u;
+  JobChunk jch;
+  int jp = 0;
+  uint32_t js0 = 0u, js1 = 0u;
+  if (has_job) {
+    job_range(a.K, ns, job, jp, js0, js1);
+    job_issue<XT>(jch, a, e, jp, js0, js1, lane);
+  }
   // the gathered scales first: lane (u, r) = (lane / 16, lane % 16) takes
   // row r of unit u's tile, from unit u's segment's first block on
   u32x4 gsv = u32x4{0u, 0u, 0u, 0u};
@@ -573,32 +655,53 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
   }
 
-  // 2. the table; a workgroup with a merged job runs it now (its unit loads
-  //    are in flight): partials to ubits as the producer workgroups store them
+  // 2. the table; then this wave's job, if any (its unit loads stay in
+  //    flight): partials to the region with device-coherent stores, then the
+  //    job counts itself; the last one readies the next launch's region
   fill_f32pair_lut<kGemvThreads>(lut, tid);
+  if (fused && tid == 0) flag[1] = par;
   lds_barrier();
-  if (int(g) < a.jm) {
-    const int ns = e.u_splits;
-    const float v = lora_u_job<XT>(a, e, int(g) / ns, int(g) % ns, ns, tid, wave, reinterpret_cast<float*>(smem));
-    const int jj = 16 * (int(g) / ns) + (tid & 15);
-    if (tid < M * 16 && jj < e.rank) {
-      const uint32_t bits = f2u(v);
-      __hip_atomic_store(&a.ubits[((int(g) % ns) * M + (tid >> 4)) * e.rank + jj], bits != 0u ? bits : 0x80000000u,
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t jc_old = 0u;
+  if (has_job) {
+    const f32x4 acc = job_finish<XT>(jch, a, e, jp, js0, js1, lane);
+    const int s = job - jp * ns, jj = 16 * jp + ln.n16;
+    uint32_t* region = a.parts + par * uint32_t(kGemvPartWords);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * ln.q + r;
+      if (m < M && jj < e.rank) {
+        const uint32_t bits = f2u(acc[r]);
+        __hip_atomic_store(&region[(s * M + m) * e.rank + jj], bits != 0u ? bits : 0x80000000u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
-    lds_barrier();  // the job's LDS reduction area is read before the units use it
+    // the count, its result awaited at the wave's end (an increment: the
+    // compiler's atomic optimizer rewrites fetch_add into a form that waits
+    // for the result at once)
+    if (lane == 0) jc_old = __builtin_amdgcn_atomic_inc32(a.jc, 0xFFFFFFFFu, __ATOMIC_RELAXED, "agent");
   }
   if (fused && tid == 0) *flag = 0u;
 
   // 3. epilogue operands, raw: LoRA B values (value t of thread tid is row
-  //    tid / 64 of tile slot t, rank tid % 64), the bias, the RND(u) partials
-  //    (waves m < M)
+  //    tid / 64 of tile slot t, rank tid % 64), the bias, the RND(u)
+  //    partials: thread tid < M rank C (C = 2^i >= u_splits / 16) takes
+  //    splits [16 c, 16 c + 16) of pr = (m, j) = (pr / rank, pr % rank),
+  //    pr = tid / C, c = tid % C
   RawElem br = RawElem{0u, 0u};
   u32x4 bvr = u32x4{0u, 0u, 0u, 0u};
-  uint32_t up[kGemvMaxUSplits];
+  uint32_t up[kUPerThread];
 #pragma unroll
-  for (int k = 0; k < kGemvMaxUSplits; ++k) up[k] = 0u;
-  const int lj = tid & (RP - 1);
+  for (int k = 0; k < kUPerThread; ++k) up[k] = 0u;
+  int uC = 1;
+  while (kUPerThread * uC < ns) uC <<= 1;
+  const int upr = tid / uC, uc = tid - upr * uC;
+  const bool u_mine = rank > 0 && upr < M * rank;
+  const uint32_t ustride = uint32_t(M) * uint32_t(rank);
+  // split 16 c + k of this thread's (m, j), or split 0 when past ns (read,
+  // never summed)
+  auto u_index = [&](int k) -> uint32_t {
+    return (kUPerThread * uc + k < ns ? uint32_t(kUPerThread * uc + k) : 0u) * ustride + uint32_t(upr);
+  };
   const uint32_t bbytes = e.lora_dt == RQ_DTYPE_F32 ? 4u : 2u;
   // LoRA B rows as 16-byte chunks (the host fuses LoRA only for such rows):
   // thread tid < TS * 16 * 2^cl takes chunk tid % 2^cl of row (tid >> cl) % 16
@@ -619,16 +722,12 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     const uint32_t cn = tile_of(cb >> 4) * 16u + uint32_t(cb & 15);
     br = buf_load_elem(bres, cn, (cb >> 4) < TS && cn < uint32_t(a.N), e.bias_dt);
   }
-  const bool stage_u = rank > 0 && wave < M;
-  auto load_u_partials = [&]() {
-    const uint32_t ns = uint32_t(e.u_splits), stride = uint32_t(M) * uint32_t(rank);
-    const __amdgpu_buffer_rsrc_t ures = buffer_rsrc(e.u, ns * stride * 4u);
-    const uint32_t u_idx = uint32_t(wave) * uint32_t(rank) + uint32_t(lj);
+  if (u_mine && !fused) {
+    // the partials of a down-projection launched before this kernel
+    const __amdgpu_buffer_rsrc_t ures = buffer_rsrc(e.u, uint32_t(ns) * ustride * 4u);
 #pragma unroll
-    for (int k = 0; k < kGemvMaxUSplits; ++k)
-      up[k] = buf_load4(ures, (uint32_t(k) < ns && lj < rank) ? (uint32_t(k) * stride + u_idx) * 4u : kOobOffset);
-  };
-  if (stage_u && !fused) load_u_partials();
+    for (int k = 0; k < kUPerThread; ++k) up[k] = buf_load4(ures, u_index(k) * 4u);
+  }
 
   // 4. the units, each as soon as its loads have landed; partials to LDS
   const uint32_t lane_off = uint32_t(lane & 31) * 8u;
@@ -675,29 +774,27 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
   }
 
-  // 5. with the LoRA down-projection in this launch: the waves m < M poll
-  //    their partials (device-coherent loads) until none reads 0 -- a
+  // 5. with the LoRA down-projection in this launch: the threads that take
+  //    partials poll them (device-coherent loads) until none reads 0 -- a
   //    bounded poll -- and thread 0 counts the workgroup past its use of
-  //    them.  A workgroup in which a poll gave up runs every job itself, in
-  //    the producers' order (the same sums), in the table's LDS, which the
-  //    unit loop no longer reads.
-  float* ufl = reinterpret_cast<float*>(lut) + kGemvWaves * 256;  // [M][RP] sums, own u only
-  uint32_t self_u = 0u, done_old = 0u;
+  //    them.  A workgroup in which a poll gave up runs every job itself, the
+  //    same way (the same sums), into the table's LDS, which the unit loop
+  //    no longer reads, and takes the partials from there.
+  uint32_t self_u = 0u;
   if (fused) {
-    if (stage_u && lj < rank) {
-      const uint32_t ns = uint32_t(e.u_splits), stride = uint32_t(M) * uint32_t(rank);
-      const uint32_t u_idx = uint32_t(wave) * uint32_t(rank) + uint32_t(lj);
+    const uint32_t* region = a.parts + flag[1] * uint32_t(kGemvPartWords);
+    if (u_mine) {
       bool ok = false;
       for (uint32_t i = 0; !ok && a.spin_limit > 0; ++i) {
         // all the loads of a poll in flight together: no branch between
-        // them (a split past ns reads split 0 again and is not checked)
+        // them (a split past ns reads the first again and is not checked)
 #pragma unroll
-        for (int k = 0; k < kGemvMaxUSplits; ++k)
-          up[k] = __hip_atomic_load(&a.ubits[(uint32_t(k) < ns ? uint32_t(k) * stride : 0u) + u_idx],
-                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = 0; k < kUPerThread; ++k)
+          up[k] = __hip_atomic_load(&region[u_index(k)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         uint32_t missing = 0u;
 #pragma unroll
-        for (int k = 0; k < kGemvMaxUSplits; ++k) missing |= uint32_t(up[k] == 0u) & uint32_t(uint32_t(k) < ns);
+        for (int k = 0; k < kUPerThread; ++k)
+          missing |= uint32_t(up[k] == 0u) & uint32_t(kUPerThread * uc + k < ns);
         ok = missing == 0u;
         if (ok || i >= a.spin_limit) break;
         __builtin_amdgcn_s_sleep(2);
@@ -706,23 +803,27 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
     lds_barrier();
     self_u = __builtin_amdgcn_readfirstlane(*flag);
-    // the count's result is needed only at the very end: an increment (the
-    // compiler's atomic optimizer rewrites fetch_add into a form that waits
-    // for the result at once) lets the epilogue run under its round trip
-    if (tid == 0) done_old = __builtin_amdgcn_atomic_inc32(a.done, 0xFFFFFFFFu, __ATOMIC_RELAXED, "agent");
     if (self_u) {
-      float* red = reinterpret_cast<float*>(lut);
-      const int ns = e.u_splits;
-      for (int pg = 0; pg < (rank + 15) / 16; ++pg) {
-        float sum = 0.0f;
-        for (int sp = 0; sp < ns; ++sp) {
-          sum = __fadd_rn(sum, lora_u_job<XT>(a, e, pg, sp, ns, tid, wave, red));
-          lds_barrier();
+      float* pl = reinterpret_cast<float*>(lut);  // [u_splits][M][rank]
+      for (int b = wave; b < a.jobs; b += kGemvWaves) {
+        int p;
+        uint32_t s0, s1;
+        job_range(a.K, ns, b, p, s0, s1);
+        JobChunk c;
+        job_issue<XT>(c, a, e, p, s0, s1, lane);
+        const f32x4 acc = job_finish<XT>(c, a, e, p, s0, s1, lane);
+        const int sp = b - p * ns, jj = 16 * p + ln.n16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 4 * ln.q + r;
+          if (m < M && jj < rank) pl[(sp * M + m) * rank + jj] = acc[r];
         }
-        const int jj = 16 * pg + (tid & 15);
-        if (tid < M * 16 && jj < rank) ufl[(tid >> 4) * RP + jj] = sum;
       }
       lds_barrier();
+      if (u_mine) {
+#pragma unroll
+        for (int k = 0; k < kUPerThread; ++k) up[k] = f2u(pl[u_index(k)]);
+      }
     }
   }
 
@@ -733,7 +834,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   asm volatile("" : "+v"(br.w4), "+v"(br.w2));
   asm volatile("" : "+v"(bvr));
 #pragma unroll
-  for (int k = 0; k < kGemvMaxUSplits; ++k) asm volatile("" : "+v"(up[k]));
+  for (int k = 0; k < kUPerThread; ++k) asm volatile("" : "+v"(up[k]));
   if (bvec_live) {
     uint16_t* dst = lbs + (bt * 16 + br_row) * RP + bc * int(16u / bbytes);
     if (e.lora_dt == RQ_DTYPE_F32) {
@@ -749,13 +850,19 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
   }
   if (a.direct && tid < TS * 16) bss[tid] = has_bias ? round_x<XT>(elem_to_f32(br, e.bias_dt)) : 0.0f;
-  if (stage_u) {
-    float sum = 0.0f;
+  if (rank > 0) {
+    // u[m, j]: each thread sums its 16 splits in order, then lane c = 0 of
+    // the (m, j) adds the C threads' sums in c order (adjacent lanes of one
+    // wave: C divides 64)
+    float l1 = 0.0f;
+    if (u_mine) {
 #pragma unroll
-    for (int k = 0; k < kGemvMaxUSplits; ++k)
-      if (k < e.u_splits) sum = __fadd_rn(sum, u2f(up[k]));
-    if (self_u) sum = ufl[wave * RP + lj];
-    us[tid] = lj < rank ? round_x<XT>(sum) : 0.0f;
+      for (int k = 0; k < kUPerThread; ++k)
+        if (kUPerThread * uc + k < ns) l1 = __fadd_rn(l1, u2f(up[k]));
+    }
+    float sum = l1;
+    for (int c = 1; c < uC; ++c) sum = __fadd_rn(sum, __shfl(l1, lane + c));
+    if (u_mine && uc == 0) us[(upr / rank) * RP + (upr - (upr / rank) * rank)] = round_x<XT>(sum);
   }
   lds_barrier();
 
@@ -805,7 +912,23 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
   };
   finish();
-  if (fused && wave == 0) gemv_last_clears(a, e, lane, __builtin_amdgcn_readfirstlane(done_old));
+  if (has_job && __builtin_amdgcn_readfirstlane(jc_old) == uint32_t(a.jobs) - 1u) {
+    // the last job: clear the other region (the previous launch's partials,
+    // whose readers have all finished), record this launch's extent in
+    // region par, reset the count and flip the parity
+    const uint32_t other_ext = par ? st.y : st.z;
+    const __amdgpu_buffer_rsrc_t other =
+        buffer_rsrc(a.parts + (par ^ 1u) * uint32_t(kGemvPartWords), uint32_t(kGemvPartBytes));
+    for (uint32_t i = uint32_t(lane); 4u * i < other_ext; i += 64u)
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, other, 16u * i, 0, kCoherent);
+    if (lane == 0) {
+      const uint32_t ext = uint32_t(ns) * uint32_t(M) * uint32_t(e.rank);
+      __hip_atomic_store(&a.state[1u + par], ext, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&a.state[2u - par], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.jc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(a.state, par ^ 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 }
 
 // Split-K finisher (and the LoRA epilogue for any M): y = finish(sum_s
@@ -918,11 +1041,11 @@ __global__ __launch_bounds__(256) void lora_u_kernel(const uint16_t* __restrict_
   }
 }
 
-// The down-projection jobs of lora_u_job as a launch of their own, for a
-// GEMV whose tile workgroups leave no compute unit free: workgroup j runs job
-// j (ranks [16 (j / u_splits), +16), K split j % u_splits) and stores its
-// partials with plain stores in the layout lora_u_kernel writes, with the
-// bits the in-launch producers would give.
+// The LoRA down-projection as a launch of its own, before a split-K GEMV or
+// one with more workgroups than compute units: workgroup j runs job j of
+// lora_u_job (ranks [16 (j / u_splits), +16), K split j % u_splits, its
+// steps spread over the 16 waves) and stores its partials in the layout
+// lora_u_kernel writes.
 template <int XT>
 __global__ __launch_bounds__(kGemvThreads) void lora_u_jobs_kernel(GemvArgs a, LinearEpi e, float* __restrict__ up) {
   __shared__ float red[kGemvWaves * 256];
@@ -951,9 +1074,9 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
   const int64_t tiles = (N + 15) / 16;
   const int64_t ncu = cus > 0 ? cus : 1;
   p.u_splits = 0;
-  // K splits of the down-projection jobs (inside the GEMV launch or as
-  // lora_u_jobs_kernel): about 256 k per job, so that a job's loads are one
-  // round of 16-byte loads per wave and the jobs end early
+  // K splits of lora_u_jobs_kernel (the down-projection before a split-K
+  // GEMV): about 256 k per workgroup job, so that a job's loads are one round
+  // of 16-byte loads per wave
   const int fused_splits = int(std::min<int64_t>((K + 255) / 256, kGemvMaxUSplits));
   if (rank > 0) {
     const int64_t steps_per_wg = 4 * kLoraUStepsPerWave;
@@ -972,55 +1095,47 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     const int R = kGemvWaves / nseg;  // tile slots per round without the slices
     const int ts_cap = xslice ? (kGemvWaves * kGemvMaxU) / nseg : kGemvMaxU * R;
     const bool direct = S == 1 && lora_fusable;
-    // the down-projection's producer workgroups need compute units the tile
-    // workgroups leave free (else the last tiles would start only after the
-    // producers end): the first pass looks for such a plan, the second runs
-    // the down-projection as its own kernel
-    const bool prod_fits = size_t(M) * rank * fused_splits * 4 <= kLinearSyncBytes - kLinearCountBytes;
-    const int jt = (direct && rank > 0 && lora_prod && prod_fits) ? int((rank + 15) / 16) * fused_splits : 0;
     // LDS of the in-launch down-projection: the wait flag
-    const size_t job_lds = jt > 0 ? 16 : 0;
-    // best tile count per workgroup, with pj producer workgroups that need
-    // compute units of their own (pj > 0) or none
-    auto search = [&](int pj, int64_t& best_cost) {
-      int bts = 0;
-      for (int TS = 1; TS <= kGemvMaxTS && TS <= ts_cap; ++TS) {
-        const int U = xslice ? (TS * nseg + kGemvWaves - 1) / kGemvWaves : (TS + R - 1) / R;
-        if (U != 1 && U != 2 && U != 4) continue;
-        if (gemv_lds_bytes(TS, nseg, int(M), gather, xslice, direct && rank > 0) + job_lds > size_t(kGemvLdsBudget))
-          continue;
-        // tiles a compute unit works through one after another
-        const int64_t grid = (tiles + TS - 1) / TS;
-        if (pj > 0 && grid * S + pj > ncu) continue;
-        const int64_t cost = ((grid * S + ncu - 1) / ncu) * TS;
-        if (bts == 0 || cost <= best_cost) {
-          bts = TS;
-          best_cost = cost;
-        }
-      }
-      return bts;
-    };
-    // The down-projection jobs run in producer workgroups of their own when
-    // the tile workgroups leave compute units free for them at most at twice
-    // the cost in tiles per compute unit (measured on the Llama-3-8B q/o
-    // shape: two tiles per workgroup with producers beat one tile per
-    // workgroup with the jobs merged); otherwise the first jt tile workgroups
-    // run them before their units (merged), and without the in-launch
-    // handshake as a launch of their own.
-    int64_t cost_prod = 0, cost_free = 0;
-    const int ts_prod = jt > 0 ? search(jt, cost_prod) : 0;
-    const int ts_free = search(0, cost_free);
+    bool in_launch = direct && rank > 0 && lora_prod;
+    const size_t job_lds = in_launch ? 16 : 0;
+    // best tile count per workgroup: the fewest tiles a compute unit works
+    // through one after another, the largest such count
     int best = 0;
-    p.jt = p.jm = 0;
-    if (ts_prod > 0 && (ts_free == 0 || cost_prod <= 2 * cost_free)) {
-      best = ts_prod;
-      p.jt = jt;
-    } else if (ts_free > 0) {
-      best = ts_free;
-      if (jt > 0 && (tiles + best - 1) / best >= jt) p.jm = jt;
+    int64_t best_cost = 0;
+    for (int TS = 1; TS <= kGemvMaxTS && TS <= ts_cap; ++TS) {
+      const int U = xslice ? (TS * nseg + kGemvWaves - 1) / kGemvWaves : (TS + R - 1) / R;
+      if (U != 1 && U != 2 && U != 4) continue;
+      if (gemv_lds_bytes(TS, nseg, int(M), gather, xslice, direct && rank > 0) + job_lds > size_t(kGemvLdsBudget))
+        continue;
+      const int64_t grid = (tiles + TS - 1) / TS;
+      const int64_t cost = ((grid * S + ncu - 1) / ncu) * TS;
+      if (best == 0 || cost <= best_cost) {
+        best = TS;
+        best_cost = cost;
+      }
     }
     if (best == 0) continue;
-    if (p.jt > 0 || p.jm > 0) p.u_splits = fused_splits;
+    p.jobs = 0;
+    // the jobs' handshake assumes every workgroup of the launch is resident
+    // at once (one per compute unit)
+    if ((tiles + best - 1) / best > ncu) in_launch = false;
+    if (in_launch) {
+      // wave jobs of one chunk each where the limits allow: C threads of
+      // 16 splits per (m, j) with M rank C <= 1024 threads (C a power of
+      // two, at most kJobMaxC; the partials then fit the synchronization
+      // area), at most one job per wave
+      const int64_t grid = (tiles + best - 1) / best;
+      const int64_t nsteps = K / 32, groups = (rank + 15) / 16, mr = M * rank;
+      int64_t cmax = 1;
+      while (cmax < kJobMaxC && mr * cmax * 2 <= kGemvThreads) cmax *= 2;
+      int64_t ns = (nsteps + kJobChunk - 1) / kJobChunk;
+      ns = std::min<int64_t>(ns, kUPerThread * cmax);
+      ns = std::min<int64_t>(ns, int64_t(kGemvPartWords) / mr);  // one partial region
+      ns = std::min<int64_t>(ns, (kGemvWaves * grid) / groups);
+      ns = std::max<int64_t>(ns, 1);
+      p.u_splits = int(ns);
+      p.jobs = int(groups * ns);
+    }
     p.S = S;
     p.nseg = nseg;
     p.TS = best;
@@ -1031,16 +1146,12 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     break;
   }
   p.lds_bytes = gemv_lds_bytes(p.TS, p.nseg, int(M), gather, p.xslice, p.direct && rank > 0);
-  if (p.jt > 0 || p.jm > 0) {
-    // the wait flag after RND(u); the jobs' 16 KiB wave partials
-    p.lds_bytes += 16;
-    if (p.lds_bytes < size_t(kGemvWaves) * 256 * 4) p.lds_bytes = size_t(kGemvWaves) * 256 * 4;
-  }
+  if (p.jobs > 0) p.lds_bytes += 16;  // the wait flag after RND(u)
   // workspace: the synchronization area (the in-launch down-projection's
   // count and partials, left zero by every launch), the split-K partials,
   // the partials of lora_u_kernel
   const size_t parts = p.direct ? 0 : size_t(p.S) * M * N * 4;
-  const bool in_launch = p.jt > 0 || p.jm > 0;
+  const bool in_launch = p.jobs > 0;
   const size_t uparts = (rank > 0 && !in_launch) ? size_t(p.u_splits) * M * rank * 4 : 0;
   p.u_offset = kLinearSyncBytes + ((parts + 255) & ~size_t(255));
   p.ws_bytes = in_launch ? kLinearSyncBytes : (parts + uparts > 0 ? p.u_offset + uparts : 0);
@@ -1100,7 +1211,7 @@ static int launch_gemv_u(const GemvArgs& a, const GemvPlan& p, Scale scale, cons
   if (int st = allow_dynamic_lds(reinterpret_cast<const void*>(kern), kGemvLdsBudget, attr_devices<XT, Scale, U, XM>());
       st != RQ_OK)
     return st;
-  dim3 grid(unsigned(p.grid + p.jt), unsigned(p.S));
+  dim3 grid(unsigned(p.grid), unsigned(p.S));
   kern<<<grid, kGemvThreads, p.lds_bytes, stream>>>(a, scale, e);
   return rq_check_launch();
 }
@@ -1122,11 +1233,11 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.direct = p.direct;
   a.xvec = gemv_xvec(L);
   a.bvec_log2 = gemv_bvec_log2(L);
-  a.jt = p.jt;
-  a.jm = p.jm;
+  a.jobs = p.jobs;
   a.spin_limit = gemv_spin_limit.load(std::memory_order_relaxed);
-  a.done = static_cast<uint32_t*>(sync);
-  a.ubits = reinterpret_cast<uint32_t*>(static_cast<char*>(sync) + kLinearCountBytes);
+  a.jc = static_cast<uint32_t*>(sync);
+  a.state = static_cast<uint32_t*>(sync) + kLinearParityWord;
+  a.parts = reinterpret_cast<uint32_t*>(static_cast<char*>(sync) + kLinearCountBytes);
   a.lora_x = static_cast<const uint16_t*>(L.lora_x);
   a.ld_lora_x = int(L.ld_lora_x);
   a.lora_a = L.lora_a;
@@ -1240,8 +1351,10 @@ int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   if ((L.M - 1) * L.ldx + L.K > (int64_t(1) << 29)) return RQ_ERR_UNSUPPORTED;
   if (L.rank > 0 && L.N * L.ld_lora_b > (int64_t(1) << 29)) return RQ_ERR_UNSUPPORTED;
   // the down-projection runs inside the GEMV launch when the x rows and A
-  // are 16-byte aligned (its producers read both 16 bytes at a time)
-  const bool lora_prod = L.rank > 0 && aligned(L.lora_x, 16) && L.ld_lora_x % 8 == 0 && aligned(L.lora_a, 16);
+  // are 16-byte aligned (its jobs read both 16 bytes at a time) and both
+  // are addressed with 32-bit offsets
+  const bool lora_prod = L.rank > 0 && aligned(L.lora_x, 16) && L.ld_lora_x % 8 == 0 && aligned(L.lora_a, 16) &&
+                         (L.M - 1) * L.ld_lora_x + L.K <= (int64_t(1) << 29) && L.rank * L.K <= (int64_t(1) << 28);
   const GemvPlan p = plan_gemv(L.M, L.N, L.K, L.rank, device_cus(), gemv_xvec(L), L.c2 == nullptr,
                                gemv_bvec_log2(L) >= 0, lora_prod);
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
@@ -1251,7 +1364,7 @@ int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   float* up = L.rank > 0 ? reinterpret_cast<float*>(wsb + p.u_offset) : nullptr;
   int st;
   const LinearEpi e = make_epi(L, up, p.u_splits);
-  if (L.rank > 0 && p.jt == 0 && p.jm == 0) {
+  if (L.rank > 0 && p.jobs == 0) {
     if (lora_prod) {
       st = L.x_dtype == RQ_DTYPE_BF16 ? launch_lora_u_jobs<RQ_DTYPE_BF16>(L, e, up, stream)
                                       : launch_lora_u_jobs<RQ_DTYPE_F16>(L, e, up, stream);
@@ -1330,13 +1443,15 @@ extern "C" int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, i
   if (workspace_bytes < 0) return RQ_ERR_BAD_SHAPE;
   if (x_dtype == RQ_DTYPE_F32) return run_nf4_linear_f32(L, workspace, size_t(workspace_bytes), stream);
   if (M <= kGemvMaxM) return run_nf4_gemv(L, workspace, size_t(workspace_bytes), stream);
-  // the GEMM's workspace follows the synchronization area, whose zeroed
-  // words past the count block serve as its K splits' tile counters
+  // the GEMM's workspace follows the synchronization area, whose last
+  // kGemmCountBytes serve as its K splits' tile counters
   const bool area = workspace && size_t(workspace_bytes) >= kLinearSyncBytes;
   return run_nf4_gemm(L, area ? static_cast<char*>(workspace) + kLinearSyncBytes : nullptr,
                       area ? size_t(workspace_bytes) - kLinearSyncBytes : 0,
-                      area ? reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kLinearCountBytes) : nullptr,
-                      (kLinearSyncBytes - kLinearCountBytes) / 4, stream);
+                      area ? reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + kLinearSyncBytes -
+                                                         kGemmCountBytes)
+                           : nullptr,
+                      kGemmCountBytes / 4, stream);
 }
 
 // ===========================================================================

@@ -13,12 +13,25 @@ namespace rq {
 constexpr int64_t kGemvMaxM = 16;
 
 // rq_nf4_linear's workspace starts with RQ_LINEAR_SYNC_BYTES of
-// synchronization area: zero before a call, zero again once its kernels are
-// done.  The decode GEMV's in-launch LoRA down-projection keeps its count in
-// the first kLinearCountBytes and its partials after them; the GEMM and the
-// split-K partials start after the area.
+// synchronization area, zero before its first use:
+//   [0, 256)               the decode GEMV's in-launch down-projection: its
+//                          job count (word 0, zero between launches)
+//                          and state (words 32-34: the parity of its next
+//                          partial region, the extents of regions 0 and 1)
+//   [256, 256 + 64 KiB)    its two partial regions of kGemvPartBytes; the
+//                          one the parity names is zero between launches
+//   [.., + 64 KiB)         the GEMM's K-split tile counters, zero between
+//                          launches
+// Every call leaves the area in that state once its kernels are done; the
+// GEMM's workspace and the split-K partials start after the area.
 constexpr size_t kLinearSyncBytes = RQ_LINEAR_SYNC_BYTES;
 constexpr size_t kLinearCountBytes = 256;
+constexpr size_t kLinearParityWord = 32;
+constexpr size_t kGemvPartBytes = 32768;
+constexpr size_t kGemvPartWords = kGemvPartBytes / 4;
+constexpr size_t kGemmCountBytes = 65536;
+static_assert(kLinearSyncBytes == kLinearCountBytes + 2 * kGemvPartBytes + kGemmCountBytes,
+              "synchronization area layout");
 
 // Unpacked arguments of rq_nf4_linear (see include/rocm_qlora_amd.h).
 struct LinearArgs {
@@ -63,8 +76,7 @@ struct LinearEpi {
 
 struct GemvPlan {
   int S, TS, U, nseg, grid, u_splits;
-  int jt;  // LoRA down-projection workgroups inside the launch (0: none)
-  int jm;  // ... or down-projection jobs merged into the first jm tile workgroups
+  int jobs;  // LoRA down-projection wave jobs inside the launch (0: none)
   bool direct, xslice;
   size_t lds_bytes, ws_bytes, u_offset;
 };

@@ -32,9 +32,9 @@ def _rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
 
 # rq_nf4_linear's workspace.  Its first RQ_LINEAR_SYNC_BYTES
 # (include/rocm_qlora_amd.h) are a synchronization area that must be zero
-# before a call and is zero again once the call's kernels are done, so one
-# buffer, zeroed once on the stream that uses it, serves every call ordered
-# on that stream.  Calls that may run at the same time need buffers of their
+# before the buffer's first call and that every call leaves ready for the
+# next one once its kernels are done, so one buffer, zeroed once on the
+# stream that uses it, serves every call ordered on that stream.  Calls that may run at the same time need buffers of their
 # own, hence the keys:
 #   * eager calls: one buffer per (device, stream), zeroed by a fill kernel
 #     on that stream when it is created; it grows by reallocation (a dropped
@@ -46,13 +46,14 @@ def _rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
 #     _CAPTURE_POOL_BYTES per device, zeroed once, with one stream
 #     synchronization, at the device's first eager call), so the graph needs
 #     no fill node: it holds zeros before the first replay and every replay
-#     leaves it zero.  Such a buffer is held for the life of the process (the
-#     graph may replay it at any time).  A capture on a device without the
+#     leaves it ready for the next.  Such a buffer is held for the life of
+#     the process (the graph may replay it at any time).  A capture on a
+#     device without the
 #     pool, with the pool used up, or needing a larger buffer allocates one
 #     from the graph's private memory pool (so it lives exactly as long as
 #     the graph), zeroed by a fill kernel recorded in the graph, which every
 #     replay runs before the captured calls.
-LINEAR_SYNC_BYTES = 65792
+LINEAR_SYNC_BYTES = 131328
 _LINEAR_WS: dict = {}
 _CAPTURE_WS: dict = {}
 _WS_MIN_BYTES = 1 << 20

@@ -28,3 +28,29 @@ def pytest_collection_modifyitems(config, items):
 def dev():
     import torch
     return torch.device("cuda", 0)
+
+
+def _sync_area_ready(ws):
+    """The state every rq_nf4_linear call leaves its workspace's
+    synchronization area in (include/rocm_qlora_amd.h): the decode GEMV's
+    workgroup count zero, the partial region its parity word names zero with
+    extent 0, the other region nonzero only within its recorded extent, and
+    the GEMM's tile counters zero."""
+    import torch
+    from rocm_qlora import ops
+    w = ws[:ops.LINEAR_SYNC_BYTES].view(torch.int32).cpu()
+    region_words = 8192
+    par, ext = int(w[32]), [int(w[33]), int(w[34])]
+    if par not in (0, 1) or ext[par] != 0 or not 0 <= ext[1 - par] <= region_words:
+        return False
+    count_block = torch.cat([w[:32], w[35:64]])
+    region = w[64 + par * region_words:64 + (par + 1) * region_words]
+    other = w[64 + (1 - par) * region_words:64 + (2 - par) * region_words]
+    gemm_counters = w[64 + 2 * region_words:]
+    return (int(count_block.count_nonzero()) == 0 and int(region.count_nonzero()) == 0
+            and int(other[ext[1 - par]:].count_nonzero()) == 0 and int(gemm_counters.count_nonzero()) == 0)
+
+
+@pytest.fixture
+def sync_ready():
+    return _sync_area_ready

@@ -104,12 +104,12 @@ def test_fp32_strided_activations_and_lora_input(dev):
     _check(y, ref)
 
 
-def test_fp32_call_leaves_sync_area_zero(dev):
+def test_fp32_call_leaves_sync_area_ready(dev, sync_ready):
     """An fp32 LoRA call shares the stream's rq_nf4_linear workspace with the
     bf16 decode GEMV, whose in-launch LoRA handshake needs the workspace's
-    synchronization area zero: the fp32 path keeps its LoRA operand after the
-    area, so a bf16 call right after it gives the same bits as on a fresh
-    stream."""
+    synchronization area in its ready state: the fp32 path keeps its LoRA
+    operand after the area, so a bf16 call right after it gives the same bits
+    as on a fresh stream."""
     ql, lora = _layer(dev, seed=12, bias=False)
     a, b = lora.lora_A.detach(), lora.lora_B.detach()
     x16 = torch.randn(2, K, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).to(dev)
@@ -123,5 +123,5 @@ def test_fp32_call_leaves_sync_area_zero(dev):
     torch.cuda.synchronize(dev)
     key = (dev.index if dev.index is not None else torch.cuda.current_device(),
            torch.cuda.current_stream(dev).cuda_stream)
-    assert int(ops._LINEAR_WS[key][:ops.LINEAR_SYNC_BYTES].cpu().count_nonzero()) == 0
+    assert sync_ready(ops._LINEAR_WS[key])
     assert torch.equal(got, want)

@@ -1,15 +1,17 @@
 """The decode GEMV with the LoRA down-projection u = x A^T computed inside the
-same launch (producer workgroups hand their partials to the tile workgroups
-through the workspace's zeroed synchronization area).  Checked against the oracle's
+same launch (one wave per K-split job, in the workgroups themselves, hands its
+partials to every workgroup through a partial region of the workspace's
+synchronization area; the launch's last job readies the other region for the
+next launch).  Checked against the oracle's
 QuantLinear.forward + LoRALinear.forward (quant_linear.py:182-197,
 lora_layer.py:60-70) at rtol = atol = 1e-2 in the activation dtype, and
 against the library's own other paths bit for bit:
 
-- calls in a row on one stream (the counters return to zero after each);
-- the workgroups' own computation of u when the producers' report is not
+- calls in a row on one stream (the area is left ready after each);
+- the workgroups' own computation of u when the jobs' partials are not
   awaited (polls forced to 0), which must give the same bits;
 - replays of a captured HIP graph with new inputs, against eager calls;
-- operands the producers cannot read 16 bytes at a time, which run the
+- operands the jobs cannot read 16 bytes at a time, which run the
   down-projection as its own kernel.
 """
 import math
@@ -51,25 +53,25 @@ def _check(got, ref):
     assert not bad.any(), f"{int(bad.sum())} of {bad.numel()} outside tol; max err {float(err.max()):.4g}"
 
 
-def _sync_words_zero(dev):
+def _sync_words_ready(dev, sync_ready):
     torch.cuda.synchronize(dev)
     key = (dev.index if dev.index is not None else torch.cuda.current_device(),
            torch.cuda.current_stream(dev).cuda_stream)
     ws = ops._LINEAR_WS.get(key)
     assert ws is not None
-    assert int(ws[:ops.LINEAR_SYNC_BYTES].cpu().count_nonzero()) == 0
+    assert sync_ready(ws)
 
 
 @pytest.mark.parametrize("K,N,M,rank", [
-    (4096, 4096, 1, 16),     # q / o: two tiles per workgroup leave room for the producers
+    (4096, 4096, 1, 16),     # q / o: 256 workgroups, 32 jobs
     (4096, 14336, 1, 16),    # gate / up
-    (14336, 4096, 1, 16),    # down: the tiles fill the CUs, the jobs run as a launch of their own
+    (14336, 4096, 1, 16),    # down: 112 jobs, partials summed by 8 threads per rank
     (4096, 1024, 2, 16),     # k / v
     (4096, 4096, 5, 8),      # activations as register operands
-    (4096, 1024, 16, 64),    # four rank groups x four K splits of producers
+    (4096, 1024, 16, 64),    # four rank groups, jobs of four chunks
     (1024, 512, 3, 32),
 ])
-def test_calls_in_a_row(dev, K, N, M, rank):
+def test_calls_in_a_row(dev, sync_ready, K, N, M, rank):
     print(f"in-launch lora K={K} N={N} M={M} rank={rank}", flush=True)
     packed, absmax, a, b = _layer(N, K, rank, seed=K + N + rank, dev=dev)
     ad, bd = a.to(dev), b.to(dev)
@@ -78,7 +80,7 @@ def test_calls_in_a_row(dev, K, N, M, rank):
         y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0)
         ref = R.nf4_lora_linear(x, packed.cpu(), absmax.cpu(), None, a, b, 2.0, N, 64)
         _check(y, ref)
-    _sync_words_zero(dev)
+    _sync_words_ready(dev, sync_ready)
 
 
 @pytest.mark.parametrize("K,N,M,rank,lora_dtype", [
@@ -86,9 +88,9 @@ def test_calls_in_a_row(dev, K, N, M, rank):
     (4096, 1024, 4, 64, torch.float32),
     (2048, 768, 2, 16, torch.bfloat16),
 ])
-def test_workgroups_own_u_same_bits(dev, K, N, M, rank, lora_dtype):
-    """Polls forced to 0: every tile workgroup computes u itself, job by job
-    in the producers' order, so y is bit-identical to the awaited path."""
+def test_workgroups_own_u_same_bits(dev, sync_ready, K, N, M, rank, lora_dtype):
+    """Polls forced to 0: every workgroup computes u itself, job by job as
+    the job waves do, so y is bit-identical to the awaited path."""
     print(f"own-u K={K} N={N} M={M} rank={rank} {lora_dtype}", flush=True)
     packed, absmax, a, b = _layer(N, K, rank, seed=7 + K, dev=dev, lora_dtype=lora_dtype)
     x = _x(M, K, seed=3).to(dev)
@@ -102,12 +104,12 @@ def test_workgroups_own_u_same_bits(dev, K, N, M, rank, lora_dtype):
         nat.set_gemv_spin_limit(old)
     y3 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
     assert torch.equal(y0, y1) and torch.equal(y0, y2) and torch.equal(y0, y3)
-    _sync_words_zero(dev)
+    _sync_words_ready(dev, sync_ready)
     ref = R.nf4_lora_linear(x.cpu(), packed.cpu(), absmax.cpu(), None, a, b, 0.5, N, 64)
     _check(y1, ref)
 
 
-def test_graph_replays_match_eager(dev):
+def test_graph_replays_match_eager(dev, sync_ready):
     K, N, M, rank = 4096, 4096, 1, 16
     packed, absmax, a, b = _layer(N, K, rank, seed=11, dev=dev)
     ad, bd = a.to(dev), b.to(dev)
@@ -130,7 +132,7 @@ def test_graph_replays_match_eager(dev):
         want = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0)
         torch.cuda.synchronize(dev)
         assert torch.equal(got, want), f"replay {i} differs from the eager call"
-    _sync_words_zero(dev)
+    _sync_words_ready(dev, sync_ready)
 
 
 def test_two_graphs_replayed_in_turn(dev):
@@ -196,11 +198,11 @@ def test_unaligned_operands_run_separate_kernel(dev, case):
     _check(y, ref)
 
 
-def test_capture_forking_side_streams(dev):
+def test_capture_forking_side_streams(dev, sync_ready):
     """A capture that forks two side streams, each running fused-LoRA M = 1
     GEMVs (the in-launch handshake) and a GEMM with K splits: each branch
     gets a workspace of its own, and every replay matches eager calls bit
-    for bit; the eager workspace's synchronization area stays zero."""
+    for bit; the eager workspace's synchronization area is left ready."""
     K, M, rank = 4096, 1, 16
     specs = [(4096, 31), (1024, 32)]
     layers = [(N,) + _layer(N, K, rank, seed=s, dev=dev) for N, s in specs]
@@ -239,4 +241,4 @@ def test_capture_forking_side_streams(dev):
         torch.cuda.synchronize(dev)
         for g, w in zip(got, want + want):
             assert torch.equal(g, w), f"replay {i} differs from the eager calls"
-    _sync_words_zero(dev)
+    _sync_words_ready(dev, sync_ready)
