@@ -83,6 +83,32 @@ def test_calls_in_a_row(dev, sync_ready, K, N, M, rank):
     _sync_words_ready(dev, sync_ready)
 
 
+def test_mixed_shapes_share_one_workspace(dev, sync_ready):
+    """Launches of different extents (K splits x M x rank) in a row on one
+    stream, twice round: each leaves its partials in one region and readies
+    the other for the next launch, so every call gives the bits of the same
+    call on a fresh workspace (a stream of its own) and the area is ready
+    after each one."""
+    specs = [(4096, 4096, 1, 16), (4096, 1024, 16, 64), (14336, 4096, 1, 16), (1024, 512, 3, 32),
+             (4096, 14336, 2, 16), (2048, 768, 1, 8)]
+    layers = [(K, N, M, r) + _layer(N, K, r, seed=K + N + r + M, dev=dev) for K, N, M, r in specs]
+    for rnd in range(2):
+        for i, (K, N, M, r, packed, absmax, a, b) in enumerate(layers):
+            print(f"mixed round {rnd} call {i}: K={K} N={N} M={M} rank={r}", flush=True)
+            x = _x(M, K, seed=10 * rnd + i).to(dev)
+            ad, bd = a.to(dev), b.to(dev)
+            got = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
+            _sync_words_ready(dev, sync_ready)
+            fresh = torch.cuda.Stream(dev)
+            fresh.wait_stream(torch.cuda.current_stream(dev))
+            with torch.cuda.stream(fresh):
+                want = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
+            torch.cuda.synchronize(dev)
+            ops._LINEAR_WS.pop((dev.index if dev.index is not None else torch.cuda.current_device(),
+                                fresh.cuda_stream), None)
+            assert torch.equal(got, want), f"call {i} of round {rnd} differs from a fresh workspace"
+
+
 @pytest.mark.parametrize("K,N,M,rank,lora_dtype", [
     (4096, 4096, 1, 16, torch.float32),
     (4096, 1024, 4, 64, torch.float32),
