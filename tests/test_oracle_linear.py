@@ -53,6 +53,30 @@ def test_nf4_dx_is_the_transposed_product():
     assert torch.allclose(dx, expect, rtol=1e-5, atol=1e-6)
 
 
+def test_nf4_dx_matches_the_autograd_grads():
+    """nf4_dx (the dX kernel's restatement) against the dX that
+    lora_linear_grads, pinned by central differences below, gives for the
+    same quantized layer: float64 operands, so both are the exact product
+    up to summation order; an nf4_dx with a dropped LoRA term or B and A
+    swapped fails here."""
+    N, K, r, M, s = 48, 128, 8, 7, 0.75
+    g = torch.Generator().manual_seed(13)
+    w = torch.randn(N, K, generator=g) * 0.02
+    packed, absmax = R.quantize_int4(w, 64)
+    wq = R.dequantize_int4(packed, absmax, 64)[:N * K]
+    a, b = _lora(N, K, r, 6)
+    a, b = a.double(), b.double()
+    x = torch.randn(M, K, generator=g, dtype=torch.float64)
+    dy = torch.randn(M, N, generator=g, dtype=torch.float64)
+    _, dx_auto, _, _ = R.lora_linear_grads(x, wq.double(), None, a, b, s, dy)
+    dx = R.nf4_dx(dy, packed, absmax, N, K, a, b, s, 64)
+    assert dx.dtype == torch.float64
+    assert torch.allclose(dx, dx_auto, rtol=1e-12, atol=1e-14)
+    # the base and the adapter term are both present (neither is negligible)
+    base_only = R.nf4_dx(dy, packed, absmax, N, K, None, None, 0.0, 64)
+    assert (dx - base_only).abs().max() > 1e-3 * dx.abs().max()
+
+
 def test_lora_grads_match_finite_differences():
     """Gradients of L = sum(dY * y) for y = x W^T + b + s (x A^T) B^T, by
     central differences in float64 on a tiny case."""
