@@ -4,8 +4,7 @@ F.linear (quant_ops.py:17-78, quant_linear.py:193-197) and the FP8
 _FP8LinearFunc recipe (fp8_linear.py:27-60).  Tolerance rtol = atol = 1e-2
 in the activation dtype for outputs; the FP8 quantization (codes and scale)
 and the INT8 weight operand are bit-exact.  Full Llama-3-70B MLP shapes
-(K=8192, N=28672) are checked on a seeded sample of output rows and
-columns, which the oracle computes from the selected weight rows only."""
+(K=8192, N=28672) are checked on every output element."""
 import pytest
 import torch
 
@@ -46,11 +45,8 @@ def test_int8_row_absmax_llama70b_mlp(dev, M):
     q, s = quantize_int8(w, per_channel=True)
     x = _x(M, K, torch.bfloat16, seed=M)
     y = ops.int8_linear(x.to(dev), q, s, N, block_size=0)
-    g = torch.Generator().manual_seed(M + 1)
-    rows = torch.randperm(M, generator=g)[:16]
-    cols = torch.cat([torch.randperm(N, generator=g)[:256], torch.tensor([0, N - 1])])
-    ref = R.int8_linear(x[rows], q[cols].cpu(), s[cols].cpu())
-    _check(y.cpu()[rows][:, cols], ref)
+    ref = R.int8_linear(x, q.cpu(), s.cpu())
+    _check(y.cpu(), ref)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
@@ -126,15 +122,12 @@ def test_fp8_llama70b_mlp(dev, M):
     wc, ws = ops.fp8_quantize(w.to(dev))
     x = _x(M, K, torch.bfloat16, seed=31 + M)
     y = ops.fp8_linear(x.to(dev), wc, ws)
-    # the oracle's recipe on the sampled output block
+    # the oracle's recipe on the whole output
     x8, xs = R.fp8_quantize_tensor(x)
     w8, wsr = R.fp8_quantize_tensor(w)
     assert float(ws) == float(wsr)
-    g = torch.Generator().manual_seed(M + 2)
-    rows = torch.randperm(M, generator=g)[:16]
-    cols = torch.cat([torch.randperm(N, generator=g)[:256], torch.tensor([0, N - 1])])
-    ref = ((x8[rows].to(torch.float32) * xs) @ (w8[cols].to(torch.float32) * wsr).T).to(torch.bfloat16)
-    _check(y.cpu()[rows][:, cols], ref)
+    ref = ((x8.to(torch.float32) * xs) @ (w8.to(torch.float32) * wsr).T).to(torch.bfloat16)
+    _check(y.cpu(), ref)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

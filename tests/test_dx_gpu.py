@@ -2,8 +2,8 @@
 HIP MFMA kernel through the C ABI vs the oracle's restatement of
 _FusedNF4MatmulFunc.backward (dequant_matmul.py:338-351) plus the adapter's
 input gradient (lora_layer.py:67 differentiated), on the same seeded inputs.
-Tolerance rtol = atol = 1e-2 in dY's dtype.  Output rows are independent, so
-the full-size Llama-3-8B cases check a seeded sample of rows."""
+Tolerance rtol = atol = 1e-2 in dY's dtype.  The full-size Llama-3-8B cases
+check every output element."""
 import math
 
 import pytest
@@ -37,13 +37,6 @@ def _check(got, ref):
     assert not bad.any(), f"{int(bad.sum())} of {bad.numel()} outside tol; max err {float(err.max()):.4g}"
 
 
-def _sample_rows(M, n, seed):
-    g = torch.Generator().manual_seed(seed)
-    rows = torch.randperm(M, generator=g)[:n]
-    edge = torch.tensor([0, 255, 256, M - 1])
-    return torch.unique(torch.cat([rows, edge[edge < M]]))
-
-
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)])
 def test_dx_llama3_shapes_bf16(dev, K, N):
     """Config: training backward dX, M=2048 bf16, dY ~ N(0, 1e-2), LoRA r=64 alpha=16."""
@@ -53,9 +46,8 @@ def test_dx_llama3_shapes_bf16(dev, K, N):
     packed, absmax = quantize_int4(w.to(dev), 64)
     dx = ops.nf4_linear_dx(dy.to(dev), packed, absmax, K, 64, lora_a=a.to(dev), lora_b=b.to(dev),
                            scaling=16.0 / rank)
-    rows = _sample_rows(M, 48, K * N + 1)
-    ref = R.nf4_dx(dy[rows], packed.cpu(), absmax.cpu(), N, K, a, b, 16.0 / rank, 64)
-    _check(dx.cpu()[rows], ref)
+    ref = R.nf4_dx(dy, packed.cpu(), absmax.cpu(), N, K, a, b, 16.0 / rank, 64)
+    _check(dx.cpu(), ref)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

@@ -2,9 +2,8 @@
 MFMA kernel through the C ABI vs the oracle's restatement of
 QuantLinear.forward + LoRALinear.forward (quant_linear.py:182-197,
 lora_layer.py:60-70) on the same seeded inputs.  Tolerance rtol = atol = 1e-2
-in the activation dtype.  Output rows are independent, so the full-size
-Llama-3-8B cases run the whole GEMM on the GPU and check a seeded sample of
-rows (always including the first and last tile rows) against the oracle."""
+in the activation dtype.  The full-size Llama-3-8B cases check every output
+element against the oracle."""
 import math
 
 import pytest
@@ -39,13 +38,6 @@ def _check(got, ref):
     assert not bad.any(), f"{int(bad.sum())} of {bad.numel()} outside tol; max err {float(err.max()):.4g}"
 
 
-def _sample_rows(M, n, seed):
-    g = torch.Generator().manual_seed(seed)
-    rows = torch.randperm(M, generator=g)[:n]
-    edge = torch.tensor([0, 255, 256, M - 1])
-    return torch.unique(torch.cat([rows, edge[edge < M]]))
-
-
 @pytest.mark.parametrize("K,N", [(4096, 4096), (4096, 1024), (4096, 14336), (14336, 4096)])
 def test_gemm_llama3_shapes_bf16(dev, K, N):
     """Config: prefill dequant-GEMM, M=2048 bf16 tokens, LoRA r=64 alpha=16 fused."""
@@ -55,9 +47,8 @@ def test_gemm_llama3_shapes_bf16(dev, K, N):
     packed, absmax = quantize_int4(w.to(dev), 64)
     y = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=a.to(dev), lora_b=b.to(dev),
                        scaling=16.0 / rank)
-    rows = _sample_rows(M, 60, K * N)
-    ref = R.nf4_lora_linear(x[rows], packed.cpu(), absmax.cpu(), None, a, b, 16.0 / rank, N, 64)
-    _check(y.cpu()[rows], ref)
+    ref = R.nf4_lora_linear(x, packed.cpu(), absmax.cpu(), None, a, b, 16.0 / rank, N, 64)
+    _check(y.cpu(), ref)
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

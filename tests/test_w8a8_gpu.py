@@ -6,8 +6,8 @@ recipe is quantize_int8's per-row one (quant_ops.py:29-35) in fp32.
 
 Everything here is integer arithmetic plus a fixed chain of fp32 roundings,
 so the bar is bit-exact: codes, scales and outputs.  Full Llama-3-70B MLP
-shapes (K=8192, N=28672) are checked on seeded samples of output rows and
-columns (rows are independent: each is quantized on its own)."""
+shapes (K=8192, N=28672) are checked on every column of seeded output rows
+(rows are independent: each is quantized on its own)."""
 import pytest
 import torch
 
@@ -79,7 +79,7 @@ def test_w8a8_linear_bit_exact(dev, dtype, M, N, K):
 
 
 @pytest.mark.parametrize("M", [1, 512, 4096])
-def test_w8a8_llama70b_mlp_sampled(dev, M):
+def test_w8a8_llama70b_mlp_rows(dev, M):
     """K=8192, N=28672, weights N(0,0.02) per-row int8 (bf16 scales, as
     quantize_int8 returns them for a bf16 weight), bf16 x N(0,1)."""
     K, N = 8192, 28672
@@ -88,11 +88,12 @@ def test_w8a8_llama70b_mlp_sampled(dev, M):
     q, s = quantize_int8(w, per_channel=True)
     x = _x(M, K, torch.bfloat16, seed=M)
     y = ops.int8_linear_w8a8(x.to(dev), q, s).cpu()
+    # every column of 64 seeded rows (the first and last included): the
+    # oracle's exact integer sums run in float64 on the CPU
     g = torch.Generator().manual_seed(M + 1)
-    rows = torch.randperm(M, generator=g)[:16]
-    cols = torch.cat([torch.randperm(N, generator=g)[:512], torch.tensor([0, N - 1])])
-    want = R.w8a8_linear(x[rows], q[cols].cpu(), s[cols].cpu())
-    _equal(y[rows][:, cols], want, f"M={M}")
+    rows = torch.unique(torch.cat([torch.randperm(M, generator=g)[:64], torch.tensor([0, M - 1])]))
+    want = R.w8a8_linear(x[rows], q.cpu(), s.cpu())
+    _equal(y[rows], want, f"M={M}")
 
 
 def test_w8a8_close_to_w8a16(dev):
