@@ -932,40 +932,71 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
 }
 
 // Split-K finisher (and the LoRA epilogue for any M): y = finish(sum_s
-// ws[s]).  One thread per output (row blockIdx.y, column n): the bias, the
-// LoRA B row and the first splits' partials are all requested before any is
-// used, so a launch costs about one memory round trip (a thread per column
-// walking 16 rows took one round trip per row).  The sums keep their order:
-// splits ascending, ranks ascending.
+// ws[s]).  One thread per output (row blockIdx.y, column n).  Every load a
+// thread needs -- the bias, its splits' partials (up to 8), its LoRA B row
+// (up to 16 ranks) and, in threads j < rank, the 16 first u partials of rank
+// j -- is requested before any of them is used, so a launch costs about one
+// memory round trip.  The sums keep their order: splits ascending, ranks
+// ascending.
 template <int XT>
 __global__ __launch_bounds__(256) void splitk_epilogue_kernel(const float* __restrict__ ws, int S, int64_t M,
                                                               int64_t N, LinearEpi e) {
   extern __shared__ float us[];  // RND(u) of this row, [rank]
   const int64_t m = blockIdx.y;
-  stage_u<XT>(e, M, m, 1, us, threadIdx.x, blockDim.x);
-  __syncthreads();
-  const int64_t n = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  if (n >= N) return;
+  const int tid = threadIdx.x;
+  const int64_t n0 = int64_t(blockIdx.x) * 256 + tid;
+  const bool live = n0 < N;
+  const int64_t n = live ? n0 : N - 1;  // a thread past N loads (and discards) the last column's operands
   const bool has_bias = e.bias != nullptr;
   const Raw16x2 br = load_raw(has_bias ? e.bias : ws, has_bias ? n : 0, has_bias ? e.bias_dt : RQ_DTYPE_F32);
-  float v = 0.0f;
-  for (int s0 = 0; s0 < S; s0 += 8) {
-    float p[8];
+  float p[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) p[k] = (s0 + k < S) ? ws[(int64_t(s0 + k) * M + m) * N + n] : 0.0f;
+  for (int k = 0; k < 8; ++k) p[k] = ws[(int64_t(k < S ? k : 0) * M + m) * N + n];
+  const int rb = e.rank < 16 ? e.rank : 16;
+  Raw16x2 b[16];
+  if (rb > 0) {
+#pragma unroll
+    for (int jj = 0; jj < 16; ++jj) b[jj] = load_raw(e.lora_b, n * e.ld_lora_b + (jj < rb ? jj : 0), e.lora_dt);
+  }
+  // u[m, j] for j = tid < rank: the u_splits partials in order, 16 requested at once
+  if (tid < e.rank) {
+    float q[16];
+    float sum = 0.0f;
+    for (int k0 = 0; k0 < e.u_splits; k0 += 16) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) q[k] = e.u[(int64_t(k0 + k < e.u_splits ? k0 + k : k0) * M + m) * e.rank + tid];
+#pragma unroll
+      for (int k = 0; k < 16; ++k)
+        if (k0 + k < e.u_splits) sum = __fadd_rn(sum, q[k]);
+    }
+    us[tid] = round_x<XT>(sum);
+  }
+  __syncthreads();
+  if (!live) return;
+  float v = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < S) v = __fadd_rn(v, p[k]);
+  for (int s0 = 8; s0 < S; s0 += 8) {
+    float p2[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) p2[k] = (s0 + k < S) ? ws[(int64_t(s0 + k) * M + m) * N + n] : 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-      if (s0 + k < S) v = __fadd_rn(v, p[k]);
+      if (s0 + k < S) v = __fadd_rn(v, p2[k]);
   }
   float lsum = 0.0f;
-  for (int j0 = 0; j0 < e.rank; j0 += 8) {
-    Raw16x2 b[8];
+#pragma unroll
+  for (int jj = 0; jj < 16; ++jj)
+    if (jj < rb) lsum = __fmaf_rn(us[jj], round_x<XT>(raw_to_f32(b[jj], e.lora_dt)), lsum);
+  for (int j0 = 16; j0 < e.rank; j0 += 8) {
+    Raw16x2 b2[8];
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj)
-      b[jj] = load_raw(e.lora_b, n * e.ld_lora_b + (j0 + jj < e.rank ? j0 + jj : 0), e.lora_dt);
+      b2[jj] = load_raw(e.lora_b, n * e.ld_lora_b + (j0 + jj < e.rank ? j0 + jj : 0), e.lora_dt);
 #pragma unroll
     for (int jj = 0; jj < 8; ++jj)
-      if (j0 + jj < e.rank) lsum = __fmaf_rn(us[j0 + jj], round_x<XT>(raw_to_f32(b[jj], e.lora_dt)), lsum);
+      if (j0 + jj < e.rank) lsum = __fmaf_rn(us[j0 + jj], round_x<XT>(raw_to_f32(b2[jj], e.lora_dt)), lsum);
   }
   if (has_bias) v = __fadd_rn(v, round_x<XT>(raw_to_f32(br, e.bias_dt)));
   v = round_x<XT>(v);
