@@ -111,7 +111,8 @@ struct GemvArgs {
   // LoRA down-projection inside this launch (jobs > 0): job b computes the
   // fp32 partials of ranks [16 (b / u_splits), +16) over K split
   // b % u_splits, one wave per job (wave b / G of workgroup b % G, G the
-  // workgroups), into region P [u_splits][M][rank] of parts, P = bit 0 of
+  // workgroups, counted from the last wave when the last waves have fewer
+  // units), into region P [u_splits][M][rank] of parts, P = bit 0 of
   // state[0] as read at the launch's start, +0.0 stored as -0.0 so that 0
   // means "not written yet"; after its units every workgroup polls the
   // partials until none is 0.  No workgroup waits on a count at its end:
@@ -589,7 +590,11 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   // out before the unit loads, so that waiting for them never waits for the
   // weights
   const int ns = e.u_splits;
-  const int job = wave * int(G) + int(g);
+  // jobs go to the waves with the fewest units: the last waves when some
+  // waves have one unit fewer (or none), else the first (the oldest wave of
+  // a SIMD finishes its units first)
+  const bool light_top = XM == 1 ? (TS * nseg) % kGemvWaves != 0 : (kGemvWaves / nseg) * nseg < kGemvWaves;
+  const int job = (light_top ? kGemvWaves - 1 - wave : wave) * int(G) + int(g);
   const bool has_job = fused && job < a.jobs;
   // this launch's partial region and the other region's extent, loaded by
   // wave 0 (which passes the parity on through LDS) and the job waves (the
