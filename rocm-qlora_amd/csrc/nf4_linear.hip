@@ -111,10 +111,10 @@ struct GemvArgs {
   // LoRA down-projection inside this launch (jobs > 0): job b computes the
   // fp32 partials of ranks [16 (b / u_splits), +16) over K split
   // b % u_splits, one wave per job (wave b / G of workgroup b % G, G the
-  // workgroups, counted from the last wave when the last waves have fewer
-  // units), into region P [u_splits][M][rank] of parts, P = bit 0 of
-  // state[0] as read at the launch's start, +0.0 stored as -0.0 so that 0
-  // means "not written yet"; after its units every workgroup polls the
+  // workgroups, waves counted from the last when the last waves have fewer
+  // units, else from wave 1), into region P [u_splits][M][rank] of parts,
+  // P = bit 0 of state[0] as read at the launch's start, +0.0 stored as -0.0
+  // so that 0 means "not written yet"; after its units every workgroup polls the
   // partials until none is 0.  No workgroup waits on a count at its end:
   // region P is zero at the start of every launch (but for partials the
   // launch itself writes), and the other region holds the previous launch's
@@ -591,10 +591,11 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   // weights
   const int ns = e.u_splits;
   // jobs go to the waves with the fewest units: the last waves when some
-  // waves have one unit fewer (or none), else the first (the oldest wave of
-  // a SIMD finishes its units first)
+  // waves have one unit fewer (or none), else from wave 1 on, so that wave
+  // 0, which polls the partials, reaches its poll as early as it can (the
+  // oldest wave of a SIMD finishes its units first)
   const bool light_top = XM == 1 ? (TS * nseg) % kGemvWaves != 0 : (kGemvWaves / nseg) * nseg < kGemvWaves;
-  const int job = (light_top ? kGemvWaves - 1 - wave : wave) * int(G) + int(g);
+  const int job = (light_top ? kGemvWaves - 1 - wave : (wave + kGemvWaves - 1) % kGemvWaves) * int(G) + int(g);
   const bool has_job = fused && job < a.jobs;
   // this launch's partial region and the other region's extent, loaded by
   // wave 0 (which passes the parity on through LDS) and the job waves (the
