@@ -944,7 +944,9 @@ def main():
             ops.nf4_linear(x_roof, packed, absmax, N, BLOCK)
 
     rg = _capture(roof_pass, stream)
-    reps = 10
+    # 150 replays (1800 launches): single batches of a few replays vary by
+    # +-5 % from one to the next on the same machine
+    reps = 150
     with _Range(f"rq-roofline nf4_gemv_kernel M={M} K={K} N={N}"):
         us_launch = _time_graph(rg, reps) * 1e3 / len(roof_w)
     kb = kernel_bytes(M, N, K)
