@@ -710,21 +710,25 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   };
   const uint32_t bbytes = e.lora_dt == RQ_DTYPE_F32 ? 4u : 2u;
   // LoRA B rows as 16-byte chunks (the host fuses LoRA only for such rows):
-  // thread tid < TS * 16 * 2^cl takes chunk tid % 2^cl of row (tid >> cl) % 16
-  // of tile slot tid >> (4 + cl)
+  // thread et < TS * 16 * 2^cl takes chunk et % 2^cl of row (et >> cl) % 16
+  // of tile slot et >> (4 + cl), and the bias loads go to wave ew = 0, where
+  // et and ew count threads and waves from the last when every wave has one
+  // unit (so that wave 0, which polls the partials, has no epilogue loads
+  // ahead of its poll), else from the first
   const int cl = rank > 0 ? a.bvec_log2 : 0;
-  const int bt = tid >> (4 + cl), br_row = (tid >> cl) & 15, bc = tid & ((1 << cl) - 1);
-  const bool bvec_live = rank > 0 && tid < (TS * 16 << cl);
-  if (rank > 0 && wave * 64 < (TS * 16 << cl)) {
+  const int et = U == 1 ? kGemvThreads - 1 - tid : tid, ew = U == 1 ? kGemvWaves - 1 - wave : wave;
+  const int bt = et >> (4 + cl), br_row = (et >> cl) & 15, bc = et & ((1 << cl) - 1);
+  const bool bvec_live = rank > 0 && et < (TS * 16 << cl);
+  if (rank > 0 && ew * 64 < (TS * 16 << cl)) {
     const __amdgpu_buffer_rsrc_t bres = buffer_rsrc(e.lora_b, uint32_t(a.N) * uint32_t(e.ld_lora_b) * bbytes);
     const uint32_t bn = tile_of(bt) * 16u + uint32_t(br_row);
     const bool live = bvec_live && bn < uint32_t(a.N);
     bvr = buf_load16(bres, live ? bn * uint32_t(e.ld_lora_b) * bbytes + 16u * uint32_t(bc) : kOobOffset);
   }
   const bool has_bias = a.direct && e.bias != nullptr;
-  if (has_bias && wave == 0) {
+  if (has_bias && ew == 0) {
     const __amdgpu_buffer_rsrc_t bres = buffer_rsrc(e.bias, uint32_t(a.N) * (e.bias_dt == RQ_DTYPE_F32 ? 4u : 2u));
-    const int cb = tid & (kGemvMaxTS * 16 - 1);
+    const int cb = et & (kGemvMaxTS * 16 - 1);
     const uint32_t cn = tile_of(cb >> 4) * 16u + uint32_t(cb & 15);
     br = buf_load_elem(bres, cn, (cb >> 4) < TS && cn < uint32_t(a.N), e.bias_dt);
   }
@@ -855,7 +859,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
       }
     }
   }
-  if (a.direct && tid < TS * 16) bss[tid] = has_bias ? round_x<XT>(elem_to_f32(br, e.bias_dt)) : 0.0f;
+  if (a.direct && et < TS * 16) bss[et] = has_bias ? round_x<XT>(elem_to_f32(br, e.bias_dt)) : 0.0f;
   if (rank > 0) {
     // u[m, j]: each thread sums its 16 splits in order, then lane c = 0 of
     // the (m, j) adds the C threads' sums in c order (adjacent lanes of one
