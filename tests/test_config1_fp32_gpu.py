@@ -51,7 +51,7 @@ def _layer(dev, seed, bias):
 
 
 @pytest.mark.parametrize("bias", [False, True])
-@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 16])
 def test_config1_fp32_lora_linear(dev, M, bias):
     print(f"config 1 fp32 M={M} bias={bias}", flush=True)
     ql, lora = _layer(dev, seed=1 + M, bias=bias)
@@ -66,11 +66,12 @@ def test_config1_fp32_lora_linear(dev, M, bias):
     _check(y, ref)
 
 
-@pytest.mark.parametrize("M", [1, 16, 37])
+@pytest.mark.parametrize("M", [1, 3, 16, 35, 37])
 def test_fp32_base_and_double_quant(dev, M):
     """The base layer alone (no adapter) and after enable_double_quant
-    (double_quant.py:160-200), against dequantize -> F.linear in fp32; M = 37
-    runs as 16-row blocks."""
+    (double_quant.py:160-200), against dequantize -> F.linear in fp32; M = 35
+    and 37 run as 16-row blocks (tails of 3 and 5 rows: the vector-ALU and
+    the MFMA kernel)."""
     ql, _ = _layer(dev, seed=5, bias=True)
     x = torch.randn(M, K, generator=torch.Generator().manual_seed(7 + M))
     w32 = R.dequantize_int4(ql.weight_quant.cpu(), ql.weight_scales.cpu(), 64)
@@ -85,11 +86,12 @@ def test_fp32_base_and_double_quant(dev, M):
     _check(y2, R.quant_linear_forward(x, w2, ql.bias.cpu(), N, K))
 
 
-def test_fp32_strided_activations_and_lora_input(dev):
+@pytest.mark.parametrize("M", [2, 5])
+def test_fp32_strided_activations_and_lora_input(dev, M):
     """Activation rows with a stride, bf16 LoRA weights widened to fp32, and a
-    separate LoRA input (the dropout path) through ops.nf4_linear."""
+    separate LoRA input (the dropout path) through ops.nf4_linear (M = 2: the
+    vector-ALU kernel, M = 5: the MFMA kernel)."""
     ql, lora = _layer(dev, seed=9, bias=False)
-    M = 5
     g = torch.Generator().manual_seed(3)
     big = torch.randn(M, K + 12, generator=g)
     x = big[:, 4:4 + K]
