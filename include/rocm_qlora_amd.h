@@ -200,12 +200,13 @@ int rq_nf4_linear_noalloc(const void* x, int x_dtype, int64_t M, int64_t K, int6
                           int64_t ld_lora_b, int lora_dtype, int64_t rank, float scaling,
                           void* y, int64_t ldy, hipStream_t stream);
 
-/* Test hook, no counterpart in the reference: how many times a decode-GEMV
- * workgroup polls for the workgroups that compute the LoRA down-projection
- * inside the same launch before it computes the down-projection itself
- * (the same sums in the same order).  0 forces that path.  Returns the
+/* Test hook, no counterpart in the reference: how long (microseconds, timed
+ * on the device's constant-rate real-time counter) a decode-GEMV workgroup
+ * polls for the workgroups that compute the LoRA down-projection inside the
+ * same launch before it computes the down-projection itself (the same sums
+ * in the same order).  0 forces that path; the default is 40.  Returns the
  * previous value. */
-uint32_t rq_set_gemv_spin_limit(uint32_t polls);
+uint32_t rq_set_gemv_wait_us(uint32_t us);
 
 /* Tile configuration of the MFMA GEMM behind rq_nf4_linear (M > 16),
  * rq_nf4_linear_dx and rq_int8_linear: out[0..4] = rows and

@@ -127,7 +127,7 @@ struct GemvArgs {
   // that starts later (the device shared with other work) finds no partials
   // and computes u itself.
   int jobs;
-  uint32_t spin_limit;     // polls before a workgroup computes u itself
+  uint32_t wait_ticks;     // real-time ticks a workgroup waits before it computes u itself
   uint32_t* jc;            // jobs done (zero between launches)
   uint32_t* state;         // parity of the next launch's region, extents of regions 0 and 1
   uint32_t* parts;         // two regions of kGemvPartWords: partials as fp32 bits
@@ -352,12 +352,15 @@ __device__ __forceinline__ f32x4 gemv_tile(const GemvUnit<Scale>& U, float s1, f
 // global load, which would serialize the prefetched units.)
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Polls of the LoRA partials before a workgroup gives up waiting for the
-// other workgroups' jobs and computes u itself.  A job runs before its
-// wave's units and never waits, so every job ends once its workgroup has
-// been dispatched; the bound keeps the wait finite when the device is
-// shared with other work (a workgroup still waiting for a compute unit).
-constexpr uint32_t kGemvSpinLimit = 1u << 16;
+// How long (microseconds of the device's constant-rate real-time counter,
+// s_memrealtime) a workgroup polls for the LoRA partials before it gives up
+// waiting for the other workgroups' jobs and computes u itself.  A job runs
+// before its wave's units and never waits, so every job ends once its
+// workgroup has been dispatched (a few microseconds into the launch); the
+// bound keeps the wait finite when the device is shared with other work (a
+// workgroup still waiting for a compute unit).  A workgroup thus waits at
+// most this long plus one poll's round trip, and then runs every job itself.
+constexpr uint32_t kGemvDefaultWaitUs = 40;
 
 // In-launch LoRA down-projection jobs: one wave computes the 16 x 16 fp32
 // sums x[m, k] RND(A[16 p + jj, k]) (tokens m < 16, ranks 16 p + jj) over the
@@ -795,7 +798,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     const uint32_t* region = a.parts + flag[1] * uint32_t(kGemvPartWords);
     if (u_mine) {
       bool ok = false;
-      for (uint32_t i = 0; !ok && a.spin_limit > 0; ++i) {
+      auto poll = [&]() {
         // all the loads of a poll in flight together: no branch between
         // them (a split past ns reads the first again and is not checked)
 #pragma unroll
@@ -806,8 +809,19 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
         for (int k = 0; k < kUPerThread; ++k)
           missing |= uint32_t(up[k] == 0u) & uint32_t(kUPerThread * uc + k < ns);
         ok = missing == 0u;
-        if (ok || i >= a.spin_limit) break;
-        __builtin_amdgcn_s_sleep(2);
+      };
+      if (a.wait_ticks > 0) {
+        poll();
+        // the clock starts only when the first poll finds a partial missing
+        // (the common case, every partial there, reads no clock)
+        if (!ok) {
+          const uint32_t t0 = uint32_t(__builtin_amdgcn_s_memrealtime());
+          do {
+            __builtin_amdgcn_s_sleep(2);
+            poll();
+            // (unsigned difference: the counter's low word may wrap)
+          } while (!ok && uint32_t(__builtin_amdgcn_s_memrealtime()) - t0 < a.wait_ticks);
+        }
       }
       if (!ok) *flag = 1u;
     }
@@ -931,6 +945,15 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
         buffer_rsrc(a.parts + (par ^ 1u) * uint32_t(kGemvPartWords), uint32_t(kGemvPartBytes));
     for (uint32_t i = uint32_t(lane); 4u * i < other_ext; i += 64u)
       __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, other, 16u * i, 0, kCoherent);
+    // the zeros are visible device-wide before the parity flips: a
+    // workgroup of this launch that starts late reads the flipped parity
+    // and must find the region it then polls cleared, not the previous
+    // launch's partials.  The zeros are device-coherent (sc1) stores, which
+    // write through the L2 and count as done only once written, so waiting
+    // for every lane's stores orders them before the state stores; a
+    // release fence would also write back the whole L2 (buffer_wbl2),
+    // which no store here needs, for about 0.25 us per launch.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     if (lane == 0) {
       const uint32_t ext = uint32_t(ns) * uint32_t(M) * uint32_t(e.rank);
       __hip_atomic_store(&a.state[1u + par], ext, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1100,11 +1123,30 @@ __global__ __launch_bounds__(kGemvThreads) void lora_u_jobs_kernel(GemvArgs a, L
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-// The poll bound of rq_set_gemv_spin_limit (a test hook): an atomic, so
-// that setting it from one host thread while another launches is defined.
-static std::atomic<uint32_t> gemv_spin_limit{kGemvSpinLimit};
+// The wait bound of rq_set_gemv_wait_us (a test hook): an atomic, so that
+// setting it from one host thread while another launches is defined.
+static std::atomic<uint32_t> gemv_wait_us{kGemvDefaultWaitUs};
 
-uint32_t set_gemv_spin_limit(uint32_t polls) { return gemv_spin_limit.exchange(polls, std::memory_order_relaxed); }
+uint32_t set_gemv_wait_us(uint32_t us) { return gemv_wait_us.exchange(us, std::memory_order_relaxed); }
+
+// Ticks of s_memrealtime per microsecond on the current device (the
+// counter's rate is hipDeviceAttributeWallClockRate, in kHz), cached per
+// device index.
+static uint32_t realtime_ticks_per_us() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<uint32_t> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 100u;
+  uint32_t t = cache[dev].load(std::memory_order_relaxed);
+  if (t == 0u) {
+    int khz = 0;
+    t = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) == hipSuccess && khz >= 1000
+            ? uint32_t(khz / 1000)
+            : 100u;
+    cache[dev].store(t, std::memory_order_relaxed);
+  }
+  return t;
+}
 
 // Work plan of the GEMV: K splits, tiles per workgroup, units per wave, the
 // unit table, the activation stage, and the workspace layout.
@@ -1275,7 +1317,10 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.xvec = gemv_xvec(L);
   a.bvec_log2 = gemv_bvec_log2(L);
   a.jobs = p.jobs;
-  a.spin_limit = gemv_spin_limit.load(std::memory_order_relaxed);
+  {
+    const uint64_t ticks = uint64_t(gemv_wait_us.load(std::memory_order_relaxed)) * realtime_ticks_per_us();
+    a.wait_ticks = uint32_t(std::min<uint64_t>(ticks, 0xFFFFFFFFull));
+  }
   a.jc = static_cast<uint32_t*>(sync);
   a.state = static_cast<uint32_t*>(sync) + kLinearParityWord;
   a.parts = reinterpret_cast<uint32_t*>(static_cast<char*>(sync) + kLinearCountBytes);
@@ -1448,7 +1493,7 @@ static LinearArgs pack_linear_args(const void* x, int x_dtype, int64_t M, int64_
   return L;
 }
 
-extern "C" uint32_t rq_set_gemv_spin_limit(uint32_t polls) { return set_gemv_spin_limit(polls); }
+extern "C" uint32_t rq_set_gemv_wait_us(uint32_t us) { return set_gemv_wait_us(us); }
 
 extern "C" int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, int64_t N, int64_t rank,
                                             int64_t* bytes) {

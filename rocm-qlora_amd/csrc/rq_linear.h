@@ -83,10 +83,10 @@ struct GemvPlan {
 
 GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool xvec, bool gather,
                    bool lora_vec, bool lora_prod);
-// Polls of the GEMV's wait for its LoRA producers before a workgroup computes
-// the down-projection itself (a test hook: 0 forces that path).  Returns the
-// previous value.
-uint32_t set_gemv_spin_limit(uint32_t polls);
+// Microseconds the GEMV waits for its LoRA producers before a workgroup
+// computes the down-projection itself (a test hook: 0 forces that path).
+// Returns the previous value.
+uint32_t set_gemv_wait_us(uint32_t us);
 int validate_linear(const LinearArgs& L);
 LinearEpi make_epi(const LinearArgs& L, float* u_parts, int u_splits);
 int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream);

@@ -48,7 +48,7 @@ SIGNATURES = {
                               _P, _I32,                      # bias, dtype
                               _P, _I64, _P, _P, _I64, _I32, _I64, _F32,  # lora x, ld, A, B, ldB, dtype, rank, scaling
                               _P, _I64, _P],                 # y, ldy, stream
-    "rq_set_gemv_spin_limit": [ctypes.c_uint32],
+    "rq_set_gemv_wait_us": [ctypes.c_uint32],
     "rq_gemm_tile_config": [_P],
     "rq_stream_capture_id": [_P, _P],
     "rq_nf4_linear_dx_workspace_size": [_I32, _I64, _I64, _I64, _I64, _P],
@@ -81,7 +81,7 @@ SIGNATURES = {
                             _P, _I64, _P, _I64, _P],         # y, ldy, workspace, bytes, stream
 }
 _RESTYPE = {"rq_status_string": ctypes.c_char_p, "rq_build_arch": ctypes.c_char_p,
-            "rq_set_gemv_spin_limit": ctypes.c_uint32}
+            "rq_set_gemv_wait_us": ctypes.c_uint32}
 
 _lib: Optional[ctypes.CDLL] = None
 _lock = threading.Lock()
@@ -130,11 +130,11 @@ def call(name: str, *args) -> None:
         raise RuntimeError(f"{name} failed: {status_string(status)} (status {status})")
 
 
-def set_gemv_spin_limit(polls: int) -> int:
-    """Test hook: polls of the decode GEMV's wait for its in-launch LoRA
+def set_gemv_wait_us(us: int) -> int:
+    """Test hook: microseconds the decode GEMV waits for its in-launch LoRA
     down-projection before a workgroup computes it itself (0 forces that).
     Returns the previous value."""
-    return int(load().rq_set_gemv_spin_limit(polls))
+    return int(load().rq_set_gemv_wait_us(us))
 
 
 def capture_id(device: torch.device) -> int:

@@ -9,7 +9,9 @@ against the library's own other paths bit for bit:
 
 - calls in a row on one stream (the area is left ready after each);
 - the workgroups' own computation of u when the jobs' partials are not
-  awaited (polls forced to 0), which must give the same bits;
+  awaited (wait forced to 0) or awaited only briefly (a wait of a few
+  microseconds, after which some workgroups give up and others do not),
+  which must give the same bits;
 - replays of a captured HIP graph with new inputs, against eager calls;
 - operands the jobs cannot read 16 bytes at a time, which run the
   down-projection as its own kernel.
@@ -115,24 +117,49 @@ def test_mixed_shapes_share_one_workspace(dev, sync_ready):
     (2048, 768, 2, 16, torch.bfloat16),
 ])
 def test_workgroups_own_u_same_bits(dev, sync_ready, K, N, M, rank, lora_dtype):
-    """Polls forced to 0: every workgroup computes u itself, job by job as
+    """Wait forced to 0: every workgroup computes u itself, job by job as
     the job waves do, so y is bit-identical to the awaited path."""
     print(f"own-u K={K} N={N} M={M} rank={rank} {lora_dtype}", flush=True)
     packed, absmax, a, b = _layer(N, K, rank, seed=7 + K, dev=dev, lora_dtype=lora_dtype)
     x = _x(M, K, seed=3).to(dev)
     ad, bd = a.to(dev), b.to(dev)
     y0 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
-    old = nat.set_gemv_spin_limit(0)
+    old = nat.set_gemv_wait_us(0)
     try:
         y1 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
         y2 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
     finally:
-        nat.set_gemv_spin_limit(old)
+        nat.set_gemv_wait_us(old)
     y3 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
     assert torch.equal(y0, y1) and torch.equal(y0, y2) and torch.equal(y0, y3)
     _sync_words_ready(dev, sync_ready)
     ref = R.nf4_lora_linear(x.cpu(), packed.cpu(), absmax.cpu(), None, a, b, 0.5, N, 64)
     _check(y1, ref)
+
+
+@pytest.mark.parametrize("wait_us", [1, 3])
+def test_short_wait_same_bits(dev, sync_ready, wait_us):
+    """A wait bounded at a few microseconds of the device's real-time
+    counter: workgroups that give up compute u themselves, the others take
+    the jobs' partials; either way y has the same bits, over several calls
+    in a row, and the area is left ready for the default wait."""
+    K, N, M, rank = 14336, 4096, 1, 64
+    print(f"short wait {wait_us} us K={K} N={N} M={M} rank={rank}", flush=True)
+    packed, absmax, a, b = _layer(N, K, rank, seed=91, dev=dev)
+    x = _x(M, K, seed=13).to(dev)
+    ad, bd = a.to(dev), b.to(dev)
+    y0 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
+    old = nat.set_gemv_wait_us(wait_us)
+    try:
+        ys = [ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5) for _ in range(4)]
+    finally:
+        nat.set_gemv_wait_us(old)
+    y5 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=0.5)
+    for i, y in enumerate(ys + [y5]):
+        assert torch.equal(y0, y), f"call {i} after a {wait_us} us wait differs"
+    _sync_words_ready(dev, sync_ready)
+    ref = R.nf4_lora_linear(x.cpu(), packed.cpu(), absmax.cpu(), None, a, b, 0.5, N, 64)
+    _check(y5, ref)
 
 
 def test_graph_replays_match_eager(dev, sync_ready):
