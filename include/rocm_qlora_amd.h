@@ -154,13 +154,19 @@ int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, int64_t N, i
  *   y[M, N] = RND(RND(x W^T + RND(bias)) + RND(RND(RND(xl A^T) RND(B)^T) * scaling))
  * with RND the rounding to x_dtype (bf16 or fp16) and W = T[code] * scale.
  * x_dtype fp32 computes everything in fp32 as the reference's fp32 path does
- * (W = T[code] * scale rounded to fp32, no other roundings; x rows, A and the
- * packed weights 16-byte aligned, rank <= 64); its workspace holds the LoRA
- * operand u after the synchronization area.
- *   x: [M, K] rows of stride ldx; w_packed: flat N*K/2 bytes; block_size a
- *   power of two >= 64 dividing K; absmax: N*K/block_size scales of
- *   absmax_dtype, or -- when c2 != NULL -- the c2_scales of the double
- *   quantization (one per block2 codes in c2, format c2_format).
+ * (W = T[code] * scale rounded to fp32, no other roundings); its workspace
+ * holds the LoRA operand u after the synchronization area.
+ *   x: [M, K] rows of stride ldx; w_packed: the flat N*K codes, two per byte
+ *   (element 2j in the low nibble of byte j), as quantize_int4 packs the
+ *   flattened weight; block_size any (blocks run over the flat weight and may
+ *   straddle rows); absmax: ceil(N*K/block_size) scales of absmax_dtype, or --
+ *   when c2 != NULL -- the c2_scales of the double quantization (one per
+ *   block2 codes in c2, format c2_format).  Any K, block size and operand
+ *   alignment (elements aligned to their size) is taken: calls outside the
+ *   specialized kernels' shapes (K % 64 != 0, a block size that is not a
+ *   power of two >= 64 dividing K, operands they cannot read 16 bytes at a
+ *   time, fp32 activations with rank > 64) run on generic kernels with the
+ *   same roundings.
  *   bias: [N] or NULL.  LoRA (rank > 0, lora_a and lora_b non-NULL): xl
  *   (lora_x, or x when NULL) [M, K] stride ld_lora_x, A [rank, K], B [N, rank]
  *   stride ld_lora_b, both of lora_dtype.  y: [M, N] stride ldy, x_dtype.
@@ -216,7 +222,8 @@ uint32_t rq_set_gemv_wait_us(uint32_t us);
  * tiles. */
 int rq_gemm_tile_config(int32_t* out);
 
-/* Bytes of device workspace rq_nf4_linear_dx needs (0 when none). */
+/* Bytes of device workspace rq_nf4_linear_dx needs (0 when none; dy_dtype
+ * fp32, bf16 or fp16). */
 int rq_nf4_linear_dx_workspace_size(int dy_dtype, int64_t M, int64_t N, int64_t K, int64_t rank,
                                     int64_t* bytes);
 
@@ -224,12 +231,14 @@ int rq_nf4_linear_dx_workspace_size(int dy_dtype, int64_t M, int64_t N, int64_t 
  * 338-351: dX = dY . W_deq in dY's dtype) together with the adapter's input
  * gradient of LoRALinear.forward (lora_layer.py:67 differentiated):
  *   dX[M, K] = RND(RND(dY W) + RND(RND(RND(RND(dY * scaling) RND(B)) RND(A)) * d))
- * with RND the rounding to dy_dtype (bf16 or fp16), W = T[code] * scale, and
+ * with RND the rounding to dy_dtype (bf16 or fp16; fp32: none), W = T[code] * scale, and
  * d = 1, or -- with the adapter's input dropout (lora_layer.py:67's
  * self.lora_dropout(x)) -- dropout's backward d = lora_mask[m, k] ? mask_scale
  * : 0 (mask_scale = 1 / (1 - p)).
- *   dy: [M, N] rows of stride lddy (N % 64 == 0); w_packed, block_size,
- *   absmax, c2, c2_format, block2 as for rq_nf4_linear (K % 64 == 0);
+ *   dy: [M, N] rows of stride lddy; w_packed, block_size, absmax, c2,
+ *   c2_format, block2 as for rq_nf4_linear (any K and block size: shapes
+ *   outside the MFMA kernel's -- N or K not multiples of 64, other block
+ *   sizes, fp32 dy, dy rows not 16-byte aligned -- run on generic kernels);
  *   LoRA (rank > 0, lora_a and lora_b non-NULL): A [rank, K], B [N, rank]
  *   stride ld_lora_b, both of lora_dtype; lora_mask: NULL or [M, K] bytes
  *   (non-zero = kept) of row stride ld_lora_mask.  dx: [M, K] stride lddx,
@@ -251,15 +260,30 @@ int rq_nf4_linear_dx(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t
  * dequantize_int8, quant_ops.py:55-78) and the reference's native entry point
  * launch_int8_dequant_matmul (hip_kernels/int4_matmul.hip:440-458):
  *   y[M, N] = RND(x W^T + RND(bias)),  W = RND(float(q) * scale)
- *   x: [M, K] bf16/fp16 rows of stride ldx (K % 64 == 0); q: [N, K] int8;
+ *   with RND the rounding to x_dtype (fp32: none).
+ *   x: [M, K] fp32/bf16/fp16 rows of stride ldx; q: [N, K] int8;
  *   block_size 0: one scale per output row (scales [N]); otherwise blockwise
- *   over the flat weight (power of two >= 64 dividing K; scales [N*K/block]);
- *   scales of scales_dtype; bias [N] or NULL; y: [M, N] stride ldy.
- * M <= 16 runs a weight-streaming GEMV, larger M the MFMA GEMM. */
+ *   over the flat weight (scales [ceil(N*K/block)]); scales of scales_dtype;
+ *   bias [N] or NULL; y: [M, N] stride ldy.
+ * 16-bit x with K % 64 == 0, a power-of-two block >= 64 dividing K (or per
+ * row) and 16-byte aligned rows runs a weight-streaming GEMV (M <= 16) or the
+ * MFMA GEMM; every other call runs on generic kernels with the same
+ * roundings. */
 int rq_int8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                    const int8_t* q, int64_t N, int64_t block_size,
                    const void* scales, int scales_dtype, const void* bias, int bias_dtype,
                    void* y, int64_t ldy, hipStream_t stream);
+
+/* Replaces the backward of _FusedInt8MatmulFunc (kernels/dequant_matmul.py:
+ * 308-324: dX = dY . W_deq in dY's dtype):
+ *   dX[M, K] = RND(dY RND(W)),  W = float(q) * scale
+ * with RND the rounding to dy_dtype (fp32: none); dy: [M, N] fp32/bf16/fp16
+ * rows of stride lddy; q, block_size, scales, scales_dtype as for
+ * rq_int8_linear; dx: [M, K] stride lddx.  Runs on the generic kernels (the
+ * int8 codes decoded inside the multiply, MFMA for 16-bit dY). */
+int rq_int8_linear_dx(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t lddy, const int8_t* q,
+                      int64_t K, int64_t block_size, const void* scales, int scales_dtype, void* dx,
+                      int64_t lddx, hipStream_t stream);
 
 /* Bytes of workspace rq_fp8_quantize needs. */
 int rq_fp8_quantize_workspace_size(int64_t* bytes);
@@ -292,9 +316,15 @@ int rq_fp8_linear_workspace_size(int64_t M, int64_t K, int64_t* bytes);
  * codes = e4m3fnuz(RND(x / scale)) re-encoded to e4m3fn), then
  *   y = RND(RND(sum_k x8 w8 * x_scale * w_scale) + RND(bias))
  * with the fp8 products summed by the fp8 matrix cores in fp32.
- *   x: [M, K] bf16/fp16 stride ldx (K % 64 == 0); w_codes: [N, K] e4m3fn;
+ *   x: [M, K] fp32/bf16/fp16 stride ldx; w_codes: [N, K] e4m3fn;
  *   w_scale: device fp32; bias [N] or NULL; y: [M, N] stride ldy.
- * M <= 16 runs a weight-streaming GEMV, larger M the fp8 MFMA GEMM. */
+ * 16-bit x with K % 64 == 0 and 16-byte aligned rows runs a weight-streaming
+ * GEMV (M <= 16) or the fp8 MFMA GEMM.  Every other call (fp32 x among them)
+ * quantizes x to e4m3fnuz codes the same way and runs on generic kernels as
+ * the reference computes it: y = RND(RND(sum_k (x8 x_scale)(w8 w_scale)) +
+ * RND(bias)), each code decoded and multiplied by its scale in fp32 (the
+ * e4m3fn weight codes hold the reference's values but for the 8 re-encoded
+ * magnitudes below 2^-6 noted at rq_fp8_fnuz_to_e4m3fn). */
 int rq_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, int64_t ldx,
                   const uint8_t* w_codes, int64_t N, const float* w_scale,
                   const void* bias, int bias_dtype, void* y, int64_t ldy,

@@ -15,6 +15,8 @@
 // cores (fp8_mfma.hip).
 #include "rq_gemm_core.h"
 #include "rq_gemm8.h"
+#include "rq_fp8.h"
+#include "rq_generic.h"
 
 namespace rq {
 
@@ -264,16 +266,35 @@ struct ByteLinearArgs {
 
 static int validate_byte(const ByteLinearArgs& A) {
   if (!A.x || !A.w || !A.y || !A.scales) return RQ_ERR_NULL_POINTER;
-  if (A.x_dtype != RQ_DTYPE_BF16 && A.x_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
-  if (A.M < 0 || A.N <= 0 || A.K <= 0 || A.K % 64 != 0) return RQ_ERR_BAD_SHAPE;
+  if (!valid_float_dtype(A.x_dtype)) return RQ_ERR_BAD_DTYPE;
+  if (A.M < 0 || A.N <= 0 || A.K <= 0 || A.block_size < 0) return RQ_ERR_BAD_SHAPE;
   if (A.ldx < A.K || A.ldy < A.N) return RQ_ERR_BAD_SHAPE;
-  if (A.scales_dtype != RQ_DTYPE_F32 && A.scales_dtype != RQ_DTYPE_BF16 && A.scales_dtype != RQ_DTYPE_F16)
-    return RQ_ERR_BAD_DTYPE;
-  if (A.block_size != 0 && (A.block_size < 64 || (A.block_size & (A.block_size - 1)) || A.K % A.block_size))
-    return RQ_ERR_BAD_SHAPE;
-  if (!aligned(A.x, 16) || A.ldx % 8 != 0 || !aligned(A.w, 16)) return RQ_ERR_BAD_ALIGNMENT;
-  if (!offsets_fit(A.M, A.ldx, A.N, 2 * A.K)) return RQ_ERR_UNSUPPORTED;
+  if (!valid_float_dtype(A.scales_dtype)) return RQ_ERR_BAD_DTYPE;
+  if (A.bias && !valid_float_dtype(A.bias_dtype)) return RQ_ERR_BAD_DTYPE;
+  if (!aligned(A.x, dtype_size(A.x_dtype)) || !aligned(A.y, dtype_size(A.x_dtype))) return RQ_ERR_BAD_ALIGNMENT;
   return RQ_OK;
+}
+
+// Whether the byte GEMV / MFMA GEMM take the call: 16-bit activations read
+// 16 bytes at a time, K a multiple of 64, per-row scales or a power-of-two
+// block of at least 64 dividing K, 32-bit offsets.  Every other valid call
+// (fp32 activations among them) runs on the generic kernels.
+static bool byte_fast_ok(const ByteLinearArgs& A) {
+  if (A.x_dtype != RQ_DTYPE_BF16 && A.x_dtype != RQ_DTYPE_F16) return false;
+  if (A.K % 64 != 0) return false;
+  if (A.block_size != 0 && (A.block_size < 64 || (A.block_size & (A.block_size - 1)) || A.K % A.block_size))
+    return false;
+  if (!aligned(A.x, 16) || A.ldx % 8 != 0 || !aligned(A.w, 16)) return false;
+  return offsets_fit(A.M, A.ldx, A.N, 2 * A.K);
+}
+
+static GenericInt8 generic_args(const ByteLinearArgs& A) {
+  GenericInt8 g{};
+  g.x = A.x; g.x_dtype = A.x_dtype; g.M = A.M; g.K = A.K; g.N = A.N; g.ldx = A.ldx;
+  g.q = reinterpret_cast<const int8_t*>(A.w); g.block_size = A.block_size;
+  g.scales = A.scales; g.scales_dtype = A.scales_dtype;
+  g.bias = A.bias; g.bias_dtype = A.bias_dtype; g.y = A.y; g.ldy = A.ldy;
+  return g;
 }
 
 template <int XT, class Scale>
@@ -320,6 +341,7 @@ static int byte_linear(const ByteLinearArgs& A, hipStream_t stream) {
   int st = validate_byte(A);
   if (st != RQ_OK) return st;
   if (A.M == 0) return RQ_OK;
+  if (!byte_fast_ok(A)) return run_generic_int8_linear(generic_args(A), stream);
   if (A.x_dtype == RQ_DTYPE_BF16) return run_byte<RQ_DTYPE_BF16>(A, stream);
   return run_byte<RQ_DTYPE_F16>(A, stream);
 }
@@ -335,8 +357,8 @@ static int fp8_quantize_t(const void* t, int64_t rows, int64_t cols, int64_t ld,
   return rq_check_launch();
 }
 
-static int fp8_quantize(int dt, const void* t, int64_t rows, int64_t cols, int64_t ld, float* part, float* scale,
-                        uint8_t* codes, hipStream_t stream) {
+int fp8_quantize(int dt, const void* t, int64_t rows, int64_t cols, int64_t ld, float* part, float* scale,
+                 uint8_t* codes, hipStream_t stream) {
   switch (dt) {
     case RQ_DTYPE_F32: return fp8_quantize_t<RQ_DTYPE_F32>(t, rows, cols, ld, part, scale, codes, stream);
     case RQ_DTYPE_BF16: return fp8_quantize_t<RQ_DTYPE_BF16>(t, rows, cols, ld, part, scale, codes, stream);
@@ -359,6 +381,22 @@ extern "C" int rq_int8_linear(const void* x, int x_dtype, int64_t M, int64_t K, 
   A.block_size = block_size; A.scales = scales; A.scales_dtype = scales_dtype;
   A.bias = bias; A.bias_dtype = bias_dtype; A.y = y; A.ldy = ldy;
   return rq::byte_linear(A, stream);
+}
+
+extern "C" int rq_int8_linear_dx(const void* dy, int dy_dtype, int64_t M, int64_t N, int64_t lddy, const int8_t* q,
+                                 int64_t K, int64_t block_size, const void* scales, int scales_dtype, void* dx,
+                                 int64_t lddx, hipStream_t stream) {
+  if (!dy || !q || !scales || !dx) return RQ_ERR_NULL_POINTER;
+  if (!rq::valid_float_dtype(dy_dtype) || !rq::valid_float_dtype(scales_dtype)) return RQ_ERR_BAD_DTYPE;
+  if (M < 0 || N <= 0 || K <= 0 || block_size < 0 || lddy < N || lddx < K) return RQ_ERR_BAD_SHAPE;
+  if (!rq::aligned(dy, rq::dtype_size(dy_dtype)) || !rq::aligned(dx, rq::dtype_size(dy_dtype)))
+    return RQ_ERR_BAD_ALIGNMENT;
+  if (M == 0) return RQ_OK;
+  rq::GenericInt8 g{};
+  g.x = dy; g.x_dtype = dy_dtype; g.M = M; g.K = K; g.N = N; g.ldx = lddy;
+  g.q = q; g.block_size = block_size; g.scales = scales; g.scales_dtype = scales_dtype;
+  g.y = dx; g.ldy = lddx;
+  return rq::run_generic_int8_dx(g, stream);
 }
 
 extern "C" int rq_fp8_quantize_workspace_size(int64_t* bytes) {

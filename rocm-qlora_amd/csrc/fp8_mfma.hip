@@ -25,6 +25,7 @@
 // The GEMV and GEMM are templates on the operand policy: Fp8Mma here, I8Mma
 // for the W8A8 int8 mode (int8 activations quantized per row, int32 sums).
 #include "rq_fp8.h"
+#include "rq_generic.h"
 #include "rq_gemm_core.h"
 
 namespace rq {
@@ -738,16 +739,32 @@ extern "C" int rq_fp8_linear(const void* x, int x_dtype, int64_t M, int64_t K, i
                              int64_t N, const float* w_scale, const void* bias, int bias_dtype, void* y, int64_t ldy,
                              void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   if (!x || !w_codes || !w_scale || !y) return RQ_ERR_NULL_POINTER;
-  if (x_dtype != RQ_DTYPE_BF16 && x_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
+  if (!rq::valid_float_dtype(x_dtype)) return RQ_ERR_BAD_DTYPE;
   if (bias && !rq::valid_float_dtype(bias_dtype)) return RQ_ERR_BAD_DTYPE;
-  if (M < 0 || N <= 0 || K <= 0 || K % 64 != 0 || ldx < K || ldy < N) return RQ_ERR_BAD_SHAPE;
-  if (!rq::aligned(x, 16) || ldx % 8 != 0 || !rq::aligned(w_codes, 16)) return RQ_ERR_BAD_ALIGNMENT;
-  // the GEMM addresses both code matrices with 32-bit byte offsets
-  if (double(M) * double(K) >= 4294967296.0 || double(N) * double(K) >= 4294967296.0) return RQ_ERR_UNSUPPORTED;
+  if (M < 0 || N <= 0 || K <= 0 || ldx < K || ldy < N) return RQ_ERR_BAD_SHAPE;
+  if (!rq::aligned(x, rq::dtype_size(x_dtype)) || !rq::aligned(y, rq::dtype_size(x_dtype)))
+    return RQ_ERR_BAD_ALIGNMENT;
   if (M == 0) return RQ_OK;
   if (!workspace) return RQ_ERR_NULL_POINTER;
   if (workspace_bytes < int64_t(rq::fp8_act_ws_bytes(M, K))) return RQ_ERR_WORKSPACE;
   if (!rq::aligned(workspace, 256)) return RQ_ERR_BAD_ALIGNMENT;
+  // the fp8 matrix cores take 16-bit activations read 16 bytes at a time, K a
+  // multiple of 64 and code matrices within 32-bit byte offsets; every other
+  // call (fp32 activations among them) quantizes x the same way and runs on
+  // the generic kernels, which decode both code matrices and sum the fp32
+  // products (fp8_linear.py:44-52)
+  const bool fast = x_dtype != RQ_DTYPE_F32 && K % 64 == 0 && rq::aligned(x, 16) && ldx % 8 == 0 &&
+                    rq::aligned(w_codes, 16) && double(M) * double(K) < 4294967296.0 &&
+                    double(N) * double(K) < 4294967296.0;
+  if (!fast) {
+    char* ws = static_cast<char*>(workspace);
+    float* part = reinterpret_cast<float*>(ws);
+    float* xs = reinterpret_cast<float*>(ws + size_t(rq::kFp8AbsmaxBlocks) * 4);
+    uint8_t* xq = reinterpret_cast<uint8_t*>(ws + size_t(rq::kFp8AbsmaxBlocks) * 4 + 256);
+    int st = rq::fp8_quantize(x_dtype, x, M, K, ldx, part, xs, xq, stream);
+    if (st != RQ_OK) return st;
+    return rq::run_generic_fp8(x_dtype, xq, xs, M, K, w_codes, w_scale, N, bias, bias_dtype, y, ldy, stream);
+  }
   rq::Fp8LinearCall c{};
   c.x = x; c.x_dtype = x_dtype; c.M = M; c.K = K; c.ldx = ldx;
   c.w = w_codes; c.N = N; c.w_scale = w_scale; c.bias = bias; c.bias_dtype = bias_dtype;

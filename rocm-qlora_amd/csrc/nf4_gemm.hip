@@ -43,6 +43,7 @@
 // k loops start staggered so that only one of them misses on each slice.
 #include "rq_gemm_core.h"
 #include "rq_gemm8.h"
+#include "rq_generic.h"
 
 namespace rq {
 
@@ -241,29 +242,46 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t
 // ---------------------------------------------------------------------------
 int validate_dx(const DxArgs& D) {
   if (!D.dy || !D.w_packed || !D.absmax || !D.dx) return RQ_ERR_NULL_POINTER;
-  if (D.dy_dtype != RQ_DTYPE_BF16 && D.dy_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
+  if (!valid_float_dtype(D.dy_dtype)) return RQ_ERR_BAD_DTYPE;
   if (D.absmax_dtype != RQ_DTYPE_F32 && D.absmax_dtype != RQ_DTYPE_BF16 && D.absmax_dtype != RQ_DTYPE_F16)
     return RQ_ERR_BAD_DTYPE;
-  if (D.M < 0 || D.N <= 0 || D.K <= 0) return RQ_ERR_BAD_SHAPE;
-  if (D.N % 64 != 0 || D.K % 64 != 0 || D.block_size < 64 || (D.block_size & (D.block_size - 1)) != 0 ||
-      D.K % D.block_size != 0)
-    return RQ_ERR_BAD_SHAPE;
+  if (D.M < 0 || D.N <= 0 || D.K <= 0 || D.block_size < 1) return RQ_ERR_BAD_SHAPE;
   if (D.lddy < D.N || D.lddx < D.K) return RQ_ERR_BAD_SHAPE;
   if (D.c2 && (D.block2 <= 0 || (D.c2_format != RQ_C2_FP8_E4M3FNUZ && D.c2_format != RQ_C2_INT8)))
     return RQ_ERR_BAD_SHAPE;
-  if (!aligned(D.dy, 16) || D.lddy % 8 != 0 || !aligned(D.w_packed, 4)) return RQ_ERR_BAD_ALIGNMENT;
-  if (!offsets_fit(D.M, D.lddy, D.N, D.K)) return RQ_ERR_UNSUPPORTED;
+  if (!aligned(D.dy, dtype_size(D.dy_dtype)) || !aligned(D.dx, dtype_size(D.dy_dtype))) return RQ_ERR_BAD_ALIGNMENT;
   if (D.rank > 0) {
     if (!D.lora_a || !D.lora_b) return RQ_ERR_NULL_POINTER;
     if (D.rank > 256 || D.ld_lora_b < D.rank) return RQ_ERR_BAD_SHAPE;
-    if (D.lora_dtype != RQ_DTYPE_F32 && D.lora_dtype != D.dy_dtype) return RQ_ERR_BAD_DTYPE;
+    // fp32 (the trainable parameters) or dY's dtype; with fp32 dY any float
+    // dtype (widened exactly, as B.to(dy.dtype) does)
+    if (D.lora_dtype != RQ_DTYPE_F32 && D.lora_dtype != D.dy_dtype &&
+        !(D.dy_dtype == RQ_DTYPE_F32 && valid_float_dtype(D.lora_dtype)))
+      return RQ_ERR_BAD_DTYPE;
     if (D.lora_mask && D.ld_lora_mask < D.K) return RQ_ERR_BAD_SHAPE;
   }
   return RQ_OK;
 }
 
+// Whether the MFMA dX kernel takes the call: 16-bit dY read 16 bytes at a
+// time, N and K multiples of 64, a power-of-two block size of at least 64
+// dividing K, 32-bit offsets; every other valid call runs on the generic
+// kernels.
+bool dx_fast_ok(const DxArgs& D) {
+  if (D.dy_dtype != RQ_DTYPE_BF16 && D.dy_dtype != RQ_DTYPE_F16) return false;
+  if (D.N % 64 != 0 || D.K % 64 != 0 || D.block_size < 64 || (D.block_size & (D.block_size - 1)) != 0 ||
+      D.K % D.block_size != 0)
+    return false;
+  if (!aligned(D.dy, 16) || D.lddy % 8 != 0 || !aligned(D.w_packed, 4)) return false;
+  return offsets_fit(D.M, D.lddy, D.N, D.K);
+}
+
 int dx_workspace(const DxArgs& D, size_t* bytes) {
-  *bytes = plan_gemm(D.M, D.K, D.N, D.rank > 0 ? D.rank : 0, device_cus()).ws_bytes;
+  // the larger of the MFMA kernel's and the generic kernels' (the operands'
+  // alignment and the block size, unknown here, decide which runs)
+  const size_t g = generic_lora_bytes(D.dy_dtype, D.M, D.rank);
+  const bool fast = D.dy_dtype != RQ_DTYPE_F32 && D.N % 64 == 0 && D.K % 64 == 0;
+  *bytes = std::max(g, fast ? plan_gemm(D.M, D.K, D.N, D.rank > 0 ? D.rank : 0, device_cus()).ws_bytes : size_t(0));
   return RQ_OK;
 }
 
@@ -271,6 +289,7 @@ int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t st
   int st = validate_dx(D);
   if (st != RQ_OK) return st;
   if (D.M == 0) return RQ_OK;
+  if (!dx_fast_ok(D)) return run_generic_nf4_dx(D, workspace, ws_bytes, stream);
   const int64_t rank = D.rank > 0 ? D.rank : 0;
   const GemmPlan p = plan_gemm(D.M, D.K, D.N, rank, device_cus());
   if (p.ws_bytes > 0 && (!workspace || ws_bytes < p.ws_bytes)) return RQ_ERR_WORKSPACE;
@@ -344,10 +363,10 @@ static rq::DxArgs pack_dx_args(const void* dy, int dy_dtype, int64_t M, int64_t 
 extern "C" int rq_nf4_linear_dx_workspace_size(int dy_dtype, int64_t M, int64_t N, int64_t K, int64_t rank,
                                                int64_t* bytes) {
   if (!bytes) return RQ_ERR_NULL_POINTER;
-  if (dy_dtype != RQ_DTYPE_BF16 && dy_dtype != RQ_DTYPE_F16) return RQ_ERR_BAD_DTYPE;
+  if (!rq::valid_float_dtype(dy_dtype)) return RQ_ERR_BAD_DTYPE;
   if (M < 0 || N <= 0 || K <= 0 || rank < 0) return RQ_ERR_BAD_SHAPE;
   rq::DxArgs D{};
-  D.M = M; D.N = N; D.K = K; D.rank = rank;
+  D.dy_dtype = dy_dtype; D.M = M; D.N = N; D.K = K; D.rank = rank;
   size_t b = 0;
   const int st = rq::dx_workspace(D, &b);
   *bytes = int64_t(b);

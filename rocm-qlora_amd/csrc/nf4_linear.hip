@@ -20,6 +20,7 @@
 #include "rq_launch.h"
 #include "rq_linear.h"
 #include "rq_linear_dev.h"
+#include "rq_generic.h"
 
 namespace rq {
 
@@ -1382,9 +1383,7 @@ int validate_linear(const LinearArgs& L) {
       !(L.x_dtype == RQ_DTYPE_F32 && valid_float_dtype(L.lora_dtype)))
     return RQ_ERR_BAD_DTYPE;
   if (L.c2 && L.c2_format != RQ_C2_FP8_E4M3FNUZ && L.c2_format != RQ_C2_INT8) return RQ_ERR_BAD_DTYPE;
-  if (L.M < 0 || L.N < 1 || L.K < 64 || L.K % 64 != 0) return RQ_ERR_BAD_SHAPE;
-  if (L.block_size < 64 || L.block_size % 64 != 0 || L.K % L.block_size != 0) return RQ_ERR_BAD_SHAPE;
-  if ((L.block_size & (L.block_size - 1)) != 0) return RQ_ERR_BAD_SHAPE;
+  if (L.M < 0 || L.N < 1 || L.K < 1 || L.block_size < 1) return RQ_ERR_BAD_SHAPE;
   if (L.c2 && L.block2 < 1) return RQ_ERR_BAD_SHAPE;
   if (L.ldx < L.K || L.ldy < L.N) return RQ_ERR_BAD_SHAPE;
   if (L.rank < 0 || L.rank > 256) return RQ_ERR_BAD_SHAPE;
@@ -1392,9 +1391,29 @@ int validate_linear(const LinearArgs& L) {
   if (L.M == 0) return RQ_OK;
   if (!L.x || !L.w_packed || !L.absmax || !L.y) return RQ_ERR_NULL_POINTER;
   if (L.rank > 0 && (!L.lora_x || !L.lora_a || !L.lora_b)) return RQ_ERR_NULL_POINTER;
-  if (!aligned(L.w_packed, 8)) return RQ_ERR_BAD_ALIGNMENT;
   if (!aligned(L.x, dtype_size(L.x_dtype)) || !aligned(L.y, dtype_size(L.x_dtype))) return RQ_ERR_BAD_ALIGNMENT;
+  if (L.rank > 0 && !aligned(L.lora_x, dtype_size(L.x_dtype))) return RQ_ERR_BAD_ALIGNMENT;
   return RQ_OK;
+}
+
+// Whether the specialized kernels take the call (the decode GEMV, the MFMA
+// GEMM, the fp32 path): K a multiple of 64, a power-of-two block size of at
+// least 64 dividing K, the operands they read 16 bytes at a time aligned,
+// offsets within their 32-bit addressing.  Every other valid call runs on
+// the generic kernels.
+bool linear_fast_ok(const LinearArgs& L) {
+  if (L.K % 64 != 0 || L.block_size < 64 || (L.block_size & (L.block_size - 1)) != 0 || L.K % L.block_size != 0)
+    return false;
+  if (!aligned(L.w_packed, 8)) return false;
+  if (L.x_dtype == RQ_DTYPE_F32)
+    return L.rank <= 64 && aligned(L.x, 16) && L.ldx % 4 == 0 && aligned(L.w_packed, 16) &&
+           (L.rank == 0 || (aligned(L.lora_x, 16) && L.ld_lora_x % 4 == 0 && aligned(L.lora_a, 16)));
+  if (L.M <= kGemvMaxM)
+    return L.N * (L.K / 2) <= int64_t(INT32_MAX) - 256 && L.K < (int64_t(1) << 27) &&
+           (L.M - 1) * L.ldx + L.K <= (int64_t(1) << 29) && (L.rank == 0 || L.N * L.ld_lora_b <= (int64_t(1) << 29));
+  return aligned(L.x, 16) && L.ldx % 8 == 0 && double(L.M) * double(L.ldx) * 2.0 < 4294967296.0 &&
+         double(L.N) * double(L.K) * 0.5 < 4294967296.0 &&
+         (L.rank == 0 || (aligned(L.lora_x, 16) && L.ld_lora_x % 8 == 0));
 }
 
 LinearEpi make_epi(const LinearArgs& L, float* u_parts, int u_splits) {
@@ -1499,18 +1518,26 @@ extern "C" int rq_nf4_linear_workspace_size(int x_dtype, int64_t M, int64_t K, i
                                             int64_t* bytes) {
   if (!bytes) return RQ_ERR_NULL_POINTER;
   if (!valid_float_dtype(x_dtype)) return RQ_ERR_BAD_DTYPE;
-  if (M < 0 || N < 1 || K < 64 || K % 64 || rank < 0 || rank > 256) return RQ_ERR_BAD_SHAPE;
-  size_t b = 0;
-  LinearArgs L{};
-  L.x_dtype = x_dtype; L.M = M; L.K = K; L.N = N; L.rank = rank;
-  if (x_dtype == RQ_DTYPE_F32) {
-    f32_linear_workspace(L, &b);
+  if (M < 0 || N < 1 || K < 1 || rank < 0 || rank > 256) return RQ_ERR_BAD_SHAPE;
+  // the larger of what the specialized kernels need (when K % 64 == 0; the
+  // block size and the operands' alignment, unknown here, decide whether
+  // they run) and what the generic kernels need
+  size_t b = rank > 0 ? kLinearSyncBytes + generic_lora_bytes(x_dtype, M, rank) : 0;
+  if (K % 64 != 0) {
     *bytes = int64_t(b);
     return RQ_OK;
   }
-  int st = M <= kGemvMaxM ? gemv_workspace(L, &b) : gemm_workspace(L, &b);
-  if (M > kGemvMaxM && b > 0) b += kLinearSyncBytes;
-  *bytes = int64_t(b);
+  size_t f = 0;
+  LinearArgs L{};
+  L.x_dtype = x_dtype; L.M = M; L.K = K; L.N = N; L.rank = rank;
+  int st = RQ_OK;
+  if (x_dtype == RQ_DTYPE_F32) {
+    f32_linear_workspace(L, &f);
+  } else {
+    st = M <= kGemvMaxM ? gemv_workspace(L, &f) : gemm_workspace(L, &f);
+    if (M > kGemvMaxM && f > 0) f += kLinearSyncBytes;
+  }
+  *bytes = int64_t(std::max(b, f));
   return st;
 }
 
@@ -1527,6 +1554,7 @@ extern "C" int rq_nf4_linear(const void* x, int x_dtype, int64_t M, int64_t K, i
   int st = validate_linear(L);
   if (st != RQ_OK || M == 0) return st;
   if (workspace_bytes < 0) return RQ_ERR_BAD_SHAPE;
+  if (!linear_fast_ok(L)) return run_generic_nf4_linear(L, workspace, size_t(workspace_bytes), stream);
   if (x_dtype == RQ_DTYPE_F32) return run_nf4_linear_f32(L, workspace, size_t(workspace_bytes), stream);
   if (M <= kGemvMaxM) return run_nf4_gemv(L, workspace, size_t(workspace_bytes), stream);
   // the GEMM's workspace follows the synchronization area, whose last
@@ -1601,7 +1629,9 @@ extern "C" int rq_nf4_linear_noalloc(const void* x, int x_dtype, int64_t M, int6
   // the smallest workspace the call runs with (the GEMM drops its K splits
   // when their partial tiles do not fit)
   int64_t need = 0;
-  if (x_dtype != RQ_DTYPE_F32 && M > kGemvMaxM) {
+  if (!linear_fast_ok(L)) {
+    need = L.rank > 0 ? int64_t(kLinearSyncBytes + generic_lora_bytes(x_dtype, M, L.rank)) : 0;
+  } else if (x_dtype != RQ_DTYPE_F32 && M > kGemvMaxM) {
     const size_t b = gemm_min_workspace(L);
     need = b > 0 ? int64_t(b + kLinearSyncBytes) : 0;
   } else {

@@ -79,5 +79,10 @@ int i8_quantize_rows(const void* x, int x_dtype, int64_t M, int64_t K, int64_t l
                      hipStream_t stream);
 int fp8_linear_run(const Fp8LinearCall& c, void* workspace, hipStream_t stream);
 int fp8_fnuz_to_fn(const uint8_t* in, int64_t n, uint8_t* out, hipStream_t stream);
+// Per-tensor FP8 quantization of a [rows, cols] tensor of dtype dt (row
+// stride ld): part holds 1024 fp32 partial maxima, scale one fp32, codes the
+// e4m3fnuz codes, dense.
+int fp8_quantize(int dt, const void* t, int64_t rows, int64_t cols, int64_t ld, float* part, float* scale,
+                 uint8_t* codes, hipStream_t stream);
 
 }  // namespace rq

@@ -88,6 +88,7 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
 // Returns the previous value.
 uint32_t set_gemv_wait_us(uint32_t us);
 int validate_linear(const LinearArgs& L);
+bool linear_fast_ok(const LinearArgs& L);
 LinearEpi make_epi(const LinearArgs& L, float* u_parts, int u_splits);
 int run_lora_u(const LinearArgs& L, int ks, float* up, hipStream_t stream);
 int gemv_workspace(const LinearArgs& L, size_t* bytes);

@@ -61,6 +61,9 @@ SIGNATURES = {
     "rq_int8_linear": [_P, _I32, _I64, _I64, _I64,           # x, dtype, M, K, ldx
                        _P, _I64, _I64, _P, _I32,             # q, N, block, scales, dtype
                        _P, _I32, _P, _I64, _P],              # bias, dtype, y, ldy, stream
+    "rq_int8_linear_dx": [_P, _I32, _I64, _I64, _I64,        # dy, dtype, M, N, lddy
+                          _P, _I64, _I64, _P, _I32,          # q, K, block, scales, dtype
+                          _P, _I64, _P],                     # dx, lddx, stream
     "rq_merge_lora": [_P, _I32, _I64, _I64, _I64,           # w, format, N, K, block
                       _P, _I32, _P, _I32, _I64,             # scales, dtype, c2, c2 format, block2
                       _P, _P, _I64, _I32, _I64, _F32,       # A, B, ldB, dtype, rank, scaling

@@ -14,7 +14,6 @@ from typing import Any, Dict, Optional, Tuple
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from rocm_qlora import ops
 from rocm_qlora import torch_ops
@@ -26,17 +25,11 @@ _FNUZ_MAX = 240.0
 
 def _fp8_forward(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor],
                  w_q: Optional[Tuple[torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
-    if x.dtype in (torch.bfloat16, torch.float16):
-        wc, ws = w_q if w_q is not None else torch_ops.call_fp8_quantize(w)
-        return torch_ops.call_fp8_linear(x, wc, ws, bias)
-    # fp32 activations: the same codes and scales from the HIP quantizer,
-    # decoded and multiplied by the library GEMM in fp32
-    x2 = x.reshape(-1, x.shape[-1])
-    xc, xs = torch_ops.call_fp8_quantize(x2)
+    # 16-bit activations run on the fp8 matrix cores; fp32 activations on the
+    # generic kernels, which decode both code matrices and sum the fp32
+    # products (fp8_linear.py:44-52)
     wc, ws = w_q if w_q is not None else torch_ops.call_fp8_quantize(w)
-    out = (xc.to(torch.float32) * xs) @ (wc.to(torch.float32) * ws).T
-    out = out.to(x.dtype).reshape(*x.shape[:-1], -1)
-    return out + bias if bias is not None else out
+    return torch_ops.call_fp8_linear(x, wc, ws, bias)
 
 
 class _FP8LinearFunc(torch.autograd.Function):
@@ -81,10 +74,8 @@ class FP8LinearWrapper(nn.Module):
                getattr(ql, "c2", ql.weight_scales).data_ptr())
         if self._cache_key != key:
             w = ql.dequantized_weight(dtype)
-            wq = None
-            if dtype != torch.float32:
-                codes, scale = ops.fp8_quantize(w)
-                wq = (ops.fp8_to_e4m3fn(codes), scale)
+            codes, scale = ops.fp8_quantize(w)
+            wq = (ops.fp8_to_e4m3fn(codes), scale)
             self._cache = (w, wq)
             self._cache_key = key
         return self._cache

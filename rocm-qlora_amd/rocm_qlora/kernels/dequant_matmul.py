@@ -7,11 +7,13 @@ term fused.  Backward returns dX only, as the reference does
 (dequant_matmul.py:338-351), plus dA / dB when LoRA adapters are passed:
 dX = dY . W_deq (+ ((dY * s) . B) . A) by the NF4 dX kernel.
 
-Shapes and dtypes the fused kernels do not take (fp32 activations, K not a
-multiple of 64, block sizes that split rows) run the same arithmetic as the
-reference's dequantize-then-F.linear path on the GPU: the weight is
-dequantized by the HIP codec kernel and multiplied by the library GEMM.
-Tensors on the CPU raise; there is no CPU path.
+Every shape, block size and activation dtype (fp32 included) runs on the
+library's HIP kernels: shapes the specialized kernels do not take (K not a
+multiple of 64, block sizes that are not powers of two >= 64 dividing K,
+unaligned rows) run on its generic kernels, which decode the weight inside
+the multiply with the same roundings as the reference's
+dequantize-then-F.linear path.  INT8 backward is dX = dY . W_deq on those
+kernels too.  Tensors on the CPU raise; there is no CPU or library path.
 """
 from __future__ import annotations
 
@@ -19,19 +21,12 @@ from dataclasses import dataclass
 from typing import Optional
 
 import torch
-import torch.nn.functional as F
 
 from rocm_qlora import _native as nat
 from rocm_qlora import torch_ops
 
-# activation dtypes of the fused forward kernels (fp32: the fp32-MFMA path)
+# activation dtypes of the HIP linear kernels
 _KERNEL_DTYPES = (torch.bfloat16, torch.float16, torch.float32)
-# ... and of the NF4 dX kernel
-_DX_DTYPES = (torch.bfloat16, torch.float16)
-
-
-def _pow2(v: int) -> bool:
-    return v > 0 and (v & (v - 1)) == 0
 
 
 @dataclass
@@ -49,17 +44,9 @@ class NF4Weight:
     blocksize_2: int = 256
     use_fp8_c2: bool = True
 
-    def _shape_ok(self) -> bool:
-        return (self.K % 64 == 0 and self.block_size >= 64 and _pow2(self.block_size)
-                and self.K % self.block_size == 0)
-
     def kernel_ok(self, dtype: torch.dtype) -> bool:
-        """The fused forward kernels take this weight and activation dtype."""
-        return dtype in _KERNEL_DTYPES and self._shape_ok()
-
-    def dx_ok(self, dtype: torch.dtype) -> bool:
-        """The NF4 dX kernel takes it (bf16/fp16, N % 64 == 0)."""
-        return dtype in _DX_DTYPES and self.kernel_ok(dtype) and self.N % 64 == 0
+        """The HIP kernels take this activation dtype (any shape)."""
+        return dtype in _KERNEL_DTYPES
 
     def dq_kwargs(self) -> dict:
         if self.c2 is None:
@@ -93,9 +80,8 @@ class Int8Weight:
     block_size: int = 64
 
     def kernel_ok(self, dtype: torch.dtype) -> bool:
-        b = self.block_size
-        return (dtype in _DX_DTYPES and self.K % 64 == 0
-                and (b == 0 or (b >= 64 and _pow2(b) and self.K % b == 0)))
+        """The HIP kernels take this activation dtype (any shape)."""
+        return dtype in _KERNEL_DTYPES
 
     def dense(self, dtype: torch.dtype) -> torch.Tensor:
         """[N, K] dequantized weight (dequantize_int8, quant_ops.py:55-78), cast."""
@@ -152,17 +138,9 @@ class _FusedNF4LinearFunc(torch.autograd.Function):
         need_x, need_a, need_b = ctx.needs_input_grad[:3]
         dx = da = db = None
         if need_x:
-            if w.dx_ok(dy.dtype):
-                dx = torch_ops.call_nf4_linear_dx(dy, w.packed, w.scales, w.K, w.block_size,
-                                                  lora_a=A, lora_b=B, scaling=s, lora_mask=mask,
-                                                  mask_scale=ctx.mask_scale, **w.dq_kwargs())
-            else:
-                dx = dy @ w.dense(dy.dtype)
-                if ctx.lora:
-                    dl = ((dy * s) @ B.to(dy.dtype)) @ A.to(dy.dtype)
-                    if mask is not None:
-                        dl = torch.ops.aten.native_dropout_backward(dl, mask, ctx.mask_scale)
-                    dx = dx + dl
+            dx = torch_ops.call_nf4_linear_dx(dy, w.packed, w.scales, w.K, w.block_size,
+                                              lora_a=A, lora_b=B, scaling=s, lora_mask=mask,
+                                              mask_scale=ctx.mask_scale, **w.dq_kwargs())
         if ctx.lora and (need_a or need_b):
             # lora_out = ((xl A^T) B^T) * s in x's dtype, xl = drop(x) or x:
             # dv = dY * s, dB = dv^T (xl A^T), dA = (dv B)^T xl, cast to the
@@ -180,7 +158,7 @@ class _FusedNF4LinearFunc(torch.autograd.Function):
 
 class _FusedInt8LinearFunc(torch.autograd.Function):
     """y = x . (q * s)^T + bias by the HIP int8 kernels; backward dX =
-    dY . W_deq (dequantize kernel + library GEMM, as dequant_matmul.py:308-319)."""
+    dY . RND(W_deq) (dequant_matmul.py:308-324) by the HIP int8 dX kernel."""
 
     @staticmethod
     def forward(ctx, x, bias, w: Int8Weight):
@@ -191,35 +169,30 @@ class _FusedInt8LinearFunc(torch.autograd.Function):
     def backward(ctx, dy):
         if not ctx.needs_input_grad[0]:
             return None, None, None
-        return dy @ ctx.w.dense(dy.dtype), None, None
+        w: Int8Weight = ctx.w
+        return torch_ops.call_int8_linear_dx(dy, w.q, w.scales, w.K, w.block_size), None, None
 
 
 def nf4_linear(x: torch.Tensor, w: NF4Weight, bias: Optional[torch.Tensor] = None,
                lora_a: Optional[torch.Tensor] = None, lora_b: Optional[torch.Tensor] = None,
                scaling: float = 0.0, dropout_p: float = 0.0) -> torch.Tensor:
     """Autograd-aware NF4 linear (+ LoRA, its input through dropout of
-    probability dropout_p when > 0): fused HIP kernels where they apply,
-    otherwise the HIP dequantizer followed by the library GEMM."""
+    probability dropout_p when > 0) on the HIP kernels."""
     nat.require_gpu(x, w.packed)
+    if not w.kernel_ok(x.dtype):
+        raise TypeError(f"NF4 linear takes fp32/bf16/fp16 activations, got {x.dtype}")
     # the reference adds bias.to(x.dtype) (quant_linear.py:196)
     bias = bias.to(x.dtype) if bias is not None else None
-    if w.kernel_ok(x.dtype):
-        return _FusedNF4LinearFunc.apply(x, lora_a, lora_b, bias, w, scaling, float(dropout_p))
-    y = F.linear(x, w.dense(x.dtype), bias)
-    if _lora_present(lora_a, lora_b):
-        xl = F.dropout(x, dropout_p, True) if dropout_p > 0.0 else x
-        y = y + _lora_term(xl, lora_a, lora_b, scaling).to(y.dtype)
-    return y
+    return _FusedNF4LinearFunc.apply(x, lora_a, lora_b, bias, w, scaling, float(dropout_p))
 
 
 def int8_linear(x: torch.Tensor, w: Int8Weight, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Autograd-aware INT8 linear: fused HIP kernels where they apply,
-    otherwise the HIP dequantizer followed by the library GEMM."""
+    """Autograd-aware INT8 linear on the HIP kernels."""
     nat.require_gpu(x, w.q)
+    if not w.kernel_ok(x.dtype):
+        raise TypeError(f"INT8 linear takes fp32/bf16/fp16 activations, got {x.dtype}")
     bias = bias.to(x.dtype) if bias is not None else None
-    if w.kernel_ok(x.dtype):
-        return _FusedInt8LinearFunc.apply(x, bias, w)
-    return F.linear(x, w.dense(x.dtype), bias)
+    return _FusedInt8LinearFunc.apply(x, bias, w)
 
 
 def fused_dequant_nf4_matmul(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Tensor,

@@ -2,15 +2,14 @@
 
 Each function validates and lays out torch tensors, then calls one C-ABI
 entry point of librocm_qlora_amd.so on the current HIP stream.  There is no
-CPU or library fallback for bf16/fp16 activations: a tensor off the GPU, or a
-missing library, raises.
+CPU or library fallback for any activation dtype or shape: a tensor off the
+GPU, or a missing library, raises.
 """
 from __future__ import annotations
 
 from typing import Optional, Tuple
 
 import torch
-import torch.nn.functional as F
 
 from rocm_qlora import _native as nat
 from rocm_qlora._device import on
@@ -131,7 +130,9 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
     (quant_linear.py:182-197 and lora_layer.py:60-70 in one kernel launch
     sequence).  x: [..., K] bf16/fp16 (bf16/fp16 MFMA kernels) or fp32 (the
     fp32-MFMA kernel, everything in fp32 as the reference computes it) on the
-    GPU; output has x's dtype."""
+    GPU; output has x's dtype.  Any K and block size: shapes the specialized
+    kernels do not take (K % 64 != 0, other block sizes, fp32 with rank > 64)
+    run on the library's generic kernels with the same roundings."""
     K = x.shape[-1]
     N = int(out_features)
     xcode = nat.dtype_code(x.dtype)
@@ -145,10 +146,9 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
         raise RuntimeError(f"weight_quant holds {packed.numel() * 2} codes, need {N}x{K}")
     packed = packed.contiguous()
     scales = scales.reshape(-1).contiguous()
-    if K % 64 or block_size % 64 or K % block_size or block_size & (block_size - 1):
-        raise RuntimeError(f"NF4 linear needs K % 64 == 0 and a power-of-two block_size >= 64 "
-                           f"dividing K (K={K}, block_size={block_size})")
-    n_blocks = N * K // block_size
+    if block_size < 1:
+        raise RuntimeError(f"block_size must be positive, got {block_size}")
+    n_blocks = -(-N * K // block_size)
     if dq:
         if c2.numel() < n_blocks or scales.numel() * blocksize_2 < n_blocks:
             raise RuntimeError("c2 / c2_scales too short for the weight")
@@ -158,7 +158,7 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
     with on(dev):
         x2, ldx = _rows(x, K)
         M = x2.shape[0]
-        if M > GEMV_MAX_M or x.dtype == torch.float32:  # 16-byte activation loads
+        if (M > GEMV_MAX_M or x.dtype == torch.float32) and K % 64 == 0:  # 16-byte activation loads
             x2, ldx = _aligned_rows(x2, K)
         y = torch.empty((M, N), dtype=x.dtype, device=dev)
         if M == 0:
@@ -187,7 +187,7 @@ def nf4_linear(x: torch.Tensor, weight_quant: torch.Tensor, weight_scales: Optio
             if lora_x is not None:
                 # the GEMM's and the fp32 path's LoRA operand kernels load 16
                 # bytes at a time
-                wide = M > GEMV_MAX_M or x.dtype == torch.float32
+                wide = (M > GEMV_MAX_M or x.dtype == torch.float32) and K % 64 == 0
                 xl, ldxl = (_aligned_rows if wide else _rows)(lora_x.to(x.dtype), K)
         b = bias.contiguous() if bias is not None else None
         ws = _workspace(x.dtype, M, K, N, rank, dev)
@@ -214,8 +214,9 @@ def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: O
     weight stored flat (dequant_matmul.py:338-351, lora_layer.py:67
     differentiated).  With lora_mask (the dropout mask of the adapter's input,
     [..., K] bool), the LoRA term goes through dropout's backward: times
-    mask * mask_scale.  dy: [..., N] bf16/fp16 on the GPU, N % 64 == 0;
-    output [..., K] in dy's dtype."""
+    mask * mask_scale.  dy: [..., N] fp32/bf16/fp16 on the GPU; output
+    [..., K] in dy's dtype.  Shapes outside the MFMA dX kernel's (N or K not
+    multiples of 64, other block sizes, fp32 dy) run on the generic kernels."""
     N = dy.shape[-1]
     K = int(in_features)
     dq = c2 is not None
@@ -231,7 +232,7 @@ def nf4_linear_dx(dy: torch.Tensor, weight_quant: torch.Tensor, weight_scales: O
     lead = dy.shape[:-1]
     with on(dev):
         # the dX kernel loads dY rows 16 bytes at a time
-        dy2, lddy = _aligned_rows(dy, N)
+        dy2, lddy = _aligned_rows(dy, N) if N % 64 == 0 else _rows(dy, N)
         M = dy2.shape[0]
         dx = torch.empty((M, K), dtype=dy.dtype, device=dev)
         if M == 0:
@@ -290,14 +291,10 @@ def int8_linear(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, out_feat
     quant_linear.py:193-197).  q: [N, K] (or flat N*K) int8; block_size 0 ->
     one scale per output row ([N] scales, the row-absmax recipe), otherwise
     blockwise over the flat weight (QuantLinear bits=8 uses 64).
-    x: [..., K] bf16/fp16 on the GPU; output has x's dtype."""
+    x: [..., K] fp32/bf16/fp16 on the GPU; output has x's dtype.  Shapes and
+    dtypes the int8 GEMV / MFMA GEMM do not take run on the generic kernels."""
     K = x.shape[-1]
     N = int(out_features)
-    if x.dtype == torch.float32:
-        from rocm_qlora.quantization.quant_ops import dequantize_int8
-        w = dequantize_int8(q.reshape(N, K) if block_size == 0 else q.reshape(-1), scales,
-                            block_size if block_size else 64)
-        return F.linear(x, w.reshape(-1)[:N * K].reshape(N, K), bias)
     dev = nat.require_gpu(x, q, scales, bias)
     if q.dtype != torch.int8:
         raise TypeError(f"int8 weights expected, got {q.dtype}")
@@ -305,12 +302,12 @@ def int8_linear(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, out_feat
     if qf.numel() < N * K:
         raise RuntimeError(f"q holds {qf.numel()} values, need {N}x{K}")
     sc = scales.reshape(-1).contiguous()
-    need = N if block_size == 0 else N * K // block_size
+    need = N if block_size == 0 else -(-N * K // block_size)
     if sc.numel() < need:
         raise RuntimeError(f"scales hold {sc.numel()} values, need {need}")
     lead = x.shape[:-1]
     with on(dev):
-        x2, ldx = _aligned_rows(x, K)
+        x2, ldx = _aligned_rows(x, K) if K % 64 == 0 and x.dtype != torch.float32 else _rows(x, K)
         M = x2.shape[0]
         y = torch.empty((M, N), dtype=x.dtype, device=dev)
         if M == 0:
@@ -321,6 +318,38 @@ def int8_linear(x: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, out_feat
                  nat.ptr(b), nat.dtype_code(b.dtype) if b is not None else 0,
                  y.data_ptr(), N, nat.stream_handle(dev))
     return y.reshape(*lead, N)
+
+
+def int8_linear_dx(dy: torch.Tensor, q: torch.Tensor, scales: torch.Tensor, in_features: int,
+                   block_size: int = 0) -> torch.Tensor:
+    """dX = dY . (q * scale) for int8 weights (the backward of
+    dequant_matmul.py:308-324: the dequantized weight rounded to dY's dtype,
+    then the product), decoded inside the multiply.  q: [N, K] (or flat)
+    int8, scales as for int8_linear; dy: [..., N] fp32/bf16/fp16 on the GPU;
+    output [..., K] in dy's dtype."""
+    N = dy.shape[-1]
+    K = int(in_features)
+    dev = nat.require_gpu(dy, q, scales)
+    if q.dtype != torch.int8:
+        raise TypeError(f"int8 weights expected, got {q.dtype}")
+    qf = q.reshape(-1).contiguous()
+    if qf.numel() < N * K:
+        raise RuntimeError(f"q holds {qf.numel()} values, need {N}x{K}")
+    sc = scales.reshape(-1).contiguous()
+    need = N if block_size == 0 else -(-N * K // block_size)
+    if sc.numel() < need:
+        raise RuntimeError(f"scales hold {sc.numel()} values, need {need}")
+    lead = dy.shape[:-1]
+    with on(dev):
+        dy2, lddy = _rows(dy, N)
+        M = dy2.shape[0]
+        dx = torch.empty((M, K), dtype=dy.dtype, device=dev)
+        if M == 0:
+            return dx.reshape(*lead, K)
+        nat.call("rq_int8_linear_dx", dy2.data_ptr(), nat.dtype_code(dy.dtype), M, N, lddy,
+                 qf.data_ptr(), K, block_size, sc.data_ptr(), nat.dtype_code(sc.dtype),
+                 dx.data_ptr(), K, nat.stream_handle(dev))
+    return dx.reshape(*lead, K)
 
 
 def fp8_quantize(t: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -363,7 +392,9 @@ def fp8_linear(x: torch.Tensor, w_codes: torch.Tensor, w_scale: torch.Tensor,
     the fp8 matrix cores in fp32, scaled by x_scale * w_scale, rounded to x's
     dtype, and the bias is added.  w_codes: torch.float8_e4m3fn (fp8_to_e4m3fn
     of the quantized weight, used as is) or torch.float8_e4m3fnuz / uint8
-    (re-encoded on every call).  x: [..., K] bf16/fp16 on the GPU."""
+    (re-encoded on every call).  x: [..., K] fp32/bf16/fp16 on the GPU (fp32
+    x, K % 64 != 0 or unaligned rows: the generic kernels, which decode the
+    codes and sum the fp32 products as fp8_linear.py:44-52 does)."""
     K = x.shape[-1]
     dev = nat.require_gpu(x, w_codes, w_scale, bias)
     if w_codes.dtype != torch.float8_e4m3fn:
@@ -375,7 +406,7 @@ def fp8_linear(x: torch.Tensor, w_codes: torch.Tensor, w_scale: torch.Tensor,
     ws_scale = w_scale.reshape(()).to(torch.float32).contiguous()
     lead = x.shape[:-1]
     with on(dev):
-        x2, ldx = _aligned_rows(x, K)
+        x2, ldx = _aligned_rows(x, K) if K % 64 == 0 and x.dtype != torch.float32 else _rows(x, K)
         M = x2.shape[0]
         y = torch.empty((M, N), dtype=x.dtype, device=dev)
         if M == 0:

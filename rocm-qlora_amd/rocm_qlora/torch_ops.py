@@ -71,6 +71,16 @@ def _int8_linear_fake(x, q, scales, out_features, block_size, bias):
     return x.new_empty((*x.shape[:-1], out_features))
 
 
+@torch.library.custom_op("rocm_qlora::int8_linear_dx", mutates_args=())
+def int8_linear_dx(dy: Tensor, q: Tensor, scales: Tensor, in_features: int, block_size: int) -> Tensor:
+    return ops.int8_linear_dx(dy, q, scales, in_features, block_size)
+
+
+@int8_linear_dx.register_fake
+def _int8_linear_dx_fake(dy, q, scales, in_features, block_size):
+    return dy.new_empty((*dy.shape[:-1], in_features))
+
+
 @torch.library.custom_op("rocm_qlora::fp8_quantize", mutates_args=())
 def fp8_quantize(t: Tensor) -> Tuple[Tensor, Tensor]:
     return ops.fp8_quantize(t)
@@ -146,6 +156,13 @@ def call_int8_linear(x, q, scales, out_features, block_size=0, bias=None):
     if _compiling():
         return torch.ops.rocm_qlora.int8_linear(x, q, scales, int(out_features), int(block_size), bias)
     return ops.int8_linear(x, q, scales, out_features, block_size, bias)
+
+
+def call_int8_linear_dx(dy, q, scales, in_features, block_size=0):
+    """ops.int8_linear_dx, through the registered operator while being traced."""
+    if _compiling():
+        return torch.ops.rocm_qlora.int8_linear_dx(dy, q, scales, int(in_features), int(block_size))
+    return ops.int8_linear_dx(dy, q, scales, in_features, block_size)
 
 
 def call_fp8_quantize(t):
