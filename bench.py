@@ -15,9 +15,13 @@ Also reported:
   config        p10 / p50 / p90 of the headline's per-step times, from a
                 second pass with an event after every step (which adds about
                 4 us per step; `value` comes from the uninstrumented pass).
-  roofline      the dominant kernel (the GEMV at the gate/up shape, no LoRA),
-                timed with HIP events over back-to-back launches on the stream
-                they run on; algorithmic bytes / average launch time vs 8 TB/s.
+  roofline      the dominant kernel as the headline step runs it (the GEMV at
+                the gate/up shape with the LoRA term fused), timed with HIP
+                events over back-to-back launches on the stream they run on;
+                algorithmic bytes / average launch time vs 8 TB/s.  `traffic`
+                is the HBM bytes per launch that the committed counter
+                profile (profiles/nf4_gemv_kernel_traffic.md) holds for the
+                same kernel, mode and shape, or null.
   decode_m      the same decode step at the configuration's other batch sizes
                 (M in {1, 4, 8, 16}), 50 steps each.
   decode_per_shape
@@ -25,14 +29,16 @@ Also reported:
                 LoRA term fused and without it, and a minimal launch (a 4-byte
                 fill) of the same graph structure.
   config1       one NF4 4096x4096 QuantLinear with LoRA r = 16 on fp32
-                activations (M = 1 and 16), the fp32-MFMA path.
+                activations (M = 1 and 16), the fp32-MFMA path, rotating 60
+                weight copies (565 MB).
   gemm          the prefill/training shapes: the same seven projections at
                 M = 2048 tokens with LoRA r = 64, alpha = 16, forward and dX
                 backward, TFLOP/s and fraction of the 2.5 PFLOP/s bf16 MFMA peak.
   codec         NF4 + double quantization of an 11008x4096 bf16 weight (N(0,0.02)
                 with 0.1 % outliers at +-8 sigma, blocks 64 / 256): quantize ->
                 pack -> double-quantize the absmax, and double-dequantize ->
-                bf16; algorithmic bytes / time vs 8 TB/s.
+                bf16, over 5 weight copies (565 MB); algorithmic bytes / time
+                vs 8 TB/s.
   byte_linears  INT8 (per-row absmax: W8A16 on the bf16 MFMA, and the
                 separate W8A8 mode on the int8 MFMA) and FP8 (e4m3
                 per-tensor scales, fp8 MFMA) linears at the Llama-3-70B MLP
@@ -55,7 +61,8 @@ Also reported:
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--m M] [--no-gemm] [--no-extra] [--no-cpu]
     python bench.py --summarize-profile DIR   # per-kernel, per-grid rocprofv3 kernel-trace table
     python bench.py --counters [gemv|fp8_gemm|int8_gemm|nf4_gemm]   # short eager run for rocprofv3 --pmc passes
-    python bench.py --summarize-counters DIR [DIR ...]   # HBM bytes per launch from those passes
+    python bench.py --summarize-counters DIR [DIR ...]   # per-kernel counter means; for the gemv run,
+                                                         # HBM bytes per launch per (shape, mode)
 """
 import argparse
 import csv
@@ -83,13 +90,32 @@ LLAMA3_8B_PROJ = [("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o",
 RANK, ALPHA, BLOCK = 16, 32, 64
 SCALING = ALPHA / RANK
 GEMM_M, GEMM_RANK, GEMM_ALPHA = 2048, 64, 16
+CONFIG1_COPIES = 60            # 4096x4096 NF4 weights: 60 x 9.4 MB = 565 MB
+CODEC_COPIES = 5               # 11008x4096 bf16 weights and their codes: 5 x 113 MB = 565 MB
 
-# HBM traffic of the roofline kernel per launch, measured with rocprofv3 --pmc
-# FETCH_SIZE / WRITE_SIZE and scaled by the same counters' reading for a copy
-# kernel of known size (factors 0.5 for FETCH_SIZE, 1.0 for WRITE_SIZE on a
-# 512 MiB device copy); keyed by (kernel, M, K, N).  None where not measured.
-MEASURED_TRAFFIC = {("nf4_gemv_kernel", 1, 4096, 14336): 33331494}
+# The counter profile of the decode GEMV: `bench.py --summarize-counters`
+# output for `bench.py --counters` (FETCH_SIZE and WRITE_SIZE passes), whose
+# table rows "| nf4_gemv_kernel | shape | mode | M | K | N | fetch | write |
+# total | algorithmic | ratio |" give the HBM bytes per launch.
+GEMV_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "nf4_gemv_kernel_traffic.md")
 COPY_BYTES = 512 << 20         # calibration copy: 512 MiB read + 512 MiB written
+# (shape, LoRA fused) of the counter run, in launch order
+GEMV_COUNTER_CONFIGS = [("gate", False), ("gate", True), ("k", False), ("k", True)]
+
+
+def profiled_traffic(shape, mode, M, K, N, path=GEMV_TRAFFIC_PROFILE):
+    """HBM bytes per launch of nf4_gemv_kernel for (shape, mode, M, K, N) from
+    the committed counter profile, or None when it holds no such row."""
+    try:
+        with open(path) as fh:
+            for line in fh:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) >= 9 and cells[0] == "nf4_gemv_kernel" and cells[1:6] == \
+                        [shape, mode, str(M), str(K), str(N)]:
+                    return int(cells[8].replace(",", ""))
+    except OSError:
+        return None
+    return None
 
 
 def gemv_bytes(M, N, K, rank=RANK, scale_bytes=4):
@@ -366,21 +392,24 @@ def bench_config1(dev, stream):
     """Config 1 on the GPU: one NF4 QuantLinear 4096 -> 4096 with LoRA r = 16,
     alpha = 32 on fp32 activations (the fp32-MFMA path), M in {1, 16}; fp32
     weights N(0,0.02) quantized with block 64 and fp32 absmax, 20 replays of
-    a graph of 8 calls over 8 weight copies."""
+    a graph of 60 calls over 60 weight copies (565 MB of codes and scales,
+    past the 256 MB MALL)."""
     import torch
     from rocm_qlora import ops
     from rocm_qlora.quantization import quantize_int4
     K = N = 4096
     g = torch.Generator(device=dev).manual_seed(13)
     ws = []
-    for _ in range(8):
+    for _ in range(CONFIG1_COPIES):
         w = torch.randn(N, K, generator=g, device=dev) * 0.02
         p, s_ = quantize_int4(w, BLOCK)
         a = (torch.rand(RANK, K, generator=g, device=dev) * 2 - 1) / math.sqrt(K)
         b = torch.randn(N, RANK, generator=g, device=dev) * 0.01
         ws.append((p, s_, a, b))
         del w
-    out = {"workload": f"NF4 {K}x{N} fp32 activations, LoRA r={RANK} alpha={ALPHA}, block {BLOCK} fp32 absmax"}
+    wbytes = len(ws) * (N * K // 2 + N * K // BLOCK * 4)
+    out = {"workload": f"NF4 {K}x{N} fp32 activations, LoRA r={RANK} alpha={ALPHA}, block {BLOCK} fp32 absmax",
+           "rotation": f"{len(ws)} weight copies, {wbytes / 1e6:.0f} MB of codes and scales"}
     for m in (1, 16):
         x = torch.randn(m, K, generator=g, device=dev)
         gr = _capture(lambda: [ops.nf4_linear(x, p, s_, N, BLOCK, lora_a=a, lora_b=b, scaling=SCALING)
@@ -436,41 +465,49 @@ def bench_gemm(dev, stream):
 
 def bench_codec(dev, stream):
     """NF4 + double quantization of the down-projection weight (11008 x 4096
-    bf16, 0.1 % outliers at +-8 sigma), blocks 64 / 256, 10 graph replays
-    each way.  Algorithmic bytes (each way): 2 numel (bf16 W) + numel / 2
-    (packed) + numel / 64 (c2 codes) + 4 numel / 16384 (c2 scales)."""
+    bf16, 0.1 % outliers at +-8 sigma), blocks 64 / 256, over CODEC_COPIES
+    weight copies (each call encodes or decodes all of them, 565 MB, past the
+    256 MB MALL), 10 graph replays each way.  Algorithmic bytes (each way,
+    per copy): 2 numel (bf16 W) + numel / 2 (packed) + numel / 64 (c2 codes)
+    + 4 numel / 16384 (c2 scales)."""
     import torch
     from rocm_qlora.quantization import quantize_int4
     from rocm_qlora.quantization.double_quant import dq_quantize_absmax, dq_dequantize_to
     N, K = 11008, 4096
     numel = N * K
     g = torch.Generator(device=dev).manual_seed(5)
-    w = torch.randn(N, K, generator=g, device=dev) * 0.02
-    n_out = numel // 1000
-    idx = torch.randperm(numel, generator=g, device=dev)[:n_out]
-    sign = torch.randint(0, 2, (n_out,), generator=g, device=dev).float() * 2 - 1
-    w.view(-1)[idx] = sign * 0.16
-    w = w.to(torch.bfloat16)
-    state = {}
+    ws = []
+    for _ in range(CODEC_COPIES):
+        w = torch.randn(N, K, generator=g, device=dev) * 0.02
+        n_out = numel // 1000
+        idx = torch.randperm(numel, generator=g, device=dev)[:n_out]
+        sign = torch.randint(0, 2, (n_out,), generator=g, device=dev).float() * 2 - 1
+        w.view(-1)[idx] = sign * 0.16
+        ws.append(w.to(torch.bfloat16))
+        del w, idx, sign
+    states = [{} for _ in ws]
 
     def encode():
-        packed, c1 = quantize_int4(w, 64)
-        c2, c2s = dq_quantize_absmax(c1, 256, True)
-        state.update(packed=packed, c2=c2, c2s=c2s)
+        for w, st in zip(ws, states):
+            packed, c1 = quantize_int4(w, 64)
+            c2, c2s = dq_quantize_absmax(c1, 256, True)
+            st.update(packed=packed, c2=c2, c2s=c2s)
 
     encode()
     ge = _capture(encode, stream)
-    packed, c2, c2s = state["packed"], state["c2"], state["c2s"]
-    gd = _capture(lambda: dq_dequantize_to(packed, c2, c2s, 64, 256, True, torch.bfloat16, numel), stream)
+    codes = [(st["packed"], st["c2"], st["c2s"]) for st in states]
+    gd = _capture(lambda: [dq_dequantize_to(p, c2, c2s, 64, 256, True, torch.bfloat16, numel)
+                           for p, c2, c2s in codes], stream)
     nbytes = 2 * numel + numel // 2 + numel // 64 + 4 * numel // 16384
-    with _Range(f"rq-codec encode {N}x{K}"):
-        ms_e = _time_graph(ge, 10)
-    with _Range(f"rq-codec decode {N}x{K}"):
-        ms_d = _time_graph(gd, 10)
+    with _Range(f"rq-codec encode {N}x{K} x{CODEC_COPIES}"):
+        ms_e = _time_graph(ge, 10) / CODEC_COPIES
+    with _Range(f"rq-codec decode {N}x{K} x{CODEC_COPIES}"):
+        ms_d = _time_graph(gd, 10) / CODEC_COPIES
     del ge, gd
     enc, dec = nbytes / ms_e / 1e6, nbytes / ms_d / 1e6
     return {"workload": f"NF4 + double quantization (blocks 64/256, fp8 c2) of a {N}x{K} bf16 weight with "
                         f"0.1% outliers at +-8 sigma",
+            "rotation": f"{CODEC_COPIES} weight copies, {CODEC_COPIES * nbytes / 1e6:.0f} MB per pass",
             "bytes": nbytes, "encode_us": round(ms_e * 1e3, 2), "encode_gbs": round(enc, 1),
             "encode_frac": round(enc / HBM_PEAK_GBS, 4), "decode_us": round(ms_d * 1e3, 2),
             "decode_gbs": round(dec, 1), "decode_frac": round(dec / HBM_PEAK_GBS, 4)}
@@ -734,73 +771,122 @@ def run_counters_kernel(which, reps=4):
 def run_counters(reps=4):
     """Eager launches for counter collection: one plain device copy of
     COPY_BYTES (calibration: its FETCH_SIZE / WRITE_SIZE readings against the
-    bytes it must move), then the roofline GEMV (M=1, K=4096, N=14336, no
-    LoRA) over the gate and up weights of six layer copies, `reps` rounds."""
+    bytes it must move), then the decode GEMV (M = 1) for each of
+    GEMV_COUNTER_CONFIGS in turn -- the gate/up shape (K = 4096, N = 14336)
+    over the gate and up weights of six layer copies, the k/v shape (K =
+    4096, N = 1024) over the k and v weights, plain and with the LoRA term
+    fused (r = 16) -- `reps` rounds over the 12 weights each, so every
+    launch reads its weights from HBM (past the 256 MB MALL)."""
     import torch
     from rocm_qlora import ops
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    layers = [make_layer(dev, 1000 + c) for c in range(6)]
+    x = torch.randn(1, 4096, device=dev).to(torch.bfloat16)
     src = torch.randint(0, 255, (COPY_BYTES,), dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
+    torch.cuda.synchronize()
     dst.copy_(src)
     torch.cuda.synchronize()
-    K, N = 4096, 14336
-    weights = []
-    for c in range(6):
-        layer = make_layer(dev, 1000 + c)
-        weights += [(layer[nm][0], layer[nm][1]) for nm in ("gate", "up")]
-        del layer
-    x = torch.randn(1, K, device=dev).to(torch.bfloat16)
-    for _ in range(reps):
-        for packed, absmax in weights:
-            ops.nf4_linear(x, packed, absmax, N, BLOCK)
-    torch.cuda.synchronize()
-    print(f"counters: copy {COPY_BYTES} B, {reps * len(weights)} nf4_gemv_kernel launches M=1 K={K} N={N}",
-          flush=True)
+    del src, dst
+    names = {"gate": ("gate", "up"), "k": ("k", "v")}
+    for shape, lora in GEMV_COUNTER_CONFIGS:
+        ws = [layer[nm] for layer in layers for nm in names[shape]]
+        for _ in range(reps):
+            for packed, absmax, a, b, N, K in ws:
+                if lora:
+                    ops.nf4_linear(x, packed, absmax, N, BLOCK, lora_a=a, lora_b=b, scaling=SCALING)
+                else:
+                    ops.nf4_linear(x, packed, absmax, N, BLOCK)
+        torch.cuda.synchronize()
+        print(f"counters: {reps * len(ws)} launches {shape} {'lora' if lora else 'plain'}", flush=True)
+    print(f"counters: copy {COPY_BYTES} B, then {GEMV_COUNTER_CONFIGS}", flush=True)
 
 
 def summarize_counters(paths):
     """Per-kernel mean of each counter over the dispatches in rocprofv3 CSV
-    counter files (`-f csv`), and the GEMV's HBM bytes per launch: FETCH_SIZE
-    and WRITE_SIZE (KiB per dispatch) divided by what the same counter reads
-    per byte for the calibration copy."""
+    counter files (`-f csv`).  For a `--counters gemv` run, also per (shape,
+    mode) of GEMV_COUNTER_CONFIGS: the dispatches after the calibration copy
+    are taken in dispatch order, the library's kernels only (a LoRA operand
+    kernel counts with the GEMV launch that follows it), and each counter's
+    mean per launch printed; FETCH_SIZE and WRITE_SIZE (KiB per dispatch)
+    become HBM bytes per launch by dividing by what the same counter reads
+    per byte for the calibration copy, printed as the table rows
+    profiled_traffic reads."""
     files = []
     for p in paths:
         files += glob.glob(os.path.join(p, "**", "*counter_collection.csv"), recursive=True)
     if not files:
         sys.exit(f"no *counter_collection.csv under {paths}")
     per = {}   # (kernel, counter) -> {dispatch: value}
+    seq = {}   # file -> {dispatch id: (kernel, {counter: value})}
     for f in files:
         with open(f, newline="") as fh:
             for row in csv.DictReader(fh):
                 key = (row["Kernel_Name"], row["Counter_Name"])
                 d = per.setdefault(key, {})
-                did = (f, row.get("Dispatch_Id", row.get("Correlation_Id")))
-                d[did] = d.get(did, 0.0) + float(row["Counter_Value"])
-    means = {}
-    for (kname, cname), d in per.items():
-        short = "copy" if "copy" in kname.lower() else ("nf4_gemv_kernel" if "nf4_gemv_kernel" in kname else None)
+                did = int(row.get("Dispatch_Id", row.get("Correlation_Id")) or 0)
+                d[(f, did)] = d.get((f, did), 0.0) + float(row["Counter_Value"])
+                ent = seq.setdefault(f, {}).setdefault(did, (row["Kernel_Name"], {}))
+                ent[1][row["Counter_Name"]] = ent[1].get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    for (kname, cname), d in sorted(per.items()):
         vals = list(d.values())
-        print(f"{_short(kname):<70} {cname:<12} n={len(vals):<4} mean={sum(vals) / len(vals):.1f}")
-        if short:
-            means.setdefault((short, cname), []).extend(vals)
-    M, K, N = 1, 4096, 14336
-    kb = kernel_bytes(M, N, K)
-    out = {}
-    for cname, expect in (("FETCH_SIZE", COPY_BYTES), ("WRITE_SIZE", COPY_BYTES)):
-        c = means.get(("copy", cname))
-        g = means.get(("nf4_gemv_kernel", cname))
-        if not c or not g:
+        print(f"{_short(kname):<70} {cname:<24} n={len(vals):<4} mean={sum(vals) / len(vals):.1f}")
+    # per (shape, mode) of the gemv run
+    acc = {}    # (config index, counter) -> [sum, launches]
+    factor = {}
+    for f, disp in seq.items():
+        order = sorted(disp.items())
+        copies = [i for i, (_, (k, _)) in enumerate(order) if "copy" in k.lower()]
+        if not copies:
             continue
-        factor = (max(c) * 1024.0) / expect
-        gem = sum(g) / len(g) * 1024.0
-        out[cname] = gem / factor
-        print(f"{cname}: copy reads {max(c) * 1024.0 / 2**20:.1f} MiB for {expect / 2**20:.0f} MiB "
-              f"(factor {factor:.4f}); nf4_gemv_kernel {gem / 1e6:.3f} MB raw -> {gem / factor / 1e6:.3f} MB")
-    if len(out) == 2:
-        t = out["FETCH_SIZE"] + out["WRITE_SIZE"]
-        print(f"nf4_gemv_kernel M={M} K={K} N={N}: HBM traffic {t:.0f} B per launch "
-              f"(algorithmic {kb} B, ratio {t / kb:.3f})")
+        i0 = copies[-1]
+        for cname, v in order[i0][1][1].items():
+            factor[cname] = v * 1024.0 / COPY_BYTES
+        gemv, pending = 0, {}
+        launches = [(k, c) for _, (k, c) in order[i0 + 1:] if "rq::" in k or k.startswith("_ZN2rq")]
+        n_gemv = sum(1 for k, _ in launches if "nf4_gemv_kernel" in k)
+        per_cfg = n_gemv // len(GEMV_COUNTER_CONFIGS) if n_gemv else 0
+        for k, c in launches:
+            for cname, v in c.items():
+                pending[cname] = pending.get(cname, 0.0) + v
+            if "nf4_gemv_kernel" not in k:
+                continue
+            ci = min(gemv // per_cfg, len(GEMV_COUNTER_CONFIGS) - 1) if per_cfg else 0
+            for cname, v in pending.items():
+                a = acc.setdefault((ci, cname), [0.0, 0])
+                a[0] += v
+                a[1] += 1
+            pending = {}
+            gemv += 1
+    if not acc:
+        return
+    print()
+    shapes = {"gate": (4096, 14336), "k": (4096, 1024)}
+    counters = sorted({c for _, c in acc})
+    print("| config | " + " | ".join(counters) + " |")
+    for ci, (shape, lora) in enumerate(GEMV_COUNTER_CONFIGS):
+        cells = []
+        for cname in counters:
+            a = acc.get((ci, cname))
+            cells.append(f"{a[0] / a[1]:,.0f}" if a else "-")
+        print(f"| {shape} {'lora' if lora else 'plain'} | " + " | ".join(cells) + " |")
+    if "FETCH_SIZE" in factor and "WRITE_SIZE" in factor:
+        print()
+        print(f"calibration: FETCH_SIZE factor {factor['FETCH_SIZE']:.4f}, WRITE_SIZE factor "
+              f"{factor['WRITE_SIZE']:.4f} (counter bytes per copied byte)")
+        print("| kernel | shape | mode | M | K | N | fetch B | write B | total B | algorithmic B | ratio |")
+        print("|---|---|---|---|---|---|---|---|---|---|---|")
+        for ci, (shape, lora) in enumerate(GEMV_COUNTER_CONFIGS):
+            fe, wr = acc.get((ci, "FETCH_SIZE")), acc.get((ci, "WRITE_SIZE"))
+            if not fe or not wr:
+                continue
+            K, N = shapes[shape]
+            fb = fe[0] / fe[1] * 1024.0 / factor["FETCH_SIZE"]
+            wb = wr[0] / wr[1] * 1024.0 / factor["WRITE_SIZE"]
+            alg = gemv_bytes(1, N, K) if lora else kernel_bytes(1, N, K)
+            print(f"| nf4_gemv_kernel | {shape} | {'lora' if lora else 'plain'} | 1 | {K} | {N} | {fb:,.0f} | "
+                  f"{wb:,.0f} | {fb + wb:,.0f} | {alg:,} | {(fb + wb) / alg:.3f} |")
 
 
 def main():
@@ -934,24 +1020,32 @@ def main():
                            "plain_gbs": round(kernel_bytes(M, N, K) / (tp["mean"] * 1e-3 / nl) / 1e9, 1)}
     per_shape["minimal_launch_us"] = round(t_min["mean"] * 1e3 / n_copies, 2)
 
-    # roofline of the dominant kernel: plain GEMV launches at the gate/up shape
+    # roofline of the dominant kernel as the step runs it: the GEMV at the
+    # gate/up shape with the LoRA term fused (and, beside it, plain)
     K, N = 4096, 14336
-    roof_w = [(layer[nm][0], layer[nm][1]) for layer in layers for nm in ("gate", "up")]
+    roof_w = [layer[nm][:4] for layer in layers for nm in ("gate", "up")]
     x_roof = xs[K]
 
-    def roof_pass():
-        for packed, absmax in roof_w:
-            ops.nf4_linear(x_roof, packed, absmax, N, BLOCK)
+    def roof_pass(lora):
+        for packed, absmax, a, b in roof_w:
+            if lora:
+                ops.nf4_linear(x_roof, packed, absmax, N, BLOCK, lora_a=a, lora_b=b, scaling=SCALING)
+            else:
+                ops.nf4_linear(x_roof, packed, absmax, N, BLOCK)
 
-    rg = _capture(roof_pass, stream)
     # 150 replays (1800 launches): single batches of a few replays vary by
     # +-5 % from one to the next on the same machine
     reps = 150
-    with _Range(f"rq-roofline nf4_gemv_kernel M={M} K={K} N={N}"):
+    rg = _capture(lambda: roof_pass(True), stream)
+    with _Range(f"rq-roofline nf4_gemv_kernel lora M={M} K={K} N={N}"):
         us_launch = _time_graph(rg, reps) * 1e3 / len(roof_w)
-    kb = kernel_bytes(M, N, K)
-    achieved = kb / (us_launch * 1e-6) / 1e9
     del rg
+    rg = _capture(lambda: roof_pass(False), stream)
+    with _Range(f"rq-roofline nf4_gemv_kernel plain M={M} K={K} N={N}"):
+        us_plain = _time_graph(rg, reps) * 1e3 / len(roof_w)
+    del rg
+    kb = gemv_bytes(M, N, K)
+    achieved = kb / (us_launch * 1e-6) / 1e9
     print(f"bench: decode {ms_step * 1e3:.1f} us/step, {value:.0f} GB/s; gate/up GEMV {us_launch:.2f} us",
           file=sys.stderr, flush=True)
 
@@ -1013,7 +1107,7 @@ def main():
                "configs": configs}
         print(f"bench: cpu decode step {t3['median'] * 1e3:.1f} ms", file=sys.stderr, flush=True)
 
-    traffic = MEASURED_TRAFFIC.get(("nf4_gemv_kernel", M, K, N))
+    traffic = profiled_traffic("gate", "lora", M, K, N)
     rec = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -1032,8 +1126,12 @@ def main():
                    "tokens": M, "layer_copies": n_copies, "step_bytes": step_bytes, **step_pct},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "nf4_gemv_kernel", "shape": f"M={M} K={K} N={N}",
-                     "bytes_per_launch": kb, "us_per_launch": round(us_launch, 3)},
+                     "kernel": "nf4_gemv_kernel", "mode": f"LoRA r={RANK} fused",
+                     "shape": f"M={M} K={K} N={N}", "bytes_per_launch": kb,
+                     "us_per_launch": round(us_launch, 3),
+                     "plain": {"us_per_launch": round(us_plain, 3), "bytes_per_launch": kernel_bytes(M, N, K),
+                               "frac": round(kernel_bytes(M, N, K) / (us_plain * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                               "traffic": profiled_traffic("gate", "plain", M, K, N)}},
         "decode_m": decode_m,
         "decode_per_shape": per_shape,
         "config1": cfg1,

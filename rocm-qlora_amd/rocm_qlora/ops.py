@@ -42,16 +42,19 @@ def _rows(t: torch.Tensor, K: int) -> Tuple[torch.Tensor, int]:
 #   * graph capture: one buffer per (device, capture, stream) -- the branches
 #     of a capture that forks side streams each get their own.  It is taken
 #     from a pool of pre-zeroed buffers (_CAPTURE_POOL_ENTRIES of
-#     _CAPTURE_POOL_BYTES per device, zeroed once, with one stream
-#     synchronization, at the device's first eager call), so the graph needs
-#     no fill node: it holds zeros before the first replay and every replay
-#     leaves it ready for the next.  Such a buffer is held for the life of
-#     the process (the graph may replay it at any time).  A capture on a
-#     device without the
-#     pool, with the pool used up, or needing a larger buffer allocates one
-#     from the graph's private memory pool (so it lives exactly as long as
-#     the graph), zeroed by a fill kernel recorded in the graph, which every
-#     replay runs before the captured calls.
+#     _CAPTURE_POOL_BYTES per device, zeroed at the device's first eager
+#     call; and every eager call that finds no free entry as large as its own
+#     workspace adds one, zeroed, with one stream synchronization, up to
+#     _CAPTURE_POOL_LIMIT bytes per device), so the graph needs no fill node:
+#     it holds zeros before the first replay and every replay leaves it ready
+#     for the next.  Captures are normally preceded by an eager warm-up call
+#     of the same work, which leaves an entry of the size the capture needs.
+#     Such a buffer is held for the life of the process (the graph may replay
+#     it at any time).  A capture on a device without the pool, or finding
+#     no free entry large enough, allocates one from the graph's private
+#     memory pool (so it lives exactly as long as the graph), zeroed by a
+#     fill kernel recorded in the graph, which every replay runs before the
+#     captured calls.
 LINEAR_SYNC_BYTES = 131328
 _LINEAR_WS: dict = {}
 _CAPTURE_WS: dict = {}
@@ -61,18 +64,33 @@ _CAPTURE_POOL_ENTRIES = 32
 # partials) for the common layer shapes, so that a capture's calls share one
 # pre-zeroed buffer rather than recording a fill kernel at each larger need
 _CAPTURE_POOL_BYTES = 2 << 20
+_CAPTURE_POOL_LIMIT = 1 << 30  # pre-zeroed capture buffers per device, at most (bytes)
 _CAPTURE_POOL: dict = {}       # device index -> pre-zeroed buffers not yet handed out
-_CAPTURE_POOL_BASE: dict = {}  # device index -> the allocation they are views of (kept for good)
+_CAPTURE_POOL_BASE: dict = {}  # device index -> the allocations they are views of (kept for good)
+_CAPTURE_POOL_TOTAL: dict = {}  # device index -> bytes of those allocations
 
 
-def _ensure_capture_pool(dev, idx: int) -> None:
-    if idx in _CAPTURE_POOL_BASE:
+def _ensure_capture_pool(dev, idx: int, need: int) -> None:
+    """The device's pool exists and holds a free entry of at least `need`
+    bytes (while the pool stays within _CAPTURE_POOL_LIMIT)."""
+    if idx not in _CAPTURE_POOL_BASE:
+        base = torch.zeros(_CAPTURE_POOL_ENTRIES * _CAPTURE_POOL_BYTES, dtype=torch.uint8, device=dev)
+        torch.cuda.current_stream(dev).synchronize()  # zero before any later capture, on any stream, replays it
+        _CAPTURE_POOL_BASE[idx] = [base]
+        _CAPTURE_POOL_TOTAL[idx] = base.numel()
+        _CAPTURE_POOL[idx] = [base[i * _CAPTURE_POOL_BYTES:(i + 1) * _CAPTURE_POOL_BYTES]
+                              for i in range(_CAPTURE_POOL_ENTRIES)]
+    pool = _CAPTURE_POOL[idx]
+    if any(e.numel() >= need for e in pool):
         return
-    base = torch.zeros(_CAPTURE_POOL_ENTRIES * _CAPTURE_POOL_BYTES, dtype=torch.uint8, device=dev)
-    torch.cuda.current_stream(dev).synchronize()  # zero before any later capture, on any stream, replays it
-    _CAPTURE_POOL_BASE[idx] = base
-    _CAPTURE_POOL[idx] = [base[i * _CAPTURE_POOL_BYTES:(i + 1) * _CAPTURE_POOL_BYTES]
-                          for i in range(_CAPTURE_POOL_ENTRIES)]
+    size = -(-max(need, _CAPTURE_POOL_BYTES) // _CAPTURE_POOL_BYTES) * _CAPTURE_POOL_BYTES
+    if _CAPTURE_POOL_TOTAL[idx] + size > _CAPTURE_POOL_LIMIT:
+        return
+    buf = torch.zeros(size, dtype=torch.uint8, device=dev)
+    torch.cuda.current_stream(dev).synchronize()
+    _CAPTURE_POOL_BASE[idx].append(buf)
+    _CAPTURE_POOL_TOTAL[idx] += size
+    pool.append(buf)
 
 
 def _zeroed_area(nbytes: int, dev, min_bytes: int = _WS_MIN_BYTES) -> torch.Tensor:
@@ -104,14 +122,15 @@ def _workspace(x_dtype: torch.dtype, M: int, K: int, N: int, rank: int, dev) -> 
         if ws is None or ws.numel() < need:
             # a larger buffer replaces a smaller one for the calls captured
             # from here on; calls captured before keep theirs
-            pool = _CAPTURE_POOL.get(idx)
-            if pool and need <= _CAPTURE_POOL_BYTES:
-                ws = pool.pop()
+            pool = _CAPTURE_POOL.get(idx) or []
+            fits = [i for i, e in enumerate(pool) if e.numel() >= need]
+            if fits:
+                ws = pool.pop(min(fits, key=lambda i: pool[i].numel()))
             else:
                 ws = _zeroed_area(need, dev, min_bytes=LINEAR_SYNC_BYTES)
             _CAPTURE_WS[key] = ws
         return ws
-    _ensure_capture_pool(dev, idx)
+    _ensure_capture_pool(dev, idx, need)
     key = (idx, stream)
     ws = _LINEAR_WS.get(key)
     if ws is None or ws.numel() < need:

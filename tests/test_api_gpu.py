@@ -159,8 +159,9 @@ def test_lora_forward_and_grads_vs_oracle(dev, dtype, M, bias):
 
 
 def test_lora_dropout_path_and_int8_base(dev):
-    """Active dropout runs the composed (unfused) path; an INT8 base adds the
-    adapter after the int8 kernel.  Both give LoRA gradients."""
+    """With active dropout an NF4 base runs the fused kernels on drop(x) (the
+    dX kernel applies dropout's backward); an INT8 base adds the adapter after
+    the int8 kernel.  Both give LoRA gradients."""
     for bits in (4, 8):
         ql = QuantLinear.from_linear(_linear(256, 192, seed=8).to(dev), bits=bits)
         lora = LoRALinear(ql, r=8, lora_dropout=0.1)

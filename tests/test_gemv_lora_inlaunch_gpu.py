@@ -295,3 +295,34 @@ def test_capture_forking_side_streams(dev, sync_ready):
         for g, w in zip(got, want + want):
             assert torch.equal(g, w), f"replay {i} differs from the eager calls"
     _sync_words_ready(dev, sync_ready)
+
+
+def test_captured_gemm_holds_no_fill_node(dev):
+    """A capture preceded by an eager call of the same work takes a
+    pre-zeroed workspace of the size it needs (here the M = 2048 GEMM's with
+    its K-split partials, larger than the pool's first entries), so its
+    replays run the library's kernels only -- no fill node -- and give the
+    eager call's bits."""
+    from torch.profiler import ProfilerActivity, profile
+    K, N, M, rank = 4096, 1024, 2048, 16
+    print(f"captured GEMM K={K} N={N} M={M} rank={rank}", flush=True)
+    packed, absmax, a, b = _layer(N, K, rank, seed=111, dev=dev)
+    ad, bd = a.to(dev), b.to(dev)
+    x = _x(M, K, seed=112).to(dev)
+    y0 = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        y = ops.nf4_linear(x, packed, absmax, N, 64, lora_a=ad, lora_b=bd, scaling=2.0)
+    graph.replay()
+    torch.cuda.synchronize(dev)
+    assert torch.equal(y, y0)
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        graph.replay()
+        torch.cuda.synchronize(dev)
+    assert torch.equal(y, y0)
+    names = sorted({e.name for e in prof.events() if e.device_type.name in ("CUDA", "PrivateUse1")})
+    if not names:
+        pytest.skip("the profiler recorded no GPU kernels of the replay on this system")
+    foreign = [n for n in names if "rq::" not in n and not n.startswith("_ZN2rq")]
+    assert not foreign, f"the replay ran kernels outside the library: {foreign}"
