@@ -5,6 +5,7 @@ from __future__ import annotations
 import logging
 from typing import Dict, List, Tuple
 
+import torch
 import torch.nn as nn
 
 from rocm_qlora.quantization.quant_linear import QuantLinear
@@ -44,6 +45,46 @@ def print_model_summary(model: nn.Module) -> None:
             print(f"{name[:40]:<40} | {type(module).__name__:<20} | {n:<12,} | {str(tr):<10}")
 
 
+def _target_linears(model: nn.Module, target_modules: List[str]) -> List[Tuple[nn.Module, str, nn.Linear]]:
+    """(parent, attribute, layer) of every nn.Linear whose name ends with one
+    of target_modules and whose smaller side is >= 64 (quantize_model.py:58-70)."""
+    found = []
+    for name, module in model.named_modules():
+        if isinstance(module, nn.Linear) and any(name.endswith(t) for t in target_modules):
+            if min(module.in_features, module.out_features) < 64:
+                logger.warning(f"Skipping layer '{name}' because it is too small "
+                               f"({module.in_features}x{module.out_features} < 64)")
+                continue
+            parent, attr = _get_parent_and_attr(model, name)
+            found.append((parent, attr, module))
+    return found
+
+
+def quantized_skeleton(model: nn.Module, bits: int = 8, lora_r: int = 8, lora_alpha: int = 16,
+                       lora_dropout: float = 0.05, target_modules: List[str] = ["q_proj", "v_proj"],
+                       block_size: int = 64, lora_dtype: torch.dtype = torch.float32) -> nn.Module:
+    """The module tree quantize_model produces, without quantizing anything:
+    every target nn.Linear becomes LoRALinear(QuantLinear.empty_quantized(...))
+    on the layer's device (meta while transformers builds a model), with the
+    buffer shapes and dtypes quantization of that layer's weight gives and
+    `lora_dtype` adapters.  A state_dict saved after quantization then loads
+    into it key for key (the reference reaches the same tree by quantizing the
+    skeleton, hf_integration/quantizer.py:56-69)."""
+    if bits not in (4, 8):
+        raise ValueError(f"Invalid bit-depth: {bits}. Only 4 and 8 bits are supported.")
+    model.requires_grad_(False)
+    for parent, attr, linear in _target_linears(model, target_modules):
+        w = linear.weight
+        ql = QuantLinear.empty_quantized(linear.in_features, linear.out_features, bits=bits,
+                                         bias=linear.bias is not None, block_size=block_size, dtype=w.dtype,
+                                         device=w.device)
+        ll = LoRALinear(ql, r=lora_r, lora_alpha=lora_alpha, lora_dropout=lora_dropout)
+        ll.lora_A = nn.Parameter(ll.lora_A.detach().to(lora_dtype))
+        ll.lora_B = nn.Parameter(ll.lora_B.detach().to(lora_dtype))
+        setattr(parent, attr, ll)
+    return model
+
+
 def quantize_model(model: nn.Module, bits: int = 8, lora_r: int = 8, lora_alpha: int = 16,
                    lora_dropout: float = 0.05, target_modules: List[str] = ["q_proj", "v_proj"],
                    block_size: int = 64) -> nn.Module:
@@ -53,15 +94,7 @@ def quantize_model(model: nn.Module, bits: int = 8, lora_r: int = 8, lora_alpha:
     if bits not in (4, 8):
         raise ValueError(f"Invalid bit-depth: {bits}. Only 4 and 8 bits are supported.")
     model.requires_grad_(False)
-    replacements = []
-    for name, module in model.named_modules():
-        if isinstance(module, nn.Linear) and any(name.endswith(t) for t in target_modules):
-            if min(module.in_features, module.out_features) < 64:
-                logger.warning(f"Skipping layer '{name}' because it is too small "
-                               f"({module.in_features}x{module.out_features} < 64)")
-                continue
-            parent, attr = _get_parent_and_attr(model, name)
-            replacements.append((parent, attr, module))
+    replacements = _target_linears(model, target_modules)
     # one layer at a time, each source layer released once replaced, so the
     # peak holds one layer's 16-bit weight beside the quantized model
     replacements.reverse()

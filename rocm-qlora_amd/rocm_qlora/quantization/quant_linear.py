@@ -6,8 +6,9 @@ merged_fp16_weight), flat layouts, flags and state_dict keys as the
 reference, so checkpoints and model surgery carry over unchanged.  The
 forward pass is the HIP kernels': the weight is never materialised for bf16 /
 fp16 activations with K % 64 == 0 -- it is dequantized inside the GEMV / GEMM
--- and the other cases dequantize with the HIP codec kernel and call the
-library GEMM.  Inputs must be on the GPU.
+-- and the shapes the specialized kernels do not take (any K and block
+size, fp32 activations) run the generic HIP dequantize-and-multiply kernel.
+Inputs must be on the GPU.
 """
 from __future__ import annotations
 
@@ -71,6 +72,30 @@ class QuantLinear(nn.Module):
         del linear.weight
         if linear.bias is not None:
             del linear.bias
+        return inst
+
+    @classmethod
+    def empty_quantized(cls, in_features: int, out_features: int, bits: int = 8, bias: bool = True,
+                        block_size: int = 64, dtype: torch.dtype = torch.float32,
+                        device: Optional[torch.device] = None) -> "QuantLinear":
+        """A layer whose buffers have the shapes and dtypes from_linear gives
+        a `dtype` weight (codes [numel_padded] int8 or [numel_padded / 2]
+        uint8, squeezed absmax in `dtype`, bias in `dtype`), uninitialised:
+        the target of a state_dict saved after quantization."""
+        if bits not in (4, 8):
+            raise ValueError(f"Unsupported bit depth: {bits}")
+        if bits == 4 and (block_size < 2 or block_size % 2):
+            raise ValueError(f"block_size must be even and >= 2, got {block_size}")
+        if bits == 8 and block_size < 1:
+            raise ValueError("block_size must be >= 1")
+        inst = cls(in_features, out_features, bits=bits, bias=bias, block_size=block_size)
+        nb = -(-in_features * out_features // block_size)
+        n_codes = nb * block_size if bits == 8 else nb * block_size // 2
+        inst.weight_quant = torch.empty((n_codes,), dtype=torch.int8 if bits == 8 else torch.uint8, device=device)
+        inst.weight_scales = torch.empty((nb,), dtype=dtype, device=device).view(-1, 1).squeeze()
+        inst.weight_zeros = torch.zeros(1, device=device)
+        if bias:
+            inst.bias = torch.zeros(out_features, dtype=dtype, device=device)
         return inst
 
     def enable_kernel(self) -> bool:

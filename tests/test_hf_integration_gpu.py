@@ -5,7 +5,10 @@ loaded weights are quantized).  The codes of every target layer equal the
 oracle's quantize_int4 / quantize_int8 of the checkpoint's weight bit for
 bit, the logits match the same model run with the oracle's dequantized
 weights (tolerance 1e-2 of the largest logit: only summation order
-differs), and only the LoRA adapters train."""
+differs), and only the LoRA adapters train.  A quantized model saved with
+save_pretrained loads back (quantizer.py:90-91 of the reference: the
+quantizer is serializable) with the same codes, absmax, adapters and
+logits, bit for bit."""
 import os
 
 import pytest
@@ -88,3 +91,42 @@ def test_quantized_model_trains_with_paged_adamw(dev, tmp_path):
         losses.append(float(out.loss.detach()))
     assert all(torch.isfinite(torch.tensor(losses)))
     assert losses[-1] < losses[0]
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+def test_save_pretrained_round_trip(dev, tmp_path, bits):
+    from transformers import AutoModelForCausalLM
+    print(f"hf save/load bits={bits}", flush=True)
+    src, dst = tmp_path / "src", tmp_path / "dst"
+    _checkpoint(str(src))
+    qc = RocmQLoraConfig(bits=bits, lora_r=8, lora_alpha=16, lora_dropout=0.0, target_modules=TARGETS)
+    model = AutoModelForCausalLM.from_pretrained(str(src), quantization_config=qc, dtype=torch.bfloat16,
+                                                 device_map={"": dev.index or 0})
+    g = torch.Generator().manual_seed(3)
+    with torch.no_grad():
+        for mod in model.modules():
+            if isinstance(mod, LoRALinear):
+                mod.lora_B.copy_(0.02 * torch.randn(mod.lora_B.shape, generator=g))
+    model.save_pretrained(str(dst))
+    back = AutoModelForCausalLM.from_pretrained(str(dst), dtype=torch.bfloat16, device_map={"": dev.index or 0})
+    assert back.hf_quantizer.pre_quantized
+    n = 0
+    mods = dict(back.named_modules())
+    for name, mod in model.named_modules():
+        if not isinstance(mod, LoRALinear):
+            continue
+        n += 1
+        other = mods[name]
+        assert isinstance(other, LoRALinear), name
+        for a, b in ((mod.base_layer.weight_quant, other.base_layer.weight_quant),
+                     (mod.base_layer.weight_scales, other.base_layer.weight_scales),
+                     (mod.lora_A, other.lora_A), (mod.lora_B, other.lora_B)):
+            assert a.dtype == b.dtype and torch.equal(a, b), name
+    assert n == 2 * len(TARGETS)
+    ids = torch.randint(0, 512, (2, 16), generator=torch.Generator().manual_seed(4)).to(dev)
+    with torch.no_grad():
+        want = model(ids).logits
+        got = back(ids).logits
+    assert torch.equal(got, want)
+    trainable = {nm for nm, p in back.named_parameters() if p.requires_grad}
+    assert trainable and all(nm.endswith(("lora_A", "lora_B")) for nm in trainable)
