@@ -402,11 +402,12 @@ int rq_merge_lora(const void* w, int w_format, int64_t N, int64_t K, int64_t blo
 
 /* One tensor of a fused AdamW step (72 bytes).  The fp32 scalars are the
  * reference's Python doubles rounded to fp32 (as torch passes them to its
- * kernels), for this tensor's step count t:
+ * GPU kernels), for this tensor's step count t:
  *   decay = 1 - lr * weight_decay (applied when apply_decay, i.e. wd != 0),
  *   beta1, one_minus_beta1 = 1 - beta1, beta2, one_minus_beta2 = 1 - beta2,
- *   bias_correction2_sqrt = (1 - beta2 ** t) ** 0.5, eps,
- *   neg_step_size = -(lr / (1 - beta1 ** t)). */
+ *   inv_bias_correction2_sqrt = 1 / (1 - beta2 ** t) ** 0.5 (the reciprocal
+ *   taken in double: torch's GPU division by a host scalar multiplies by it),
+ *   eps, neg_step_size = -(lr / (1 - beta1 ** t)). */
 typedef struct rq_adamw_tensor {
   void* param;            /* [numel] of dtype, updated in place */
   const void* grad;       /* [numel] of dtype */
@@ -414,19 +415,20 @@ typedef struct rq_adamw_tensor {
   int64_t state_offset;   /* first element in the state buffers; multiple of RQ_ADAMW_CHUNK */
   int32_t dtype;          /* RQ_DTYPE_F32 / BF16 / F16, parameter and gradient */
   int32_t apply_decay;
-  float decay, beta1, one_minus_beta1, beta2, one_minus_beta2, bias_correction2_sqrt, eps, neg_step_size;
+  float decay, beta1, one_minus_beta1, beta2, one_minus_beta2, inv_bias_correction2_sqrt, eps, neg_step_size;
 } rq_adamw_tensor;
 
 /* Replaces the per-parameter update of PagedAdamW.step
  * (optim/paged_adamw.py:84-113): AdamW with decoupled weight decay on every
- * listed tensor in one launch, in the reference's order of operations --
- *   p = RND_p(p * decay); m = fma(1 - b1, g, RND(m * b1));
- *   v = fma(RND((1 - b2) * g), g, RND(v * b2));
- *   d = RND(RND(sqrt(v)) / bias_correction2_sqrt) + eps;
- *   p = RND_p(p + RND(RND(neg_step_size * m) / d))
- * (fp32 arithmetic, the square root correctly rounded, RND_p the rounding to
- * the parameter's dtype; the fused multiply-adds are where torch's kernels
- * fuse them).  The exp_avg (m) and exp_avg_sq (v) states are fp32 buffers
+ * listed tensor in one launch, with the roundings of the reference's ops as
+ * torch runs them on the GPU (the reference moves the states to the
+ * parameter's device for the update) --
+ *   p = RND_p(RND(p * decay)); m = fma(1 - b1, g, RND(m * b1));
+ *   v = fma(1 - b2, RND(g * g), RND(v * b2));
+ *   d = RND(RND(sqrt(v)) * inv_bias_correction2_sqrt) + eps;
+ *   p = RND_p(fma(neg_step_size, RND(m / d), p))
+ * (fp32 arithmetic, the square root and division correctly rounded, RND_p
+ * the rounding to the parameter's dtype).  The exp_avg (m) and exp_avg_sq (v) states are fp32 buffers
  * indexed by state offset: this call updates the chunks chunk_begin ..
  * chunk_end - 1, and exp_avg / exp_avg_sq (16-byte aligned) point at the
  * element chunk_begin * RQ_ADAMW_CHUNK and hold (chunk_end - chunk_begin) *

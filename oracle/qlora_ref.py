@@ -39,6 +39,12 @@ tests/test_oracle_linear.py:
     own implementation) over several steps; zero gradients give exactly
     p * (1 - lr wd)^t; a constant gradient moves p by lr * t * g / (|g| + eps)
     (bias-corrected moments equal g and g^2).
+  * fma32: exact rational arithmetic (fractions.Fraction) on random and on
+    constructed double-rounding cases.
+  * paged_adamw_step_device: the reference's ops run by torch on the GPU
+    (paged_adamw_step on device tensors), bit for bit, in the GPU tests;
+    within an ulp of paged_adamw_step per step and the same closed forms on
+    the CPU.
 No function of this module is left without such a check.
 """
 from __future__ import annotations
@@ -283,6 +289,73 @@ def paged_adamw_step(params, grads, exp_avgs, exp_avg_sqs, steps, lr: float = 2e
         denom = (root / (bias_correction2 ** 0.5)).add_(eps)                # :110
         step_size = lr / bias_correction1                                   # :111
         p.addcdiv_(exp_avg, denom, value=-step_size)                        # :113
+
+
+
+def fma32(a: torch.Tensor, b: torch.Tensor, c: torch.Tensor) -> torch.Tensor:
+    """RN32(a * b + c) with one rounding (an fp32 fused multiply-add) of fp32
+    tensors: the product is exact in float64, TwoSum gives the float64 sum's
+    rounding error, and a float64 sum that lands exactly on an fp32 rounding
+    midpoint is rounded to the side that error lies on."""
+    a64, b64, c64 = a.double(), b.double(), c.double()
+    s = a64 * b64
+    hi = s + c64
+    bb = hi - s
+    lo = (s - (hi - bb)) + (c64 - bb)
+    r = hi.float()
+    r64 = r.double()
+    up = torch.nextafter(r, torch.full_like(r, math.inf))
+    down = torch.nextafter(r, torch.full_like(r, -math.inf))
+    other = torch.where(hi > r64, up, down)
+    mid = (r64 + other.double()) * 0.5
+    tie = (hi == mid) & (lo != 0)
+    toward_other = torch.sign(lo) == torch.sign(other.double() - r64)
+    return torch.where(tie & toward_other, other, r)
+
+
+def _r32(x: float) -> torch.Tensor:
+    """A Python double rounded to fp32, as torch passes a scalar to an fp32
+    kernel."""
+    return torch.tensor(x, dtype=torch.float64).float()
+
+
+def paged_adamw_step_device(params, grads, exp_avgs, exp_avg_sqs, steps, lr: float = 2e-4,
+                            betas: Tuple[float, float] = (0.9, 0.999), eps: float = 1e-8,
+                            weight_decay: float = 0.01) -> None:
+    """One PagedAdamW step (paged_adamw.py:84-113) with the roundings torch's
+    GPU kernels give the reference's ops -- the reference moves the states to
+    the parameter's device (:98-99) and updates there -- restated on the CPU,
+    in place, arguments as paged_adamw_step.  Scalars are rounded to fp32;
+    p.mul_ is RND_p(RND(p * decay)); add_(g, alpha), addcmul_ and addcdiv_ are
+    fp32 fused multiply-adds of alpha * g, alpha * RND(g * g) and
+    alpha * RND(m / d) onto the first operand; the division by the host
+    scalar bc2 ** 0.5 is a multiply by RND(1 / bc2 ** 0.5), the reciprocal
+    taken in double; square root, division and the addition of eps are
+    correctly rounded (through float64, a second rounding that cannot change
+    an fp32 result: 53 >= 2 * 24 + 2)."""
+    beta1, beta2 = betas
+    for p, grad, exp_avg, exp_avg_sq, t in zip(params, grads, exp_avgs, exp_avg_sqs, steps):
+        if grad is None:
+            continue
+        bc1 = 1 - beta1 ** t                                                # :94
+        bc2 = 1 - beta2 ** t                                                # :95
+        g = grad.float()
+        pf = p.float()
+        if weight_decay != 0:                                               # :103-104
+            pf = (pf.double() * _r32(1 - lr * weight_decay).double()).float().to(p.dtype).float()
+        m = fma32(_r32(1 - beta1).expand_as(g), g,                          # :107
+                  (exp_avg.double() * _r32(beta1).double()).float())
+        gg = (g.double() * g.double()).float()
+        v = fma32(_r32(1 - beta2).expand_as(g), gg,                         # :108
+                  (exp_avg_sq.double() * _r32(beta2).double()).float())
+        root = v.double().sqrt().float()                                    # :110
+        den = (root.double() * _r32(1.0 / bc2 ** 0.5).double()).float()
+        den = (den.double() + _r32(eps).double()).float()
+        q = (m.double() / den.double()).float()                             # :111-113
+        new_p = fma32(_r32(-(lr / bc1)).expand_as(q), q, pf)
+        p.copy_(new_p.to(p.dtype))
+        exp_avg.copy_(m)
+        exp_avg_sq.copy_(v)
 
 
 # ----------------------------------------------------------- merge / export

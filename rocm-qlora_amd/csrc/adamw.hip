@@ -8,17 +8,21 @@
 // workgroup finds its tensor by binary search over the tensors' state
 // offsets in a small descriptor table.
 //
-// Per element, in the reference's order, fp32 arithmetic rounding where
-// torch's CPU kernels round (they fuse the multiply-adds of add_(alpha) and
-// addcmul_):
-//   p  = RND_p(p * decay)                       p.mul_(1 - lr * wd)     (wd != 0)
-//   m  = fma(1 - b1, g, RND(m * b1))            exp_avg.mul_(b1).add_(g, alpha=1 - b1)
-//   v  = fma(RND((1 - b2) * g), g, RND(v * b2)) exp_avg_sq.mul_(b2).addcmul_(g, g, value=1 - b2)
-//   d  = RND(RND(sqrt(v)) / sqrt(bc2)) + eps    (exp_avg_sq.sqrt() / bc2 ** 0.5).add_(eps)
-//   p  = RND_p(p + RND(RND(-step * m) / d))     p.addcdiv_(exp_avg, denom, value=-step_size)
+// Per element, the reference's ops with the roundings torch's GPU kernels
+// give them (the reference moves the states to the parameter's device and
+// updates there; its element-wise kernels evaluate `a + alpha * b`,
+// `a + alpha * (b * c)` and `a + alpha * (b / c)` in fp32 with the multiply
+// and add fused, and divide by a host scalar by multiplying with its
+// reciprocal, taken in double and rounded to fp32):
+//   p  = RND_p(RND(p * decay))                 p.mul_(1 - lr * wd)     (wd != 0)
+//   m  = fma(1 - b1, g, RND(m * b1))           exp_avg.mul_(b1).add_(g, alpha=1 - b1)
+//   v  = fma(1 - b2, RND(g * g), RND(v * b2))  exp_avg_sq.mul_(b2).addcmul_(g, g, value=1 - b2)
+//   d  = RND(RND(sqrt(v)) * RND(1 / sqrt(bc2))) + eps
+//                                              (exp_avg_sq.sqrt() / bc2 ** 0.5).add_(eps)
+//   p  = RND_p(fma(-step, RND(m / d), p))      p.addcdiv_(exp_avg, denom, value=-step_size)
 // with RND_p the rounding to the parameter's dtype (fp32, bf16, fp16), m and
-// v fp32, and the square root correctly rounded.  The memory traffic is 4
-// reads and 3 writes per element (p, g, m, v): HBM-bound.
+// v fp32, and the square root and division correctly rounded.  The memory
+// traffic is 4 reads and 3 writes per element (p, g, m, v): HBM-bound.
 #include "rq_common.h"
 #include "rq_launch.h"
 
@@ -39,12 +43,12 @@ template <int DT>
 __device__ __forceinline__ void adam_update(const rq_adamw_tensor& e, float& p, float g, float& m, float& v) {
   if (e.apply_decay) p = round_param<DT>(__fmul_rn(p, e.decay));
   m = __builtin_fmaf(e.one_minus_beta1, g, __fmul_rn(m, e.beta1));
-  v = __builtin_fmaf(__fmul_rn(e.one_minus_beta2, g), g, __fmul_rn(v, e.beta2));
+  v = __builtin_fmaf(e.one_minus_beta2, __fmul_rn(g, g), __fmul_rn(v, e.beta2));
   // __builtin_sqrtf is correctly rounded under hipcc's default fp32 options
   // (HIP's __fsqrt_rn is the approximate hardware square root unless
   // OCML_BASIC_ROUNDED_OPERATIONS is defined)
-  const float d = __fadd_rn(__fdiv_rn(__builtin_sqrtf(v), e.bias_correction2_sqrt), e.eps);
-  p = round_param<DT>(__fadd_rn(p, __fdiv_rn(__fmul_rn(e.neg_step_size, m), d)));
+  const float d = __fadd_rn(__fmul_rn(__builtin_sqrtf(v), e.inv_bias_correction2_sqrt), e.eps);
+  p = round_param<DT>(__builtin_fmaf(e.neg_step_size, __fdiv_rn(m, d), p));
 }
 
 // 8 elements from offset i of a tensor of dtype DT (16-byte aligned run).

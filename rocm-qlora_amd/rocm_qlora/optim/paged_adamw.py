@@ -38,7 +38,7 @@ _TABLE = np.dtype([
     ("param", "<u8"), ("grad", "<u8"), ("numel", "<i8"), ("state_offset", "<i8"),
     ("dtype", "<i4"), ("apply_decay", "<i4"),
     ("decay", "<f4"), ("beta1", "<f4"), ("one_minus_beta1", "<f4"), ("beta2", "<f4"),
-    ("one_minus_beta2", "<f4"), ("bias_correction2_sqrt", "<f4"), ("eps", "<f4"), ("neg_step_size", "<f4"),
+    ("one_minus_beta2", "<f4"), ("inv_bias_correction2_sqrt", "<f4"), ("eps", "<f4"), ("neg_step_size", "<f4"),
 ])
 assert _TABLE.itemsize == 72
 
@@ -187,14 +187,16 @@ class PagedAdamW(Optimizer):
                 lr, wd, eps, t = grp["lr"], grp["weight_decay"], grp["eps"], key[1]
                 bc1 = 1 - beta1 ** t                                      # paged_adamw.py:94-95
                 bc2 = 1 - beta2 ** t
-                v = cache[key] = (int(wd != 0), 1 - lr * wd, beta1, 1 - beta1, beta2, 1 - beta2, bc2 ** 0.5, eps,
-                                  -(lr / bc1))
+                # the division by bc2 ** 0.5 (paged_adamw.py:110) is a multiply
+                # by its reciprocal, taken in double, in torch's GPU kernel
+                v = cache[key] = (int(wd != 0), 1 - lr * wd, beta1, 1 - beta1, beta2, 1 - beta2,
+                                  1.0 / bc2 ** 0.5, eps, -(lr / bc1))
             vals.append(v)
         if vals:
             cols = list(zip(*vals))
             rows["apply_decay"] = cols[0]
             for name, col in zip(("decay", "beta1", "one_minus_beta1", "beta2", "one_minus_beta2",
-                                  "bias_correction2_sqrt", "eps", "neg_step_size"), cols[1:]):
+                                  "inv_bias_correction2_sqrt", "eps", "neg_step_size"), cols[1:]):
                 rows[name] = np.asarray(col, dtype=np.float64)  # rounded to fp32 once, to nearest
         first = rows["state_offset"] // ADAMW_CHUNK
         spans = list(zip(first.tolist(), (first + (rows["numel"] + ADAMW_CHUNK - 1) // ADAMW_CHUNK).tolist()))
