@@ -37,19 +37,20 @@ namespace rq {
 // tiles per wave for shorter K, several segments of one tile per wave for
 // longer K.
 //
-// HBM access of a unit: two 1 KiB loads, 8 lanes x 16 B per row (full
-// 128-byte lines; narrower per-row pieces cost HBM efficiency):
-//   load A: lane (n = l % 16, q = l / 16) reads row n % 8,     chunk q + 4 [n >= 8]
-//   load B: lane (n, q)                   reads row 8 + n % 8, chunk q + 4 [n < 8]
-// (chunk = 16 B = 32 k).  Then X1 = n < 8 ? A : B holds row n, chunk q in
-// every lane, and X2 = row_ror8(n >= 8 ? A : B) (a DPP rotate by 8 within
-// each 16-lane row) holds row n, chunk q + 4: the 16x16x32 MFMA B-operand
-// layout (lane l = row l % 16, k group l / 16) with no LDS round trip.
-// Steps 0-3 take X1's dwords, steps 4-7 X2's; the activation operand (A,
-// rows = tokens, zero past M) uses the same k order.  Each dword of codes
-// becomes RND(T[code] * scale) through the LDS pair table.  Every address is
-// a per-lane constant plus a wave-uniform unit offset, so a unit's loads cost
-// a few adds.
+// HBM access of a unit: two 1 KiB loads, 4 lanes x 16 B per row and load
+// (the two loads together read each row's 128-byte line):
+//   load A: lane (n = l % 16, q = l / 16) reads row n, chunk q      -> X1
+//   load B: lane (n, q)                   reads row n, chunk q + 4  -> X2
+// (chunk = 16 B = 32 k): the 16x16x32 MFMA B-operand layout (lane l = row
+// l % 16, k group l / 16) straight from the loads, with no lane exchange or
+// LDS round trip.  Steps 0-3 take X1's dwords, steps 4-7 X2's; the
+// activation operand (A, rows = tokens, zero past M) uses the same k order.
+// Each dword of codes becomes RND(T[code] * scale) through the LDS pair
+// table.  Every address is a per-lane constant plus a wave-uniform unit
+// offset, so a unit's loads cost a few adds.  (Loads of 8 lanes x 16 B per
+// row, with the halves exchanged by a select and a DPP row rotate, measured
+// 0.4-0.7 us slower per launch at the 14336 x 4096 shapes: the twelve lane
+// operations per unit cost more than the wider pieces gain.)
 //
 // Schedule.  The code is straight-line: the units are unrolled, no load sits
 // under a branch and no loaded value is carried around a loop, so the
@@ -105,7 +106,12 @@ struct GemvArgs {
   int bs_log2;             // log2(block_size)
   int nseg;                // segments per K split
   int TS;                  // tiles per workgroup
-  bool direct;             // epilogue in this kernel (else fp32 partials to ws)
+  bool direct;             // one K split: the epilogue in this kernel
+  // K splits (gridDim.y > 1): fp32 partials [S][M][N] to ws; with tile_cnt
+  // the last split of a workgroup column to count itself (tile_cnt[g],
+  // zero between launches) sums the splits' partials in split order and
+  // runs the epilogue, else a finisher launch does
+  uint32_t* tile_cnt;
   bool xvec;               // x rows 16-byte aligned (vector loads)
   int bvec_log2;           // LoRA B rows read as 16-byte chunks, 2^bvec_log2 per row (-1: by element)
   float* ws;               // [S, M, N] partials when !direct
@@ -325,17 +331,10 @@ __device__ __forceinline__ void gemv_issue(GemvUnit<Scale>& U, const GemvArgs& a
   }
 }
 
-__device__ __forceinline__ uint32_t row_ror8(uint32_t v) {
-  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x128, 0xF, 0xF, false));
-}
-
 template <int XT, class Scale>
 __device__ __forceinline__ f32x4 gemv_tile(const GemvUnit<Scale>& U, float s1, float s2, const u32x4 (&xa)[8],
-                                           const u32x2* lut, uint32_t lane_off, int n16) {
-  const bool lo = n16 < 8;
-  const u32x4 X1 = lo ? U.a : U.b;
-  const u32x4 Y = lo ? U.b : U.a;
-  const u32x4 X2 = u32x4{row_ror8(Y.x), row_ror8(Y.y), row_ror8(Y.z), row_ror8(Y.w)};
+                                           const u32x2* lut, uint32_t lane_off) {
+  const u32x4 X1 = U.a, X2 = U.b;
   f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   acc = mfma16x16x32<XT>(xa[0], expand8_scaled<XT>(lut, X1.x, lane_off, s1), acc);
   acc = mfma16x16x32<XT>(xa[1], expand8_scaled<XT>(lut, X1.y, lane_off, s1), acc);
@@ -512,7 +511,9 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   const int M = a.M, TS = a.TS, nseg = a.nseg;
   const bool fused = a.jobs > 0;
   const uint32_t g = blockIdx.x, G = gridDim.x;  // this workgroup, their number
-  const int rank = (a.direct && e.rank > 0) ? e.rank : 0;  // LoRA staging only when fused here
+  const bool fold = !a.direct && a.tile_cnt != nullptr;  // K splits finished in this launch
+  const bool epi = a.direct || fold;                     // the epilogue runs in this launch
+  const int rank = (epi && e.rank > 0) ? e.rank : 0;     // LoRA staging only when fused here
   constexpr int RP = kGemvMaxFusedRank;                    // staging pitch
   constexpr bool kGather = GemvScale<Scale>::kGather;
   float* part = reinterpret_cast<float*>(smem);
@@ -533,10 +534,9 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   ln.n16 = lane & 15;
   ln.q = lane >> 4;
   {
-    const uint32_t half_k = uint32_t(a.K) >> 1, n7 = uint32_t(ln.n16 & 7);
-    const uint32_t cA = uint32_t(ln.q) + (ln.n16 >= 8 ? 4u : 0u), cB = uint32_t(ln.q) + (ln.n16 < 8 ? 4u : 0u);
-    ln.offA = n7 * half_k + 16u * cA;
-    ln.offB = (8u + n7) * half_k + 16u * cB;
+    const uint32_t half_k = uint32_t(a.K) >> 1;
+    ln.offA = uint32_t(ln.n16) * half_k + 16u * uint32_t(ln.q);
+    ln.offB = uint32_t(ln.n16) * half_k + 16u * (uint32_t(ln.q) + 4u);
     // block offsets of k1 = 32 q and k2 = 128 + 32 q within a segment (zero
     // when a block spans whole segments), from the tile's first row
     const uint32_t rowb = uint32_t(ln.n16) * uint32_t(a.bpr);
@@ -582,14 +582,24 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   }
   const __amdgpu_buffer_rsrc_t xres =
       buffer_rsrc(a.x, uint32_t(M - 1) * uint32_t(a.ldx) * 2u + uint32_t(a.K) * 2u);
+  // units in flight ahead of the one being computed (two measured slower:
+  // the extra bytes in flight only lengthened the loaded latency)
+  constexpr int D = 1;
+  GemvUnit<Scale> L[U];
+  // without the slices (M > 2) the first unit's weights go out before
+  // anything else (0.4-1 us faster per launch at M = 4-16 than after the
+  // LoRA and scale loads); with them the activations and weights go out
+  // after those loads (weights first measured 0.5-0.9 us slower at M = 1)
+  if constexpr (XM == 0) {
+#pragma unroll
+    for (int u = 0; u < D; ++u)
+      gemv_issue<XM>(L[u], a, sc, wres, xres, ln, tile_of(ut[u]), seg0 + uint32_t(useg[u]), ulive[u]);
+  }
 
   // 1. the first unit's loads; without the slice, this wave's own
   //    activation operands (its units share one segment): step c covers k =
   //    seg * 256 + 128 (c / 4) + 32 q + 8 (c % 4) of token n16; a token past M
   //    or a k past K reads zeros
-  // units in flight ahead of the one being computed (two measured slower:
-  // the extra bytes in flight only lengthened the loaded latency)
-  constexpr int D = 1;
   // this wave's LoRA down-projection job, if any: its first chunk's loads go
   // out before the unit loads, so that waiting for them never waits for the
   // weights
@@ -634,10 +644,11 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     const uint32_t blk = (tile_of(gt) * 16u + uint32_t(ln.n16)) * uint32_t(a.bpr) + first;
     gsv = sc.gather(glive && gu < U ? blk : kDeadBlock);
   }
-  GemvUnit<Scale> L[U];
+  if constexpr (XM == 1) {
 #pragma unroll
-  for (int u = 0; u < D; ++u)
-    gemv_issue<XM>(L[u], a, sc, wres, xres, ln, tile_of(ut[u]), seg0 + uint32_t(useg[u]), ulive[u]);
+    for (int u = 0; u < D; ++u)
+      gemv_issue<XM>(L[u], a, sc, wres, xres, ln, tile_of(ut[u]), seg0 + uint32_t(useg[u]), ulive[u]);
+  }
   u32x4 xa[8];
   if constexpr (XM == 0) {
     const uint32_t sg = seg0 + uint32_t(useg[0]);
@@ -729,7 +740,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     const bool live = bvec_live && bn < uint32_t(a.N);
     bvr = buf_load16(bres, live ? bn * uint32_t(e.ld_lora_b) * bbytes + 16u * uint32_t(bc) : kOobOffset);
   }
-  const bool has_bias = a.direct && e.bias != nullptr;
+  const bool has_bias = epi && e.bias != nullptr;
   if (has_bias && ew == 0) {
     const __amdgpu_buffer_rsrc_t bres = buffer_rsrc(e.bias, uint32_t(a.N) * (e.bias_dt == RQ_DTYPE_F32 ? 4u : 2u));
     const int cb = et & (kGemvMaxTS * 16 - 1);
@@ -778,7 +789,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
         s1 = sc.v1(L[u].sp);
         s2 = sc.v2(L[u].sp);
       }
-      const f32x4 acc = gemv_tile<XT>(L[u], s1, s2, xa, lut, lane_off, ln.n16);
+      const f32x4 acc = gemv_tile<XT>(L[u], s1, s2, xa, lut, lane_off);
       float* pp = part + (ut[u] * nseg + useg[u]) * M * 16 + ln.n16;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -874,7 +885,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
       }
     }
   }
-  if (a.direct && et < TS * 16) bss[et] = has_bias ? round_x<XT>(elem_to_f32(br, e.bias_dt)) : 0.0f;
+  if (epi && et < TS * 16) bss[et] = has_bias ? round_x<XT>(elem_to_f32(br, e.bias_dt)) : 0.0f;
   if (rank > 0) {
     // u[m, j]: each thread sums its 16 splits in order, then lane c = 0 of
     // the (m, j) adds the C threads' sums in c order (adjacent lanes of one
@@ -891,34 +902,22 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   }
   lds_barrier();
 
-  // 7. the outputs, then (in-launch LoRA) wave 0 learns whether this was
-  //    the launch's last workgroup to count itself
-  auto finish = [&]() {
-    const int t = tid >> 8, m = (tid >> 4) & 15, nn = tid & 15;
-    if (t >= TS || m >= M) return;
-    const uint32_t tile = tile_of(t);
-    const int64_t n = int64_t(tile) * 16 + nn;
-    if (tile >= n_tiles || n >= a.N) return;
-    const float* pp = part + t * nseg * M * 16 + m * 16 + nn;
-    float v = 0.0f;
-    int sgi = 0;
-    for (; sgi + 8 <= nseg; sgi += 8) {
-      float p[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) p[j] = pp[(sgi + j) * M * 16];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v = __fadd_rn(v, p[j]);
-    }
-    for (; sgi < nseg; ++sgi) v = __fadd_rn(v, pp[sgi * M * 16]);
-    if (!a.direct) {
-      a.ws[(int64_t(blockIdx.y) * a.M + m) * a.N + n] = v;
-      return;
-    }
-    if (e.bias) v = __fadd_rn(v, bss[t * 16 + nn]);
+  // 7. the outputs (with K splits: this split's partials, and in the last
+  //    split of the column to count itself, the outputs), then (in-launch
+  //    LoRA) wave 0 learns whether this was the launch's last workgroup to
+  //    count itself.  One thread per output: tile slot t = tid / 256, row m,
+  //    column nn.
+  const int ft = tid >> 8, fm = (tid >> 4) & 15, fnn = tid & 15;
+  const uint32_t ftile = tile_of(ft);
+  const int64_t fn = int64_t(ftile) * 16 + fnn;
+  const bool fout = ft < TS && fm < M && ftile < n_tiles && fn < a.N;
+  // bias, RND, the LoRA term, RND, store
+  auto epilogue = [&](float v) {
+    if (e.bias) v = __fadd_rn(v, bss[ft * 16 + fnn]);
     v = round_x<XT>(v);
     if (rank > 0) {
-      const uint16_t* brow = lbs + (t * 16 + nn) * RP;
-      const float* urow = us + m * RP;
+      const uint16_t* brow = lbs + (ft * 16 + fnn) * RP;
+      const float* urow = us + fm * RP;
       float l = 0.0f;
       for (int j0 = 0; j0 < rank; j0 += 8) {
         float uu[8], bb[8];
@@ -934,9 +933,65 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
       l = round_x<XT>(__fmul_rn(round_x<XT>(l), e.scaling));
       v = round_x<XT>(__fadd_rn(v, l));
     }
-    static_cast<uint16_t*>(e.y)[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
+    static_cast<uint16_t*>(e.y)[fm * e.ldy + fn] = uint16_t(to_x16<XT>(v));
   };
-  finish();
+  if (fout) {
+    // this workgroup's segments in order
+    const float* pp = part + ft * nseg * M * 16 + fm * 16 + fnn;
+    float v = 0.0f;
+    int sgi = 0;
+    for (; sgi + 8 <= nseg; sgi += 8) {
+      float p[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) p[j] = pp[(sgi + j) * M * 16];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v = __fadd_rn(v, p[j]);
+    }
+    for (; sgi < nseg; ++sgi) v = __fadd_rn(v, pp[sgi * M * 16]);
+    if (a.direct) {
+      epilogue(v);
+    } else {
+      float* dst = a.ws + (int64_t(blockIdx.y) * a.M + fm) * a.N + fn;
+      // device-coherent when another workgroup sums it
+      if (fold) __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else *dst = v;
+    }
+  }
+  if (fold) {
+    // every thread's partials written (the stores complete, device-wide),
+    // then the column counts this split; the last one to count sums every
+    // split's partials, in split order (the same sums whichever is last),
+    // and resets the count for the next launch
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    uint32_t* last_flag = reinterpret_cast<uint32_t*>(lut);  // the table is no longer read
+    if (tid == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(&a.tile_cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const bool last = old == gridDim.y - 1u;
+      if (last) __hip_atomic_store(&a.tile_cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *last_flag = last ? 1u : 0u;
+    }
+    __syncthreads();
+    if (__builtin_amdgcn_readfirstlane(*last_flag) && fout) {
+      const int S = int(gridDim.y);
+      const float* src = a.ws + int64_t(fm) * a.N + fn;
+      const int64_t sstride = int64_t(a.M) * a.N;
+      float v = 0.0f;
+      for (int s0 = 0; s0 < S; s0 += 8) {
+        // eight splits' partials in flight together (a split past S
+        // re-reads the first and is not added)
+        float p[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          p[k] = __hip_atomic_load(src + (s0 + k < S ? s0 + k : 0) * sstride, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (s0 + k < S) v = __fadd_rn(v, p[k]);
+      }
+      epilogue(v);
+    }
+  }
   if (has_job && __builtin_amdgcn_readfirstlane(jc_old) == uint32_t(a.jobs) - 1u) {
     // the last job: clear the other region (the previous launch's partials,
     // whose readers have all finished), record this launch's extent in
@@ -1179,6 +1234,10 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     const int R = kGemvWaves / nseg;  // tile slots per round without the slices
     const int ts_cap = xslice ? (kGemvWaves * kGemvMaxU) / nseg : kGemvMaxU * R;
     const bool direct = S == 1 && lora_fusable;
+    // K splits whose last split runs the epilogue: the LoRA term's operands
+    // staged like the direct epilogue's, one counter per workgroup column
+    const bool fold = S > 1 && lora_fusable;
+    const bool epi_lds = (direct || fold) && rank > 0;
     // LDS of the in-launch down-projection: the wait flag
     bool in_launch = direct && rank > 0 && lora_prod;
     const size_t job_lds = in_launch ? 16 : 0;
@@ -1189,7 +1248,7 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     for (int TS = 1; TS <= kGemvMaxTS && TS <= ts_cap; ++TS) {
       const int U = xslice ? (TS * nseg + kGemvWaves - 1) / kGemvWaves : (TS + R - 1) / R;
       if (U != 1 && U != 2 && U != 4) continue;
-      if (gemv_lds_bytes(TS, nseg, int(M), gather, xslice, direct && rank > 0) + job_lds > size_t(kGemvLdsBudget))
+      if (gemv_lds_bytes(TS, nseg, int(M), gather, xslice, epi_lds) + job_lds > size_t(kGemvLdsBudget))
         continue;
       const int64_t grid = (tiles + TS - 1) / TS;
       const int64_t cost = ((grid * S + ncu - 1) / ncu) * TS;
@@ -1227,9 +1286,10 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     p.U = xslice ? (best * nseg + kGemvWaves - 1) / kGemvWaves : (best + R - 1) / R;
     p.grid = int((tiles + best - 1) / best);
     p.direct = direct;
+    p.fold = fold && p.grid <= int(kGemmCountBytes / 4);
     break;
   }
-  p.lds_bytes = gemv_lds_bytes(p.TS, p.nseg, int(M), gather, p.xslice, p.direct && rank > 0);
+  p.lds_bytes = gemv_lds_bytes(p.TS, p.nseg, int(M), gather, p.xslice, (p.direct || p.fold) && rank > 0);
   if (p.jobs > 0) p.lds_bytes += 16;  // the wait flag after RND(u)
   // workspace: the synchronization area (the in-launch down-projection's
   // count and partials, left zero by every launch), the split-K partials,
@@ -1315,6 +1375,8 @@ static int launch_gemv_t(const LinearArgs& L, const GemvPlan& p, Scale scale, co
   a.nseg = p.nseg;
   a.TS = p.TS;
   a.direct = p.direct;
+  a.tile_cnt = p.fold ? reinterpret_cast<uint32_t*>(static_cast<char*>(sync) + kLinearCountBytes + 2 * kGemvPartBytes)
+                      : nullptr;
   a.xvec = gemv_xvec(L);
   a.bvec_log2 = gemv_bvec_log2(L);
   a.jobs = p.jobs;
@@ -1480,7 +1542,7 @@ int run_nf4_gemv(const LinearArgs& L, void* workspace, size_t ws_bytes, hipStrea
   }
   if (L.x_dtype == RQ_DTYPE_BF16) st = run_gemv<RQ_DTYPE_BF16>(L, p, e, ws, workspace, stream);
   else st = run_gemv<RQ_DTYPE_F16>(L, p, e, ws, workspace, stream);
-  if (st != RQ_OK || p.direct) return st;
+  if (st != RQ_OK || p.direct || p.fold) return st;
   if (L.x_dtype == RQ_DTYPE_BF16) return launch_splitk_epilogue<RQ_DTYPE_BF16>(L, p, e, ws, stream);
   return launch_splitk_epilogue<RQ_DTYPE_F16>(L, p, e, ws, stream);
 }

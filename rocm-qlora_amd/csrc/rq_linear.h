@@ -20,8 +20,8 @@ constexpr int64_t kGemvMaxM = 16;
 //                          partial region, the extents of regions 0 and 1)
 //   [256, 256 + 64 KiB)    its two partial regions of kGemvPartBytes; the
 //                          one the parity names is zero between launches
-//   [.., + 64 KiB)         the GEMM's K-split tile counters, zero between
-//                          launches
+//   [.., + 64 KiB)         the GEMM's and the decode GEMV's K-split
+//                          counters, zero between launches
 // Every call leaves the area in that state once its kernels are done; the
 // GEMM's workspace and the split-K partials start after the area.
 constexpr size_t kLinearSyncBytes = RQ_LINEAR_SYNC_BYTES;
@@ -78,6 +78,7 @@ struct GemvPlan {
   int S, TS, U, nseg, grid, u_splits;
   int jobs;  // LoRA down-projection wave jobs inside the launch (0: none)
   bool direct, xslice;
+  bool fold;  // K splits finished by the last split of each column (no finisher launch)
   size_t lds_bytes, ws_bytes, u_offset;
 };
 

@@ -105,6 +105,26 @@ def test_gemv_tiling_cases(dev, N, K, M, rank):
     _check(y, ref)
 
 
+@pytest.mark.parametrize("M,rank", [(4, 16), (16, 64), (8, 96)])
+def test_gemv_k_splits(dev, M, rank):
+    """K = 14336 at M > 2 runs as 4 K splits.  With rank <= 64 the last split
+    of each workgroup column to count itself sums the splits' partials and
+    runs the epilogue in the same launch (rank 96: the finisher launch).
+    Bias + LoRA against the oracle; three calls bit-identical, whichever split
+    counts itself last, which also shows the counters left at zero."""
+    N, K = 4096, 14336
+    print(f"gemv k splits M={M} r={rank}", flush=True)
+    w, x, a, b, bvec = _inputs(N, K, M, torch.bfloat16, seed=M + rank, rank=rank, bias=True)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    args = (x.to(dev), packed, absmax, N, 64)
+    kw = dict(bias=bvec.to(dev), lora_a=a.to(dev), lora_b=b.to(dev), scaling=0.25)
+    ys = [ops.nf4_linear(*args, **kw) for _ in range(3)]
+    wf = R.dequantize_int4(packed.cpu(), absmax.cpu(), 64)
+    ref = R.lora_forward(x, R.quant_linear_forward(x, wf, bvec, N, K), a, b, 0.25)
+    _check(ys[0], ref)
+    assert torch.equal(ys[0], ys[1]) and torch.equal(ys[0], ys[2])
+
+
 def test_gemv_double_quant(dev):
     N, K, M = 2048, 4096, 3
     w, x, a, b, _ = _inputs(N, K, M, torch.bfloat16, seed=21)
