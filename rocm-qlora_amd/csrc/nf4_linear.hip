@@ -118,8 +118,9 @@ struct GemvArgs {
   // LoRA down-projection inside this launch (jobs > 0): job b computes the
   // fp32 partials of ranks [16 (b / u_splits), +16) over K split
   // b % u_splits, one wave per job (wave b / G of workgroup b % G, G the
-  // workgroups, waves counted from the last when the last waves have fewer
-  // units, else from wave 1), into region P [u_splits][M][rank] of parts,
+  // workgroups of the launch, workgroup (g, s) of K split s counted as
+  // s gridDim.x + g; waves counted from the last when the last waves have
+  // fewer units, else from wave 1), into region P [u_splits][M][rank] of parts,
   // P = bit 0 of state[0] as read at the launch's start, +0.0 stored as -0.0
   // so that 0 means "not written yet"; after its units every workgroup polls the
   // partials until none is 0.  No workgroup waits on a count at its end:
@@ -609,7 +610,9 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   // 0, which polls the partials, reaches its poll as early as it can (the
   // oldest wave of a SIMD finishes its units first)
   const bool light_top = XM == 1 ? (TS * nseg) % kGemvWaves != 0 : (kGemvWaves / nseg) * nseg < kGemvWaves;
-  const int job = (light_top ? kGemvWaves - 1 - wave : (wave + kGemvWaves - 1) % kGemvWaves) * int(G) + int(g);
+  // (workgroups counted over the K splits too: G columns per split)
+  const int job = (light_top ? kGemvWaves - 1 - wave : (wave + kGemvWaves - 1) % kGemvWaves) * int(G * gridDim.y) +
+                  int(blockIdx.y * G + g);
   const bool has_job = fused && job < a.jobs;
   // this launch's partial region and the other region's extent, loaded by
   // wave 0 (which passes the parity on through LDS) and the job waves (the
@@ -1222,6 +1225,7 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     const int64_t ks = (K / 32 + steps_per_wg - 1) / steps_per_wg;
     p.u_splits = lora_prod ? fused_splits : int(ks < kGemvMaxUSplits ? ks : kGemvMaxUSplits);
   }
+  const int launched_splits = p.u_splits;  // of the down-projection launched before the GEMV
   const bool lora_fusable = rank <= 0 || (rank <= kGemvMaxFusedRank && lora_vec);
   for (int slice = 1; slice >= 0; --slice) {
     // activations through the waves' LDS slices: any unit to any wave
@@ -1239,7 +1243,7 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     const bool fold = S > 1 && lora_fusable;
     const bool epi_lds = (direct || fold) && rank > 0;
     // LDS of the in-launch down-projection: the wait flag
-    bool in_launch = direct && rank > 0 && lora_prod;
+    bool in_launch = (direct || fold) && rank > 0 && lora_prod;
     const size_t job_lds = in_launch ? 16 : 0;
     // best tile count per workgroup: the fewest tiles a compute unit works
     // through one after another, the largest such count
@@ -1261,13 +1265,13 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
     p.jobs = 0;
     // the jobs' handshake assumes every workgroup of the launch is resident
     // at once (one per compute unit)
-    if ((tiles + best - 1) / best > ncu) in_launch = false;
+    if ((tiles + best - 1) / best * S > ncu) in_launch = false;
     if (in_launch) {
       // wave jobs of one chunk each where the limits allow: C threads of
       // 16 splits per (m, j) with M rank C <= 1024 threads (C a power of
       // two, at most kJobMaxC; the partials then fit the synchronization
       // area), at most one job per wave
-      const int64_t grid = (tiles + best - 1) / best;
+      const int64_t grid = (tiles + best - 1) / best * S;  // workgroups of the launch
       const int64_t nsteps = K / 32, groups = (rank + 15) / 16, mr = M * rank;
       int64_t cmax = 1;
       while (cmax < kJobMaxC && mr * cmax * 2 <= kGemvThreads) cmax *= 2;
@@ -1278,6 +1282,13 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
       ns = std::max<int64_t>(ns, 1);
       p.u_splits = int(ns);
       p.jobs = int(groups * ns);
+      // with K splits, only jobs of one chunk each: longer jobs end after
+      // the splits' units (a 14-step job at M = 16, K = 14336 made the
+      // launch 5 us slower than the down-projection launched before it)
+      if (fold && ns * kJobChunk < nsteps) {
+        p.jobs = 0;
+        p.u_splits = launched_splits;
+      }
     }
     p.S = S;
     p.nseg = nseg;
@@ -1298,7 +1309,7 @@ GemvPlan plan_gemv(int64_t M, int64_t N, int64_t K, int64_t rank, int cus, bool 
   const bool in_launch = p.jobs > 0;
   const size_t uparts = (rank > 0 && !in_launch) ? size_t(p.u_splits) * M * rank * 4 : 0;
   p.u_offset = kLinearSyncBytes + ((parts + 255) & ~size_t(255));
-  p.ws_bytes = in_launch ? kLinearSyncBytes : (parts + uparts > 0 ? p.u_offset + uparts : 0);
+  p.ws_bytes = parts + uparts > 0 ? p.u_offset + uparts : (in_launch ? kLinearSyncBytes : 0);
   return p;
 }
 
