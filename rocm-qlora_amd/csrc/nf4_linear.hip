@@ -169,6 +169,9 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
 __device__ __forceinline__ u32x4 buf_load16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherent));
 }
+__device__ __forceinline__ uint32_t buf_load4_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return uint32_t(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCoherent));
+}
 __device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
 }
@@ -813,12 +816,14 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     const uint32_t* region = a.parts + flag[1] * uint32_t(kGemvPartWords);
     if (u_mine) {
       bool ok = false;
+      // device-coherent loads through a buffer resource: 32-bit offsets,
+      // one address add per load
+      const __amdgpu_buffer_rsrc_t rres = buffer_rsrc(region, uint32_t(kGemvPartBytes));
       auto poll = [&]() {
         // all the loads of a poll in flight together: no branch between
         // them (a split past ns reads the first again and is not checked)
 #pragma unroll
-        for (int k = 0; k < kUPerThread; ++k)
-          up[k] = __hip_atomic_load(&region[u_index(k)], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int k = 0; k < kUPerThread; ++k) up[k] = buf_load4_coherent(rres, u_index(k) * 4u);
         uint32_t missing = 0u;
 #pragma unroll
         for (int k = 0; k < kUPerThread; ++k)
