@@ -100,7 +100,8 @@ CODEC_COPIES = 5               # 11008x4096 bf16 weights and their codes: 5 x 11
 GEMV_TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "nf4_gemv_kernel_traffic.md")
 COPY_BYTES = 512 << 20         # calibration copy: 512 MiB read + 512 MiB written
 # (shape, LoRA fused) of the counter run, in launch order
-GEMV_COUNTER_CONFIGS = [("gate", False), ("gate", True), ("k", False), ("k", True)]
+GEMV_COUNTER_CONFIGS = [("gate", False, 1), ("gate", True, 1), ("k", False, 1), ("k", True, 1),
+                        ("gate", False, 16), ("gate", True, 16), ("k", False, 16), ("k", True, 16)]
 
 
 def profiled_traffic(shape, mode, M, K, N, path=GEMV_TRAFFIC_PROFILE):
@@ -771,18 +772,19 @@ def run_counters_kernel(which, reps=4):
 def run_counters(reps=4):
     """Eager launches for counter collection: one plain device copy of
     COPY_BYTES (calibration: its FETCH_SIZE / WRITE_SIZE readings against the
-    bytes it must move), then the decode GEMV (M = 1) for each of
+    bytes it must move), then the decode GEMV for each (shape, LoRA, M) of
     GEMV_COUNTER_CONFIGS in turn -- the gate/up shape (K = 4096, N = 14336)
     over the gate and up weights of six layer copies, the k/v shape (K =
     4096, N = 1024) over the k and v weights, plain and with the LoRA term
-    fused (r = 16) -- `reps` rounds over the 12 weights each, so every
-    launch reads its weights from HBM (past the 256 MB MALL)."""
+    fused (r = 16), at M = 1 and 16 -- `reps` rounds over the 12 weights
+    each, so every launch reads its weights from HBM (past the 256 MB
+    MALL)."""
     import torch
     from rocm_qlora import ops
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     layers = [make_layer(dev, 1000 + c) for c in range(6)]
-    x = torch.randn(1, 4096, device=dev).to(torch.bfloat16)
+    xs = {m: torch.randn(m, 4096, device=dev).to(torch.bfloat16) for m in sorted({c[2] for c in GEMV_COUNTER_CONFIGS})}
     src = torch.randint(0, 255, (COPY_BYTES,), dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     torch.cuda.synchronize()
@@ -790,7 +792,8 @@ def run_counters(reps=4):
     torch.cuda.synchronize()
     del src, dst
     names = {"gate": ("gate", "up"), "k": ("k", "v")}
-    for shape, lora in GEMV_COUNTER_CONFIGS:
+    for shape, lora, m in GEMV_COUNTER_CONFIGS:
+        x = xs[m]
         ws = [layer[nm] for layer in layers for nm in names[shape]]
         for _ in range(reps):
             for packed, absmax, a, b, N, K in ws:
@@ -799,14 +802,14 @@ def run_counters(reps=4):
                 else:
                     ops.nf4_linear(x, packed, absmax, N, BLOCK)
         torch.cuda.synchronize()
-        print(f"counters: {reps * len(ws)} launches {shape} {'lora' if lora else 'plain'}", flush=True)
+        print(f"counters: {reps * len(ws)} launches {shape} {'lora' if lora else 'plain'} M={m}", flush=True)
     print(f"counters: copy {COPY_BYTES} B, then {GEMV_COUNTER_CONFIGS}", flush=True)
 
 
 def summarize_counters(paths):
     """Per-kernel mean of each counter over the dispatches in rocprofv3 CSV
     counter files (`-f csv`).  For a `--counters gemv` run, also per (shape,
-    mode) of GEMV_COUNTER_CONFIGS: the dispatches after the calibration copy
+    mode, M) of GEMV_COUNTER_CONFIGS: the dispatches after the calibration copy
     are taken in dispatch order, the library's kernels only (a LoRA operand
     kernel counts with the GEMV launch that follows it), and each counter's
     mean per launch printed; FETCH_SIZE and WRITE_SIZE (KiB per dispatch)
@@ -865,27 +868,27 @@ def summarize_counters(paths):
     shapes = {"gate": (4096, 14336), "k": (4096, 1024)}
     counters = sorted({c for _, c in acc})
     print("| config | " + " | ".join(counters) + " |")
-    for ci, (shape, lora) in enumerate(GEMV_COUNTER_CONFIGS):
+    for ci, (shape, lora, m) in enumerate(GEMV_COUNTER_CONFIGS):
         cells = []
         for cname in counters:
             a = acc.get((ci, cname))
             cells.append(f"{a[0] / a[1]:,.0f}" if a else "-")
-        print(f"| {shape} {'lora' if lora else 'plain'} | " + " | ".join(cells) + " |")
+        print(f"| {shape} {'lora' if lora else 'plain'} M={m} | " + " | ".join(cells) + " |")
     if "FETCH_SIZE" in factor and "WRITE_SIZE" in factor:
         print()
         print(f"calibration: FETCH_SIZE factor {factor['FETCH_SIZE']:.4f}, WRITE_SIZE factor "
               f"{factor['WRITE_SIZE']:.4f} (counter bytes per copied byte)")
         print("| kernel | shape | mode | M | K | N | fetch B | write B | total B | algorithmic B | ratio |")
         print("|---|---|---|---|---|---|---|---|---|---|---|")
-        for ci, (shape, lora) in enumerate(GEMV_COUNTER_CONFIGS):
+        for ci, (shape, lora, m) in enumerate(GEMV_COUNTER_CONFIGS):
             fe, wr = acc.get((ci, "FETCH_SIZE")), acc.get((ci, "WRITE_SIZE"))
             if not fe or not wr:
                 continue
             K, N = shapes[shape]
             fb = fe[0] / fe[1] * 1024.0 / factor["FETCH_SIZE"]
             wb = wr[0] / wr[1] * 1024.0 / factor["WRITE_SIZE"]
-            alg = gemv_bytes(1, N, K) if lora else kernel_bytes(1, N, K)
-            print(f"| nf4_gemv_kernel | {shape} | {'lora' if lora else 'plain'} | 1 | {K} | {N} | {fb:,.0f} | "
+            alg = gemv_bytes(m, N, K) if lora else kernel_bytes(m, N, K)
+            print(f"| nf4_gemv_kernel | {shape} | {'lora' if lora else 'plain'} | {m} | {K} | {N} | {fb:,.0f} | "
                   f"{wb:,.0f} | {fb + wb:,.0f} | {alg:,} | {(fb + wb) / alg:.3f} |")
 
 

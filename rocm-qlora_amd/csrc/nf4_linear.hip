@@ -84,6 +84,14 @@ constexpr int kSegK = 256;
 constexpr int kGemvMaxU = 4;           // units per wave
 constexpr int kGemvMaxTS = 4;          // tiles per workgroup
 constexpr int kGemvMaxFusedRank = 64;  // LoRA rank the in-kernel epilogue stages
+// LDS pitches of the staged LoRA operands, padded so that the epilogue's
+// reads are free of bank conflicts: the 16 output columns of a wave read 16
+// B rows (16-bit, 144 bytes apart: 16 distinct groups of 4 banks) and its
+// four output rows read four u rows (fp32, 272 bytes apart).  Unpadded
+// (128 / 256 bytes) the reads were 8-way / 4-way conflicted: 10 % of the
+// LoRA launch's LDS cycles at M = 16.
+constexpr int kGemvBPitch = kGemvMaxFusedRank + 8;
+constexpr int kGemvUPitch = kGemvMaxFusedRank + 4;
 constexpr int kGemvMaxUSplits = 16;
 constexpr int kGemvXSliceMaxM = 2;  // activation rows through the per-wave LDS slice
 constexpr int kGemvLutQwords = 256 * 32;  // 64 KiB: code byte -> fp32 (T[lo], T[hi]), 32 copies
@@ -155,8 +163,8 @@ __host__ __device__ inline size_t gemv_lds_bytes(int TS, int nseg, int M, bool g
   size_t b = size_t(gemv_part_floats(TS, nseg, M)) * 4;
   if (gather) b += size_t(kGemvWaves) * kGemvScaleSliceBytes;
   if (xslice) b += size_t(kGemvWaves) * M * kSegK * 2;
-  b += (lora ? size_t(TS) * 16 * kGemvMaxFusedRank * 2 : 0) + size_t(TS) * 16 * 4;
-  b += lora ? size_t(M) * kGemvMaxFusedRank * 4 : 0;
+  b += (lora ? size_t(TS) * 16 * kGemvBPitch * 2 : 0) + size_t(TS) * 16 * 4;
+  b += lora ? size_t(M) * kGemvUPitch * 4 : 0;
   return b;
 }
 
@@ -518,7 +526,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   const bool fold = !a.direct && a.tile_cnt != nullptr;  // K splits finished in this launch
   const bool epi = a.direct || fold;                     // the epilogue runs in this launch
   const int rank = (epi && e.rank > 0) ? e.rank : 0;     // LoRA staging only when fused here
-  constexpr int RP = kGemvMaxFusedRank;                    // staging pitch
+  constexpr int RPB = kGemvBPitch, RPU = kGemvUPitch;      // staging pitches
   constexpr bool kGather = GemvScale<Scale>::kGather;
   float* part = reinterpret_cast<float*>(smem);
   // this wave's scale slice [64][4] (gathered absmax)
@@ -530,9 +538,9 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
   // RND(B) rows of the tiles, as activation-dtype bits (exact: RND is the
   // rounding to that dtype)
   uint16_t* lbs = xs0 + (XM == 1 ? kGemvWaves * M * kSegK : 0);
-  float* bss = reinterpret_cast<float*>(lbs + (rank > 0 ? TS * 16 * RP : 0));
+  float* bss = reinterpret_cast<float*>(lbs + (rank > 0 ? TS * 16 * RPB : 0));
   float* us = bss + TS * 16;
-  uint32_t* flag = reinterpret_cast<uint32_t*>(us + M * RP);  // in-launch LoRA: set when u is computed here
+  uint32_t* flag = reinterpret_cast<uint32_t*>(us + M * RPU);  // in-launch LoRA: set when u is computed here
 
   GemvLane ln;
   ln.n16 = lane & 15;
@@ -880,7 +888,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
 #pragma unroll
   for (int k = 0; k < kUPerThread; ++k) asm volatile("" : "+v"(up[k]));
   if (bvec_live) {
-    uint16_t* dst = lbs + (bt * 16 + br_row) * RP + bc * int(16u / bbytes);
+    uint16_t* dst = lbs + (bt * 16 + br_row) * RPB + bc * int(16u / bbytes);
     if (e.lora_dt == RQ_DTYPE_F32) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) dst[i] = uint16_t(to_x16<XT>(u2f(bvr[i])));
@@ -906,7 +914,7 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     }
     float sum = l1;
     for (int c = 1; c < uC; ++c) sum = __fadd_rn(sum, __shfl(l1, lane + c));
-    if (u_mine && uc == 0) us[(upr / rank) * RP + (upr - (upr / rank) * rank)] = round_x<XT>(sum);
+    if (u_mine && uc == 0) us[(upr / rank) * RPU + (upr - (upr / rank) * rank)] = round_x<XT>(sum);
   }
   lds_barrier();
 
@@ -924,8 +932,8 @@ void nf4_gemv_kernel(GemvArgs a, Scale scale_src, LinearEpi e) {
     if (e.bias) v = __fadd_rn(v, bss[ft * 16 + fnn]);
     v = round_x<XT>(v);
     if (rank > 0) {
-      const uint16_t* brow = lbs + (ft * 16 + fnn) * RP;
-      const float* urow = us + fm * RP;
+      const uint16_t* brow = lbs + (ft * 16 + fnn) * RPB;
+      const float* urow = us + fm * RPU;
       float l = 0.0f;
       for (int j0 = 0; j0 < rank; j0 += 8) {
         float uu[8], bb[8];
