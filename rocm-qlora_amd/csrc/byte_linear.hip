@@ -80,7 +80,7 @@ struct Byte8Producer {
     S.r[2 * hh] = pk.x;
     S.r[2 * hh + 1] = pk.y;
     if (hh == 1)
-      *reinterpret_cast<u32x4*>(tile + swz(tile_row, 2u * quarter + uint32_t(p))) =
+      *reinterpret_cast<u32x4*>(tile + swzw(tile_row, 2u * quarter + uint32_t(p))) =
           u32x4{S.r[0], S.r[1], S.r[2], S.r[3]};
   }
 };

@@ -129,7 +129,7 @@ struct Dx8Producer {
         const uint32_t ke = uint32_t(e) ^ swap;
         const uint32_t own = S.pr[e], partner = S.pr[e ^ 1];
         const uint32_t val = swap ? partner : own;
-        *reinterpret_cast<uint32_t*>(tile + swz(8u * dcol + ke, rg >> 2) + ((rg & 3u) << 2)) = val;
+        *reinterpret_cast<uint32_t*>(tile + swzw(8u * dcol + ke, rg >> 2) + ((rg & 3u) << 2)) = val;
       }
     }
   }

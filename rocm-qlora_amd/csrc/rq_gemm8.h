@@ -75,7 +75,7 @@ struct Fwd8Producer {
     for (int h = 2 * hh; h < 2 * hh + 2; ++h)
       S.r[h] = cvt_pk<XT>(__fmul_rn(u2f(S.lk[p][h].x), S.sc), __fmul_rn(u2f(S.lk[p][h].y), S.sc));
     if (hh == 1)
-      *reinterpret_cast<u32x4*>(tile + swz(tile_row, 2u * quarter + uint32_t(p))) =
+      *reinterpret_cast<u32x4*>(tile + swzw(tile_row, 2u * quarter + uint32_t(p))) =
           u32x4{S.r[0], S.r[1], S.r[2], S.r[3]};
   }
 };
@@ -101,7 +101,7 @@ __device__ __forceinline__ void gemm8_step(f32x16 (&acc)[kGemm8MB][kGemm8NB], co
       xa[mb] = *reinterpret_cast<const u32x4*>(xr + swz(uint32_t(32 * mb + i32), c));
 #pragma unroll
     for (int nb = 0; nb < kGemm8NB; ++nb)
-      b[nb] = *reinterpret_cast<const u32x4*>(wt + swz(col_base + uint32_t(32 * nb + i32), c));
+      b[nb] = *reinterpret_cast<const u32x4*>(wt + swzw(col_base + uint32_t(32 * nb + i32), c));
   };
   u32x4 xa[kGemm8MB], b[kGemm8NB], xan[kGemm8MB], bn[kGemm8NB];
   read_ops(xa, b, 0);

@@ -74,6 +74,15 @@ struct GemmEpi {
 
 // Byte offset of 16-byte chunk c of row r in a swizzled 128-byte-row tile.
 __device__ __forceinline__ uint32_t swz(uint32_t r, uint32_t c) { return r * 128u + ((c ^ ((r >> 1) & 7u)) << 4); }
+// The weight tile's swizzle: also rows 2i and 2i + 1 take different chunk
+// permutations.  The producers store a tile row's chunks from four adjacent
+// lanes; with swz the stores of rows 2i and 2i + 1 met in the same banks
+// (the forward GEMM's only LDS bank conflicts, 14 % of its LDS cycles),
+// while the MFMA operand reads (16 consecutive rows of one chunk) stay
+// conflict-free with either.
+__device__ __forceinline__ uint32_t swzw(uint32_t r, uint32_t c) {
+  return r * 128u + ((c ^ (((r >> 1) ^ (r & 1u)) & 7u)) << 4);
+}
 
 // Waits until at most N vector-memory loads of this wave are outstanding.
 // The activation ring is read through LDS, which the compiler's own wait
