@@ -25,11 +25,13 @@
 //                so lookups fold their base into the instruction offset);
 //   [64K, 128K)  activation ring: 2 steps x 4 row slices x 64 rows x 128 bytes;
 //   [128K, 160K) weight tiles: 2 steps x 128 rows x 128 bytes.
-// Both LDS layouts store 16-byte chunk c of row r at slot c ^ ((r / 2) & 7)
-// of the row: the LDS serves 16 lanes x 16 bytes (its 64 banks) per cycle,
-// and 16 consecutive rows then cover 16 distinct 16-byte bank groups (row
-// parity picks the 128-byte half), so the MFMA operand reads and the
-// dequantizer's row-segment stores are conflict-free.
+// The activation ring stores 16-byte chunk c of row r at slot c ^ ((r / 2) &
+// 7) of the row, the weight tiles at slot c ^ (((r / 2) ^ r) & 7): for the
+// MFMA operand reads (16 consecutive rows of one chunk) both put the rows on
+// 16 distinct 16-byte bank groups (row parity picks the 128-byte half); the
+// weight tile's also separates rows 2i and 2i + 1, whose chunks the
+// dequantizer stores from adjacent lanes (with the first swizzle those
+// stores met in the same banks).
 //   * Activations go from global memory straight into the ring with
 //     global_load_lds_dwordx4: each instruction moves 8 whole 128-byte rows
 //     (8 cache lines; loads that spread 32 rows over one instruction cost the
@@ -56,7 +58,11 @@ namespace rq {
 // wave hit different row parities (bank halves).
 template <int XT, class Scale>
 struct Dx8Producer {
-  static constexpr int kLoads = 2 * (1 + Scale::kLoads);
+  // vector-memory loads issue() makes (the core's waits count them): two
+  // weight words, and per row its scale loads -- or, transposed, rows n and
+  // n + 1's scales as one 8-byte load (adjacent words, which the compiler
+  // would merge into one load anyway)
+  static constexpr int kLoads = Scale::kTransposed ? 3 : 2 * (1 + Scale::kLoads);
   struct Regs {
     uint32_t w[2];
     typename Scale::Raw s[2];
@@ -89,11 +95,25 @@ struct Dx8Producer {
     boff = uint32_t(kcol >> 1);
   }
   __device__ __forceinline__ void issue(Regs& R, int64_t kstep) const {
+    const int64_t blk = kcol >> P.bs_log2;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int64_t n = kstep * kGemmBK + 2 * rg + i;
       R.w[i] = *reinterpret_cast<const uint32_t*>(P.packed + (uint32_t(n * P.row_bytes) + boff));
-      R.s[i] = scale.load(n * P.blocks_per_row + (kcol >> P.bs_log2));
+      if constexpr (!Scale::kTransposed) {
+        R.s[i] = scale.load(n * P.blocks_per_row + blk);
+        // one load per row's scale, as kLoads counts: with one block per row
+        // (K == block size) the two rows' scales are adjacent words, which the
+        // compiler would otherwise merge into one load
+        asm volatile("" ::: "memory");
+      }
+    }
+    if constexpr (Scale::kTransposed) {
+      // rows n, n + 1 (n even, rows a multiple of 64): 8-byte aligned
+      const u32x2 s2 = *reinterpret_cast<const u32x2*>(static_cast<const uint32_t*>(scale.p) + blk * P.rows +
+                                                       kstep * kGemmBK + 2 * rg);
+      R.s[0] = s2.x;
+      R.s[1] = s2.y;
     }
   }
   __device__ __forceinline__ void prep(Step& S, const Regs& R) const {
@@ -168,6 +188,67 @@ static int run_core8(const GemmArgs& a, const ProducerParams& pp, const void* ab
     case RQ_DTYPE_BF16: return launch_core8<XT, ProdT>(a, pp, ScaleAbsmax<RQ_DTYPE_BF16>{absmax}, e, stream);
     default: return launch_core8<XT, ProdT>(a, pp, ScaleAbsmax<RQ_DTYPE_F16>{absmax}, e, stream);
   }
+}
+
+// st[b][n] = scale(n, b) as fp32, the value the producer computes from the
+// absmax (or from the c2 code and its super-block scale), for the dX
+// producer's transposed scale reads.  64 x 64 tiles through LDS: rows read
+// along the blocks, written along the rows.
+template <class Scale>
+__global__ __launch_bounds__(1024) void scale_transpose_kernel(Scale sc, int64_t rows, int64_t bpr,
+                                                               float* __restrict__ st) {
+  __shared__ float tile[64][65];
+  const int t = threadIdx.x, c = t & 63;
+  const int64_t n0 = int64_t(blockIdx.x) * 64, b0 = int64_t(blockIdx.y) * 64;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t n = n0 + (t >> 6) + 16 * i, b = b0 + c;
+    v[i] = (n < rows && b < bpr) ? sc(n * bpr + b) : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) tile[(t >> 6) + 16 * i][c] = v[i];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (t >> 6) + 16 * i;
+    const int64_t b = b0 + r, n = n0 + c;
+    if (b < bpr && n < rows) st[b * rows + n] = tile[c][r];
+  }
+}
+
+template <class Scale>
+static int launch_scale_transpose(Scale sc, int64_t rows, int64_t bpr, float* st, hipStream_t stream) {
+  const dim3 grid(unsigned((rows + 63) / 64), unsigned((bpr + 63) / 64));
+  scale_transpose_kernel<Scale><<<grid, 1024, 0, stream>>>(sc, rows, bpr, st);
+  return rq_check_launch();
+}
+
+// The transposed scales of a dX call, by scale format.
+static int run_scale_transpose(const DxArgs& D, float* st, hipStream_t stream) {
+  const int64_t bpr = D.K / D.block_size;
+  if (D.c2) {
+    const int sh = pow2_shift(D.block2);
+    switch (D.absmax_dtype) {
+      case RQ_DTYPE_F32:
+        return launch_scale_transpose(ScaleDQ<RQ_DTYPE_F32>{D.c2, D.absmax, D.c2_format, sh, D.block2}, D.N, bpr, st, stream);
+      case RQ_DTYPE_BF16:
+        return launch_scale_transpose(ScaleDQ<RQ_DTYPE_BF16>{D.c2, D.absmax, D.c2_format, sh, D.block2}, D.N, bpr, st, stream);
+      default:
+        return launch_scale_transpose(ScaleDQ<RQ_DTYPE_F16>{D.c2, D.absmax, D.c2_format, sh, D.block2}, D.N, bpr, st, stream);
+    }
+  }
+  switch (D.absmax_dtype) {
+    case RQ_DTYPE_F32: return launch_scale_transpose(ScaleAbsmax<RQ_DTYPE_F32>{D.absmax}, D.N, bpr, st, stream);
+    case RQ_DTYPE_BF16: return launch_scale_transpose(ScaleAbsmax<RQ_DTYPE_BF16>{D.absmax}, D.N, bpr, st, stream);
+    default: return launch_scale_transpose(ScaleAbsmax<RQ_DTYPE_F16>{D.absmax}, D.N, bpr, st, stream);
+  }
+}
+
+// Bytes of the transposed scales (at most K / 64 blocks per row: the MFMA dX
+// kernel takes block sizes of at least 64), 256-byte padded.
+static size_t dx_scale_t_bytes(int64_t N, int64_t K, int64_t block_size) {
+  return (size_t(N) * size_t(K / block_size) * 4 + 255) & ~size_t(255);
 }
 
 int gemm_workspace(const LinearArgs& L, size_t* bytes) {
@@ -281,7 +362,8 @@ int dx_workspace(const DxArgs& D, size_t* bytes) {
   // alignment and the block size, unknown here, decide which runs)
   const size_t g = generic_lora_bytes(D.dy_dtype, D.M, D.rank);
   const bool fast = D.dy_dtype != RQ_DTYPE_F32 && D.N % 64 == 0 && D.K % 64 == 0;
-  *bytes = std::max(g, fast ? plan_gemm(D.M, D.K, D.N, D.rank > 0 ? D.rank : 0, device_cus()).ws_bytes : size_t(0));
+  const size_t core = (plan_gemm(D.M, D.K, D.N, D.rank > 0 ? D.rank : 0, device_cus()).ws_bytes + 255) & ~size_t(255);
+  *bytes = std::max(g, fast ? core + dx_scale_t_bytes(D.N, D.K, 64) : size_t(0));
   return RQ_OK;
 }
 
@@ -331,6 +413,18 @@ int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t st
   a.splits = 1;
   a.lf = p.tiles_m * p.tiles_n / 8;
   ProducerParams pp{D.w_packed, D.K / 2, D.N, D.K / D.block_size, pow2_shift(D.block_size)};
+  // With room in the workspace, the scales are decoded and transposed first
+  // (one small launch), so that a step's scales are contiguous: at the
+  // Llama-3-8B gate shape the scattered per-row scale reads kept the
+  // texture addresser 65 % busy and made the dX 12-17 % slower.
+  const size_t st_off = (p.ws_bytes + 255) & ~size_t(255);
+  if (workspace && ws_bytes >= st_off + dx_scale_t_bytes(D.N, D.K, D.block_size)) {
+    float* st = reinterpret_cast<float*>(static_cast<char*>(workspace) + st_off);
+    if (const int s2 = run_scale_transpose(D, st, stream); s2 != RQ_OK) return s2;
+    const ScaleT sct{st};
+    if (D.dy_dtype == RQ_DTYPE_BF16) return launch_core8<RQ_DTYPE_BF16, Dx8Producer>(a, pp, sct, e, stream);
+    return launch_core8<RQ_DTYPE_F16, Dx8Producer>(a, pp, sct, e, stream);
+  }
   if (D.dy_dtype == RQ_DTYPE_BF16)
     return run_core8<RQ_DTYPE_BF16, Dx8Producer>(a, pp, D.absmax, D.absmax_dtype, D.c2, D.c2_format, D.block2, e,
                                                  stream);

@@ -24,6 +24,7 @@ __device__ __forceinline__ float ld_f32(const void* __restrict__ p, int64_t i) {
 template <int SDT>
 struct ScaleAbsmax {
   static constexpr int kLoads = 1;  // vector-memory loads per scale
+  static constexpr bool kTransposed = false;  // index n * blocks_per_row + block
   const void* p;
   typedef uint32_t Raw;
   __device__ __forceinline__ Raw load(int64_t b) const {
@@ -41,6 +42,7 @@ struct ScaleAbsmax {
 template <int SDT>
 struct ScaleDQ {
   static constexpr int kLoads = 2;  // vector-memory loads per scale
+  static constexpr bool kTransposed = false;
   const uint8_t* c2;
   const void* c2s;
   int fmt;
@@ -66,6 +68,19 @@ struct ScaleDQ {
     const float lo = fmt == RQ_C2_FP8_E4M3FNUZ ? fnuz_to_f32(c) : __fdiv_rn(float(int8_t(c)), 127.0f);
     return __fmul_rn(lo, hi);
   }
+  __device__ __forceinline__ float operator()(int64_t b) const { return value(load(b)); }
+};
+
+// Decoded fp32 scales stored transposed, [blocks_per_row][rows]: the dX
+// producer's scales of one step (64 consecutive weight rows, one block)
+// are then 256 contiguous bytes instead of 64 rows' scattered words.
+struct ScaleT {
+  static constexpr int kLoads = 1;
+  static constexpr bool kTransposed = true;  // index block * rows + n
+  const void* p;
+  typedef uint32_t Raw;
+  __device__ __forceinline__ Raw load(int64_t b) const { return static_cast<const uint32_t*>(p)[b]; }
+  __device__ __forceinline__ float value(Raw r) const { return u2f(r); }
   __device__ __forceinline__ float operator()(int64_t b) const { return value(load(b)); }
 };
 

@@ -147,3 +147,54 @@ def test_dx_weight_operand_bit_exact(dev, dtype, dq):
         wf = R.dequantize_int4(packed.cpu(), absmax.cpu(), 64)[:N * K]
     ref = wf.reshape(N, K).to(dtype)[ns]
     assert torch.equal(dx.cpu().view(torch.int16), ref.contiguous().view(torch.int16))
+
+
+def _dx_call(dev, dy, packed, scales, K, block, ws_bytes, c2=None, a=None, b=None, rank=0, scaling=0.25):
+    """rq_nf4_linear_dx through the C ABI with a workspace of ws_bytes."""
+    from rocm_qlora import _native as nat
+    M, N = dy.shape
+    ws = torch.zeros(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    dx = torch.empty(M, K, dtype=dy.dtype, device=dev)
+    nat.call("rq_nf4_linear_dx", dy.data_ptr(), nat.dtype_code(dy.dtype), M, N, N, packed.data_ptr(), K, block,
+             scales.data_ptr(), nat.dtype_code(scales.dtype), nat.ptr(c2), nat.C2_FP8_E4M3FNUZ, 256,
+             nat.ptr(a), nat.ptr(b), rank, nat.dtype_code(a.dtype) if a is not None else 0, rank, scaling,
+             None, 0, 1.0, dx.data_ptr(), K, ws.data_ptr(), ws_bytes, nat.stream_handle(dev))
+    torch.cuda.synchronize()
+    return dx
+
+
+@pytest.mark.parametrize("N,K,case", [(1024, 4096, "f32"), (512, 4096, "bf16"), (1024, 4096, "dq"),
+                                      (1024, 64, "f32"), (256, 64, "bf16"), (512, 1024, "lora")])
+def test_dx_transposed_scales_match_direct(dev, N, K, case):
+    """With room in the workspace the dX kernel reads scales decoded and
+    transposed by a launch before it ([blocks][rows] fp32, a step's scales
+    contiguous); without it, the absmax (or c2 codes and their scales)
+    directly.  Both give the same bits: fp32 and bf16 absmax, double
+    quantization, one block per row (K == block size, where the two rows a
+    thread dequantizes have adjacent scales), and with the LoRA term."""
+    import ctypes
+    from rocm_qlora import _native as nat
+    M = 300
+    print(f"dx transposed scales N={N} K={K} {case}", flush=True)
+    g = torch.Generator().manual_seed(N + K)
+    w = torch.randn(N, K, generator=g) * 0.02
+    dy = (torch.randn(M, N, generator=g) * 1e-2).to(torch.bfloat16).to(dev)
+    c2 = None
+    if case == "dq":
+        st = double_quantize(w.to(dev), 64, 256)
+        packed, scales, c2 = st.W_quant.reshape(-1), st.c2_scales, st.c2.reshape(-1).view(torch.uint8)
+    else:
+        packed, scales = quantize_int4(w.to(dev).to(torch.bfloat16 if case == "bf16" else torch.float32), 64)
+    rank = 16 if case == "lora" else 0
+    a = (torch.randn(rank, K, generator=g) * 0.05).to(dev) if rank else None
+    b = (torch.randn(N, rank, generator=g) * 0.05).to(dev) if rank else None
+    nb = ctypes.c_int64(0)
+    nat.call("rq_nf4_linear_dx_workspace_size", nat.dtype_code(dy.dtype), M, N, K, rank, ctypes.byref(nb))
+    st_bytes = (N * (K // 64) * 4 + 255) // 256 * 256
+    assert nb.value >= st_bytes
+    full = _dx_call(dev, dy, packed, scales, K, 64, nb.value, c2, a, b, rank)
+    direct = _dx_call(dev, dy, packed, scales, K, 64, nb.value - st_bytes, c2, a, b, rank)
+    assert torch.equal(full.view(torch.int16), direct.view(torch.int16))
+    if case in ("f32", "bf16"):
+        ref = R.nf4_dx(dy.cpu(), packed.cpu(), scales.cpu(), N, K, None, None, 0.0, 64)
+        _check(full.cpu(), ref)
