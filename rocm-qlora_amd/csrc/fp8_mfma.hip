@@ -408,8 +408,9 @@ void byte_mfma_gemv_kernel(Fp8Args a) {
 // loads, issued four stages ahead of their MFMAs.  Eight waves, two per SIMD:
 // wave w owns rows 128 (w % 2) .. +127 and columns 64 (w / 2) .. +63 of the
 // tile as 4 x 2 blocks of the 32x32x64 MFMA; lane (i, h) (i = lane % 32, h =
-// lane / 32) feeds bytes k = 32 h .. 32 h + 31 of the stage.  D[m][n]: lane
-// (i, h), register r = row 8 (r / 4) + 4 h + r % 4, column i.
+// lane / 32) feeds bytes k = 32 h .. 32 h + 31 of the stage.  The weights
+// are the MFMAs' A operand: lane (i, h), register r holds row i of the block,
+// column 8 (r / 4) + 4 h + r % 4.
 //
 // Iteration j: wait until stages j and j + 1 have landed (this wave's loads;
 // j + 2 and j + 3 may be in flight), barrier (every wave's loads of them too,
@@ -430,6 +431,12 @@ constexpr int kF8TileBytes = kF8BM * kF8BK;       // 16 KiB
 constexpr int kF8StageBytes = 2 * kF8TileBytes;   // x tile, W tile
 static_assert(kF8BM == kF8BN, "one DMA lane map serves both operands");
 static_assert(kF8Stages * kF8StageBytes <= 160 * 1024, "LDS plan");
+
+// Output staging of a wave's 128 x 64 block after the main loop (144-byte
+// rows, in the ring's LDS)
+constexpr int kF8EpiPitch = 144;
+constexpr int kF8EpiWaveBytes = 128 * kF8EpiPitch;
+static_assert(8 * kF8EpiWaveBytes <= kF8Stages * kF8StageBytes, "output staging");
 
 __device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return r * 64u + ((c ^ ((r >> 2) & 3u)) << 4); }
 
@@ -546,7 +553,7 @@ void byte_mfma_gemm_kernel(Fp8Args a) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Op::mma32h(lo.a[mb], lo.b[nb], acc[mb][nb]);
+        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Op::mma32h(lo.b[nb], lo.a[mb], acc[mb][nb]);
       interleave();
       __builtin_amdgcn_sched_barrier(0);
       HalfFrags nlo;
@@ -554,7 +561,7 @@ void byte_mfma_gemm_kernel(Fp8Args a) {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Op::mma32h(hi.a[mb], hi.b[nb], acc[mb][nb]);
+        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Op::mma32h(hi.b[nb], hi.a[mb], acc[mb][nb]);
       interleave();
       __builtin_amdgcn_sched_barrier(0);
       lo = nlo;
@@ -571,24 +578,73 @@ void byte_mfma_gemm_kernel(Fp8Args a) {
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
-          acc[mb][nb] = Op::mma32(cur.a[mb][0], cur.a[mb][1], cur.b[nb][0], cur.b[nb][1], acc[mb][nb]);
+          acc[mb][nb] = Op::mma32(cur.b[nb][0], cur.b[nb][1], cur.a[mb][0], cur.a[mb][1], acc[mb][nb]);
       cur = nxt;
     }
   }
-  wait_vmcnt<0>();  // no load may still be landing in LDS when the workgroup ends
+  wait_vmcnt<0>();  // no load may still be landing in LDS when it holds the output
+  __syncthreads();   // and every wave is done reading the last stage
 
+  // Output.  The weights are the MFMAs' A operand, so lane (i32, h) holds row
+  // m0 + 128 wm + 32 mb + i32 of block (mb, nb) and its columns 8 g + 4 h ..
+  // + 3 in acc[mb][nb][4 g ..] (g < 4).  The values go, two per dword, into
+  // the wave's LDS region (its 128 x 64 block, 144-byte rows), are read back
+  // as 16-byte row pieces and stored eight 128-byte row pieces per
+  // instruction.  (With the activations as A, a lane held one column and
+  // stored 128 two-byte values, each behind its own bounds checks and scale
+  // loads.)  y = RND(RND(float(acc) * scale) + RND(bias)), bias -0.0 where
+  // there is none (x + -0.0 == x for every x).
+  uint8_t* ws = lds + wave * kF8EpiWaveBytes;
+  const float s_tensor = Op::kPerRow ? 0.0f : __fmul_rn(*a.sx, *a.sw);
 #pragma unroll
   for (int nb = 0; nb < 2; ++nb) {
-    const int64_t n = n0 + 64 * wn + 32 * nb + i32;
-    if (n >= a.N) continue;
+    float bias[4][4], wsc[4][4];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int g = 0; g < 4; ++g)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + 128 * wm + 32 * mb + 8 * (r >> 2) + 4 * h + (r & 3);
-        if (m >= a.M) continue;
-        a.y[m * a.ldy + n] = uint16_t(to_x16<XT>(byte_epilogue<XT, Op>(a, acc[mb][nb][r], m, n)));
+      for (int c = 0; c < 4; ++c) {
+        const int64_t n = n0 + 64 * wn + 32 * nb + 8 * g + 4 * h + c;
+        bias[g][c] = a.bias && n < a.N ? round_x<XT>(load_as_f32(a.bias, n, a.bias_dt)) : -0.0f;
+        wsc[g][c] = Op::kPerRow && n < a.N ? load_as_f32(a.w_row_scale, n, a.w_row_scale_dt) : 0.0f;
       }
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb) {
+      const int64_t m = m0 + 128 * wm + 32 * mb + i32;
+      const float sxm = Op::kPerRow && m < a.M ? a.sx[m] : 0.0f;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          v[c] = Op::kPerRow ? __fmul_rn(__fmul_rn(Op::to_f32(acc[mb][nb][4 * g + c]), sxm), wsc[g][c])
+                             : __fmul_rn(Op::to_f32(acc[mb][nb][4 * g + c]), s_tensor);
+        round2<XT>(v[0], v[1]);
+        round2<XT>(v[2], v[3]);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = __fadd_rn(v[c], bias[g][c]);
+        *reinterpret_cast<u32x2*>(ws + (32 * mb + i32) * kF8EpiPitch + (32 * nb + 8 * g + 4 * h) * 2) =
+            u32x2{cvt_pk<XT>(v[0], v[1]), cvt_pk<XT>(v[2], v[3])};
+      }
+    }
+  }
+  // the wave reads back only its own region
+  const bool full = m0 + kF8BM <= a.M && n0 + kF8BN <= a.N && (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0 &&
+                    (a.ldy & 7) == 0;
+  const int64_t col = n0 + 64 * wn + 8 * (lane & 7);
+#pragma unroll
+  for (int it = 0; it < 16; ++it) {
+    const int r = 8 * it + (lane >> 3);
+    const int64_t m = m0 + 128 * wm + r;
+    const u32x4 o = *reinterpret_cast<const u32x4*>(ws + r * kF8EpiPitch + 16 * (lane & 7));
+    uint16_t* yp = a.y + m * a.ldy + col;
+    if (full) {
+      *reinterpret_cast<u32x4*>(yp) = o;
+    } else if (m < a.M) {
+      const uint32_t w4[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        if (col + c < a.N) yp[c] = uint16_t(w4[c >> 1] >> (16 * (c & 1)));
+    }
   }
 }
 

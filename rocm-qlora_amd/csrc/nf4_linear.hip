@@ -96,14 +96,8 @@ constexpr int kGemvMaxUSplits = 16;
 constexpr int kGemvXSliceMaxM = 2;  // activation rows through the per-wave LDS slice
 constexpr int kGemvLutQwords = 256 * 32;  // 64 KiB: code byte -> fp32 (T[lo], T[hi]), 32 copies
 constexpr int kGemvLdsBudget = 160 * 1024 - kGemvLutQwords * 8;
-// Word 3 of a raw (stride 0) buffer resource on gfx9-family GPUs, gfx950
-// included: 32-bit data, bounds checked against num_records.
-constexpr int kBufferRsrcWord3 = 0x00020000;
 // A buffer offset past every range this file builds: the load returns zero.
 constexpr uint32_t kOobOffset = 0xFFFFFFF0u;
-// Cache policy of a buffer load or store that is device coherent (sc1), as
-// the agent-scope atomic loads and stores are.
-constexpr int kCoherent = 16;
 
 struct GemvArgs {
   const uint16_t* x;
@@ -168,14 +162,8 @@ __host__ __device__ inline size_t gemv_lds_bytes(int TS, int nseg, int M, bool g
   return b;
 }
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), kBufferRsrcWord3);
-}
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-__device__ __forceinline__ u32x4 buf_load16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherent));
 }
 __device__ __forceinline__ uint32_t buf_load4_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return uint32_t(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCoherent));

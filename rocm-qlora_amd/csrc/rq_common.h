@@ -243,4 +243,26 @@ __host__ __device__ inline uint8_t f32_to_fn_rne(float v) {
 
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---------------------------------------------------------------------------
+// Raw buffer accesses (stride 0, 32-bit byte offsets, bounds checked against
+// the resource's size: an access past it reads zero and writes nothing)
+// ---------------------------------------------------------------------------
+// Word 3 of a raw buffer resource on gfx9-family GPUs, gfx950 included:
+// 32-bit data, bounds checked against num_records.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+// Cache policy of a buffer load or store that is device coherent (sc1), as
+// the agent-scope atomic loads and stores are.
+constexpr int kCoherent = 16;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), kBufferRsrcWord3);
+}
+// voff: per-lane byte offset; soff: a wave-uniform byte offset added to it
+__device__ __forceinline__ u32x4 buf_load16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kCoherent));
+}
+__device__ __forceinline__ void buf_store16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, kCoherent);
+}
+
 }  // namespace rq

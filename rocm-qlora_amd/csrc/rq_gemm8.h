@@ -2,9 +2,11 @@
 // FP8 linears, by producer policy): 256 x 128 workgroup tiles, 64-k steps,
 // 512 threads, two waves per SIMD.  Wave w owns rows 64 (w % 4) .. +63 and
 // columns 64 (w / 4) .. +63 of the tile as 2 x 2 blocks of
-// v_mfma_f32_32x32x16_{bf16,f16}.  With one wave per SIMD (a 64 x 128 block
-// each) the matrix core waited whenever that wave waited (LDS reads, table
-// lookups, barrier); a second wave per SIMD issues its MFMAs in those gaps.
+// v_mfma_f32_32x32x16_{bf16,f16} (weights as the A operand, activations as
+// B, so that a lane's results lie along an output row).  With one wave per
+// SIMD (a 64 x 128 block each) the matrix core waited whenever that wave
+// waited (LDS reads, table lookups, barrier); a second wave per SIMD issues
+// its MFMAs in those gaps.
 //
 // The two waves of a row slice (w and w + 4) each bring half of the slice's
 // activation rows into the ring; the step barrier, which already waits for
@@ -113,7 +115,7 @@ __device__ __forceinline__ void gemm8_step(f32x16 (&acc)[kGemm8MB][kGemm8NB], co
 #pragma unroll
     for (int i = 0; i < kGemm8MB * kGemm8NB; ++i) {
       const int nb = i / kGemm8MB, mb = i % kGemm8MB;
-      acc[mb][nb] = mfma32x32x16<XT>(xa[mb], b[nb], acc[mb][nb]);
+      acc[mb][nb] = mfma32x32x16<XT>(b[nb], xa[mb], acc[mb][nb]);
       if (i == 0 && s < 2) {
 #pragma unroll
         for (int t = 2 * s; t < 2 * s + 2; ++t) dma16(a.x, (xo[t] + uint32_t(kx) * kGemmBK) * 2u, xdst + t * 1024);
@@ -134,6 +136,64 @@ __device__ __forceinline__ void gemm8_step(f32x16 (&acc)[kGemm8MB][kGemm8NB], co
   prod.issue(wl_fill, kfill);
   __builtin_amdgcn_sched_barrier(0);
 }
+
+// The output values of a wave's 64 x 64 block, rounded to the operand
+// dtype and packed two per dword (pk[mb][nb][h] = columns 8 h + 4 q .. + 3 of
+// row m of block (mb, nb)): y = RND(RND(acc + RND(bias)) + RND(RND(lo) * s))
+// with s the LoRA scaling (kMode 1), or mask ? mask_scale : 0 for dX with
+// LoRA dropout (kMode 2); kMode 0 has no LoRA term.  bias is -0.0 where
+// there is none (x + -0.0 == x for every x).  The flags are template
+// parameters so the 64 values per lane run without a branch.
+template <int XT, int kMode>
+__device__ __forceinline__ void gemm8_outputs(const f32x16 (&acc)[kGemm8MB][kGemm8NB],
+                                              const f32x16 (&lo)[kGemm8MB][kGemm8NB],
+                                              const float (&bias)[kGemm8NB][4][4], const GemmEpi& e,
+                                              const GemmArgs& a, int64_t m_lane, int64_t n_lane,
+                                              uint32_t (&pk)[kGemm8MB][kGemm8NB][4][2]) {
+#pragma unroll
+  for (int mb = 0; mb < kGemm8MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < kGemm8NB; ++nb)
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[c] = __fadd_rn(acc[mb][nb][4 * h + c], bias[nb][h][c]);
+        if constexpr (kMode > 0) {
+          round2<XT>(v[0], v[1]);
+          round2<XT>(v[2], v[3]);
+          float l[4], s[4];
+#pragma unroll
+          for (int c = 0; c < 4; ++c) {
+            l[c] = lo[mb][nb][4 * h + c];
+            s[c] = e.scaling;
+          }
+          if constexpr (kMode == 2) {
+            const int64_t m = m_lane + 32 * mb, n = n_lane + 32 * nb + 8 * h;
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+              s[c] = m < a.M && n + c < a.N && e.mask[m * e.ldm + n + c] ? e.mask_scale : 0.0f;
+          }
+          round2<XT>(l[0], l[1]);
+          round2<XT>(l[2], l[3]);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) l[c] = __fmul_rn(l[c], s[c]);
+          round2<XT>(l[0], l[1]);
+          round2<XT>(l[2], l[3]);
+#pragma unroll
+          for (int c = 0; c < 4; ++c) v[c] = __fadd_rn(v[c], l[c]);
+        }
+        pk[mb][nb][h][0] = cvt_pk<XT>(v[0], v[1]);
+        pk[mb][nb][h][1] = cvt_pk<XT>(v[2], v[3]);
+      }
+}
+
+// Per-wave output staging of the epilogue: a 64 x 64 block of 16-bit values,
+// 144-byte rows, in the LDS the activation ring and weight tiles use.
+constexpr int kGemm8EpiPitch = 144;
+constexpr int kGemm8EpiWaveBytes = 64 * kGemm8EpiPitch;
+constexpr int kGemm8EpiOff = kXRingOff;
+static_assert(kGemm8EpiOff + 8 * kGemm8EpiWaveBytes <= kGemmLds, "epilogue staging");
 
 template <int XT, class Prod, class Scale>
 __global__ __launch_bounds__(kGemm8Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -277,17 +337,28 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   // write-back or invalidation is needed: each thread waits for its stores
   // to complete before the workgroup counts itself.
   if (nsplit > 1) {
-    constexpr int kTileFloats = kGemm8Threads * 64;
+    // A split's tile is 16 chunks of 16 bytes per thread, chunk c of thread t
+    // at 16 (512 c + t) bytes: each store and load instruction of a wave moves
+    // 1 KiB contiguous.  (With 64 four-byte atomic stores and loads per
+    // thread the splits' exchange took 9.6 us at the k/v shapes.)
+    constexpr uint32_t kTileBytes = kGemm8Threads * 64 * 4;
     const int64_t n_split_tiles = 8 * (T / 8 - a.lf);
-    float* mine = a.part + (int64_t(split) * n_split_tiles + ti) * kTileFloats + tid;
+    const __amdgpu_buffer_rsrc_t part = buffer_rsrc(a.part, uint32_t(nsplit * n_split_tiles * kTileBytes));
+    const uint32_t lane_off = uint32_t(tid) * 16u;
+    auto chunk = [&](int sp, int c) {  // wave-uniform part of the offset
+      return __builtin_amdgcn_readfirstlane(uint32_t((int64_t(sp) * n_split_tiles + ti) * kTileBytes) +
+                                            uint32_t(c * kGemm8Threads) * 16u);
+    };
 #pragma unroll
     for (int mb = 0; mb < kGemm8MB; ++mb)
 #pragma unroll
       for (int nb = 0; nb < kGemm8NB; ++nb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          __hip_atomic_store(&mine[((mb * kGemm8NB + nb) * 16 + r) * kGemm8Threads], acc[mb][nb][r],
-                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int r4 = 0; r4 < 4; ++r4)
+          buf_store16_coherent(part, lane_off, chunk(split, (mb * kGemm8NB + nb) * 4 + r4),
+                               u32x4{__float_as_uint(acc[mb][nb][4 * r4]), __float_as_uint(acc[mb][nb][4 * r4 + 1]),
+                                     __float_as_uint(acc[mb][nb][4 * r4 + 2]),
+                                     __float_as_uint(acc[mb][nb][4 * r4 + 3])});
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     uint32_t* flag = reinterpret_cast<uint32_t*>(lds);  // the table's LDS is free now
@@ -301,37 +372,42 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
     const uint32_t last = __builtin_amdgcn_readfirstlane(*flag);
     __syncthreads();  // every wave has read the flag before the LDS is reused
     if (!last) return;
-    // a block's 16 values of every split in flight together (a split past
-    // `splits` re-reads split 0 and is not added)
-    float* base = a.part + ti * kTileFloats + tid;
+    // a block's chunks of every split in flight together, this split's too
+    // (just written, so read from the L2): the loads and the split-order sum
+    // are then the same in every workgroup, with no branch between a load
+    // and its use (the planner makes 2 or 4 splits)
+    auto reduce = [&](auto splits) {
+      constexpr int S = decltype(splits)::value;
 #pragma unroll
-    for (int mb = 0; mb < kGemm8MB; ++mb)
+      for (int mb = 0; mb < kGemm8MB; ++mb)
 #pragma unroll
-      for (int nb = 0; nb < kGemm8NB; ++nb) {
-        float o[kGemmMaxSplits][16];
+        for (int nb = 0; nb < kGemm8NB; ++nb) {
+          u32x4 o[S][4];
 #pragma unroll
-        for (int sp = 0; sp < kGemmMaxSplits; ++sp)
+          for (int sp = 0; sp < S; ++sp)
 #pragma unroll
-          for (int r = 0; r < 16; ++r)
-            o[sp][r] = __hip_atomic_load(&base[int64_t(sp < nsplit ? sp : 0) * n_split_tiles * kTileFloats +
-                                               ((mb * kGemm8NB + nb) * 16 + r) * kGemm8Threads],
-                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int r4 = 0; r4 < 4; ++r4)
+              o[sp][r4] = buf_load16_coherent(part, lane_off, chunk(sp, (mb * kGemm8NB + nb) * 4 + r4));
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float v = 0.0f;
+          for (int r = 0; r < 16; ++r) {
+            float v = 0.0f;
 #pragma unroll
-          for (int sp = 0; sp < kGemmMaxSplits; ++sp)
-            if (sp < nsplit) v = __fadd_rn(v, sp == split ? acc[mb][nb][r] : o[sp][r]);
-          acc[mb][nb][r] = v;
+            for (int sp = 0; sp < S; ++sp) v = __fadd_rn(v, __uint_as_float(o[sp][r >> 2][r & 3]));
+            acc[mb][nb][r] = v;
+          }
+          __builtin_amdgcn_sched_barrier(0);  // one block's loads in flight at a time (registers)
         }
-      }
+    };
+    static_assert(kGemmMaxSplits == 4, "the planner's split counts are 2 and 4");
+    if (nsplit == 2) reduce(std::integral_constant<int, 2>{});
+    else reduce(std::integral_constant<int, 4>{});
   }
 
   // ---- epilogue.  y = RND(RND(acc + RND(bias)) + RND(RND(lora) * scaling))
   // (dX with LoRA dropout: scaling replaced by mask ? mask_scale : 0)
   // with lora = RND(u) RND(B)^T accumulated by MFMA in chunks of 64 ranks,
   // both operands staged into LDS (u rows and B rows of the tile, 144-byte
-  // pitch); FP8: y = RND(RND(acc * post_a * post_b) + RND(bias)).
+  // pitch).
   const int rank = e.rank;
   f32x16 lo[kGemm8MB][kGemm8NB];
 #pragma unroll
@@ -374,38 +450,76 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
           const u32x4 ub =
               *reinterpret_cast<const u32x4*>(bs + (64 * ch + 32 * nb + i32) * kP + 16 * s + 8 * q);
 #pragma unroll
-          for (int mb = 0; mb < kGemm8MB; ++mb) lo[mb][nb] = mfma32x32x16<XT>(ua[mb], ub, lo[mb][nb]);
+          for (int mb = 0; mb < kGemm8MB; ++mb) lo[mb][nb] = mfma32x32x16<XT>(ub, ua[mb], lo[mb][nb]);
         }
       }
     }
   }
+  // The weights are the MFMAs' A operand, so lane (i32, q) holds row
+  // m0w + 32 mb + i32 of block (mb, nb) and its columns 8 h + 4 q .. + 3 in
+  // acc[mb][nb][4 h ..] (h < 4): four runs of four adjacent outputs.
+  float bias[kGemm8NB][4][4];
 #pragma unroll
-  for (int nb = 0; nb < kGemm8NB; ++nb) {
-    const int64_t n = n0 + 64 * ch + 32 * nb + i32;
-    if (n >= a.N) continue;
-    const float bias = e.bias ? round_x<XT>(load_as_f32(e.bias, n, e.bias_dt)) : 0.0f;
-    const float post = e.post_a ? __fmul_rn(*e.post_a, *e.post_b) : 1.0f;
+  for (int nb = 0; nb < kGemm8NB; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < kGemm8MB; ++mb) {
+    for (int h = 0; h < 4; ++h)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0w + 32 * mb + 8 * (r >> 2) + 4 * q + (r & 3);
-        if (m >= a.M) continue;
-        float v = acc[mb][nb][r];
-        if (e.post_a) {
-          v = round_x<XT>(__fmul_rn(v, post));
-          if (e.bias) v = round_x<XT>(__fadd_rn(v, bias));
-        } else {
-          if (e.bias) v = __fadd_rn(v, bias);
-          v = round_x<XT>(v);
-        }
-        if (rank > 0) {
-          const float ls = e.mask ? (e.mask[m * e.ldm + n] ? e.mask_scale : 0.0f) : e.scaling;
-          v = round_x<XT>(__fadd_rn(v, round_x<XT>(__fmul_rn(round_x<XT>(lo[mb][nb][r]), ls))));
-        }
-        e.y[m * e.ldy + n] = uint16_t(to_x16<XT>(v));
+      for (int c = 0; c < 4; ++c) {
+        const int64_t n = n0 + 64 * ch + 32 * nb + 8 * h + 4 * q + c;
+        bias[nb][h][c] = e.bias && n < a.N ? round_x<XT>(load_as_f32(e.bias, n, e.bias_dt)) : -0.0f;
       }
+  uint32_t pk[kGemm8MB][kGemm8NB][4][2];
+  if (rank == 0) gemm8_outputs<XT, 0>(acc, lo, bias, e, a, m0w + i32, n0 + 64 * ch + 4 * q, pk);
+  else if (!e.mask) gemm8_outputs<XT, 1>(acc, lo, bias, e, a, m0w + i32, n0 + 64 * ch + 4 * q, pk);
+  else gemm8_outputs<XT, 2>(acc, lo, bias, e, a, m0w + i32, n0 + 64 * ch + 4 * q, pk);
+
+  // A tile wholly inside the output goes out through LDS: each wave writes its
+  // 64 x 64 block into its own region (the ring and weight tiles, free since
+  // the last step's barrier), reads it back as 16-byte row chunks and stores
+  // eight 128-byte row pieces per instruction.  (Stored from the MFMA layout,
+  // an instruction wrote 16 bytes of each of 32 rows; the tile's output took
+  // 3 us where these stores take a fraction of that.)
+  if (m0 + kGemmBM <= a.M && n0 + kGemmBN <= a.N && (reinterpret_cast<uintptr_t>(e.y) & 15u) == 0 &&
+      (e.ldy & 7) == 0) {
+    uint8_t* ws = lds + kGemm8EpiOff + wave * kGemm8EpiWaveBytes;
+#pragma unroll
+    for (int mb = 0; mb < kGemm8MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < kGemm8NB; ++nb)
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          *reinterpret_cast<u32x2*>(ws + (32 * mb + i32) * kGemm8EpiPitch + (32 * nb + 8 * h + 4 * q) * 2) =
+              u32x2{pk[mb][nb][h][0], pk[mb][nb][h][1]};
+    uint16_t* ybase = e.y + m0w * e.ldy + n0 + 64 * ch + 8 * (lane & 7);
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int r = 8 * it + (lane >> 3);
+      *reinterpret_cast<u32x4*>(ybase + r * e.ldy) =
+          *reinterpret_cast<const u32x4*>(ws + r * kGemm8EpiPitch + 16 * (lane & 7));
     }
+    return;
+  }
+  const bool vec = (reinterpret_cast<uintptr_t>(e.y) & 7u) == 0 && (e.ldy & 3) == 0;
+#pragma unroll
+  for (int mb = 0; mb < kGemm8MB; ++mb) {
+    const int64_t m = m0w + 32 * mb + i32;
+    if (m >= a.M) continue;
+    uint16_t* yrow = e.y + m * e.ldy;
+#pragma unroll
+    for (int nb = 0; nb < kGemm8NB; ++nb)
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const int64_t n = n0 + 64 * ch + 32 * nb + 8 * h + 4 * q;
+        const uint32_t p0 = pk[mb][nb][h][0], p1 = pk[mb][nb][h][1];
+        if (vec && n + 3 < a.N) {
+          *reinterpret_cast<u32x2*>(yrow + n) = u32x2{p0, p1};
+        } else {
+          const uint16_t o[4] = {uint16_t(p0), uint16_t(p0 >> 16), uint16_t(p1), uint16_t(p1 >> 16)};
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            if (n + c < a.N) yrow[n + c] = o[c];
+        }
+      }
   }
 }
 

@@ -41,7 +41,7 @@ struct GemmArgs {
   // in split order, runs the epilogue and sets the count back to 0.
   int splits;
   int lf;
-  float* part;         // [splits][8 lt][64 x 512] fp32
+  float* part;         // [splits][8 lt][16 x 512 x 4] fp32 (chunk, thread, value)
   uint32_t* tile_cnt;  // [8 lt]
 };
 
@@ -64,10 +64,6 @@ struct GemmEpi {
   const uint8_t* mask;
   int64_t ldm;
   float mask_scale;
-  // FP8: y = RND(RND(acc * (*post_a) * (*post_b)) + RND(bias)) (the scaled
-  // product is rounded before the bias is added); nullptr otherwise
-  const float* post_a;
-  const float* post_b;
   uint16_t* y;
   int64_t ldy;
 };

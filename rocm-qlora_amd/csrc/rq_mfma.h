@@ -79,6 +79,19 @@ __device__ __forceinline__ float round_x(float v) {
   else return f16_to_f32(f32_to_f16_rne(v));
 }
 
+// RND of two values, by one conversion for bf16 (two for fp16).
+template <int XT>
+__device__ __forceinline__ void round2(float& x, float& y) {
+  if constexpr (XT == RQ_DTYPE_BF16) {
+    const uint32_t p = cvt_pk<XT>(x, y);
+    x = u2f(p << 16);
+    y = u2f(p & 0xFFFF0000u);
+  } else {
+    x = round_x<XT>(x);
+    y = round_x<XT>(y);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Byte -> fp32 codebook pair table for exact dequantization.  Entry e (a
 // packed NF4 byte) holds fp32 T[e & 15] (the even element) and T[e >> 4].
