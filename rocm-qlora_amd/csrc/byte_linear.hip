@@ -40,6 +40,7 @@ __device__ __forceinline__ uint2 decode4_pk(uint32_t w, float s) {
 template <int XT, class Scale>
 struct Byte8Producer {
   static constexpr int kLoads = 1 + Scale::kLoads;
+  static constexpr bool kLoraRegs = false;  // no LoRA term
   struct Regs {
     u32x4 w;
     typename Scale::Raw s;

@@ -63,6 +63,9 @@ struct Dx8Producer {
   // n + 1's scales as one 8-byte load (adjacent words, which the compiler
   // would merge into one load anyway)
   static constexpr int kLoads = Scale::kTransposed ? 3 : 2 * (1 + Scale::kLoads);
+  // the epilogue's LoRA operands in registers (e.lora_regs): only beside the
+  // transposed scales, which is where the host sets it
+  static constexpr bool kLoraRegs = Scale::kTransposed;
   struct Regs {
     uint32_t w[2];
     typename Scale::Raw s[2];
@@ -190,21 +193,50 @@ static int run_core8(const GemmArgs& a, const ProducerParams& pp, const void* ab
   }
 }
 
-// st[b][n] = scale(n, b) as fp32, the value the producer computes from the
-// absmax (or from the c2 code and its super-block scale), for the dX
-// producer's transposed scale reads.  64 x 64 tiles through LDS: rows read
-// along the blocks, written along the rows.
-template <class Scale>
-__global__ __launch_bounds__(1024) void scale_transpose_kernel(Scale sc, int64_t rows, int64_t bpr,
-                                                               float* __restrict__ st) {
+// The dX operands prepared by one launch before the GEMM, through 64 x 64
+// LDS tiles (read along one index, written along the other):
+//   st[b][n] = scale(n, b) as fp32, the value the producer computes from the
+//     absmax (or from the c2 code and its super-block scale), so that a dX
+//     step's scales are contiguous;
+//   at[k][j] = RND(A[j][k]) in the activation dtype, rank16 columns (zeros
+//     past the rank), when at != nullptr: the epilogue's LoRA operand A^T as
+//     rows it reads 16 bytes at a time (A [rank][K] read directly is one
+//     strided element per load).
+// Workgroups [0, st_tiles) take scale tiles, the rest A tiles.
+template <class Scale, int XT>
+__global__ __launch_bounds__(1024) void dx_prep_kernel(Scale sc, int64_t rows, int64_t bpr, float* __restrict__ st,
+                                                       const void* a, int a_dt, int64_t K, int rank, int rank16,
+                                                       uint16_t* __restrict__ at) {
   __shared__ float tile[64][65];
   const int t = threadIdx.x, c = t & 63;
-  const int64_t n0 = int64_t(blockIdx.x) * 64, b0 = int64_t(blockIdx.y) * 64;
+  const int64_t st_x = (rows + 63) / 64, st_tiles = st_x * ((bpr + 63) / 64);
+  const int64_t g = blockIdx.x;
+  if (g < st_tiles) {
+    const int64_t n0 = (g % st_x) * 64, b0 = (g / st_x) * 64;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t n = n0 + (t >> 6) + 16 * i, b = b0 + c;
+      v[i] = (n < rows && b < bpr) ? sc(n * bpr + b) : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) tile[(t >> 6) + 16 * i][c] = v[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = (t >> 6) + 16 * i;
+      const int64_t b = b0 + r, n = n0 + c;
+      if (b < bpr && n < rows) st[b * rows + n] = tile[c][r];
+    }
+    return;
+  }
+  const int64_t at_x = (K + 63) / 64, ga = g - st_tiles;
+  const int64_t k0 = (ga % at_x) * 64, j0 = (ga / at_x) * 64;
   float v[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int64_t n = n0 + (t >> 6) + 16 * i, b = b0 + c;
-    v[i] = (n < rows && b < bpr) ? sc(n * bpr + b) : 0.0f;
+    const int64_t j = j0 + (t >> 6) + 16 * i, k = k0 + c;
+    v[i] = (j < rank && k < K) ? load_as_f32(a, j * K + k, a_dt) : 0.0f;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) tile[(t >> 6) + 16 * i][c] = v[i];
@@ -212,36 +244,47 @@ __global__ __launch_bounds__(1024) void scale_transpose_kernel(Scale sc, int64_t
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = (t >> 6) + 16 * i;
-    const int64_t b = b0 + r, n = n0 + c;
-    if (b < bpr && n < rows) st[b * rows + n] = tile[c][r];
+    const int64_t k = k0 + r, j = j0 + c;
+    if (k < K && j < rank16) at[k * rank16 + j] = uint16_t(to_x16<XT>(tile[c][r]));
   }
 }
 
 template <class Scale>
-static int launch_scale_transpose(Scale sc, int64_t rows, int64_t bpr, float* st, hipStream_t stream) {
-  const dim3 grid(unsigned((rows + 63) / 64), unsigned((bpr + 63) / 64));
-  scale_transpose_kernel<Scale><<<grid, 1024, 0, stream>>>(sc, rows, bpr, st);
+static int launch_dx_prep(const DxArgs& D, Scale sc, int64_t bpr, float* st, int rank16, uint16_t* at,
+                          hipStream_t stream) {
+  const int64_t tiles = ((D.N + 63) / 64) * ((bpr + 63) / 64) + (at ? ((D.K + 63) / 64) * ((rank16 + 63) / 64) : 0);
+  const int r = at ? int(D.rank) : 0;
+  if (D.dy_dtype == RQ_DTYPE_BF16)
+    dx_prep_kernel<Scale, RQ_DTYPE_BF16><<<unsigned(tiles), 1024, 0, stream>>>(sc, D.N, bpr, st, D.lora_a,
+                                                                              D.lora_dtype, D.K, r, rank16, at);
+  else
+    dx_prep_kernel<Scale, RQ_DTYPE_F16><<<unsigned(tiles), 1024, 0, stream>>>(sc, D.N, bpr, st, D.lora_a,
+                                                                             D.lora_dtype, D.K, r, rank16, at);
   return rq_check_launch();
 }
 
-// The transposed scales of a dX call, by scale format.
-static int run_scale_transpose(const DxArgs& D, float* st, hipStream_t stream) {
+// The transposed scales of a dX call, by scale format (and RND(A)^T when at
+// is given).
+static int run_dx_prep(const DxArgs& D, float* st, int rank16, uint16_t* at, hipStream_t stream) {
   const int64_t bpr = D.K / D.block_size;
   if (D.c2) {
     const int sh = pow2_shift(D.block2);
     switch (D.absmax_dtype) {
       case RQ_DTYPE_F32:
-        return launch_scale_transpose(ScaleDQ<RQ_DTYPE_F32>{D.c2, D.absmax, D.c2_format, sh, D.block2}, D.N, bpr, st, stream);
+        return launch_dx_prep(D, ScaleDQ<RQ_DTYPE_F32>{D.c2, D.absmax, D.c2_format, sh, D.block2}, bpr, st, rank16, at,
+                              stream);
       case RQ_DTYPE_BF16:
-        return launch_scale_transpose(ScaleDQ<RQ_DTYPE_BF16>{D.c2, D.absmax, D.c2_format, sh, D.block2}, D.N, bpr, st, stream);
+        return launch_dx_prep(D, ScaleDQ<RQ_DTYPE_BF16>{D.c2, D.absmax, D.c2_format, sh, D.block2}, bpr, st, rank16,
+                              at, stream);
       default:
-        return launch_scale_transpose(ScaleDQ<RQ_DTYPE_F16>{D.c2, D.absmax, D.c2_format, sh, D.block2}, D.N, bpr, st, stream);
+        return launch_dx_prep(D, ScaleDQ<RQ_DTYPE_F16>{D.c2, D.absmax, D.c2_format, sh, D.block2}, bpr, st, rank16, at,
+                              stream);
     }
   }
   switch (D.absmax_dtype) {
-    case RQ_DTYPE_F32: return launch_scale_transpose(ScaleAbsmax<RQ_DTYPE_F32>{D.absmax}, D.N, bpr, st, stream);
-    case RQ_DTYPE_BF16: return launch_scale_transpose(ScaleAbsmax<RQ_DTYPE_BF16>{D.absmax}, D.N, bpr, st, stream);
-    default: return launch_scale_transpose(ScaleAbsmax<RQ_DTYPE_F16>{D.absmax}, D.N, bpr, st, stream);
+    case RQ_DTYPE_F32: return launch_dx_prep(D, ScaleAbsmax<RQ_DTYPE_F32>{D.absmax}, bpr, st, rank16, at, stream);
+    case RQ_DTYPE_BF16: return launch_dx_prep(D, ScaleAbsmax<RQ_DTYPE_BF16>{D.absmax}, bpr, st, rank16, at, stream);
+    default: return launch_dx_prep(D, ScaleAbsmax<RQ_DTYPE_F16>{D.absmax}, bpr, st, rank16, at, stream);
   }
 }
 
@@ -250,6 +293,8 @@ static int run_scale_transpose(const DxArgs& D, float* st, hipStream_t stream) {
 static size_t dx_scale_t_bytes(int64_t N, int64_t K, int64_t block_size) {
   return (size_t(N) * size_t(K / block_size) * 4 + 255) & ~size_t(255);
 }
+// Bytes of RND(A)^T [K][rank16] in a 16-bit dtype, 256-byte padded.
+static size_t dx_at_bytes(int64_t K, int64_t rank16) { return (size_t(K) * size_t(rank16) * 2 + 255) & ~size_t(255); }
 
 int gemm_workspace(const LinearArgs& L, size_t* bytes) {
   *bytes = plan_gemm(L.M, L.N, L.K, L.rank, device_cus(), true).ws_bytes;
@@ -295,6 +340,8 @@ int run_nf4_gemm(const LinearArgs& L, void* workspace, size_t ws_bytes, uint32_t
     e.b_sn = L.ld_lora_b;
     e.b_sj = 1;
     e.b_vec = aligned(L.lora_b, 16) && (L.lora_dtype != RQ_DTYPE_F32 || L.ld_lora_b % 4 == 0);
+    e.lora_regs = p.rank16 <= 64 && e.rank % 8 == 0 && aligned(L.lora_b, 16) &&
+                  L.ld_lora_b % (L.lora_dtype == RQ_DTYPE_F32 ? 4 : 8) == 0;
   }
   GemmArgs a{};
   a.x = static_cast<const uint16_t*>(L.x);
@@ -363,7 +410,8 @@ int dx_workspace(const DxArgs& D, size_t* bytes) {
   const size_t g = generic_lora_bytes(D.dy_dtype, D.M, D.rank);
   const bool fast = D.dy_dtype != RQ_DTYPE_F32 && D.N % 64 == 0 && D.K % 64 == 0;
   const size_t core = (plan_gemm(D.M, D.K, D.N, D.rank > 0 ? D.rank : 0, device_cus()).ws_bytes + 255) & ~size_t(255);
-  *bytes = std::max(g, fast ? core + dx_scale_t_bytes(D.N, D.K, 64) : size_t(0));
+  const int64_t r16 = D.rank > 0 ? (D.rank + 15) & ~int64_t(15) : 0;
+  *bytes = std::max(g, fast ? core + dx_scale_t_bytes(D.N, D.K, 64) + (r16 ? dx_at_bytes(D.K, r16) : 0) : size_t(0));
   return RQ_OK;
 }
 
@@ -416,11 +464,25 @@ int run_nf4_dx(const DxArgs& D, void* workspace, size_t ws_bytes, hipStream_t st
   // With room in the workspace, the scales are decoded and transposed first
   // (one small launch), so that a step's scales are contiguous: at the
   // Llama-3-8B gate shape the scattered per-row scale reads kept the
-  // texture addresser 65 % busy and made the dX 12-17 % slower.
+  // texture addresser 65 % busy and made the dX 12-17 % slower.  The same
+  // launch writes RND(A)^T in the activation dtype when there is room for it
+  // too, the epilogue's LoRA operand as 16-byte rows.
   const size_t st_off = (p.ws_bytes + 255) & ~size_t(255);
-  if (workspace && ws_bytes >= st_off + dx_scale_t_bytes(D.N, D.K, D.block_size)) {
-    float* st = reinterpret_cast<float*>(static_cast<char*>(workspace) + st_off);
-    if (const int s2 = run_scale_transpose(D, st, stream); s2 != RQ_OK) return s2;
+  const size_t st_bytes = dx_scale_t_bytes(D.N, D.K, D.block_size);
+  if (workspace && ws_bytes >= st_off + st_bytes) {
+    char* ws = static_cast<char*>(workspace);
+    float* st = reinterpret_cast<float*>(ws + st_off);
+    uint16_t* at = nullptr;
+    if (rank > 0 && ws_bytes >= st_off + st_bytes + dx_at_bytes(D.K, p.rank16)) {
+      at = reinterpret_cast<uint16_t*>(ws + st_off + st_bytes);
+      e.braw = at;
+      e.b_dt = D.dy_dtype;
+      e.b_sn = p.rank16;
+      e.b_sj = 1;
+      e.b_vec = true;
+      e.lora_regs = p.rank16 <= 64 && rank % 8 == 0;
+    }
+    if (const int s2 = run_dx_prep(D, st, p.rank16, at, stream); s2 != RQ_OK) return s2;
     const ScaleT sct{st};
     if (D.dy_dtype == RQ_DTYPE_BF16) return launch_core8<RQ_DTYPE_BF16, Dx8Producer>(a, pp, sct, e, stream);
     return launch_core8<RQ_DTYPE_F16, Dx8Producer>(a, pp, sct, e, stream);

@@ -28,6 +28,7 @@ constexpr int kGemm8NB = 2;  // 32-column blocks per wave
 template <int XT, class Scale>
 struct Fwd8Producer {
   static constexpr int kLoads = 1 + Scale::kLoads;
+  static constexpr bool kLoraRegs = true;  // takes e.lora_regs (see GemmEpi)
   struct Regs {
     u32x2 w;
     typename Scale::Raw s;
@@ -277,6 +278,31 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
   typename Prod::Regs wl[kWDepth];
 #pragma unroll
   for (int d = 0; d < kWDepth; ++d) prod.issue(wl[d], ks(d));
+  // The epilogue's LoRA operands (e.lora_regs: one staging chunk), read raw
+  // now so that their latency hides under the prologue's: slot i of thread
+  // t is 16-byte chunk c = (t + 512 i) % 8 of row (t + 512 i) / 8 of the u
+  // rows (4 slots) and of the B rows (2 slots, two 16-byte halves for fp32);
+  // chunks past rank16 / 8 re-read chunk 0 and are not staged.
+  u32x4 lu[4], lb[2][2];
+  if (Prod::kLoraRegs && e.lora_regs) {
+    const int w8 = e.rank16 >> 3, bsh = e.b_dt == RQ_DTYPE_F32 ? 2 : 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + kGemm8Threads * i, c = idx & 7;
+      int64_t m = m0 + (idx >> 3);
+      m = m < a.M ? m : a.M - 1;
+      lu[i] = *reinterpret_cast<const u32x4*>(e.u + m * e.rank16 + 8 * (c < w8 ? c : 0));
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int idx = tid + kGemm8Threads * i, c = idx & 7;
+      int64_t n = n0 + (idx >> 3);
+      n = n < a.N ? n : a.N - 1;
+      const uint8_t* row = static_cast<const uint8_t*>(e.braw) + ((n * e.b_sn + 8 * (c < w8 ? c : 0)) << bsh);
+      lb[i][0] = *reinterpret_cast<const u32x4*>(row);
+      lb[i][1] = *reinterpret_cast<const u32x4*>(row + (bsh == 2 ? 16 : 0));
+    }
+  }
   fill_f32pair_lut<kGemm8Threads>(lut, tid);
   __syncthreads();
   {
@@ -423,6 +449,20 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
     for (int j0 = 0; j0 < e.rank16; j0 += 64) {
       const int w8 = (e.rank16 - j0 < 64 ? e.rank16 - j0 : 64) / 8;  // 16-byte chunks per row
       __syncthreads();  // the tiles, ring and table (first chunk) or the last chunk's operands are free
+      if (Prod::kLoraRegs && e.lora_regs) {  // the only chunk, read in the prologue
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int idx = tid + kGemm8Threads * i, r = idx >> 3, c = idx & 7;
+          if (c < w8) *reinterpret_cast<u32x4*>(us + r * kP + 8 * c) = lu[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int idx = tid + kGemm8Threads * i, r = idx >> 3, c = idx & 7;
+          if (c < w8)
+            *reinterpret_cast<u32x4*>(bs + r * kP + 8 * c) =
+                8 * c < e.rank ? raw8_to_x<XT>(lb[i][0], lb[i][1], e.b_dt) : u32x4{0u, 0u, 0u, 0u};
+        }
+      } else {
       for (int idx = tid; idx < kGemmBM * w8; idx += kGemm8Threads) {
         const int r = idx / w8, c = idx - r * w8;
         int64_t m = m0 + r;
@@ -438,6 +478,7 @@ void nf4_gemm8_kernel(GemmArgs a, ProducerParams pp, Scale scale, GemmEpi e) {
         *reinterpret_cast<u32x4*>(bs + r * kP + 8 * c) =
             e.b_sj == 1 ? load_a8_masked<XT>(e.braw, e.b_dt, n * e.b_sn + j, e.rank - j, e.b_vec)
                         : load_a8_strided<XT>(e.braw, e.b_dt, n * e.b_sn + j * e.b_sj, e.b_sj, e.rank - j);
+      }
       }
       __syncthreads();
       for (int s = 0; s < w8 / 2; ++s) {

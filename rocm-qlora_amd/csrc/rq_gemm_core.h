@@ -57,6 +57,10 @@ struct GemmEpi {
   int b_dt;
   int64_t b_sn, b_sj;
   bool b_vec;            // b_sj == 1 and braw rows 16-byte aligned (fp32 vector loads)
+  // rank16 <= 64, rank % 8 == 0, b_sj == 1 and u and braw rows 16-byte
+  // aligned: the kernel reads the tile's u and B rows into registers during
+  // its prologue, 16 bytes at a time
+  bool lora_regs;
   float scaling;         // 1 for dX
   // dX with LoRA dropout: the adapter term is RND(RND(lora) * (mask ? mask_scale
   // : 0)) (dropout's backward, mask [M][N] bytes with row stride ldm);

@@ -171,6 +171,25 @@ __device__ __forceinline__ u32x4 load_a8(const void* p, int dt, int64_t off, boo
   return u32x4{w[0], w[1], w[2], w[3]};
 }
 
+// 8 consecutive LoRA values loaded raw as 16-byte pieces (fp32: lo holds
+// the first 4, hi the next 4; 16-bit: lo holds all 8), rounded to the
+// activation dtype as load_a8 rounds them.
+template <int XT>
+__device__ __forceinline__ u32x4 raw8_to_x(const u32x4& lo, const u32x4& hi, int dt) {
+  if (dt == RQ_DTYPE_F32)
+    return u32x4{cvt_pk<XT>(u2f(lo.x), u2f(lo.y)), cvt_pk<XT>(u2f(lo.z), u2f(lo.w)), cvt_pk<XT>(u2f(hi.x), u2f(hi.y)),
+                 cvt_pk<XT>(u2f(hi.z), u2f(hi.w))};
+  const uint32_t w[4] = {lo.x, lo.y, lo.z, lo.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float a = dt == RQ_DTYPE_BF16 ? bf16_to_f32(uint16_t(w[j])) : f16_to_f32(uint16_t(w[j]));
+    const float b = dt == RQ_DTYPE_BF16 ? bf16_to_f32(uint16_t(w[j] >> 16)) : f16_to_f32(uint16_t(w[j] >> 16));
+    o[j] = cvt_pk<XT>(a, b);
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
 // 8 consecutive values p[off + e] (e < n_live, zeros past), rounded to the
 // activation dtype; the vector path when all 8 are live.
 template <int XT>

@@ -164,14 +164,19 @@ def _dx_call(dev, dy, packed, scales, K, block, ws_bytes, c2=None, a=None, b=Non
 
 
 @pytest.mark.parametrize("N,K,case", [(512, 4096, "f32"), (512, 4096, "bf16"), (512, 4096, "dq"),
-                                      (512, 64, "f32"), (256, 64, "bf16"), (512, 1024, "lora")])
+                                      (512, 64, "f32"), (256, 64, "bf16"), (512, 1024, "lora"),
+                                      (512, 1024, "lora64"), (256, 1024, "lora12"), (256, 1024, "lora96")])
 def test_dx_transposed_scales_match_direct(dev, N, K, case):
-    """With room in the workspace the dX kernel reads scales decoded and
-    transposed by a launch before it ([blocks][rows] fp32, a step's scales
-    contiguous); without it, the absmax (or c2 codes and their scales)
-    directly.  Both give the same bits: fp32 and bf16 absmax, double
+    """With room in the workspace a launch before the dX kernel decodes and
+    transposes the scales ([blocks][rows] fp32, a step's scales contiguous)
+    and, with LoRA, writes RND(A)^T as 16-bit rows (the epilogue's operand,
+    read into registers during the kernel's prologue for ranks up to 64 that
+    are multiples of 8); with less room, the scales transposed and A read in
+    place; with less still, the absmax (or c2 codes and their scales)
+    directly.  All give the same bits: fp32 and bf16 absmax, double
     quantization, one block per row (K == block size, where the two rows a
-    thread dequantizes have adjacent scales), and with the LoRA term."""
+    thread dequantizes have adjacent scales), and LoRA ranks 16, 64, 12 and
+    96."""
     import ctypes
     from rocm_qlora import _native as nat
     M = 300
@@ -185,19 +190,26 @@ def test_dx_transposed_scales_match_direct(dev, N, K, case):
         packed, scales, c2 = st.W_quant.reshape(-1), st.c2_scales, st.c2.reshape(-1).view(torch.uint8)
     else:
         packed, scales = quantize_int4(w.to(dev).to(torch.bfloat16 if case == "bf16" else torch.float32), 64)
-    rank = 16 if case == "lora" else 0
+    rank = {"lora": 16, "lora64": 64, "lora12": 12, "lora96": 96}.get(case, 0)
     a = (torch.randn(rank, K, generator=g) * 0.05).to(dev) if rank else None
     b = (torch.randn(N, rank, generator=g) * 0.05).to(dev) if rank else None
     nb = ctypes.c_int64(0)
     nat.call("rq_nf4_linear_dx_workspace_size", nat.dtype_code(dy.dtype), M, N, K, rank, ctypes.byref(nb))
-    # the workspace ends with the transposed scales
+    # the workspace ends with the transposed scales, then RND(A)^T
     st_bytes = (N * (K // 64) * 4 + 255) // 256 * 256
-    assert nb.value >= st_bytes
+    at_bytes = (K * ((rank + 15) // 16 * 16) * 2 + 255) // 256 * 256 if rank else 0
+    assert nb.value >= st_bytes + at_bytes
     full = _dx_call(dev, dy, packed, scales, K, 64, nb.value, c2, a, b, rank)
-    direct = _dx_call(dev, dy, packed, scales, K, 64, nb.value - st_bytes, c2, a, b, rank)
+    if rank:
+        scales_only = _dx_call(dev, dy, packed, scales, K, 64, nb.value - at_bytes, c2, a, b, rank)
+        assert torch.equal(full.view(torch.int16), scales_only.view(torch.int16))
+    direct = _dx_call(dev, dy, packed, scales, K, 64, nb.value - at_bytes - st_bytes, c2, a, b, rank)
     assert torch.equal(full.view(torch.int16), direct.view(torch.int16))
     if case in ("f32", "bf16"):
         ref = R.nf4_dx(dy.cpu(), packed.cpu(), scales.cpu(), N, K, None, None, 0.0, 64)
+        _check(full.cpu(), ref)
+    if rank:
+        ref = R.nf4_dx(dy.cpu(), packed.cpu(), scales.cpu(), N, K, a.cpu(), b.cpu(), 0.25, 64)
         _check(full.cpu(), ref)
 
 

@@ -53,15 +53,15 @@ def test_gemm_llama3_shapes_bf16(dev, K, N):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", ["plain", "bias", "odd_n", "odd_m", "m17", "block128", "strided_x",
-                                  "dropout_x", "no_lora", "k64", "k320", "rank8", "rank16", "rank24", "rank96",
-                                  "rank256",
+                                  "dropout_x", "no_lora", "k64", "k320", "rank8", "rank12", "rank16", "rank24",
+                                  "rank96", "rank256",
                                   "bf16_lora", "tiles8", "strided_b"])
 def test_gemm_variants(dev, dtype, case):
     N, K, M = 640, 512, 300
     N = {"odd_n": 1000, "tiles8": 512}.get(case, N)
     M = {"odd_m": 777, "m17": 17, "tiles8": 512}.get(case, M)
     K = {"k64": 64, "k320": 320}.get(case, K)
-    rank = {"rank8": 8, "rank16": 16, "rank24": 24, "rank96": 96, "rank256": 256}.get(case, 64)
+    rank = {"rank8": 8, "rank12": 12, "rank16": 16, "rank24": 24, "rank96": 96, "rank256": 256}.get(case, 64)
     bs = 128 if case == "block128" else 64
     print(f"gemm variant {case} {dtype}", flush=True)
     w, x, a, b, bvec = _inputs(N, K, M, dtype, seed=11, rank=rank, bias=(case == "bias"))
@@ -192,3 +192,23 @@ def test_gemm_k_splits_and_shared_workspace(dev, sync_ready):
     key = (dev.index if dev.index is not None else torch.cuda.current_device(),
            torch.cuda.current_stream(dev).cuda_stream)
     assert sync_ready(ops._LINEAR_WS[key])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rank,lora_dt", [(64, torch.float32), (24, torch.float32), (64, torch.bfloat16)])
+def test_gemm_lora_operand_paths_match(dev, dtype, rank, lora_dt):
+    """The epilogue's LoRA operands are read into registers during the
+    kernel's prologue when B's rows allow 16-byte loads (rank <= 64, a
+    multiple of 8), and staged from memory after the main loop otherwise.
+    The same values as a strided view of B (rows not 16-byte aligned) take
+    the second path and give the same bits."""
+    N, K, M = 640, 512, 300
+    print(f"gemm lora operand paths rank={rank} {lora_dt} {dtype}", flush=True)
+    w, x, a, b, _ = _inputs(N, K, M, dtype, seed=19, rank=rank)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    a, b = a.to(lora_dt).to(dev), b.to(lora_dt).to(dev)
+    wide = torch.zeros(N, rank + 3, dtype=b.dtype, device=dev)
+    wide[:, 1:1 + rank] = b
+    y_regs = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=a, lora_b=b, scaling=0.5)
+    y_mem = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=a, lora_b=wide[:, 1:1 + rank], scaling=0.5)
+    assert torch.equal(y_regs.view(torch.int16), y_mem.view(torch.int16))
