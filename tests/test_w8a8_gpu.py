@@ -54,6 +54,45 @@ def test_quantize_rows_bit_exact(dev, dtype, M, K):
     _equal(q, qr, "codes")
 
 
+def _half_integer_rows(dtype, n_rows=16, K=64):
+    """Rows whose largest value m sets s = RN32(m / 127) and whose other
+    values x give quotients that round (rint) differently as RN32(x / s) and
+    as RN32(x * RN32(1 / s)): quotients on or within a few fp32 ulps of a
+    half-integer, found by brute force over every finite value of dtype."""
+    bits = torch.arange(0, 65536, dtype=torch.int32).to(torch.int16).view(dtype).float()
+    vals = bits[torch.isfinite(bits)]
+    rows = []
+    for mx in vals[(vals >= 0.5) & (vals <= 8.0)].tolist():
+        s = torch.tensor(mx, dtype=torch.float32) / 127.0
+        rs = 1.0 / s
+        x = vals[vals.abs() < mx]
+        bad = x[torch.round(x / s) != torch.round(x * rs)]  # round half to even, as rint
+        if len(bad) == 0:
+            continue
+        row = torch.zeros(K)
+        row[0] = mx
+        row[1:1 + min(len(bad), K - 1)] = bad[:K - 1]
+        rows.append(row)
+        if len(rows) == n_rows:
+            break
+    assert len(rows) >= 4
+    return torch.stack(rows).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_quantize_rows_half_integer_quotients(dev, dtype):
+    """Rows made of values whose quotients x / s lie on or within a few fp32
+    ulps of a half-integer, where a quotient through RN32(1 / s) would round
+    to the other integer: the kernel's codes match the oracle's true
+    division bit for bit."""
+    print(f"w8a8 quantize rows at half-integer quotients {dtype}", flush=True)
+    x = _half_integer_rows(dtype)
+    q, s = ops.int8_quantize_rows(x.to(dev))
+    qr, sr = R.quantize_rows_int8(x)
+    _equal(s, sr, "scales")
+    _equal(q, qr, "codes")
+
+
 def test_quantize_rows_strided_input(dev):
     x = _x(40, 640, torch.bfloat16, seed=3)
     xs = x[:, 64:576]  # row stride 640, 16-byte aligned rows
