@@ -5,7 +5,10 @@ with per-tensor scales on the gfx950 FP8 kernels: x and W are quantized
 with scale = fp32(max|t| / 240) and codes = fnuz(RND(t / scale)), their
 products are summed in fp32, scaled by x_scale * w_scale and rounded to x's
 dtype, then the bias is added (fp8_linear.py:27-60).  Backward gives dX =
-dY . W (the base weight is frozen).  The LoRA term stays in x's dtype.
+dY . W (the base weight is frozen) from the stored NF4 / INT8 codes by the
+HIP dX kernels, whose weight operand is the dequantized weight rounded to
+dY's dtype -- the reference's `grad_output @ w.to(grad_output.dtype)`.
+The LoRA term stays in x's dtype.
 """
 from __future__ import annotations
 
@@ -33,19 +36,30 @@ def _fp8_forward(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor],
 
 
 class _FP8LinearFunc(torch.autograd.Function):
-    """FP8 forward, dX = dY . W backward (fp8_linear.py:19-67)."""
+    """FP8 forward, dX = dY . W backward (fp8_linear.py:19-67).  w_q: the
+    weight's FP8 codes and scale (or None: w_fp16 is quantized here); qw: the
+    layer's quantized weight (NF4Weight or Int8Weight) the FP8 codes were
+    made from, which the backward multiplies by."""
 
     @staticmethod
-    def forward(ctx, x, w_fp16, bias, w_q=None):
-        ctx.save_for_backward(w_fp16)
+    def forward(ctx, x, w_fp16, bias, w_q, qw):
+        ctx.qw = qw
         ctx.has_bias = bias is not None
         ctx.fp8_used = True
         return _fp8_forward(x, w_fp16, bias, w_q)
 
     @staticmethod
     def backward(ctx, grad_output):
-        (w,) = ctx.saved_tensors
-        return grad_output @ w.to(grad_output.dtype), None, None, None
+        from rocm_qlora.kernels.dequant_matmul import NF4Weight
+        qw = ctx.qw
+        if not qw.kernel_ok(grad_output.dtype):
+            raise TypeError(f"FP8 backward takes fp32/bf16/fp16 gradients, got {grad_output.dtype}")
+        if isinstance(qw, NF4Weight):
+            dx = torch_ops.call_nf4_linear_dx(grad_output, qw.packed, qw.scales, qw.K, qw.block_size,
+                                              **qw.dq_kwargs())
+        else:
+            dx = torch_ops.call_int8_linear_dx(grad_output, qw.q, qw.scales, qw.K, qw.block_size)
+        return dx, None, None, None, None
 
 
 class FP8LinearWrapper(nn.Module):
@@ -54,7 +68,8 @@ class FP8LinearWrapper(nn.Module):
     else 'bf16' (the wrapped layer unchanged).  The reference's third
     backend, TransformerEngine, is not dispatched to: there is one FP8 code
     path.  The FP8 weight codes are cached, in the matrix cores' e4m3fn
-    encoding, until the stored weight changes."""
+    encoding, until the stored weight changes; the dequantized 16-bit weight
+    they come from is not kept (the backward multiplies by the stored codes)."""
 
     def __init__(self, base_lora_linear: nn.Module, config: Optional[FP8Config] = None):
         super().__init__()
@@ -73,19 +88,18 @@ class FP8LinearWrapper(nn.Module):
         key = (ql.weight_quant.data_ptr(), ql.weight_quant._version, dtype,
                getattr(ql, "c2", ql.weight_scales).data_ptr())
         if self._cache_key != key:
-            w = ql.dequantized_weight(dtype)
-            codes, scale = ops.fp8_quantize(w)
-            wq = (ops.fp8_to_e4m3fn(codes), scale)
-            self._cache = (w, wq)
+            codes, scale = ops.fp8_quantize(ql.dequantized_weight(dtype))
+            self._cache = (ops.fp8_to_e4m3fn(codes), scale)
             self._cache_key = key
         return self._cache
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.backend == "native":
             ql = self.base.base_layer
-            w, w_q = self._weight(x.dtype)
+            w_q = self._weight(x.dtype)
             bias = ql.bias.to(x.dtype) if ql.bias is not None else None
-            base_out = _FP8LinearFunc.apply(x, w, bias, w_q)
+            qw = ql.nf4_weight() if ql.bits == 4 else ql.int8_weight()
+            base_out = _FP8LinearFunc.apply(x, None, bias, w_q, qw)
             lora_out = (self.base.lora_dropout(x) @ self.base.lora_A.t().to(x.dtype)
                         @ self.base.lora_B.t().to(x.dtype) * self.base.scaling)
             return base_out + lora_out.to(base_out.dtype)

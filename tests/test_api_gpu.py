@@ -379,14 +379,15 @@ def test_dequantize_nf4_triton_bf16_bit_exact(dev):
     assert torch.equal(out.cpu().view(torch.int16), ref.view(torch.int16))
 
 
+@pytest.mark.parametrize("bits", [4, 8])
 @pytest.mark.parametrize("M", [1, 300])
-def test_fp8_wrapper_native(dev, M):
+def test_fp8_wrapper_native(dev, M, bits):
     """FP8LinearWrapper (fp8_linear.py:69-118) on gfx950: base matmul by the
     FP8 kernels (per-tensor e4m3fnuz of x and W_deq), LoRA term in bf16,
-    dX = dY . W."""
+    dX = dY . W by the NF4 / INT8 dX kernels from the stored codes."""
     from rocm_qlora.fp8 import FP8LinearWrapper, wrap_model_for_fp8
     K, N = 512, 384
-    ql = QuantLinear.from_linear(_linear(K, N, seed=11).to(dev), bits=4)
+    ql = QuantLinear.from_linear(_linear(K, N, seed=11).to(dev), bits=bits)
     lora = LoRALinear(ql, r=8, lora_alpha=16)
     with torch.no_grad():
         lora.lora_B.normal_(0, 0.01)
