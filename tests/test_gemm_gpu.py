@@ -212,3 +212,47 @@ def test_gemm_lora_operand_paths_match(dev, dtype, rank, lora_dt):
     y_regs = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=a, lora_b=b, scaling=0.5)
     y_mem = ops.nf4_linear(x.to(dev), packed, absmax, N, 64, lora_a=a, lora_b=wide[:, 1:1 + rank], scaling=0.5)
     assert torch.equal(y_regs.view(torch.int16), y_mem.view(torch.int16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gemm_output_strides(dev, dtype):
+    """The epilogue stores whole tiles through LDS as 128-byte row pieces
+    when the output rows are 16-byte aligned, four-output runs when they are
+    8-byte aligned, and single values otherwise.  Output row strides N, N + 4
+    and N + 3 (through the C ABI) give the same bits in the N columns and
+    leave the padding as it was; the forward at N = 1001 (a partial column
+    tile, rows not 8-byte aligned) matches the oracle."""
+    import ctypes
+    from rocm_qlora import _native as nat
+    M, K, N, rank = 300, 512, 512, 16
+    print(f"gemm output strides {dtype}", flush=True)
+    w, x, a, b, bvec = _inputs(N, K, M, dtype, seed=23, rank=rank, bias=True)
+    packed, absmax = quantize_int4(w.to(dev), 64)
+    xd, ad, bd, biasd = x.to(dev), a.to(dev), b.to(dev), bvec.to(dtype).to(dev)
+    nb = ctypes.c_int64(0)
+    nat.call("rq_nf4_linear_workspace_size", nat.dtype_code(dtype), M, K, N, rank, ctypes.byref(nb))
+    outs = []
+    for ld in (N, N + 4, N + 3):
+        ws = torch.zeros(nb.value, dtype=torch.uint8, device=dev)
+        y = torch.full((M, ld), -7.0, dtype=dtype, device=dev)
+        nat.call("rq_nf4_linear", xd.data_ptr(), nat.dtype_code(dtype), M, K, K,
+                 packed.data_ptr(), N, 64, absmax.data_ptr(), nat.dtype_code(absmax.dtype),
+                 None, nat.C2_FP8_E4M3FNUZ, 256, biasd.data_ptr(), nat.dtype_code(biasd.dtype),
+                 xd.data_ptr(), K, ad.data_ptr(), bd.data_ptr(), rank, nat.dtype_code(ad.dtype), rank, 0.5,
+                 y.data_ptr(), ld, ws.data_ptr(), ws.numel(), nat.stream_handle(dev))
+        torch.cuda.synchronize(dev)
+        assert bool((y[:, N:] == -7.0).all()), f"ldy={ld}: padding written"
+        outs.append(y[:, :N].contiguous())
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    wf = R.dequantize_int4(packed.cpu(), absmax.cpu(), 64)
+    ref = R.quant_linear_forward(x, wf, bvec, N, K) + \
+        (x @ a.to(dtype).T @ b.to(dtype).T * 0.5).to(dtype)
+    _check(outs[0], ref)
+    N2 = 1001
+    w2, x2, a2, b2, _ = _inputs(N2, K, M, dtype, seed=29, rank=rank)
+    p2, s2 = quantize_int4(w2.to(dev), 64)
+    y2 = ops.nf4_linear(x2.to(dev), p2, s2, N2, 64, lora_a=a2.to(dev), lora_b=b2.to(dev), scaling=0.5)
+    ref2 = R.quant_linear_forward(x2, R.dequantize_int4(p2.cpu(), s2.cpu(), 64), None, N2, K) + \
+        (x2 @ a2.to(dtype).T @ b2.to(dtype).T * 0.5).to(dtype)
+    _check(y2, ref2)
