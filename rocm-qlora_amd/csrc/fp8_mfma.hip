@@ -443,9 +443,6 @@ __device__ __forceinline__ uint32_t swz64(uint32_t r, uint32_t c) { return r * 6
 struct Fp8Frags {
   u32x4 a[4][2], b[2][2];
 };
-struct HalfFrags {  // one 16-byte k-half of a stage's fragments
-  u32x4 a[4], b[2];
-};
 
 template <int XT, class Op>
 __global__ __launch_bounds__(kF8Threads) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -504,17 +501,6 @@ void byte_mfma_gemm_kernel(Fp8Args a) {
       for (int e = 0; e < 2; ++e)
         f.a[mb][e] = *reinterpret_cast<const u32x4*>(xt + swz64(arow + 32 * mb, uint32_t(2 * h + e)));
   };
-  auto read_half = [&](HalfFrags& f, int j, int e) {
-    j = j < nk ? j : nk - 1;
-    const uint8_t* xt = lds + (j % kF8Stages) * kF8StageBytes;
-    const uint8_t* wt = xt + kF8TileBytes;
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-      f.b[nb] = *reinterpret_cast<const u32x4*>(wt + swz64(brow + 32 * nb, uint32_t(2 * h + e)));
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-      f.a[mb] = *reinterpret_cast<const u32x4*>(xt + swz64(arow + 32 * mb, uint32_t(2 * h + e)));
-  };
 
   typename Op::Acc32 acc[4][2];
 #pragma unroll
@@ -528,59 +514,32 @@ void byte_mfma_gemm_kernel(Fp8Args a) {
 #pragma unroll
   for (int s = 0; s < kF8Stages - 1; ++s) issue(s);
   step_barrier<4 * (kF8Stages - 2)>();
-  if constexpr (Op::kParts == 2) {
-    // int8: one instruction per k-half, so the fragments are double-buffered
-    // by half: half 1 of stage j is read while half 0 computes, half 0 of
-    // stage j + 1 while half 1 computes (48 fragment VGPRs beside the 128
-    // accumulators; a whole second stage of fragments would not fit)
-    // (each pass: one MFMA, one LDS read, six times, then the last two MFMAs)
-    auto interleave = [] {
+  // the next stage's fragments are read while this stage's MFMAs run; int8
+  // issues the first k-half of all eight blocks before the second, so no
+  // MFMA waits on the one just issued to its accumulator (a half-stage
+  // double buffer for int8 measured the same)
+  Fp8Frags cur;
+  read(cur, 0);
+  for (int j = 0; j < nk; ++j) {
+    step_barrier<4 * (kF8Stages - 3)>();
+    issue(j + kF8Stages - 1);
+    Fp8Frags nxt;
+    read(nxt, j + 1);
+    if constexpr (Op::kParts == 2) {
 #pragma unroll
-      for (int i = 0; i < 6; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-    };
-    HalfFrags lo;
-    read_half(lo, 0, 0);
-    for (int j = 0; j < nk; ++j) {
-      step_barrier<4 * (kF8Stages - 3)>();
-      issue(j + kF8Stages - 1);
-      __builtin_amdgcn_sched_barrier(0);
-      HalfFrags hi;
-      read_half(hi, j, 1);
+      for (int e = 0; e < 2; ++e)
 #pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
+        for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Op::mma32h(lo.b[nb], lo.a[mb], acc[mb][nb]);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
-      HalfFrags nlo;
-      read_half(nlo, j + 1, 0);
-#pragma unroll
-      for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Op::mma32h(hi.b[nb], hi.a[mb], acc[mb][nb]);
-      interleave();
-      __builtin_amdgcn_sched_barrier(0);
-      lo = nlo;
-    }
-  } else {
-    Fp8Frags cur;
-    read(cur, 0);
-    for (int j = 0; j < nk; ++j) {
-      step_barrier<4 * (kF8Stages - 3)>();
-      issue(j + kF8Stages - 1);
-      Fp8Frags nxt;
-      read(nxt, j + 1);
+          for (int nb = 0; nb < 2; ++nb) acc[mb][nb] = Op::mma32h(cur.b[nb][e], cur.a[mb][e], acc[mb][nb]);
+    } else {
 #pragma unroll
       for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
           acc[mb][nb] = Op::mma32(cur.b[nb][0], cur.b[nb][1], cur.a[mb][0], cur.a[mb][1], acc[mb][nb]);
-      cur = nxt;
     }
+    cur = nxt;
   }
   wait_vmcnt<0>();  // no load may still be landing in LDS when it holds the output
   __syncthreads();   // and every wave is done reading the last stage
