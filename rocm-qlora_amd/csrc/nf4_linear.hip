@@ -96,8 +96,6 @@ constexpr int kGemvMaxUSplits = 16;
 constexpr int kGemvXSliceMaxM = 2;  // activation rows through the per-wave LDS slice
 constexpr int kGemvLutQwords = 256 * 32;  // 64 KiB: code byte -> fp32 (T[lo], T[hi]), 32 copies
 constexpr int kGemvLdsBudget = 160 * 1024 - kGemvLutQwords * 8;
-// A buffer offset past every range this file builds: the load returns zero.
-constexpr uint32_t kOobOffset = 0xFFFFFFF0u;
 
 struct GemvArgs {
   const uint16_t* x;
@@ -162,17 +160,8 @@ __host__ __device__ inline size_t gemv_lds_bytes(int TS, int nseg, int M, bool g
   return b;
 }
 
-__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
 __device__ __forceinline__ uint32_t buf_load4_coherent(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return uint32_t(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCoherent));
-}
-__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-__device__ __forceinline__ uint32_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return uint32_t(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
 }
 __device__ __forceinline__ uint32_t buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return uint32_t(__builtin_amdgcn_raw_buffer_load_b8(r, off, 0, 0));

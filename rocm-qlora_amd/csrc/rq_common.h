@@ -257,6 +257,19 @@ constexpr int kCoherent = 16;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, int(bytes), kBufferRsrcWord3);
 }
+// A buffer offset past the end of any resource of at most 0xFFFFFFF0 bytes:
+// a load there returns zero.  (kOobOffset + 16 wraps to 0, so a second
+// piece of a dead lane needs its own select.)
+constexpr uint32_t kOobOffset = 0xFFFFFFF0u;
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ uint32_t buf_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+}
+__device__ __forceinline__ uint32_t buf_load2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return uint32_t(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+}
 // voff: per-lane byte offset; soff: a wave-uniform byte offset added to it
 __device__ __forceinline__ u32x4 buf_load16_coherent(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff = 0) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kCoherent));
