@@ -163,18 +163,22 @@ __device__ __forceinline__ float absmax8(const u32x4& v, float m) {
   return m;
 }
 
-// NaN-propagating max over a 1024-thread workgroup (deterministic tree).
-__device__ __forceinline__ float block_absmax_1024(float m, float* red) {
-  red[threadIdx.x] = m;
+// NaN-propagating max over a workgroup of T threads (T a multiple of 64):
+// lane shuffles within each wave, then the T / 64 waves' maxima through red
+// behind one barrier (a tree through LDS would take log2(T) barriers).  Max
+// is exact, so the result does not depend on the order (a NaN when any input
+// is one).  Every thread returns it; red is not written again.
+template <int T>
+__device__ __forceinline__ float block_max_nan(float m, float* red) {
+  static_assert(T % 64 == 0 && T <= 1024, "whole waves");
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) m = max_nan(m, __shfl_xor(m, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
   __syncthreads();
-  for (int o = 512; o > 0; o >>= 1) {
-    if (int(threadIdx.x) < o) {
-      const float b = red[threadIdx.x + o], c = red[threadIdx.x];
-      red[threadIdx.x] = (b > c || b != b) ? b : c;
-    }
-    __syncthreads();
-  }
-  return red[0];
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < T / 64; ++w) r = max_nan(r, red[w]);
+  return r;
 }
 
 // One workgroup: absmax, the scale (also stored), then the codes.
@@ -182,7 +186,7 @@ template <int DT>
 __global__ __launch_bounds__(1024) void fp8_quant_small_kernel(const uint16_t* __restrict__ x, int64_t rows,
                                                                int64_t cols, int64_t ld, float* __restrict__ scale,
                                                                uint8_t* __restrict__ codes) {
-  __shared__ float red[1024];
+  __shared__ float red[16];
   const int gpr = int(cols / 8);
   const int total = int(rows) * gpr;
   float m = 0.0f;
@@ -190,7 +194,7 @@ __global__ __launch_bounds__(1024) void fp8_quant_small_kernel(const uint16_t* _
     const int r = i / gpr, c = i - r * gpr;
     m = absmax8<DT>(*reinterpret_cast<const u32x4*>(x + int64_t(r) * ld + 8 * c), m);
   }
-  const float s = float(double(block_absmax_1024(m, red)) / 240.0);
+  const float s = float(double(block_max_nan<1024>(m, red)) / 240.0);
   if (threadIdx.x == 0) *scale = s;
   const float rs = recip_rn(s);
   for (int i = threadIdx.x; i < total; i += 1024) {
@@ -205,23 +209,15 @@ constexpr int kFp8AbsmaxBlocks = 1024;
 template <int DT>
 __global__ __launch_bounds__(256) void fp8_absmax16_kernel(const uint16_t* __restrict__ x, int64_t rows,
                                                            int64_t cols, int64_t ld, float* __restrict__ part) {
-  __shared__ float red[256];
+  __shared__ float red[4];
   const int64_t gpr = cols / 8, total = rows * gpr;
   float m = 0.0f;
   for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
     const int64_t r = i / gpr, c = i - r * gpr;
     m = absmax8<DT>(*reinterpret_cast<const u32x4*>(x + r * ld + 8 * c), m);
   }
-  red[threadIdx.x] = m;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (int(threadIdx.x) < o) {
-      const float b = red[threadIdx.x + o], c = red[threadIdx.x];
-      red[threadIdx.x] = (b > c || b != b) ? b : c;
-    }
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) part[blockIdx.x] = red[0];
+  m = block_max_nan<256>(m, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
 // ---------------------------------------------------------------------------
@@ -237,22 +233,13 @@ __global__ __launch_bounds__(256) void fp8_absmax16_kernel(const uint16_t* __res
 template <int DT, int T>
 __global__ __launch_bounds__(T) void i8_row_quant_kernel(const uint16_t* __restrict__ x, int64_t K, int64_t ld,
                                                          float* __restrict__ scales, int8_t* __restrict__ codes) {
-  __shared__ float red[T];
+  __shared__ float red[T / 64];
   const int64_t m = blockIdx.x;
   const uint16_t* xr = x + m * ld;
   const int64_t groups = K / 8;
   float mx = 0.0f;
   for (int64_t i = threadIdx.x; i < groups; i += T) mx = absmax8<DT>(*reinterpret_cast<const u32x4*>(xr + 8 * i), mx);
-  red[threadIdx.x] = mx;
-  __syncthreads();
-  for (int o = T / 2; o > 0; o >>= 1) {
-    if (int(threadIdx.x) < o) {
-      const float b = red[threadIdx.x + o], c = red[threadIdx.x];
-      red[threadIdx.x] = (b > c || b != b) ? b : c;
-    }
-    __syncthreads();
-  }
-  const float q127 = __fdiv_rn(red[0], 127.0f);
+  const float q127 = __fdiv_rn(block_max_nan<T>(mx, red), 127.0f);
   const float s = q127 > 1e-12f ? q127 : (q127 != q127 ? q127 : 1e-12f);  // torch.clamp keeps NaN
   if (threadIdx.x == 0) scales[m] = s;
   int8_t* cr = codes + m * K;
@@ -279,16 +266,7 @@ __device__ __forceinline__ float scale_from_parts(const float* __restrict__ part
     const float v = part[i];
     m = (v > m || v != v) ? v : m;
   }
-  red[threadIdx.x] = m;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (int(threadIdx.x) < o) {
-      const float b = red[threadIdx.x + o], c = red[threadIdx.x];
-      red[threadIdx.x] = (b > c || b != b) ? b : c;
-    }
-    __syncthreads();
-  }
-  return float(double(red[0]) / 240.0);
+  return float(double(block_max_nan<256>(m, red)) / 240.0);
 }
 
 template <int DT>
@@ -296,7 +274,7 @@ __global__ __launch_bounds__(256) void fp8_encode16_kernel(const uint16_t* __res
                                                            int64_t cols, int64_t ld, const float* __restrict__ part,
                                                            int nparts, float* __restrict__ scale,
                                                            uint8_t* __restrict__ codes) {
-  __shared__ float red[256];
+  __shared__ float red[4];
   const float s = scale_from_parts(part, nparts, red);
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale = s;
   const float rs = recip_rn(s);
